@@ -1,0 +1,341 @@
+"""PPO-update throughput on one MI355X.
+
+A "step" is one pass of the PPO update hot path over one synthetic rollout of
+T x N = 2048 x 4096 = 8,388,608 samples (BASELINE config 2's rollout):
+  1. ppo_gae_norm_f32  — GAE with bootstrap + returns + advantage
+                         normalisation (rl/deep/agents/ppo.py:123-127)
+  2. ppo_loss_cat_f32  — fused categorical PPO loss forward+backward over all
+                         B = T*N samples, A = 18 actions, vf_clip = 0.2
+                         (ppo.py:150-169; BASELINE config-4 layout)
+Inputs are resident in HBM before the timed region.  `value` is samples/s
+(B / step time).  `roofline` is for the dominant kernel (the fused loss:
+172 algorithmic bytes per sample), timed with HIP events on the stream it is
+launched on.  `cpu_baseline` times the CPU restatement of the same path
+(oracle/, torch + numpy on the host cores) on a bounded sample.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--suite]
+
+--suite additionally prints one line per BASELINE config (2-5) kernel, for
+the roofline table; the driver's contract line is always the last line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "zero-to-hero_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+T_STEPS, N_ENVS, N_ACTIONS = 2048, 4096, 18
+GAE_BYTES = 21       # r 4 + V 4 + done 1 in; adv 4 + ret 4 + adv_n 4 out
+LOSS_CAT_BYTES = 172  # logits 72 + 6 x 4 per-row inputs in; dlogits 72 + dvalue 4 out
+GAUSS_BYTES = 96     # mu 24 + actions 24 + 5 x 4 in; dmu 24 + dvalue 4 out
+SCAN_BYTES = 17      # r, V, done in; adv, ret out
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--suite", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="wall-clock budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def synthetic_rollout(torch, dev, T, N, A, seed=24):
+    """BASELINE config-2 rollout + config-4 loss inputs, generated on the GPU
+    from a seeded generator."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    B = T * N
+    x = {}
+    x["rewards"] = torch.randn(T, N, device=dev, generator=g)
+    x["values"] = torch.randn(T, N, device=dev, generator=g)
+    x["dones"] = (torch.rand(T, N, device=dev, generator=g) < 0.01).to(torch.uint8)
+    x["last_value"] = torch.randn(N, device=dev, generator=g)
+    logits = torch.randn(B, A, device=dev, generator=g)
+    old_logits = logits + 0.05 * torch.randn(B, A, device=dev, generator=g)
+    u = torch.rand(B, 1, device=dev, generator=g)
+    cdf = torch.softmax(old_logits, -1).cumsum(-1)
+    actions = (cdf < u).sum(-1).clamp_(max=A - 1)
+    x["old_log_probs"] = torch.log_softmax(old_logits, -1).gather(1, actions[:, None]).squeeze(1)
+    del old_logits, cdf, u
+    x["logits"] = logits
+    x["actions"] = actions.to(torch.int32)
+    x["new_values"] = x["values"].reshape(-1) + 0.1 * torch.randn(B, device=dev, generator=g)
+    return x
+
+
+class Step:
+    """The two C-ABI calls of one update step, on torch's current stream,
+    with preallocated outputs (nothing allocated inside the timed loop)."""
+
+    def __init__(self, torch, lib, x, dev):
+        import ctypes
+
+        from ppo_amd import _lib
+
+        self.torch, self.lib, self.x = torch, lib, x
+        T, N = x["rewards"].shape
+        B, A = x["logits"].shape
+        self.T, self.N, self.B, self.A = T, N, B, A
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.adv = torch.empty(T, N, **f32)
+        self.ret = torch.empty(T, N, **f32)
+        self.adv_n = torch.empty(T, N, **f32)
+        self.stats = torch.empty(2, **f32)
+        self.dlogits = torch.empty(B, A, **f32)
+        self.dvalues = torch.empty(B, **f32)
+        self.scalars = torch.empty(6, **f32)
+        self.ws_gae = torch.zeros(lib.ppo_gae_workspace_bytes(T, N), dtype=torch.uint8, device=dev)
+        self.ws_loss = torch.zeros(lib.ppo_loss_cat_workspace_bytes(B, A), dtype=torch.uint8,
+                                   device=dev)
+        self.params = _lib.LossParams(0.2, 0.2, 0.5, 0.01)
+        self.params_ref = ctypes.byref(self.params)
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def gae(self):
+        x = self.x
+        rc = self.lib.ppo_gae_norm_f32(
+            x["rewards"].data_ptr(), x["values"].data_ptr(), x["dones"].data_ptr(),
+            x["last_value"].data_ptr(), self.T, self.N, 0.99, 0.95, 1e-8,
+            self.adv.data_ptr(), self.ret.data_ptr(), self.adv_n.data_ptr(),
+            self.stats.data_ptr(), self.ws_gae.data_ptr(), self.ws_gae.numel(), self.stream)
+        if rc:
+            raise RuntimeError(f"ppo_gae_norm_f32 returned {rc}")
+
+    def loss(self):
+        x = self.x
+        rc = self.lib.ppo_loss_cat_f32(
+            x["logits"].data_ptr(), self.B, self.A, x["actions"].data_ptr(), 0,
+            x["old_log_probs"].data_ptr(), self.adv_n.data_ptr(), self.ret.data_ptr(),
+            x["new_values"].data_ptr(), x["values"].data_ptr(), self.params_ref,
+            self.dlogits.data_ptr(), self.dvalues.data_ptr(), self.scalars.data_ptr(),
+            self.ws_loss.data_ptr(), self.ws_loss.numel(), self.stream)
+        if rc:
+            raise RuntimeError(f"ppo_loss_cat_f32 returned {rc}")
+
+
+def read_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    profiles/<name>.md (a line 'traffic_bytes_per_launch: <int>'), or None."""
+    path = os.path.join(ROOT, "profiles", f"{name}.md")
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def cpu_baseline(torch, x, budget_s):
+    """The oracle's CPU path (GAE reverse loop vectorised over envs, torch
+    normalisation, torch Categorical loss + autograd) on a bounded sample:
+    the first `n_env` env columns of the same rollout over all T steps, and
+    their T*n_env loss rows.  Repeats until `budget_s` seconds are used."""
+    import numpy as np
+
+    from oracle import ppo_oracle as ref
+
+    T, N = x["rewards"].shape
+    n_env = 128
+    B = T * n_env
+    cols = slice(0, n_env)
+    r = x["rewards"][:, cols].cpu().numpy()
+    v = x["values"][:, cols].cpu().numpy()
+    d = x["dones"][:, cols].cpu().numpy()
+    lv = x["last_value"][cols].cpu().numpy()
+    rows = (torch.arange(T)[:, None] * N + torch.arange(n_env)[None, :]).reshape(-1)
+    rows_d = rows.to(x["logits"].device)
+    logits = x["logits"][rows_d].cpu()
+    actions = x["actions"][rows_d].cpu()
+    old_lp = x["old_log_probs"][rows_d].cpu()
+    new_v = x["new_values"][rows_d].cpu()
+    old_v = torch.from_numpy(np.ascontiguousarray(v)).reshape(-1)
+    done_samples, t0 = 0, time.perf_counter()
+    reps = 0
+    while True:
+        ref.cpu_update_step(r, v, d, lv, logits, actions, old_lp, new_v, old_v,
+                            vf_clip=0.2)
+        done_samples += B
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {
+        "value": done_samples / dt,
+        "unit": "samples/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{reps} x (T={T} x {n_env} envs = {B} samples: GAE+norm+loss fwd/bwd, A=18)",
+        "os_cpu_count": os.cpu_count(),
+        "affinity_cores": len(os.sched_getaffinity(0)),
+    }
+
+
+def time_events(torch, fn, reps):
+    """Average duration (s) of fn over `reps` launches, HIP events on the
+    current stream (the stream the kernels are enqueued on)."""
+    s = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps):
+        starts[i].record(s)
+        fn()
+        ends[i].record(s)
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in zip(starts, ends)]
+    return sum(ms) / len(ms) / 1e3
+
+
+def suite(torch, lib, dev):
+    """One line per BASELINE config kernel (2: GAE+norm, 3: long-T scan,
+    4: discrete loss, 5: Gaussian loss)."""
+    import ppo_amd
+
+    out = []
+    g = torch.Generator(device=dev).manual_seed(24)
+    # config 2
+    T, N = 2048, 4096
+    r = torch.randn(T, N, device=dev, generator=g)
+    v = torch.randn(T, N, device=dev, generator=g)
+    d = (torch.rand(T, N, device=dev, generator=g) < 0.01).to(torch.uint8)
+    lv = torch.randn(N, device=dev, generator=g)
+    t = time_events(torch, lambda: ppo_amd.gae_normalize(r, v, d, lv), 30)
+    out.append(("config2_gae_norm", T * N, GAE_BYTES, t))
+    t = time_events(torch, lambda: ppo_amd.gae(r, v, d, lv), 30)
+    out.append(("config2_gae_only", T * N, SCAN_BYTES, t))
+    del r, v, d
+    # config 3
+    T, N = 1_048_576, 16
+    r = torch.randn(T, N, device=dev, generator=g)
+    v = torch.randn(T, N, device=dev, generator=g)
+    d = (torch.rand(T, N, device=dev, generator=g) < 0.001).to(torch.uint8)
+    lv = torch.randn(N, device=dev, generator=g)
+    t = time_events(torch, lambda: ppo_amd.gae(r, v, d, lv, 0.999, 0.95), 30)
+    out.append(("config3_long_scan", T * N, SCAN_BYTES, t))
+    del r, v, d
+    # config 4
+    B, A = 1_048_576, 18
+    x = synthetic_rollout(torch, dev, 256, 4096, A, seed=25)
+    args = (x["logits"], x["actions"], x["old_log_probs"], x["rewards"].reshape(-1),
+            x["values"].reshape(-1), x["new_values"], x["values"].reshape(-1), 0.2, 0.2)
+    t = time_events(torch, lambda: ppo_amd.ppo_loss_discrete_fused(*args), 30)
+    out.append(("config4_loss_cat", B, LOSS_CAT_BYTES, t))
+    del x, args
+    # config 5
+    B, D = 2_097_152, 6
+    mu = torch.randn(B, D, device=dev, generator=g)
+    ls = torch.rand(D, device=dev, generator=g) - 1.0
+    acts = mu + 0.05 * torch.randn(B, D, device=dev, generator=g) + ls.exp() * torch.randn(
+        B, D, device=dev, generator=g)
+    olp = torch.randn(B, device=dev, generator=g) - 5.0
+    advb = torch.randn(B, device=dev, generator=g)
+    retb = torch.randn(B, device=dev, generator=g)
+    ov = torch.randn(B, device=dev, generator=g)
+    nv = ov + 0.1 * torch.randn(B, device=dev, generator=g)
+    t = time_events(torch, lambda: ppo_amd.ppo_loss_gaussian_fused(
+        mu, ls, acts, olp, advb, retb, nv, ov, 0.2, 0.2), 30)
+    out.append(("config5_loss_gauss", B, GAUSS_BYTES, t))
+    for name, units, bpu, t in out:
+        gbs = units * bpu / t / 1e9
+        print(json.dumps({"suite": name, "units": units, "bytes_per_unit": bpu,
+                          "us": round(t * 1e6, 2), "GB/s": round(gbs, 1),
+                          "frac": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build has no "
+              "multi-GPU path; run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import ppo_amd
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (no CPU fallback)", file=sys.stderr)
+        sys.exit(2)
+    lib = ppo_amd.load_library()
+    dev = torch.device("cuda:0")
+    if args.suite:
+        suite(torch, lib, dev)
+        torch.cuda.empty_cache()
+
+    x = synthetic_rollout(torch, dev, T_STEPS, N_ENVS, N_ACTIONS)
+    step = Step(torch, lib, x, dev)
+    B = step.B
+
+    def one_step():
+        step.gae()
+        step.loss()
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed / args.steps * 1e3
+
+    # per-kernel HIP-event timing on the launch stream
+    t_loss = time_events(torch, step.loss, max(args.steps, 20))
+    t_gae = time_events(torch, step.gae, max(args.steps, 20))
+    achieved = LOSS_CAT_BYTES * B / t_loss / 1e9
+    traffic = read_traffic("loss_cat_north_star")
+
+    cpu = None if args.no_cpu else cpu_baseline(torch, x, args.cpu_seconds)
+
+    line = {
+        "metric": "PPO-update samples/sec (T×N=8M) + achieved HBM GB/s vs ~8 TB/s peak",
+        "value": B / (ms_per_step / 1e3),
+        "unit": "samples/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 (GAE recurrence in f64)",
+        "data": "synthetic (seeded, BASELINE config-2 rollout + config-4 loss inputs)",
+        "config": {
+            "workload": "GAE+normalize (T=2048 x N=4096) + fused discrete PPO loss fwd/bwd "
+                        "(B=8,388,608, A=18, vf_clip=0.2)",
+            "T": T_STEPS, "N": N_ENVS, "A": N_ACTIONS, "samples_per_step": B,
+        },
+        "roofline": {
+            "kernel": "ppo_loss_cat_f32 (loss_cat_kernel)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_sample": LOSS_CAT_BYTES,
+            "avg_launch_us": round(t_loss * 1e6, 2),
+        },
+        "gae_norm": {
+            "avg_call_us": round(t_gae * 1e6, 2),
+            "achieved_GBs": round(GAE_BYTES * B / t_gae / 1e9, 1),
+            "frac": round(GAE_BYTES * B / t_gae / 1e9 / HBM_PEAK_GBS, 4),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,184 @@
+/*
+ * ppo_amd.h — C ABI of the MI355X (gfx950) PPO-update library `libppo_amd.so`.
+ *
+ * The reference (mrhooray/zero-to-hero, rl/deep) has no FFI: its PPO update is
+ * the Python method surface of `PPOAgent` (rl/deep/agents/ppo.py:113-193).  Each
+ * entry point below replaces one piece of that surface; the citation above each
+ * declaration names the reference lines whose arithmetic it performs.  The
+ * Python host package (`ppo_amd`) binds these symbols with ctypes and keeps the
+ * reference's method names and signatures on top of them.
+ *
+ * Conventions shared by every entry point
+ *   - All array pointers are DEVICE pointers owned by the caller.  Nothing here
+ *     allocates or frees memory.
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Every call only
+ *     enqueues work on that stream: no host synchronisation, no device-wide
+ *     synchronisation.
+ *   - `workspace` is caller-owned device scratch of at least the size returned
+ *     by the matching *_workspace_bytes() query.  Its first 256 bytes hold
+ *     completion counters: they must be zero before the FIRST call that uses a
+ *     workspace, and every call leaves them zero again.  Two calls that share
+ *     one workspace must be ordered (same stream, or synchronised).
+ *   - Layouts are dense and row-major.  Rollout arrays are "[T,N]
+ *     env-contiguous": element (t, n) lives at index t*N + n.
+ *   - Return value: PPO_OK (0) or one of the PPO_ERR_* codes; codes
+ *     >= PPO_ERR_HIP_BASE are PPO_ERR_HIP_BASE + hipError_t of a failed launch.
+ *     ppo_amd_strerror() renders any of them.
+ */
+#ifndef PPO_AMD_H
+#define PPO_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PPO_OK 0
+#define PPO_ERR_INVALID_ARG 1     /* null pointer, negative size, bad coefficient */
+#define PPO_ERR_WORKSPACE 2       /* workspace missing or smaller than required */
+#define PPO_ERR_TOO_LARGE 3       /* size beyond what the kernels index (2^31 rows) */
+#define PPO_ERR_HIP_BASE 1000     /* + hipError_t */
+
+/* Library version, as MAJOR*10000 + MINOR*100 + PATCH. */
+int ppo_amd_version(void);
+
+/* Human-readable text for a return code (static storage). */
+const char* ppo_amd_strerror(int code);
+
+/* ------------------------------------------------------------------------ */
+/* GAE — generalized advantage estimation over a [T,N] rollout.             */
+/* ------------------------------------------------------------------------ */
+
+/* Scratch needed by ppo_gae_f32 / ppo_gae_norm_f32 for a T x N rollout. */
+size_t ppo_gae_workspace_bytes(int64_t T, int64_t N);
+
+/*
+ * Replaces PPOAgent._advantages (rl/deep/agents/ppo.py:173-193) together with
+ * `returns = advantages + old_values` (ppo.py:124), generalised from one
+ * episode to N independent environments with a bootstrap value.
+ *
+ * For each env n, walking t from T-1 down to 0 (Python float64 semantics of
+ * ppo.py:177-190, evaluated in fp64 in the same operation order):
+ *     mask   = 1 - dones[t,n]                      (dones: 0/1 bytes)
+ *     next_v = t+1 < T ? values[t+1,n] : last_value[n]
+ *     delta  = (rewards[t,n] + (gamma*next_v)*mask) - values[t,n]
+ *     adv    = delta + ((gamma*lam)*mask)*adv      (adv = 0 after step T-1)
+ *     adv_out[t,n] = (float)adv
+ *     ret_out[t,n] = adv_out[t,n] + values[t,n]    (fp32 add, as ppo.py:124)
+ * last_value may be NULL, meaning zeros: that is the reference's own
+ * end-of-episode rule (ppo.py:175-176, `next_value = 0.0`).
+ * A non-zero byte in dones counts as done.  ret_out may be NULL.
+ */
+int ppo_gae_f32(const float* rewards, const float* values, const uint8_t* dones,
+                const float* last_value, int64_t T, int64_t N, double gamma,
+                double lam, float* adv_out, float* ret_out, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/*
+ * ppo_gae_f32 followed by advantage normalisation over all T*N advantages
+ * (ppo.py:126-127):  if T*N > 1,
+ *     adv_norm_out = (adv - mean(adv)) / (std(adv) + eps)     [std unbiased]
+ * else adv_norm_out = adv.  mean and std are accumulated in fp64 during the
+ * GAE pass and rounded to fp32; the final expression is evaluated in fp32.
+ * adv_norm_out may alias adv_out (normalisation in place, unnormalised
+ * advantages then lost).  stats_out (may be NULL) receives {mean, std} as two
+ * floats.
+ */
+int ppo_gae_norm_f32(const float* rewards, const float* values,
+                     const uint8_t* dones, const float* last_value, int64_t T,
+                     int64_t N, double gamma, double lam, double eps,
+                     float* adv_out, float* ret_out, float* adv_norm_out,
+                     float* stats_out, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Advantage normalisation on its own.                                      */
+/* ------------------------------------------------------------------------ */
+
+size_t ppo_adv_norm_workspace_bytes(int64_t n);
+
+/*
+ * Replaces ppo.py:126-127:
+ *     if n > 1: out = (adv - adv.mean()) / (adv.std() + eps)  (unbiased std)
+ *     else:     out = adv
+ * out may alias adv.  stats_out (may be NULL) receives {mean, std}.
+ */
+int ppo_adv_norm_f32(const float* adv, int64_t n, double eps, float* out,
+                     float* stats_out, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Fused PPO loss, forward and backward in one pass.                        */
+/* ------------------------------------------------------------------------ */
+
+typedef struct ppo_loss_params {
+  /* Doubles, like the Python floats of PPOConfig; the kernels round them to
+     fp32 where torch's scalar-tensor arithmetic does. */
+  double clip_ratio;    /* PPOConfig.clip_ratio (ppo.py:18), epsilon of the clip */
+  double vf_clip;       /* value clipping range; <= 0 or +inf disables it      */
+  double value_coef;    /* PPOConfig.value_coef (ppo.py:20)                     */
+  double entropy_coef;  /* PPOConfig.entropy_coef (ppo.py:21)                   */
+} ppo_loss_params;
+
+/* Index of each reported scalar inside scalars_out[PPO_NUM_SCALARS]. */
+#define PPO_SCALAR_LOSS 0        /* total loss (ppo.py:163-167)               */
+#define PPO_SCALAR_POLICY 1      /* mean clipped-surrogate loss               */
+#define PPO_SCALAR_VALUE 2       /* value loss (mse, or clipped mse)          */
+#define PPO_SCALAR_ENTROPY 3     /* mean entropy                              */
+#define PPO_SCALAR_APPROX_KL 4   /* mean(old_log_prob - log_prob)             */
+#define PPO_SCALAR_CLIPFRAC 5    /* fraction of rows with |ratio-1| > clip     */
+#define PPO_NUM_SCALARS 6
+
+size_t ppo_loss_cat_workspace_bytes(int64_t B, int32_t A);
+
+/*
+ * Replaces the loss part of PPOAgent._update_batch (rl/deep/agents/ppo.py:150-167)
+ * and its backward (ppo.py:169) down to the policy logits and the value head:
+ *   dist     = Categorical(logits)          (logits [B,A])
+ *   lp       = dist.log_prob(actions)       (actions [B], int32 or int64)
+ *   ratio    = exp(lp - old_log_probs)
+ *   policy   = -minimum(ratio*adv, clamp(ratio, 1-clip, 1+clip)*adv)
+ *   value    = mse_loss(values, returns)              when vf_clip disabled
+ *            = mean(maximum((v-R)^2, (v_old + clamp(v-v_old,-c,c) - R)^2))
+ *   loss     = mean(policy) + value_coef*value - entropy_coef*mean(entropy)
+ * Writes dloss/dlogits [B,A] and dloss/dvalues [B] (torch autograd
+ * semantics, including the 1/2-1/2 split of minimum/maximum ties and the
+ * inclusive clamp bounds) and scalars_out[PPO_NUM_SCALARS].
+ * old_values may be NULL when vf_clip is disabled.  An action outside [0,A)
+ * makes that row's log-prob NaN (the host layer validates, as torch does).
+ */
+int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A,
+                     const void* actions, int actions_are_int64,
+                     const float* old_log_probs, const float* advantages,
+                     const float* returns, const float* values,
+                     const float* old_values, const ppo_loss_params* params,
+                     float* dlogits, float* dvalues, float* scalars_out,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+size_t ppo_loss_gauss_workspace_bytes(int64_t B, int32_t D);
+
+/*
+ * Gaussian-policy counterpart (no reference code: the reference policy is
+ * categorical only, ppo.py:150).  dist = Normal(mu, exp(log_std)) with a
+ * state-independent log_std[D]; log-prob and entropy are summed over the D
+ * action dims (torch Normal.log_prob / Normal.entropy); the rest of the loss
+ * is ppo_loss_cat_f32's.  Writes dmu [B,D], dlog_std [D] (a reduction over B),
+ * dvalues [B] and scalars_out[PPO_NUM_SCALARS].  D <= 24 (PPO_ERR_TOO_LARGE
+ * otherwise).
+ */
+int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t B,
+                       int32_t D, const float* actions,
+                       const float* old_log_probs, const float* advantages,
+                       const float* returns, const float* values,
+                       const float* old_values, const ppo_loss_params* params,
+                       float* dmu, float* dlog_std, float* dvalues,
+                       float* scalars_out, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PPO_AMD_H */

@@ -1,0 +1,160 @@
+"""GPU parity of the GAE kernels (ppo_gae_f32 / ppo_gae_norm_f32) against the
+CPU oracle (oracle/gae_ref.c: the reference recurrence, ppo.py:173-193, in
+fp64 with the reference's operation order).
+
+Tolerance: the kernel evaluates the same fp64 recurrence in the same order;
+only the carries entering each thread's segment are composed with a scan
+(reassociated fp64), so outputs may differ from the oracle by at most one
+fp32 ulp, or by 1e-9 absolute where the fp32 result is a near-cancellation.
+BASELINE's bar (rel 1e-5) is far looser.  Returns = advantages + values must
+then match bit for bit wherever the advantages do.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import ppo_amd
+from oracle import ppo_oracle as ref
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _c_oracle():
+    ref.build_c()
+
+
+def _inputs(T, N, p_done, seed, last=True):
+    g = torch.Generator().manual_seed(seed)
+    r = torch.randn(T, N, generator=g)
+    v = torch.randn(T, N, generator=g)
+    d = (torch.rand(T, N, generator=g) < p_done).to(torch.uint8)
+    lv = torch.randn(N, generator=g) if last else None
+    return r, v, d, lv
+
+
+def assert_gae_close(adv, adv_ref):
+    adv = np.asarray(adv, dtype=np.float32)
+    adv_ref = np.asarray(adv_ref, dtype=np.float32)
+    assert adv.shape == adv_ref.shape
+    ulp = np.abs(adv.view(np.int32).astype(np.int64) - adv_ref.view(np.int32).astype(np.int64))
+    absdiff = np.abs(adv.astype(np.float64) - adv_ref.astype(np.float64))
+    bad = (ulp > 1) & (absdiff > 1e-9)
+    assert not bad.any(), (
+        f"{int(bad.sum())} elements off by >1 ulp; worst abs {absdiff.max():.3e} "
+        f"at {np.unravel_index(absdiff.argmax(), absdiff.shape)}"
+    )
+    return float((ulp == 0).mean())
+
+
+def _run(dev, T, N, p, seed, gamma=0.99, lam=0.95, last=True):
+    r, v, d, lv = _inputs(T, N, p, seed, last)
+    print(f"gae T={T} N={N} p={p} seed={seed} last={last}", flush=True)
+    adv, ret = ppo_amd.gae(r.to(dev), v.to(dev), d.to(dev),
+                           None if lv is None else lv.to(dev), gamma, lam)
+    a_ref, r_ref = ref.gae_c(r.numpy(), v.numpy(), d.numpy(),
+                             None if lv is None else lv.numpy(), gamma, lam)
+    exact = assert_gae_close(adv.cpu().numpy(), a_ref)
+    # returns are the fp32 sum of the (checked) advantages and the values
+    np.testing.assert_array_equal(ret.cpu().numpy(), adv.cpu().numpy() + v.numpy())
+    return exact
+
+
+def test_reference_known_answer_n1(dev):
+    """rl/deep/tests/test_ppo.py:34-44 through the GPU kernel."""
+    with open(os.path.join(GOLDEN, "reference_kat.json")) as f:
+        kat = json.load(f)
+    r = torch.tensor(kat["rewards"], device=dev)
+    v = torch.tensor(kat["values"], device=dev)
+    d = torch.tensor([a or b for a, b in zip(kat["terminated"], kat["truncated"])],
+                     dtype=torch.bool, device=dev)
+    adv, ret = ppo_amd.gae(r, v, d, None, kat["gamma"], kat["gae_lambda"])
+    assert adv.cpu().tolist() == pytest.approx(kat["advantages"])
+    a_ref = ref.advantages_python(kat["rewards"], d.cpu().tolist(), kat["values"],
+                                  kat["gamma"], kat["gae_lambda"])
+    np.testing.assert_array_equal(adv.cpu().numpy(), np.array(a_ref, np.float32))
+
+
+def test_golden_fixture(dev):
+    z = np.load(os.path.join(GOLDEN, "gae_small.npz"))
+    t = lambda k: torch.from_numpy(z[k]).to(dev)  # noqa: E731
+    adv, ret, adv_n = ppo_amd.gae_normalize(t("rewards"), t("values"), t("dones"),
+                                            t("last_value"), float(z["gamma"]), float(z["lam"]))
+    np.testing.assert_array_equal(adv.cpu().numpy(), z["adv"])
+    np.testing.assert_array_equal(ret.cpu().numpy(), z["ret"])
+    np.testing.assert_allclose(adv_n.cpu().numpy(), z["adv_norm"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize(
+    "T,N,p",
+    [
+        (1, 1, 0.0), (1, 1, 1.0), (2, 1, 0.0), (5, 1, 0.2), (300, 1, 0.01),
+        (5000, 1, 0.001),                     # N=1 across several tiles (scalar path)
+        (37, 3, 0.1), (129, 7, 0.05),         # N not a multiple of 4
+        (1, 4, 0.0), (33, 4, 0.1), (100, 8, 0.05), (128, 8, 0.005),
+        (64, 12, 0.3), (513, 16, 0.01), (2000, 16, 0.001),
+        (7, 260, 0.1), (65, 1028, 0.02), (257, 4096, 0.01),
+    ],
+)
+def test_gae_matches_oracle(dev, T, N, p):
+    _run(dev, T, N, p, seed=T * 7919 + N)
+
+
+@pytest.mark.parametrize("p", [0.0, 1.0])
+def test_gae_all_or_no_dones(dev, p):
+    _run(dev, 700, 20, p, seed=3)
+
+
+def test_gae_without_bootstrap(dev):
+    _run(dev, 1000, 12, 0.01, seed=4, last=False)
+
+
+def test_gae_misaligned_buffers(dev):
+    """Views that start one element into an allocation are not 16-byte
+    aligned: the kernel must take its scalar path and still agree."""
+    T, N = 300, 8
+    r, v, d, lv = _inputs(T, N, 0.05, seed=9)
+    rb = torch.empty(T * N + 1, device=dev)
+    vb = torch.empty(T * N + 1, device=dev)
+    db = torch.empty(T * N + 1, dtype=torch.uint8, device=dev)
+    rb[1:] = r.reshape(-1).to(dev)
+    vb[1:] = v.reshape(-1).to(dev)
+    db[1:] = d.reshape(-1).to(dev)
+    adv, ret = ppo_amd.gae(rb[1:].view(T, N), vb[1:].view(T, N), db[1:].view(T, N),
+                           lv.to(dev), 0.99, 0.95)
+    a_ref, _ = ref.gae_c(r.numpy(), v.numpy(), d.numpy(), lv.numpy(), 0.99, 0.95)
+    assert_gae_close(adv.cpu().numpy(), a_ref)
+
+
+def test_gae_nonzero_done_bytes_count_as_done(dev):
+    T, N = 50, 4
+    r, v, d, lv = _inputs(T, N, 0.2, seed=10)
+    d2 = d * torch.randint(1, 255, (T, N), dtype=torch.uint8)
+    a1, _ = ppo_amd.gae(r.to(dev), v.to(dev), d.to(dev), lv.to(dev))
+    a2, _ = ppo_amd.gae(r.to(dev), v.to(dev), d2.to(dev), lv.to(dev))
+    torch.testing.assert_close(a1, a2, rtol=0, atol=0)
+
+
+def test_gae_config2_full_size(dev):
+    """T=2048, N=4096, dones Bernoulli(0.01)."""
+    exact = _run(dev, 2048, 4096, 0.01, seed=24)
+    assert exact > 0.99
+
+
+def test_gae_config3_full_size(dev):
+    """T=1,048,576, N=16, dones Bernoulli(0.001), gamma .999."""
+    exact = _run(dev, 1_048_576, 16, 0.001, seed=24, gamma=0.999, lam=0.95)
+    assert exact > 0.99
+
+
+def test_gae_repeatable(dev):
+    r, v, d, lv = _inputs(1024, 64, 0.01, seed=12)
+    args = (r.to(dev), v.to(dev), d.to(dev), lv.to(dev))
+    a1, _, n1 = ppo_amd.gae_normalize(*args)
+    a2, _, n2 = ppo_amd.gae_normalize(*args)
+    assert torch.equal(a1, a2) and torch.equal(n1, n2)

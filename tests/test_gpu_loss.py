@@ -1,0 +1,231 @@
+"""GPU parity of the fused PPO loss kernels against the reference loss and
+torch autograd on the CPU (oracle.loss_categorical_reference /
+loss_gaussian_reference, which run ppo.py:150-169's own torch calls).
+
+Tolerances (BASELINE): loss scalars rel 1e-5; gradients rel 1e-4 per element
+with an absolute floor of 1e-5 * max|g_ref| for elements near zero (the
+gradient of a softmax row sums to zero, so some entries are cancellations).
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import ppo_amd
+from oracle import ppo_oracle as ref
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+NAMES = ("loss", "policy", "value", "entropy", "approx_kl", "clipfrac")
+
+
+def assert_grad_close(got, expect, rtol=1e-4, floor=1e-5):
+    got = got.detach().cpu().double()
+    expect = expect.detach().cpu().double()
+    atol = floor * float(expect.abs().max()) if expect.numel() else 0.0
+    torch.testing.assert_close(got, expect, rtol=rtol, atol=atol)
+
+
+def assert_scalars_close(scalars, o, rtol=1e-5):
+    s = scalars.detach().cpu()
+    for i, k in enumerate(NAMES):
+        e = o[k].item()
+        assert s[i].item() == pytest.approx(e, rel=rtol, abs=1e-7), k
+
+
+def cat_inputs(B, A, seed, act_dtype=torch.int32):
+    """BASELINE config-4 distributions: logits ~ N(0,1); actions sampled from
+    softmax(old_logits), old_logits = logits + N(0, 0.05); adv, ret, old
+    values ~ N(0,1); values = old values + N(0, 0.1)."""
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(B, A, generator=g)
+    old_logits = logits + 0.05 * torch.randn(B, A, generator=g)
+    actions = torch.multinomial(torch.softmax(old_logits, -1), 1, generator=g).squeeze(1)
+    old_lp = torch.log_softmax(old_logits, -1).gather(1, actions[:, None]).squeeze(1)
+    adv = torch.randn(B, generator=g)
+    ret = torch.randn(B, generator=g)
+    old_v = torch.randn(B, generator=g)
+    val = old_v + 0.1 * torch.randn(B, generator=g)
+    return logits, actions.to(act_dtype), old_lp, adv, ret, val, old_v
+
+
+def run_cat(dev, B, A, seed, vf_clip=0.2, act_dtype=torch.int32, inputs=None):
+    inp = inputs if inputs is not None else cat_inputs(B, A, seed, act_dtype)
+    logits, actions, old_lp, adv, ret, val, old_v = inp
+    print(f"loss_cat B={B} A={A} vf_clip={vf_clip} act={actions.dtype}", flush=True)
+    scalars, dlogits, dvalues = ppo_amd.ppo_loss_discrete_fused(
+        logits.to(dev), actions.to(dev), old_lp.to(dev), adv.to(dev), ret.to(dev),
+        val.to(dev), old_v.to(dev), 0.2, vf_clip, 0.5, 0.01,
+    )
+    o = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val, old_v,
+                                       0.2, vf_clip, 0.5, 0.01)
+    assert_scalars_close(scalars, o)
+    assert_grad_close(dlogits, o["dlogits"])
+    assert_grad_close(dvalues, o["dvalues"])
+    return scalars, dlogits, dvalues
+
+
+def test_golden_fixture_cat(dev):
+    z = np.load(os.path.join(GOLDEN, "loss_cat_small.npz"))
+    t = lambda k: torch.from_numpy(z[k]).to(dev)  # noqa: E731
+    scalars, dlogits, dvalues = ppo_amd.ppo_loss_discrete_fused(
+        t("logits"), t("actions"), t("old_log_probs"), t("advantages"), t("returns"),
+        t("values"), t("old_values"), float(z["clip_ratio"]), float(z["vf_clip"]),
+        float(z["value_coef"]), float(z["entropy_coef"]),
+    )
+    np.testing.assert_allclose(scalars.cpu().numpy(), z["scalars"], rtol=1e-5, atol=1e-7)
+    assert_grad_close(dlogits, torch.from_numpy(z["dlogits"]))
+    assert_grad_close(dvalues, torch.from_numpy(z["dvalues"]))
+
+
+@pytest.mark.parametrize("B,A", [(1, 2), (7, 2), (256, 2), (257, 18), (1000, 18), (3, 1),
+                                 (300, 5), (511, 33), (777, 48)])
+@pytest.mark.parametrize("vf_clip", [None, 0.2])
+def test_cat_row_kernel(dev, B, A, vf_clip):
+    run_cat(dev, B, A, seed=B * 131 + A, vf_clip=vf_clip)
+
+
+@pytest.mark.parametrize("B,A", [(5, 49), (300, 64), (300, 100), (1025, 257)])
+def test_cat_wave_kernel(dev, B, A):
+    """A > 64 goes through the wave-per-row kernel."""
+    run_cat(dev, B, A, seed=B + A, vf_clip=0.2)
+
+
+def test_cat_int64_actions(dev):
+    run_cat(dev, 1000, 18, seed=3, act_dtype=torch.int64)
+
+
+def test_cat_ties_and_zero_advantage(dev):
+    """ratio == 1 exactly (old_lp == lp) and adv == 0 rows hit the 1/2-1/2
+    tie rule of torch.minimum; v - v_old at the clip bound hits clamp's
+    inclusive edge."""
+    B, A = 512, 6
+    logits, actions, old_lp, adv, ret, val, old_v = cat_inputs(B, A, seed=4)
+    lp = torch.log_softmax(logits, -1).gather(1, actions.long()[:, None]).squeeze(1)
+    old_lp[: B // 2] = lp[: B // 2]
+    adv[::7] = 0.0
+    run_cat(dev, B, A, seed=0, inputs=(logits, actions, old_lp, adv, ret, val, old_v))
+
+
+def test_cat_misaligned_logits(dev):
+    B, A = 300, 18
+    inp = cat_inputs(B, A, seed=6)
+    logits = inp[0]
+    buf = torch.empty(B * A + 1, device=dev)
+    buf[1:] = logits.reshape(-1).to(dev)
+    lg = buf[1:].view(B, A)
+    _, actions, old_lp, adv, ret, val, old_v = inp
+    scalars, dlogits, dvalues = ppo_amd.ppo_loss_discrete_fused(
+        lg, actions.to(dev), old_lp.to(dev), adv.to(dev), ret.to(dev), val.to(dev), None,
+    )
+    o = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val)
+    assert_scalars_close(scalars, o)
+    assert_grad_close(dlogits, o["dlogits"])
+
+
+def test_cat_config4_full_size(dev):
+    """B=1,048,576, A=18, vf_clip=0.2."""
+    scalars, dlogits, _ = run_cat(dev, 1_048_576, 18, seed=24, vf_clip=0.2)
+    # size-independent invariant: each softmax row of the gradient sums to 0
+    rows = dlogits.double().sum(1).abs().max().item()
+    assert rows < 1e-9
+
+
+def test_cat_autograd_matches_fused(dev):
+    B, A = 999, 4
+    logits, actions, old_lp, adv, ret, val, old_v = cat_inputs(B, A, seed=8)
+    lg = logits.to(dev).requires_grad_(True)
+    vv = val.to(dev).requires_grad_(True)
+    loss, stats = ppo_amd.ppo_loss_discrete(lg, actions.to(dev), old_lp.to(dev), adv.to(dev),
+                                            ret.to(dev), vv)
+    (2.0 * loss).backward()
+    o = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val)
+    assert loss.item() == pytest.approx(o["loss"].item(), rel=1e-5)
+    assert_grad_close(lg.grad, 2.0 * o["dlogits"])
+    assert_grad_close(vv.grad, 2.0 * o["dvalues"])
+    assert stats["entropy"].item() == pytest.approx(o["entropy"].item(), rel=1e-5)
+
+
+def test_cat_out_of_range_action(dev):
+    B, A = 16, 3
+    logits, actions, old_lp, adv, ret, val, _ = cat_inputs(B, A, seed=9)
+    actions[5] = 3
+    args = [x.to(dev) for x in (logits, actions, old_lp, adv, ret, val)]
+    with pytest.raises(ValueError):
+        ppo_amd.ppo_loss_discrete_fused(*args, validate_args=True)
+    scalars, _, _ = ppo_amd.ppo_loss_discrete_fused(*args)
+    assert torch.isnan(scalars[0]).item()
+
+
+# ---------------------------------------------------------------------------
+# Gaussian
+# ---------------------------------------------------------------------------
+def gauss_inputs(B, D, seed):
+    """BASELINE config-5 distributions: mu ~ N(0,1); log_std ~ U(-1,0);
+    actions ~ N(mu_old, exp(log_std)), mu_old = mu + N(0, 0.05)."""
+    g = torch.Generator().manual_seed(seed)
+    mu = torch.randn(B, D, generator=g)
+    log_std = torch.rand(D, generator=g) - 1.0
+    mu_old = mu + 0.05 * torch.randn(B, D, generator=g)
+    acts = mu_old + log_std.exp() * torch.randn(B, D, generator=g)
+    old_lp = torch.distributions.Normal(mu_old, log_std.exp()).log_prob(acts).sum(-1)
+    adv = torch.randn(B, generator=g)
+    ret = torch.randn(B, generator=g)
+    old_v = torch.randn(B, generator=g)
+    val = old_v + 0.1 * torch.randn(B, generator=g)
+    return mu, log_std, acts, old_lp, adv, ret, val, old_v
+
+
+def run_gauss(dev, B, D, seed, vf_clip=0.2):
+    inp = gauss_inputs(B, D, seed)
+    print(f"loss_gauss B={B} D={D} vf_clip={vf_clip}", flush=True)
+    mu, log_std, acts, old_lp, adv, ret, val, old_v = inp
+    scalars, dmu, dls, dv = ppo_amd.ppo_loss_gaussian_fused(
+        *[x.to(dev) for x in inp], 0.2, vf_clip, 0.5, 0.01
+    )
+    o = ref.loss_gaussian_reference(*inp, 0.2, vf_clip, 0.5, 0.01)
+    assert_scalars_close(scalars, o)
+    assert_grad_close(dmu, o["dmu"])
+    assert_grad_close(dls, o["dlog_std"])
+    assert_grad_close(dv, o["dvalues"])
+
+
+def test_golden_fixture_gauss(dev):
+    z = np.load(os.path.join(GOLDEN, "loss_gauss_small.npz"))
+    t = lambda k: torch.from_numpy(z[k]).to(dev)  # noqa: E731
+    scalars, dmu, dls, dv = ppo_amd.ppo_loss_gaussian_fused(
+        t("mu"), t("log_std"), t("actions"), t("old_log_probs"), t("advantages"),
+        t("returns"), t("values"), t("old_values"), float(z["clip_ratio"]),
+        float(z["vf_clip"]), float(z["value_coef"]), float(z["entropy_coef"]),
+    )
+    np.testing.assert_allclose(scalars.cpu().numpy(), z["scalars"], rtol=1e-5, atol=1e-7)
+    assert_grad_close(dmu, torch.from_numpy(z["dmu"]))
+    assert_grad_close(dls, torch.from_numpy(z["dlog_std"]))
+    assert_grad_close(dv, torch.from_numpy(z["dvalues"]))
+
+
+@pytest.mark.parametrize("B,D", [(1, 1), (5, 6), (256, 6), (1000, 6), (333, 17), (300, 24)])
+@pytest.mark.parametrize("vf_clip", [None, 0.2])
+def test_gauss(dev, B, D, vf_clip):
+    run_gauss(dev, B, D, seed=B * 7 + D, vf_clip=vf_clip)
+
+
+def test_gauss_config5_full_size(dev):
+    """B=2,097,152, D=6, vf_clip=0.2."""
+    run_gauss(dev, 2_097_152, 6, seed=24)
+
+
+def test_gauss_autograd(dev):
+    mu, log_std, acts, old_lp, adv, ret, val, old_v = gauss_inputs(500, 6, seed=11)
+    m = mu.to(dev).requires_grad_(True)
+    ls = log_std.to(dev).requires_grad_(True)
+    vv = val.to(dev).requires_grad_(True)
+    loss, _ = ppo_amd.ppo_loss_gaussian(m, ls, acts.to(dev), old_lp.to(dev), adv.to(dev),
+                                        ret.to(dev), vv)
+    loss.backward()
+    o = ref.loss_gaussian_reference(mu, log_std, acts, old_lp, adv, ret, val)
+    assert_grad_close(m.grad, o["dmu"])
+    assert_grad_close(ls.grad, o["dlog_std"])
+    assert_grad_close(vv.grad, o["dvalues"])

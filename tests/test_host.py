@@ -1,0 +1,93 @@
+"""Host-side logic that needs no GPU: the reference-mirroring surface
+(configs, records, cartpole_sizes, rollout storage) and the ops' argument
+validation, which must raise rather than fall back to the CPU."""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+import ppo_amd
+from ppo_amd.agent import PPOAgent, PPOConfig, TrainingConfig
+
+
+def cartpole_like():
+    return SimpleNamespace(observation_space=SimpleNamespace(shape=(4,)),
+                           action_space=SimpleNamespace(n=2))
+
+
+def test_config_defaults_match_reference():
+    # rl/deep/type.py:30-41 and rl/deep/agents/ppo.py:15-22
+    t = TrainingConfig()
+    assert (t.gamma, t.lr, t.seed, t.hidden_size, t.batch_size) == (0.99, 3e-4, 24, 128, 128)
+    p = PPOConfig()
+    assert (p.epochs, p.clip_ratio, p.gae_lambda, p.value_coef, p.entropy_coef,
+            p.gradient_clip, p.vf_clip) == (4, 0.2, 0.95, 0.5, 0.01, 0.5, None)
+
+
+def test_cartpole_sizes_errors():
+    assert ppo_amd.cartpole_sizes(cartpole_like()) == (4, 2)
+    with pytest.raises(TypeError, match="Box"):
+        ppo_amd.cartpole_sizes(SimpleNamespace(observation_space=None,
+                                               action_space=SimpleNamespace(n=2)))
+    with pytest.raises(TypeError, match="Discrete"):
+        ppo_amd.cartpole_sizes(SimpleNamespace(observation_space=SimpleNamespace(shape=(4,)),
+                                               action_space=SimpleNamespace(shape=(2,))))
+
+
+def test_ppo_stores_rollout_step_after_update():
+    """rl/deep/tests/test_ppo.py:11-31 (acting needs no kernel)."""
+    agent = PPOAgent(cartpole_like(), TrainingConfig(hidden_size=16, seed=24), device="cpu")
+    observation = np.zeros(4, dtype=np.float32)
+    action = agent.select_action(observation)
+    agent.update(observation, action, reward=1.0, next_observation=np.ones(4, np.float32),
+                 terminated=False, truncated=True)
+    assert agent.pending_step is None
+    assert len(agent.rollout) == 1
+    assert agent.rollout[0].transition.truncated
+    assert agent.rollout[0].log_prob.shape == torch.Size([])
+    assert agent.rollout[0].value.shape == torch.Size([])
+
+
+def test_agent_init_matches_reference_init():
+    """Same seed -> the same initial weights as the reference's CPU MLPs."""
+    torch.manual_seed(24)
+    pol = ppo_amd.MLP(4, 16, 2)
+    val = ppo_amd.MLP(4, 16, 1)
+    agent = PPOAgent(cartpole_like(), TrainingConfig(hidden_size=16), device="cpu")
+    for a, b in zip(agent.parameters, list(pol.parameters()) + list(val.parameters())):
+        assert torch.equal(a, b)
+
+
+def test_ops_refuse_cpu_tensors():
+    r = torch.zeros(4, 2)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ppo_amd.gae(r, r, torch.zeros(4, 2, dtype=torch.uint8))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ppo_amd.normalize_advantages(torch.zeros(5))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ppo_amd.ppo_loss_discrete_fused(torch.zeros(3, 2), torch.zeros(3, dtype=torch.int64),
+                                        *[torch.zeros(3)] * 4)
+
+
+def test_agent_update_on_cpu_raises_not_falls_back():
+    agent = PPOAgent(cartpole_like(), TrainingConfig(hidden_size=16), device="cpu")
+    obs = np.zeros(4, np.float32)
+    for _ in range(3):
+        a = agent.select_action(obs)
+        agent.update(obs, a, 1.0, obs, False, False)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        agent.end_episode()
+
+
+def test_rollout_buffer_validation():
+    with pytest.raises(ValueError):
+        ppo_amd.RolloutBuffer(0, 4, (4,), device="cpu")
+    buf = ppo_amd.RolloutBuffer(2, 3, (4,), device="cpu")
+    z = torch.zeros(3)
+    buf.add(torch.zeros(3, 4), torch.zeros(3, dtype=torch.int32), z, z.to(torch.uint8), z, z)
+    buf.add(torch.zeros(3, 4), torch.zeros(3, dtype=torch.int32), z, z.to(torch.uint8), z, z)
+    with pytest.raises(IndexError):
+        buf.add(torch.zeros(3, 4), torch.zeros(3, dtype=torch.int32), z, z.to(torch.uint8), z, z)
+    assert buf.observations.shape == (2, 3, 4) and buf.dones.dtype == torch.uint8

@@ -1,0 +1,344 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the checker.
+
+Each oracle function is checked against something other than itself: the
+reference's own known answer (rl/deep/tests/test_ppo.py:34-44), closed forms,
+an O(T^2) brute-force sum, fp64 finite differences, and invariants chosen so
+that a dropped term, a wrong sign or index, or a swapped operand fails.
+CPU only.
+"""
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ppo_oracle as ref
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _c_oracle():
+    ref.build_c()
+
+
+def _rollout(T, N, p_done, seed, last=True):
+    g = torch.Generator().manual_seed(seed)
+    r = torch.randn(T, N, generator=g).numpy()
+    v = torch.randn(T, N, generator=g).numpy()
+    d = (torch.rand(T, N, generator=g) < p_done).to(torch.uint8).numpy()
+    lv = torch.randn(N, generator=g).numpy() if last else None
+    return r, v, d, lv
+
+
+# ---------------------------------------------------------------------------
+# GAE
+# ---------------------------------------------------------------------------
+def test_reference_known_answer():
+    with open(os.path.join(GOLDEN, "reference_kat.json")) as f:
+        kat = json.load(f)
+    dones = [a or b for a, b in zip(kat["terminated"], kat["truncated"])]
+    got = ref.advantages_python(kat["rewards"], dones, kat["values"], kat["gamma"],
+                                kat["gae_lambda"])
+    assert got == pytest.approx(kat["advantages"])
+    # the [T,N] forms agree on the same episode
+    r = np.array(kat["rewards"], np.float32)[:, None]
+    v = np.array(kat["values"], np.float32)[:, None]
+    d = np.array(dones, np.uint8)[:, None]
+    for fn in (ref.gae_numpy, ref.gae_c):
+        adv, ret = fn(r, v, d, None, kat["gamma"], kat["gae_lambda"])
+        assert adv[:, 0].tolist() == pytest.approx(kat["advantages"])
+        np.testing.assert_array_equal(ret, adv + v)
+
+
+@pytest.mark.parametrize("T,N,p", [(1, 1, 0.0), (17, 1, 0.1), (64, 5, 0.05), (200, 8, 0.3)])
+def test_python_numpy_c_bit_identical(T, N, p):
+    r, v, d, _ = _rollout(T, N, p, seed=T * 31 + N)
+    a_np, r_np = ref.gae_numpy(r, v, d, None, 0.99, 0.95)
+    a_c, r_c = ref.gae_c(r, v, d, None, 0.99, 0.95)
+    np.testing.assert_array_equal(a_np, a_c)
+    np.testing.assert_array_equal(r_np, r_c)
+    for n in range(N):
+        col = ref.advantages_python(
+            [float(x) for x in r[:, n]], d[:, n].tolist(), [float(x) for x in v[:, n]],
+            0.99, 0.95,
+        )
+        np.testing.assert_array_equal(a_np[:, n], np.array(col, dtype=np.float32))
+
+
+def test_bootstrap_value_enters_last_delta():
+    # at t = T-1 the carried advantage is 0 and next_value = last_value
+    r, v, d, lv = _rollout(30, 4, 0.1, seed=5)
+    adv, _ = ref.gae_c(r, v, d, lv, 0.97, 0.9)
+    m = 1.0 - d[-1].astype(np.float64)
+    expect = (r[-1].astype(np.float64) + (0.97 * lv.astype(np.float64)) * m) - v[-1]
+    np.testing.assert_array_equal(adv[-1], expect.astype(np.float32))
+
+
+def test_lambda_zero_is_td_error():
+    r, v, d, lv = _rollout(50, 6, 0.1, seed=1)
+    adv, _ = ref.gae_c(r, v, d, lv, 0.99, 0.0)
+    vn = np.concatenate([v[1:], lv[None]], 0).astype(np.float64)
+    delta = r + 0.99 * vn * (1.0 - d) - v
+    np.testing.assert_allclose(adv, delta.astype(np.float32), rtol=0, atol=2e-7)
+
+
+def test_lambda_one_zero_value_is_discounted_return():
+    # reinforce.py:57-63: value = reward + gamma * value, one episode
+    g = torch.Generator().manual_seed(3)
+    rewards = torch.randn(40, generator=g).numpy()
+    ret = []
+    value = 0.0
+    for reward in reversed(rewards.tolist()):
+        value = reward + 0.95 * value
+        ret.append(value)
+    ret.reverse()
+    adv, _ = ref.gae_c(rewards[:, None], np.zeros((40, 1), np.float32),
+                       np.zeros((40, 1), np.uint8), None, 0.95, 1.0)
+    np.testing.assert_array_equal(adv[:, 0], np.array(ret, dtype=np.float32))
+
+
+def test_all_done_is_reward_minus_value():
+    r, v, _, lv = _rollout(20, 3, 0.0, seed=2)
+    adv, _ = ref.gae_c(r, v, np.ones_like(r, dtype=np.uint8), lv, 0.99, 0.95)
+    np.testing.assert_array_equal(adv, (r.astype(np.float64) - v).astype(np.float32))
+
+
+def test_constant_reward_geometric_series():
+    T, c, gamma, lam = 300, 0.7, 0.99, 0.95
+    r = np.full((T, 1), c, np.float32)
+    adv, _ = ref.gae_c(r, np.zeros((T, 1), np.float32), np.zeros((T, 1), np.uint8),
+                       None, gamma, lam)
+    k = T - np.arange(T)
+    gl = gamma * lam
+    closed = np.float64(c) * (1 - gl ** k) / (1 - gl)
+    np.testing.assert_allclose(adv[:, 0], closed, rtol=2e-6)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_bruteforce_sum(seed):
+    r, v, d, lv = _rollout(25, 3, 0.15, seed=seed)
+    brute = ref.gae_bruteforce(r, v, d, lv, 0.99, 0.95)
+    adv, _ = ref.gae_c(r, v, d, lv, 0.99, 0.95)
+    np.testing.assert_allclose(adv, brute, rtol=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# normalisation
+# ---------------------------------------------------------------------------
+def test_normalize_matches_fp64_formula():
+    g = torch.Generator().manual_seed(7)
+    a = torch.randn(10_000, generator=g) * 3 + 1.5
+    got = ref.normalize_reference(a).numpy()
+    x = a.numpy().astype(np.float64)
+    expect = (x - x.mean()) / (x.std(ddof=1) + 1e-8)
+    np.testing.assert_allclose(got, expect, rtol=2e-5, atol=2e-6)
+    assert abs(float(got.mean())) < 1e-5
+    assert float(got.std(ddof=1)) == pytest.approx(1.0, rel=1e-5)
+
+
+def test_normalize_single_element_identity():
+    a = torch.tensor([3.25])
+    assert ref.normalize_reference(a) is a
+
+
+# ---------------------------------------------------------------------------
+# loss (categorical)
+# ---------------------------------------------------------------------------
+def _cat_inputs(B, A, seed, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(B, A, generator=g, dtype=dtype)
+    actions = torch.randint(0, A, (B,), generator=g)
+    old_lp = torch.log_softmax(logits + 0.3 * torch.randn(B, A, generator=g, dtype=dtype), -1)
+    old_lp = old_lp.gather(1, actions[:, None]).squeeze(1)
+    adv = torch.randn(B, generator=g, dtype=dtype)
+    ret = torch.randn(B, generator=g, dtype=dtype)
+    old_v = torch.randn(B, generator=g, dtype=dtype)
+    val = old_v + 0.3 * torch.randn(B, generator=g, dtype=dtype)
+    return logits, actions, old_lp, adv, ret, val, old_v
+
+
+def _cat_loss_fp64(logits, actions, old_lp, adv, ret, val, old_v, vf_clip):
+    return ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val, old_v,
+                                          0.2, vf_clip, 0.5, 0.01)["loss"].item()
+
+
+@pytest.mark.parametrize("vf_clip", [None, 0.2])
+def test_cat_loss_finite_differences(vf_clip):
+    inp = _cat_inputs(5, 4, seed=11)
+    logits, actions, old_lp, adv, ret, val, old_v = inp
+    o = ref.loss_categorical_reference(*inp, 0.2, vf_clip, 0.5, 0.01)
+    h = 1e-6
+    fd = torch.zeros_like(logits)
+    for i in range(logits.shape[0]):
+        for j in range(logits.shape[1]):
+            lp_, lm_ = logits.clone(), logits.clone()
+            lp_[i, j] += h
+            lm_[i, j] -= h
+            fd[i, j] = (_cat_loss_fp64(lp_, actions, old_lp, adv, ret, val, old_v, vf_clip)
+                        - _cat_loss_fp64(lm_, actions, old_lp, adv, ret, val, old_v, vf_clip)) / (2 * h)
+    torch.testing.assert_close(o["dlogits"], fd, rtol=1e-6, atol=1e-8)
+    fdv = torch.zeros_like(val)
+    for i in range(val.shape[0]):
+        vp, vm = val.clone(), val.clone()
+        vp[i] += h
+        vm[i] -= h
+        fdv[i] = (_cat_loss_fp64(logits, actions, old_lp, adv, ret, vp, old_v, vf_clip)
+                  - _cat_loss_fp64(logits, actions, old_lp, adv, ret, vm, old_v, vf_clip)) / (2 * h)
+    torch.testing.assert_close(o["dvalues"], fdv, rtol=1e-6, atol=1e-8)
+
+
+def test_cat_loss_invariants():
+    B, A = 64, 7
+    logits, actions, old_lp, adv, ret, val, old_v = _cat_inputs(B, A, seed=12)
+    o = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val)
+    # softmax-normalised logits: every row of the gradient sums to zero
+    torch.testing.assert_close(o["dlogits"].sum(1), torch.zeros(B, dtype=torch.float64),
+                               atol=1e-15, rtol=0)
+    # with old log-probs equal to the new ones the ratio is 1: nothing clipped,
+    # kl 0, policy loss = -mean(adv)
+    lp = torch.log_softmax(logits, -1).gather(1, actions[:, None]).squeeze(1)
+    o1 = ref.loss_categorical_reference(logits, actions, lp, adv, ret, val)
+    assert o1["clipfrac"].item() == 0.0
+    assert abs(o1["approx_kl"].item()) < 1e-15
+    assert o1["policy"].item() == pytest.approx(-adv.mean().item(), abs=1e-14)
+    # value loss: no 1/2, mean over rows (ppo.py:160)
+    assert o["value"].item() == pytest.approx(((val - ret) ** 2).mean().item(), rel=1e-14)
+    # vf_clip -> infinity reduces to the plain mse
+    o_big = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val, old_v,
+                                           vf_clip=1e30)
+    assert o_big["value"].item() == pytest.approx(o["value"].item(), rel=1e-14)
+    torch.testing.assert_close(o_big["dvalues"], o["dvalues"])
+    # uniform logits: entropy log(A)
+    ou = ref.loss_categorical_reference(torch.zeros(B, A, dtype=torch.float64), actions,
+                                        old_lp, adv, ret, val)
+    assert ou["entropy"].item() == pytest.approx(math.log(A), rel=1e-14)
+    # total = policy + 0.5 value - 0.01 entropy
+    assert o["loss"].item() == pytest.approx(
+        o["policy"].item() + 0.5 * o["value"].item() - 0.01 * o["entropy"].item(), rel=1e-12)
+
+
+def test_cat_loss_closed_form_gradient():
+    """The closed-form gradient the fused kernel writes, derived by hand
+    (torch minimum ties split 1/2-1/2; clamp passes its inclusive bounds),
+    against the oracle's autograd in fp64."""
+    B, A = 40, 5
+    logits, actions, old_lp, adv, ret, val, old_v = _cat_inputs(B, A, seed=13)
+    # force ties: a few rows with ratio exactly inside and at the clip bound
+    lp = torch.log_softmax(logits, -1).gather(1, actions[:, None]).squeeze(1)
+    old_lp[:4] = lp[:4]
+    adv[4:6] = 0.0
+    o = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val)
+    z = logits.numpy()
+    lse = np.log(np.exp(z - z.max(1, keepdims=True)).sum(1)) + z.max(1)
+    logp = z - lse[:, None]
+    p = np.exp(logp)
+    H = -(p * logp).sum(1)
+    a = actions.numpy()
+    lpa = logp[np.arange(B), a]
+    r = np.exp(lpa - old_lp.numpy())
+    rc = np.clip(r, 0.8, 1.2)
+    A_ = adv.numpy()
+    u, w = r * A_, rc * A_
+    su = np.where(u < w, 1.0, np.where(u == w, 0.5, 0.0))
+    sw = np.where(w < u, 1.0, np.where(u == w, 0.5, 0.0))
+    inr = ((r >= 0.8) & (r <= 1.2)).astype(float)
+    g_lp = -(A_ * (su + sw * inr)) / B * r
+    onehot = np.eye(A)[a]
+    dz = g_lp[:, None] * (onehot - p) + (0.01 / B) * p * (logp + H[:, None])
+    np.testing.assert_allclose(o["dlogits"].numpy(), dz, rtol=1e-10, atol=1e-15)
+    dv = 0.5 * 2 * (val.numpy() - ret.numpy()) / B
+    np.testing.assert_allclose(o["dvalues"].numpy(), dv, rtol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# loss (Gaussian)
+# ---------------------------------------------------------------------------
+def _gauss_inputs(B, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    dt = torch.float64
+    mu = torch.randn(B, D, generator=g, dtype=dt)
+    log_std = torch.rand(D, generator=g, dtype=dt) - 1.0
+    acts = mu + 0.2 * torch.randn(B, D, generator=g, dtype=dt)
+    old_lp = torch.distributions.Normal(mu + 0.05, log_std.exp()).log_prob(acts).sum(-1)
+    adv = torch.randn(B, generator=g, dtype=dt)
+    ret = torch.randn(B, generator=g, dtype=dt)
+    old_v = torch.randn(B, generator=g, dtype=dt)
+    val = old_v + 0.3 * torch.randn(B, generator=g, dtype=dt)
+    return mu, log_std, acts, old_lp, adv, ret, val, old_v
+
+
+def test_gauss_loss_finite_differences():
+    inp = _gauss_inputs(6, 3, seed=21)
+    mu, log_std, acts, old_lp, adv, ret, val, old_v = inp
+    o = ref.loss_gaussian_reference(*inp, 0.2, 0.2, 0.5, 0.01)
+
+    def f(mu_, ls_, v_):
+        return ref.loss_gaussian_reference(mu_, ls_, acts, old_lp, adv, ret, v_, old_v,
+                                           0.2, 0.2, 0.5, 0.01)["loss"].item()
+
+    h = 1e-6
+    for name, x, idx in (("dmu", mu, 0), ("dlog_std", log_std, 1), ("dvalues", val, 2)):
+        fd = torch.zeros_like(x)
+        flat = fd.view(-1)
+        for k in range(x.numel()):
+            xp, xm = x.clone(), x.clone()
+            xp.view(-1)[k] += h
+            xm.view(-1)[k] -= h
+            args_p = [mu, log_std, val]
+            args_m = [mu, log_std, val]
+            args_p[idx], args_m[idx] = xp, xm
+            flat[k] = (f(*args_p) - f(*args_m)) / (2 * h)
+        torch.testing.assert_close(o[name], fd, rtol=1e-6, atol=1e-8)
+
+
+def test_gauss_entropy_closed_form():
+    mu, log_std, acts, old_lp, adv, ret, val, old_v = _gauss_inputs(16, 6, seed=22)
+    o = ref.loss_gaussian_reference(mu, log_std, acts, old_lp, adv, ret, val)
+    expect = 6 * (0.5 + 0.5 * math.log(2 * math.pi)) + log_std.sum().item()
+    assert o["entropy"].item() == pytest.approx(expect, rel=1e-14)
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures
+# ---------------------------------------------------------------------------
+def test_golden_gae():
+    z = np.load(os.path.join(GOLDEN, "gae_small.npz"))
+    adv, ret = ref.gae_c(z["rewards"], z["values"], z["dones"], z["last_value"],
+                         float(z["gamma"]), float(z["lam"]))
+    np.testing.assert_array_equal(adv, z["adv"])
+    np.testing.assert_array_equal(ret, z["ret"])
+    n = ref.normalize_reference(torch.from_numpy(adv).reshape(-1)).reshape(adv.shape)
+    np.testing.assert_array_equal(n.numpy(), z["adv_norm"])
+
+
+def test_golden_loss_cat():
+    z = np.load(os.path.join(GOLDEN, "loss_cat_small.npz"))
+    o = ref.loss_categorical_reference(
+        torch.from_numpy(z["logits"]), torch.from_numpy(z["actions"]),
+        torch.from_numpy(z["old_log_probs"]), torch.from_numpy(z["advantages"]),
+        torch.from_numpy(z["returns"]), torch.from_numpy(z["values"]),
+        torch.from_numpy(z["old_values"]), float(z["clip_ratio"]), float(z["vf_clip"]),
+        float(z["value_coef"]), float(z["entropy_coef"]),
+    )
+    np.testing.assert_allclose(o["dlogits"].numpy(), z["dlogits"], rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(o["dvalues"].numpy(), z["dvalues"], rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(o["loss"].item(), z["scalars"][0], rtol=1e-6)
+
+
+def test_golden_loss_gauss():
+    z = np.load(os.path.join(GOLDEN, "loss_gauss_small.npz"))
+    o = ref.loss_gaussian_reference(
+        torch.from_numpy(z["mu"]), torch.from_numpy(z["log_std"]),
+        torch.from_numpy(z["actions"]), torch.from_numpy(z["old_log_probs"]),
+        torch.from_numpy(z["advantages"]), torch.from_numpy(z["returns"]),
+        torch.from_numpy(z["values"]), torch.from_numpy(z["old_values"]),
+        float(z["clip_ratio"]), float(z["vf_clip"]), float(z["value_coef"]),
+        float(z["entropy_coef"]),
+    )
+    np.testing.assert_allclose(o["dmu"].numpy(), z["dmu"], rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(o["dlog_std"].numpy(), z["dlog_std"], rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(o["loss"].item(), z["scalars"][0], rtol=1e-6)

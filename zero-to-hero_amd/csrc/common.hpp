@@ -1,0 +1,163 @@
+// Shared device/host helpers for libppo_amd (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ppo_amd.h"
+
+namespace ppo {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;              // threads per workgroup for streaming kernels
+constexpr size_t kHeaderBytes = 256;     // counters/flags at the front of every workspace
+
+// Workspace header: completion counters used by the "last workgroup finalises"
+// pattern.  Each kernel that uses a counter leaves it at zero on exit.
+struct WsHeader {
+  unsigned int done[4];   // [0] stats/scalar combine of the kernel that owns it
+  float stats[4];         // {mean, std, denom, 0} written by the stats finaliser
+};
+static_assert(sizeof(WsHeader) <= kHeaderBytes, "header too big");
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+inline int hip_status(hipError_t e) { return e == hipSuccess ? PPO_OK : PPO_ERR_HIP_BASE + (int)e; }
+
+// Launch-error check after a hipLaunchKernelGGL.
+inline int last_launch_status() { return hip_status(hipGetLastError()); }
+
+// ---------------------------------------------------------------------------
+// Running (count, mean, M2) triple and Chan et al.'s pairwise combine (1979):
+//   n = na + nb, d = mb - ma, mean = ma + d*nb/n, M2 = M2a + M2b + d^2*na*nb/n
+// Evaluated in fp64 so that 8M fp32 advantages keep ~1e-15 relative accuracy.
+// ---------------------------------------------------------------------------
+struct Moments {
+  double n, mean, m2;
+};
+
+__device__ __forceinline__ Moments moments_combine(Moments a, Moments b) {
+  if (a.n == 0.0) return b;
+  if (b.n == 0.0) return a;
+  const double n = a.n + b.n;
+  const double d = b.mean - a.mean;
+  const double fb = b.n / n;
+  Moments r;
+  r.n = n;
+  r.mean = a.mean + d * fb;
+  r.m2 = a.m2 + b.m2 + d * d * a.n * fb;
+  return r;
+}
+
+__device__ __forceinline__ Moments moments_shfl_xor(Moments m, int lane_mask) {
+  Moments o;
+  o.n = __shfl_xor(m.n, lane_mask, kWave);
+  o.mean = __shfl_xor(m.mean, lane_mask, kWave);
+  o.m2 = __shfl_xor(m.m2, lane_mask, kWave);
+  return o;
+}
+
+// Butterfly over the 64 lanes; every lane ends with the same value.  The
+// combine order is fixed, so results are run-to-run deterministic.
+__device__ __forceinline__ Moments wave_moments(Moments m) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) m = moments_combine(m, moments_shfl_xor(m, off));
+  return m;
+}
+
+__device__ __forceinline__ double wave_sum(double x) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) x += __shfl_xor(x, off, kWave);
+  return x;
+}
+
+// Block-wide moments for a 1-D block of blockDim.x (multiple of 64, <= 1024)
+// threads.  Result valid in thread 0.
+__device__ inline Moments block_moments(Moments m) {
+  __shared__ Moments s_part[16];
+  m = wave_moments(m);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  if (lane == 0) s_part[wid] = m;
+  __syncthreads();
+  Moments r = {0.0, 0.0, 0.0};
+  if (threadIdx.x == 0) {
+    const int nw = blockDim.x / kWave;
+    for (int w = 0; w < nw; ++w) r = moments_combine(r, s_part[w]);
+  }
+  __syncthreads();
+  return r;
+}
+
+// Block-wide sum of K doubles per thread; result valid in thread 0.
+template <int K>
+__device__ inline void block_sum(double (&x)[K]) {
+  __shared__ double s_part[16][K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) x[k] = wave_sum(x[k]);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) s_part[wid][k] = x[k];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int nw = blockDim.x / kWave;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      double s = 0.0;
+      for (int w = 0; w < nw; ++w) s += s_part[w][k];
+      x[k] = s;
+    }
+  }
+  __syncthreads();
+}
+
+// "Last workgroup finalises": call after thread 0 has stored this block's
+// partial result.  Returns true (in every thread) for the single block that
+// arrives last; that block then sees every other block's partials.  The
+// counter is reset by reset_counter() from the last block, so a workspace is
+// left zeroed for the next call.
+__device__ inline bool arrive_last(unsigned int* counter, unsigned int total) {
+  __shared__ int s_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();  // publish this block's partial before counting in
+    const unsigned int prev = atomicAdd(counter, 1u);
+    s_last = (prev == total - 1u);
+  }
+  __syncthreads();
+  const bool last = s_last != 0;
+  if (last) __threadfence();  // acquire: order the partial reads after the count
+  return last;
+}
+
+__device__ inline void reset_counter(unsigned int* counter) {
+  if (threadIdx.x == 0) atomicExch(counter, 0u);
+}
+
+// Moments of `count` partial triples (stored as 4 doubles each: n, mean, m2,
+// pad) combined in a fixed order by one block.  Result valid in thread 0.
+__device__ inline Moments combine_partials(const double* part, long count) {
+  Moments acc = {0.0, 0.0, 0.0};
+  // contiguous range per thread keeps the order fixed
+  const long per = (count + blockDim.x - 1) / blockDim.x;
+  const long lo = (long)threadIdx.x * per;
+  const long hi = lo + per < count ? lo + per : count;
+  for (long i = lo; i < hi; ++i) {
+    Moments p = {part[4 * i + 0], part[4 * i + 1], part[4 * i + 2]};
+    acc = moments_combine(acc, p);
+  }
+  return block_moments(acc);
+}
+
+__host__ __device__ inline unsigned int pow2_ceil(unsigned int x) {
+  unsigned int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace ppo

@@ -1,0 +1,492 @@
+// Generalized advantage estimation over an env-contiguous [T,N] rollout.
+//
+// Reference: PPOAgent._advantages, rl/deep/agents/ppo.py:173-193, plus
+// `returns = advantages + old_values` (ppo.py:124).  The reference walks one
+// episode backwards in Python floats:
+//     mask  = 1 - float(terminated or truncated)                   (:179)
+//     delta = reward + gamma*next_value*mask - value               (:180-184)
+//     adv   = delta + gamma*lambda*mask*adv                        (:185-188)
+//     next_value = value                                           (:190)
+// Every thread here performs that recurrence in fp64 with the same operation
+// order and no fused multiply-adds, so an element whose carry is exact is
+// bit-identical to the reference after the final fp32 cast.
+//
+// Parallel structure (three kernels, all HBM-streaming):
+//   The recurrence is affine in the carried advantage: adv_t = delta_t +
+//   c_t*adv_{t+1} with c_t = gamma*lambda*mask_t.  A run of steps therefore
+//   maps the advantage entering it from the right, x, to a + P*x.
+//   * A "segment" is L consecutive steps of VW adjacent envs owned by one
+//     thread (VW=4: float4 row loads, dones read as one 32-bit word).
+//   * A "tile" is Sw consecutive segments x Qw adjacent env-groups owned by
+//     one 256-thread workgroup; segments are composed with a Kogge-Stone scan
+//     in LDS.
+//   1. gae_tile_kernel<.., kFinal=false>: per tile and env, the composite
+//      (a, P) of all its steps -> workspace `summary` [Tt][N].
+//   2. gae_carry_kernel: per env, a reverse scan over the tiles' (a, P) ->
+//      `carry` [Tt][N], the advantage entering each tile from the right.
+//   3. gae_tile_kernel<.., kFinal=true>: re-reads the tile, rebuilds the
+//      segment composites, applies the tile carry, and runs the exact serial
+//      recurrence per segment, writing adv and ret (and, for the fused
+//      normaliser, per-block (n, mean, M2) of the advantages).
+// When the whole horizon fits in one tile (Tt == 1) steps 1-2 are skipped.
+#include <algorithm>
+
+#include "common.hpp"
+#include "stats.hpp"
+
+namespace ppo {
+namespace {
+
+struct GaeArgs {
+  const float* r;
+  const float* v;
+  const uint8_t* d;
+  const float* lastv;  // may be null (zeros)
+  long T, N;
+  double gamma, gl;    // gamma and gamma*lambda (the product rounded once, as in Python)
+  float* adv;
+  float* ret;          // may be null
+  double2* summary;    // [Tt][N] (a, P)
+  const double* carry; // [Tt][N] or null (all-zero carries)
+  double* partial;     // [blocks][4] moments, fused-normalise only
+  WsHeader* hdr;
+  float* stats_out;
+  double eps;
+  long Q, Tq, Tt;
+  int Qw, Sw;
+};
+
+struct GaePlan {
+  int vw, L, Qw, Sw;
+  long Q, Tq, Tt, span;
+  long blocks() const { return Tt * Tq; }
+};
+
+GaePlan make_plan(long T, long N, int vw) {
+  GaePlan p;
+  p.vw = vw;
+  p.L = vw == 4 ? 8 : 16;
+  p.Q = N / vw;
+  p.Qw = (int)std::min<long>(64, (long)pow2_ceil((unsigned)std::min<long>(p.Q, 64)));
+  p.Sw = kBlock / p.Qw;
+  p.span = (long)p.Sw * p.L;
+  p.Tt = (T + p.span - 1) / p.span;
+  p.Tq = (p.Q + p.Qw - 1) / p.Qw;
+  return p;
+}
+
+struct GaeLayout {
+  size_t summary, carry, partial, total;
+};
+
+GaeLayout make_layout(const GaePlan& p, long N) {
+  GaeLayout l;
+  size_t off = kHeaderBytes;
+  l.summary = off;
+  off += align_up((size_t)p.Tt * N * sizeof(double2), 256);
+  l.carry = off;
+  off += align_up((size_t)p.Tt * N * sizeof(double), 256);
+  l.partial = off;
+  off += align_up((size_t)p.blocks() * 4 * sizeof(double), 256);
+  l.total = off;
+  return l;
+}
+
+// fp64 multiply / add with no contraction into FMA: the reference evaluates
+// each Python float operation with its own rounding.
+__device__ __forceinline__ double mul(double a, double b) { return __dmul_rn(a, b); }
+__device__ __forceinline__ double add(double a, double b) { return __dadd_rn(a, b); }
+__device__ __forceinline__ double sub(double a, double b) { return __dsub_rn(a, b); }
+
+template <int VW>
+__device__ __forceinline__ void load_f(const float* p, float (&x)[VW]) {
+  if constexpr (VW == 4) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+  } else {
+    x[0] = *p;
+  }
+}
+
+template <int VW>
+__device__ __forceinline__ void store_f(float* p, const float (&x)[VW]) {
+  if constexpr (VW == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+  } else {
+    *p = x[0];
+  }
+}
+
+// Returns one bit per env: bit k set when dones[.., env0+k] != 0.
+template <int VW>
+__device__ __forceinline__ unsigned load_done(const uint8_t* p) {
+  if constexpr (VW == 4) {
+    const unsigned w = *reinterpret_cast<const unsigned*>(p);
+    return ((w & 0xffu) != 0u) | (((w >> 8) & 0xffu) != 0u) << 1 |
+           (((w >> 16) & 0xffu) != 0u) << 2 | ((w >> 24) != 0u) << 3;
+  } else {
+    return *p != 0;
+  }
+}
+
+template <int VW, int L, bool kFinal, bool kStats>
+__global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
+  static_assert(L * VW <= 32, "done bits must fit one word");
+  __shared__ double s_a[kBlock * VW];
+  __shared__ double s_p[kBlock * VW];
+
+  const long bid = blockIdx.x;
+  const long tile_t = bid / a.Tq;
+  const long tile_q = bid - tile_t * a.Tq;
+  const int tid = threadIdx.x;
+  const int q = tid % a.Qw;
+  const int s = tid / a.Qw;
+  const long col = tile_q * a.Qw + q;
+  const bool col_ok = col < a.Q;
+  const long env0 = col * VW;
+  const long t0 = (tile_t * a.Sw + s) * (long)L;
+  const long remain = a.T - t0;
+  const int nvalid = col_ok ? (int)(remain <= 0 ? 0 : (remain < L ? remain : L)) : 0;
+
+  float r[L][VW], v[L][VW], nv[VW];
+  unsigned dbits = 0;
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    if (i < nvalid) {
+      const long off = (t0 + i) * a.N + env0;
+      load_f<VW>(a.r + off, r[i]);
+      load_f<VW>(a.v + off, v[i]);
+      dbits |= load_done<VW>(a.d + off) << (i * VW);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) r[i][k] = v[i][k] = 0.0f;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < VW; ++k) nv[k] = 0.0f;
+  if (nvalid > 0) {
+    if (t0 + L < a.T)
+      load_f<VW>(a.v + (t0 + L) * a.N + env0, nv);
+    else if (a.lastv)
+      load_f<VW>(a.lastv + env0, nv);
+  }
+
+  // Composite (a, P) of this segment with a zero carry.
+  double ia[VW], ip[VW];
+  {
+    double nvd[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) { ia[k] = 0.0; ip[k] = 1.0; nvd[k] = nv[k]; }
+#pragma unroll
+    for (int i = L - 1; i >= 0; --i) {
+      if (i < nvalid) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          const double m = ((dbits >> (i * VW + k)) & 1u) ? 0.0 : 1.0;
+          const double vd = (double)v[i][k];
+          const double delta = sub(add((double)r[i][k], mul(mul(a.gamma, nvd[k]), m)), vd);
+          const double c = mul(a.gl, m);
+          ia[k] = add(delta, mul(c, ia[k]));
+          ip[k] = mul(ip[k], c);
+          nvd[k] = vd;
+        }
+      }
+    }
+  }
+
+  // Reverse inclusive scan over the Sw segments of the tile:
+  // (a_s, P_s) <- (a_s + P_s*a_{s+off}, P_s*P_{s+off}).
+#pragma unroll
+  for (int k = 0; k < VW; ++k) { s_a[tid * VW + k] = ia[k]; s_p[tid * VW + k] = ip[k]; }
+  for (int off = 1; off < a.Sw; off <<= 1) {
+    __syncthreads();
+    const bool has = s + off < a.Sw;
+    double pa[VW], pp[VW];
+    if (has) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) {
+        pa[k] = s_a[(tid + off * a.Qw) * VW + k];
+        pp[k] = s_p[(tid + off * a.Qw) * VW + k];
+      }
+    }
+    __syncthreads();
+    if (has) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) {
+        ia[k] = ia[k] + ip[k] * pa[k];
+        ip[k] = ip[k] * pp[k];
+        s_a[tid * VW + k] = ia[k];
+        s_p[tid * VW + k] = ip[k];
+      }
+    }
+  }
+  __syncthreads();
+
+  if constexpr (!kFinal) {
+    if (s == 0 && col_ok) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k)
+        a.summary[tile_t * a.N + env0 + k] = make_double2(ia[k], ip[k]);
+    }
+    return;
+  } else {
+    // Advantage entering this segment from the right.
+    double cin[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      const double C = (a.carry && col_ok) ? a.carry[tile_t * a.N + env0 + k] : 0.0;
+      if (s + 1 < a.Sw)
+        cin[k] = s_a[(tid + a.Qw) * VW + k] + s_p[(tid + a.Qw) * VW + k] * C;
+      else
+        cin[k] = C;
+    }
+
+    // Exact serial recurrence over the segment; r[][] is reused for adv.
+    {
+      double adv[VW], nvd[VW];
+#pragma unroll
+      for (int k = 0; k < VW; ++k) { adv[k] = cin[k]; nvd[k] = nv[k]; }
+#pragma unroll
+      for (int i = L - 1; i >= 0; --i) {
+        if (i < nvalid) {
+#pragma unroll
+          for (int k = 0; k < VW; ++k) {
+            const double m = ((dbits >> (i * VW + k)) & 1u) ? 0.0 : 1.0;
+            const double vd = (double)v[i][k];
+            const double delta = sub(add((double)r[i][k], mul(mul(a.gamma, nvd[k]), m)), vd);
+            adv[k] = add(delta, mul(mul(a.gl, m), adv[k]));
+            r[i][k] = (float)adv[k];
+            nvd[k] = vd;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+      if (i < nvalid) {
+        const long off = (t0 + i) * a.N + env0;
+        store_f<VW>(a.adv + off, r[i]);
+        if (a.ret) {
+          float rt[VW];
+#pragma unroll
+          for (int k = 0; k < VW; ++k) rt[k] = r[i][k] + v[i][k];
+          store_f<VW>(a.ret + off, rt);
+        }
+      }
+    }
+
+    if constexpr (kStats) {
+      Moments m = {0.0, 0.0, 0.0};
+      if (nvalid > 0) {
+        double sum = 0.0;
+#pragma unroll
+        for (int i = 0; i < L; ++i)
+          if (i < nvalid)
+#pragma unroll
+            for (int k = 0; k < VW; ++k) sum += (double)r[i][k];
+        m.n = (double)(nvalid * VW);
+        m.mean = sum / m.n;
+        double m2 = 0.0;
+#pragma unroll
+        for (int i = 0; i < L; ++i)
+          if (i < nvalid)
+#pragma unroll
+            for (int k = 0; k < VW; ++k) {
+              const double dv = (double)r[i][k] - m.mean;
+              m2 += dv * dv;
+            }
+        m.m2 = m2;
+      }
+      m = block_moments(m);
+      if (tid == 0) {
+        a.partial[bid * 4 + 0] = m.n;
+        a.partial[bid * 4 + 1] = m.mean;
+        a.partial[bid * 4 + 2] = m.m2;
+        a.partial[bid * 4 + 3] = 0.0;
+      }
+      const long nblocks = a.Tt * a.Tq;
+      if (arrive_last(&a.hdr->done[0], (unsigned)nblocks)) {
+        finalize_stats(a.partial, nblocks, a.eps, a.hdr, a.stats_out);
+        reset_counter(&a.hdr->done[0]);
+      }
+    }
+  }
+}
+
+// Reverse scan of tile composites into per-tile carries.  One block covers Ew
+// envs; its Rw thread-rows split each round of Rw*G tiles into contiguous
+// groups of G held in registers.  Rounds run from the last tile backwards.
+constexpr int kCarryBlock = 1024;
+constexpr int kCarryG = 8;
+
+__global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* __restrict__ summary,
+                                                                 double* __restrict__ carry, long Tt,
+                                                                 long N, int Ew, int Rw) {
+  __shared__ double s_a[kCarryBlock];
+  __shared__ double s_p[kCarryBlock];
+  const int tid = threadIdx.x;
+  const int e = tid % Ew;
+  const int g = tid / Ew;
+  const long env = (long)blockIdx.x * Ew + e;
+  const bool ok = env < N;
+  const long round_tiles = (long)Rw * kCarryG;
+
+  double C = 0.0;  // advantage entering the current round from the right
+  for (long hi = Tt; hi > 0; hi -= round_tiles) {
+    const long lo = hi - round_tiles > 0 ? hi - round_tiles : 0;
+    const long k0 = lo + (long)g * kCarryG;
+    double ta[kCarryG], tp[kCarryG];
+#pragma unroll
+    for (int j = 0; j < kCarryG; ++j) {
+      const long k = k0 + j;
+      if (ok && k < hi) {
+        const double2 t = summary[k * N + env];
+        ta[j] = t.x;
+        tp[j] = t.y;
+      } else {
+        ta[j] = 0.0;
+        tp[j] = 1.0;
+      }
+    }
+    double ga = 0.0, gp = 1.0;
+#pragma unroll
+    for (int j = kCarryG - 1; j >= 0; --j) {
+      ga = ta[j] + tp[j] * ga;
+      gp = tp[j] * gp;
+    }
+    s_a[tid] = ga;
+    s_p[tid] = gp;
+    for (int off = 1; off < Rw; off <<= 1) {
+      __syncthreads();
+      const bool has = g + off < Rw;
+      double pa = 0.0, pp = 1.0;
+      if (has) {
+        pa = s_a[tid + off * Ew];
+        pp = s_p[tid + off * Ew];
+      }
+      __syncthreads();
+      if (has) {
+        ga = ga + gp * pa;
+        gp = gp * pp;
+        s_a[tid] = ga;
+        s_p[tid] = gp;
+      }
+    }
+    __syncthreads();
+    double c = (g + 1 < Rw) ? s_a[tid + Ew] + s_p[tid + Ew] * C : C;
+    const double c_next = s_a[e] + s_p[e] * C;
+#pragma unroll
+    for (int j = kCarryG - 1; j >= 0; --j) {
+      const long k = k0 + j;
+      if (ok && k < hi) {
+        carry[k * N + env] = c;
+        c = ta[j] + tp[j] * c;
+      }
+    }
+    C = c_next;
+    __syncthreads();
+  }
+}
+
+template <int VW, int L>
+int launch_gae(const GaePlan& p, GaeArgs a, bool stats, hipStream_t stream) {
+  const long blocks = p.blocks();
+  a.Q = p.Q;
+  a.Tq = p.Tq;
+  a.Tt = p.Tt;
+  a.Qw = p.Qw;
+  a.Sw = p.Sw;
+  int st;
+  if (p.Tt > 1) {
+    hipLaunchKernelGGL((gae_tile_kernel<VW, L, false, false>), dim3((unsigned)blocks),
+                       dim3(kBlock), 0, stream, a);
+    if ((st = last_launch_status())) return st;
+    const int Ew = (int)std::min<long>(64, (long)pow2_ceil((unsigned)std::min<long>(a.N, 64)));
+    const int Rw = kCarryBlock / Ew;
+    const long cblocks = (a.N + Ew - 1) / Ew;
+    hipLaunchKernelGGL(gae_carry_kernel, dim3((unsigned)cblocks), dim3(kCarryBlock), 0, stream,
+                       a.summary, const_cast<double*>(a.carry), p.Tt, a.N, Ew, Rw);
+    if ((st = last_launch_status())) return st;
+  } else {
+    a.carry = nullptr;
+  }
+  if (stats)
+    hipLaunchKernelGGL((gae_tile_kernel<VW, L, true, true>), dim3((unsigned)blocks), dim3(kBlock),
+                       0, stream, a);
+  else
+    hipLaunchKernelGGL((gae_tile_kernel<VW, L, true, false>), dim3((unsigned)blocks),
+                       dim3(kBlock), 0, stream, a);
+  return last_launch_status();
+}
+
+int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
+             const float* last_value, int64_t T, int64_t N, double gamma, double lam, double eps,
+             float* adv_out, float* ret_out, float* adv_norm_out, float* stats_out, bool norm,
+             void* workspace, size_t workspace_bytes, void* stream_ptr) {
+  if (T < 0 || N < 0) return PPO_ERR_INVALID_ARG;
+  if (T == 0 || N == 0) return PPO_OK;
+  if (!rewards || !values || !dones || !adv_out) return PPO_ERR_INVALID_ARG;
+  if (norm && !adv_norm_out) return PPO_ERR_INVALID_ARG;
+  if (N > (1L << 31) || T > (1L << 40) || T * N > (1L << 50)) return PPO_ERR_TOO_LARGE;
+  if (!workspace || workspace_bytes < ppo_gae_workspace_bytes(T, N)) return PPO_ERR_WORKSPACE;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+
+  const bool vec = (N % 4 == 0) && aligned(rewards, 16) && aligned(values, 16) &&
+                   aligned(adv_out, 16) && (!ret_out || aligned(ret_out, 16)) &&
+                   aligned(dones, 4) && (!last_value || aligned(last_value, 16));
+  const GaePlan p = make_plan(T, N, vec ? 4 : 1);
+  if (p.blocks() > 0x7fffffffL) return PPO_ERR_TOO_LARGE;
+  const GaeLayout l = make_layout(p, N);
+  char* ws = static_cast<char*>(workspace);
+
+  GaeArgs a = {};
+  a.r = rewards;
+  a.v = values;
+  a.d = dones;
+  a.lastv = last_value;
+  a.T = T;
+  a.N = N;
+  a.gamma = gamma;
+  a.gl = gamma * lam;
+  a.adv = adv_out;
+  a.ret = ret_out;
+  a.summary = reinterpret_cast<double2*>(ws + l.summary);
+  a.carry = reinterpret_cast<double*>(ws + l.carry);
+  a.partial = reinterpret_cast<double*>(ws + l.partial);
+  a.hdr = reinterpret_cast<WsHeader*>(ws);
+  a.stats_out = stats_out;
+  a.eps = eps;
+
+  int st = vec ? launch_gae<4, 8>(p, a, norm, stream) : launch_gae<1, 16>(p, a, norm, stream);
+  if (st || !norm) return st;
+  return launch_normalize(adv_out, adv_norm_out, T * N, a.hdr, stream);
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" size_t ppo_gae_workspace_bytes(int64_t T, int64_t N) {
+  using namespace ppo;
+  if (T <= 0 || N <= 0) return kHeaderBytes;
+  size_t b = make_layout(make_plan(T, N, 1), N).total;
+  if (N % 4 == 0) b = std::max(b, make_layout(make_plan(T, N, 4), N).total);
+  return b;
+}
+
+extern "C" int ppo_gae_f32(const float* rewards, const float* values, const uint8_t* dones,
+                           const float* last_value, int64_t T, int64_t N, double gamma,
+                           double lam, float* adv_out, float* ret_out, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return ppo::gae_impl(rewards, values, dones, last_value, T, N, gamma, lam, 0.0, adv_out,
+                       ret_out, nullptr, nullptr, false, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ppo_gae_norm_f32(const float* rewards, const float* values, const uint8_t* dones,
+                                const float* last_value, int64_t T, int64_t N, double gamma,
+                                double lam, double eps, float* adv_out, float* ret_out,
+                                float* adv_norm_out, float* stats_out, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return ppo::gae_impl(rewards, values, dones, last_value, T, N, gamma, lam, eps, adv_out,
+                       ret_out, adv_norm_out, stats_out, true, workspace, workspace_bytes,
+                       stream);
+}

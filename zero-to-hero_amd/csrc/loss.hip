@@ -1,0 +1,616 @@
+// Fused PPO loss: forward scalars and backward gradients in one pass.
+//
+// Reference: PPOAgent._update_batch, rl/deep/agents/ppo.py:149-169.  The
+// forward is
+//     dist    = Categorical(logits=logits)                        (:150)
+//     lp      = dist.log_prob(actions)                             (:151)
+//     ratio   = exp(lp - old_log_probs)                            (:154)
+//     clipped = ratio.clamp(1 - clip, 1 + clip)                    (:155-158)
+//     policy  = -minimum(ratio * adv, clipped * adv)               (:159)
+//     value   = mse_loss(values, returns)                          (:160)
+//     loss    = policy.mean() + vc * value - ec * dist.entropy().mean()  (:163-167)
+// and loss.backward() (:169) is replaced, down to the logits and the value
+// head, by the closed-form gradient written directly (B rows, p = softmax):
+//     g_lp      = -(adv/B) * ratio * (s_u + s_w * [lo <= ratio <= hi])
+//                 with s_u/s_w the torch.minimum tie weights (1, 0, or 1/2)
+//     dlogit_k  = g_lp * (1[k == a] - p_k) + (ec/B) * p_k * (log p_k + H)
+//     dvalue    = vc * 2 * (v - R) / B          (or the clipped-value form)
+// Gaussian variant: Normal(mu, exp(log_std)) summed over the action dims.
+//
+// Layout: one thread per row.  A workgroup stages its 256 rows of [B,A]
+// logits (a contiguous block of 256*A floats) through LDS with float4 loads,
+// row stride padded to an odd number of words so row-per-thread LDS reads are
+// bank-conflict-free, and writes dlogits back through the same tile.
+// Loss scalars are summed per block in fp64 and combined by the last block in
+// a fixed order (deterministic, no float atomics).
+#include <float.h>
+
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace ppo {
+namespace {
+
+// Widths handled by the row-per-thread kernels, chosen so that the LDS tiles
+// (256 rows x odd-padded width, one tile for logits, two for mu/actions) plus
+// the static reduction arrays stay under the 64 KiB a workgroup may address.
+constexpr int kMaxCatRowWidth = 48;  // A above this uses the wave-per-row kernel
+constexpr int kMaxGaussDim = 24;     // D limit of the Gaussian kernel
+constexpr int kScalarSlots = 8;      // per-block partial doubles for the loss scalars
+constexpr int kGaussSlots = kScalarSlots + kMaxGaussDim;
+constexpr long kWaveRowBlocks = 4096;  // grid cap of the wave-per-row kernel
+
+struct LossArgs {
+  const float* x;        // logits [B,A] or mu [B,D]
+  const float* log_std;  // [D] (Gaussian)
+  long B;
+  int A;                 // A or D
+  const void* actions;   // int32/int64 [B] or float [B,D]
+  const float* old_lp;
+  const float* adv;
+  const float* ret;
+  const float* val;
+  const float* old_val;
+  float lo, hi, clip;    // ratio clamp bounds and the clip parameter
+  float vclip;
+  int use_vclip;
+  float vc, ec;          // value / entropy coefficients as fp32 (torch scalar math)
+  float inv_b;
+  float* dx;
+  float* dlog_std;
+  float* dval;
+  float* scalars;
+  double* partial;
+  WsHeader* hdr;
+};
+
+__device__ __forceinline__ float nan_min(float u, float w) {
+  if (u != u) return u;
+  if (w != w) return w;
+  return u < w ? u : w;
+}
+__device__ __forceinline__ float nan_max(float u, float w) {
+  if (u != u) return u;
+  if (w != w) return w;
+  return u > w ? u : w;
+}
+// torch.clamp(x, lo, hi): NaN stays NaN.
+__device__ __forceinline__ float clampf(float x, float lo, float hi) {
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
+struct RowOut {
+  float g_lp;     // dloss/dlog_prob for this row
+  double pol, vl, kl, clipped;
+};
+
+// Everything per row that does not depend on the policy family: ratio,
+// clipped surrogate, value loss, their gradients.  Writes dvalue.
+__device__ __forceinline__ RowOut ppo_row(const LossArgs& a, long row, float lp) {
+  RowOut o;
+  const float old_lp = a.old_lp[row];
+  const float A = a.adv[row];
+  const float ratio = expf(lp - old_lp);
+  const float rc = clampf(ratio, a.lo, a.hi);
+  const float u = ratio * A;
+  const float w = rc * A;
+  const float pol = -nan_min(u, w);
+  const float su = u < w ? 1.0f : (u == w ? 0.5f : 0.0f);
+  const float sw = w < u ? 1.0f : (u == w ? 0.5f : 0.0f);
+  const float inr = (ratio >= a.lo && ratio <= a.hi) ? 1.0f : 0.0f;
+  // d(policy_i)/d(ratio) = -A*(su + sw*inr); times 1/B (mean) and ratio (exp').
+  o.g_lp = -(A * (su + sw * inr)) * a.inv_b * ratio;
+
+  const float v = a.val[row];
+  const float R = a.ret[row];
+  const float d = v - R;
+  float vl, dvl;
+  if (a.use_vclip) {
+    const float vo = a.old_val[row];
+    const float dv = v - vo;
+    const float vcl = vo + clampf(dv, -a.vclip, a.vclip);
+    const float d2 = vcl - R;
+    const float l1 = d * d;
+    const float l2 = d2 * d2;
+    vl = nan_max(l1, l2);
+    const float s1 = l1 > l2 ? 1.0f : (l1 == l2 ? 0.5f : 0.0f);
+    const float s2 = l2 > l1 ? 1.0f : (l1 == l2 ? 0.5f : 0.0f);
+    const float in2 = (dv >= -a.vclip && dv <= a.vclip) ? 1.0f : 0.0f;
+    dvl = s1 * (2.0f * d) + s2 * (2.0f * d2) * in2;
+  } else {
+    vl = d * d;
+    dvl = 2.0f * d;
+  }
+  a.dval[row] = a.vc * (dvl * a.inv_b);
+  o.pol = pol;
+  o.vl = vl;
+  o.kl = (double)old_lp - (double)lp;
+  o.clipped = fabsf(ratio - 1.0f) > a.clip ? 1.0 : 0.0;
+  return o;
+}
+
+// Copy `count` floats from global (contiguous) into an LDS tile of row
+// stride `ws` (count = rows * width).
+template <bool kVec>
+__device__ __forceinline__ void stage_in(const float* src, int count, int width, int ws,
+                                         float* lds) {
+  int start = 0;
+  if constexpr (kVec) {
+    const int n4 = count >> 2;
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+      const float4 x = s4[i];
+      const int e = i << 2;
+      int r = e / width;
+      int c = e - r * width;
+      const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        lds[r * ws + c] = xs[k];
+        if (++c == width) { c = 0; ++r; }
+      }
+    }
+    start = n4 << 2;
+  }
+  for (int e = start + threadIdx.x; e < count; e += blockDim.x) {
+    const int r = e / width;
+    lds[r * ws + (e - r * width)] = src[e];
+  }
+}
+
+template <bool kVec>
+__device__ __forceinline__ void stage_out(float* dst, int count, int width, int ws,
+                                          const float* lds) {
+  int start = 0;
+  if constexpr (kVec) {
+    const int n4 = count >> 2;
+    float4* d4 = reinterpret_cast<float4*>(dst);
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+      const int e = i << 2;
+      int r = e / width;
+      int c = e - r * width;
+      float xs[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        xs[k] = lds[r * ws + c];
+        if (++c == width) { c = 0; ++r; }
+      }
+      d4[i] = make_float4(xs[0], xs[1], xs[2], xs[3]);
+    }
+    start = n4 << 2;
+  }
+  for (int e = start + threadIdx.x; e < count; e += blockDim.x) {
+    const int r = e / width;
+    dst[e] = lds[r * ws + (e - r * width)];
+  }
+}
+
+// Block partial of the 5 loss sums -> partial[block*stride + 0..4]; the last
+// block combines all partials (fixed order) and writes scalars_out.
+__device__ inline void reduce_scalars(const LossArgs& a, double (&acc)[5], long block,
+                                      long nblocks, int stride, float h_const,
+                                      bool const_entropy) {
+  block_sum<5>(acc);
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k) a.partial[block * stride + k] = acc[k];
+  }
+  if (!arrive_last(&a.hdr->done[0], (unsigned)nblocks)) return;
+  double tot[5] = {0, 0, 0, 0, 0};
+  const long per = (nblocks + blockDim.x - 1) / blockDim.x;
+  const long lo = (long)threadIdx.x * per;
+  const long hi = lo + per < nblocks ? lo + per : nblocks;
+  for (long b = lo; b < hi; ++b)
+#pragma unroll
+    for (int k = 0; k < 5; ++k) tot[k] += a.partial[b * stride + k];
+  block_sum<5>(tot);
+  if (threadIdx.x == 0) {
+    const double nb = (double)a.B;
+    const float pol = (float)(tot[0] / nb);
+    const float vl = (float)(tot[1] / nb);
+    const float ent = const_entropy ? h_const : (float)(tot[2] / nb);
+    a.scalars[PPO_SCALAR_POLICY] = pol;
+    a.scalars[PPO_SCALAR_VALUE] = vl;
+    a.scalars[PPO_SCALAR_ENTROPY] = ent;
+    a.scalars[PPO_SCALAR_APPROX_KL] = (float)(tot[3] / nb);
+    a.scalars[PPO_SCALAR_CLIPFRAC] = (float)(tot[4] / nb);
+    a.scalars[PPO_SCALAR_LOSS] = (pol + a.vc * vl) - a.ec * ent;
+  }
+  reset_counter(&a.hdr->done[0]);
+}
+
+// Action index of a row, or -1 when it lies outside [0, A).
+template <typename ActT>
+__device__ __forceinline__ int row_action(const LossArgs& a, long row) {
+  const long act = (long)reinterpret_cast<const ActT*>(a.actions)[row];
+  return (act >= 0 && act < a.A) ? (int)act : -1;
+}
+
+// ---------------------------------------------------------------------------
+// Categorical, A <= kMaxCatRowWidth: one thread per row, logits staged through LDS.
+// ---------------------------------------------------------------------------
+template <typename ActT, bool kVec>
+__global__ void __launch_bounds__(kBlock) loss_cat_kernel(LossArgs a) {
+  extern __shared__ float s_tile[];
+  const int A = a.A;
+  const int AS = A | 1;
+  const long row0 = (long)blockIdx.x * kBlock;
+  const int nrows = (int)std::min<long>(kBlock, a.B - row0);
+  stage_in<kVec>(a.x + row0 * A, nrows * A, A, AS, s_tile);
+  __syncthreads();
+
+  double acc[5] = {0, 0, 0, 0, 0};
+  const int tid = threadIdx.x;
+  if (tid < nrows) {
+    const long row = row0 + tid;
+    float* z = s_tile + tid * AS;
+    float m = -INFINITY;
+    for (int j = 0; j < A; ++j) m = fmaxf(m, z[j]);
+    float se = 0.0f;
+    for (int j = 0; j < A; ++j) se += expf(z[j] - m);
+    const float lse = m + logf(se);
+    float H = 0.0f;
+    for (int j = 0; j < A; ++j) {
+      const float lpj = z[j] - lse;
+      H -= fmaxf(lpj, -FLT_MAX) * expf(lpj);
+    }
+    const int ai = row_action<ActT>(a, row);
+    const float lp = ai >= 0 ? z[ai] - lse : __builtin_nanf("");
+    const RowOut o = ppo_row(a, row, lp);
+    const float ge = a.ec * a.inv_b;
+    for (int j = 0; j < A; ++j) {
+      const float lpj = z[j] - lse;
+      const float pj = expf(lpj);
+      const float onehot = j == ai ? 1.0f : 0.0f;
+      z[j] = o.g_lp * (onehot - pj) + ge * (pj * (fmaxf(lpj, -FLT_MAX) + H));
+    }
+    acc[0] = o.pol;
+    acc[1] = o.vl;
+    acc[2] = H;
+    acc[3] = o.kl;
+    acc[4] = o.clipped;
+  }
+  __syncthreads();
+  stage_out<kVec>(a.dx + row0 * A, nrows * A, A, AS, s_tile);
+  reduce_scalars(a, acc, blockIdx.x, gridDim.x, kScalarSlots, 0.0f, false);
+}
+
+// ---------------------------------------------------------------------------
+// Categorical, any A: one wave per row (lanes stride the actions).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max_f(float x) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) x = fmaxf(x, __shfl_xor(x, off, kWave));
+  return x;
+}
+__device__ __forceinline__ float wave_sum_f(float x) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) x += __shfl_xor(x, off, kWave);
+  return x;
+}
+
+template <typename ActT>
+__global__ void __launch_bounds__(kBlock) loss_cat_wave_kernel(LossArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const long wave = ((long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
+  const long nwaves = (long)gridDim.x * blockDim.x / kWave;
+  const int A = a.A;
+  double acc[5] = {0, 0, 0, 0, 0};
+  for (long row = wave; row < a.B; row += nwaves) {
+    const float* z = a.x + row * A;
+    float m = -INFINITY;
+    for (int j = lane; j < A; j += kWave) m = fmaxf(m, z[j]);
+    m = wave_max_f(m);
+    float se = 0.0f;
+    for (int j = lane; j < A; j += kWave) se += expf(z[j] - m);
+    se = wave_sum_f(se);
+    const float lse = m + logf(se);
+    float H = 0.0f;
+    for (int j = lane; j < A; j += kWave) {
+      const float lpj = z[j] - lse;
+      H -= fmaxf(lpj, -FLT_MAX) * expf(lpj);
+    }
+    H = wave_sum_f(H);
+    const int ai = row_action<ActT>(a, row);
+    const float lp = ai >= 0 ? z[ai] - lse : __builtin_nanf("");
+    // every lane evaluates the row terms; only lane 0 stores dvalue and sums
+    RowOut o = {0.0f, 0.0, 0.0, 0.0, 0.0};
+    if (lane == 0) {
+      o = ppo_row(a, row, lp);
+    }
+    o.g_lp = __shfl(o.g_lp, 0, kWave);
+    const float ge = a.ec * a.inv_b;
+    float* dz = a.dx + row * A;
+    for (int j = lane; j < A; j += kWave) {
+      const float lpj = z[j] - lse;
+      const float pj = expf(lpj);
+      const float onehot = j == ai ? 1.0f : 0.0f;
+      dz[j] = o.g_lp * (onehot - pj) + ge * (pj * (fmaxf(lpj, -FLT_MAX) + H));
+    }
+    if (lane == 0) {
+      acc[0] += o.pol;
+      acc[1] += o.vl;
+      acc[2] += H;
+      acc[3] += o.kl;
+      acc[4] += o.clipped;
+    }
+  }
+  reduce_scalars(a, acc, blockIdx.x, gridDim.x, kScalarSlots, 0.0f, false);
+}
+
+// ---------------------------------------------------------------------------
+// Gaussian, D <= kMaxGaussDim: one thread per row; mu and actions staged through LDS.
+// torch Normal(loc, scale): log_prob = -(x-loc)^2/(2*scale^2) - log(scale)
+// - log(sqrt(2*pi)); entropy = 0.5 + 0.5*log(2*pi) + log(scale).
+// ---------------------------------------------------------------------------
+template <bool kVec>
+__global__ void __launch_bounds__(kBlock) loss_gauss_kernel(LossArgs a) {
+  extern __shared__ float s_lds[];
+  __shared__ float s_2var[kMaxGaussDim], s_var[kMaxGaussDim], s_logscale[kMaxGaussDim];
+  __shared__ float s_hconst;
+  const int D = a.A;
+  const int DS = D | 1;
+  float* s_mu = s_lds;
+  float* s_act = s_lds + kBlock * DS;
+  const long row0 = (long)blockIdx.x * kBlock;
+  const int nrows = (int)std::min<long>(kBlock, a.B - row0);
+  const float kLogSqrt2Pi = 0.91893853320467274178f;   // log(sqrt(2*pi))
+  const float kEntConst = 1.41893853320467274178f;     // 0.5 + 0.5*log(2*pi)
+  if (threadIdx.x < D) {
+    const float scale = expf(a.log_std[threadIdx.x]);
+    const float var = scale * scale;
+    s_2var[threadIdx.x] = 2.0f * var;
+    s_var[threadIdx.x] = var;
+    s_logscale[threadIdx.x] = logf(scale);
+  }
+  stage_in<kVec>(a.x + row0 * D, nrows * D, D, DS, s_mu);
+  stage_in<kVec>(reinterpret_cast<const float*>(a.actions) + row0 * D, nrows * D, D, DS, s_act);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float h = 0.0f;
+    for (int d = 0; d < D; ++d) h += kEntConst + s_logscale[d];
+    s_hconst = h;
+  }
+
+  double acc[5] = {0, 0, 0, 0, 0};
+  const int tid = threadIdx.x;
+  if (tid < nrows) {
+    const long row = row0 + tid;
+    float* mu = s_mu + tid * DS;
+    float* act = s_act + tid * DS;
+    float lp = 0.0f;
+    for (int d = 0; d < D; ++d) {
+      const float diff = act[d] - mu[d];
+      lp += ((-(diff * diff)) / s_2var[d] - s_logscale[d]) - kLogSqrt2Pi;
+    }
+    const RowOut o = ppo_row(a, row, lp);
+    for (int d = 0; d < D; ++d) {
+      const float diff = act[d] - mu[d];
+      const float z2 = (diff * diff) / s_var[d];
+      mu[d] = o.g_lp * (diff / s_var[d]);   // dmu
+      act[d] = o.g_lp * (z2 - 1.0f);           // this row's dlog_std term
+    }
+    acc[0] = o.pol;
+    acc[1] = o.vl;
+    acc[2] = 0.0;
+    acc[3] = o.kl;
+    acc[4] = o.clipped;
+  } else if (tid < kBlock) {
+    float* act = s_act + tid * DS;
+    for (int d = 0; d < D; ++d) act[d] = 0.0f;
+  }
+  __syncthreads();
+  stage_out<kVec>(a.dx + row0 * D, nrows * D, D, DS, s_mu);
+
+  // Column sums of the dlog_std terms over this block's rows: `groups`
+  // threads per column, then one thread per column, fixed order, fp64.
+  {
+    __shared__ double s_col[kBlock];
+    const int groups = kBlock / D;
+    double sum = 0.0;
+    const int t = threadIdx.x;
+    if (t < groups * D) {
+      const int d = t % D;
+      const int g = t / D;
+      for (int r = g; r < kBlock; r += groups) sum += (double)s_act[r * DS + d];
+    }
+    s_col[t] = sum;
+    __syncthreads();
+    if (t < D) {
+      double c = 0.0;
+      for (int g = 0; g < groups; ++g) c += s_col[g * D + t];
+      a.partial[(long)blockIdx.x * kGaussSlots + kScalarSlots + t] = c;
+    }
+  }
+  const float h_const = s_hconst;
+  // the last block also finishes dlog_std = sum_b partial - ec
+  block_sum<5>(acc);
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int k = 0; k < 5; ++k) a.partial[(long)blockIdx.x * kGaussSlots + k] = acc[k];
+  }
+  const long nblocks = gridDim.x;
+  if (!arrive_last(&a.hdr->done[0], (unsigned)nblocks)) return;
+  {
+    __shared__ double s_red[kBlock];
+    // dlog_std: column d summed over blocks; `groups` threads per column.
+    const int groups = kBlock / D;
+    const int t = threadIdx.x;
+    double sum = 0.0;
+    if (t < groups * D) {
+      const int d = t % D;
+      const int g = t / D;
+      for (long b = g; b < nblocks; b += groups)
+        sum += a.partial[b * kGaussSlots + kScalarSlots + d];
+    }
+    s_red[t] = sum;
+    __syncthreads();
+    if (t < D) {
+      double c = 0.0;
+      for (int g = 0; g < groups; ++g) c += s_red[g * D + t];
+      a.dlog_std[t] = (float)c - a.ec;
+    }
+  }
+  double tot[5] = {0, 0, 0, 0, 0};
+  const long per = (nblocks + blockDim.x - 1) / blockDim.x;
+  const long lo = (long)threadIdx.x * per;
+  const long hi = lo + per < nblocks ? lo + per : nblocks;
+  for (long b = lo; b < hi; ++b)
+#pragma unroll
+    for (int k = 0; k < 5; ++k) tot[k] += a.partial[b * kGaussSlots + k];
+  block_sum<5>(tot);
+  if (threadIdx.x == 0) {
+    const double nb = (double)a.B;
+    const float pol = (float)(tot[0] / nb);
+    const float vl = (float)(tot[1] / nb);
+    const float ent = h_const;
+    a.scalars[PPO_SCALAR_POLICY] = pol;
+    a.scalars[PPO_SCALAR_VALUE] = vl;
+    a.scalars[PPO_SCALAR_ENTROPY] = ent;
+    a.scalars[PPO_SCALAR_APPROX_KL] = (float)(tot[3] / nb);
+    a.scalars[PPO_SCALAR_CLIPFRAC] = (float)(tot[4] / nb);
+    a.scalars[PPO_SCALAR_LOSS] = (pol + a.vc * vl) - a.ec * ent;
+  }
+  reset_counter(&a.hdr->done[0]);
+}
+
+int fill_common(LossArgs& a, long B, const ppo_loss_params* p, const float* old_lp,
+                const float* adv, const float* ret, const float* val, const float* old_val,
+                float* dval, float* scalars) {
+  if (!p || !old_lp || !adv || !ret || !val || !dval || !scalars) return PPO_ERR_INVALID_ARG;
+  if (!(p->clip_ratio >= 0.0)) return PPO_ERR_INVALID_ARG;
+  a.B = B;
+  a.old_lp = old_lp;
+  a.adv = adv;
+  a.ret = ret;
+  a.val = val;
+  a.old_val = old_val;
+  // torch: ratio.clamp(1.0 - clip, 1.0 + clip) takes Python-double bounds
+  // and compares in fp32.
+  a.lo = (float)(1.0 - p->clip_ratio);
+  a.hi = (float)(1.0 + p->clip_ratio);
+  a.clip = (float)p->clip_ratio;
+  a.use_vclip = (p->vf_clip > 0.0 && p->vf_clip < INFINITY) ? 1 : 0;
+  if (a.use_vclip && !old_val) return PPO_ERR_INVALID_ARG;
+  a.vclip = (float)p->vf_clip;
+  a.vc = (float)p->value_coef;
+  a.ec = (float)p->entropy_coef;
+  a.inv_b = 1.0f / (float)B;
+  a.dval = dval;
+  a.scalars = scalars;
+  return PPO_OK;
+}
+
+long cat_blocks(long B, int A) {
+  if (A <= kMaxCatRowWidth) return (B + kBlock - 1) / kBlock;
+  return std::max(1L, std::min((B + 3) / 4, kWaveRowBlocks));
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" size_t ppo_loss_cat_workspace_bytes(int64_t B, int32_t A) {
+  using namespace ppo;
+  if (B <= 0 || A <= 0) return kHeaderBytes;
+  return kHeaderBytes + align_up((size_t)cat_blocks(B, A) * kScalarSlots * sizeof(double), 256);
+}
+
+extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const void* actions,
+                                int actions_are_int64, const float* old_log_probs,
+                                const float* advantages, const float* returns,
+                                const float* values, const float* old_values,
+                                const ppo_loss_params* params, float* dlogits, float* dvalues,
+                                float* scalars_out, void* workspace, size_t workspace_bytes,
+                                void* stream_ptr) {
+  using namespace ppo;
+  if (B <= 0 || A <= 0) return PPO_ERR_INVALID_ARG;
+  if (!logits || !actions || !dlogits) return PPO_ERR_INVALID_ARG;
+  if (B > 0x7fffffffL * (long)kBlock / 2 || (long)B * A > (1L << 50)) return PPO_ERR_TOO_LARGE;
+  if (!workspace || workspace_bytes < ppo_loss_cat_workspace_bytes(B, A)) return PPO_ERR_WORKSPACE;
+  LossArgs a = {};
+  int st = fill_common(a, B, params, old_log_probs, advantages, returns, values, old_values,
+                       dvalues, scalars_out);
+  if (st) return st;
+  a.x = logits;
+  a.A = A;
+  a.actions = actions;
+  a.dx = dlogits;
+  a.hdr = reinterpret_cast<WsHeader*>(workspace);
+  a.partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  const long blocks = cat_blocks(B, A);
+  if (A <= kMaxCatRowWidth) {
+    const bool vec = aligned(logits, 16) && aligned(dlogits, 16);
+    const size_t lds = (size_t)kBlock * (A | 1) * sizeof(float);
+    if (actions_are_int64) {
+      if (vec)
+        hipLaunchKernelGGL((loss_cat_kernel<int64_t, true>), dim3((unsigned)blocks), dim3(kBlock),
+                           lds, stream, a);
+      else
+        hipLaunchKernelGGL((loss_cat_kernel<int64_t, false>), dim3((unsigned)blocks),
+                           dim3(kBlock), lds, stream, a);
+    } else {
+      if (vec)
+        hipLaunchKernelGGL((loss_cat_kernel<int32_t, true>), dim3((unsigned)blocks), dim3(kBlock),
+                           lds, stream, a);
+      else
+        hipLaunchKernelGGL((loss_cat_kernel<int32_t, false>), dim3((unsigned)blocks),
+                           dim3(kBlock), lds, stream, a);
+    }
+  } else {
+    if (actions_are_int64)
+      hipLaunchKernelGGL(loss_cat_wave_kernel<int64_t>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                         stream, a);
+    else
+      hipLaunchKernelGGL(loss_cat_wave_kernel<int32_t>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                         stream, a);
+  }
+  return last_launch_status();
+}
+
+extern "C" size_t ppo_loss_gauss_workspace_bytes(int64_t B, int32_t D) {
+  using namespace ppo;
+  if (B <= 0 || D <= 0) return kHeaderBytes;
+  const long blocks = (B + kBlock - 1) / kBlock;
+  return kHeaderBytes + align_up((size_t)blocks * kGaussSlots * sizeof(double), 256);
+}
+
+extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t B, int32_t D,
+                                  const float* actions, const float* old_log_probs,
+                                  const float* advantages, const float* returns,
+                                  const float* values, const float* old_values,
+                                  const ppo_loss_params* params, float* dmu, float* dlog_std,
+                                  float* dvalues, float* scalars_out, void* workspace,
+                                  size_t workspace_bytes, void* stream_ptr) {
+  using namespace ppo;
+  if (B <= 0 || D <= 0) return PPO_ERR_INVALID_ARG;
+  if (D > kMaxGaussDim) return PPO_ERR_TOO_LARGE;
+  if (!mu || !log_std || !actions || !dmu || !dlog_std) return PPO_ERR_INVALID_ARG;
+  if (B > 0x7fffffffL * (long)kBlock / 2) return PPO_ERR_TOO_LARGE;
+  if (!workspace || workspace_bytes < ppo_loss_gauss_workspace_bytes(B, D))
+    return PPO_ERR_WORKSPACE;
+  LossArgs a = {};
+  int st = fill_common(a, B, params, old_log_probs, advantages, returns, values, old_values,
+                       dvalues, scalars_out);
+  if (st) return st;
+  a.x = mu;
+  a.log_std = log_std;
+  a.A = D;
+  a.actions = actions;
+  a.dx = dmu;
+  a.dlog_std = dlog_std;
+  a.hdr = reinterpret_cast<WsHeader*>(workspace);
+  a.partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  const long blocks = (B + kBlock - 1) / kBlock;
+  const size_t lds = (size_t)2 * kBlock * (D | 1) * sizeof(float);
+  const bool vec = aligned(mu, 16) && aligned(actions, 16) && aligned(dmu, 16);
+  if (vec)
+    hipLaunchKernelGGL(loss_gauss_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), lds, stream,
+                       a);
+  else
+    hipLaunchKernelGGL(loss_gauss_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds,
+                       stream, a);
+  return last_launch_status();
+}

@@ -1,0 +1,66 @@
+"""ppo_amd — the PPO update path of mrhooray/zero-to-hero (rl/deep) on MI355X.
+
+Hand-written HIP kernels for gfx950 (libppo_amd.so, C ABI in
+include/ppo_amd.h) behind the reference's own PPO surface:
+
+  ops       gae, gae_normalize, normalize_advantages, ppo_loss_discrete,
+            ppo_loss_gaussian (+ *_fused functional forms)
+  agent     PPOAgent, PPOConfig, TrainingConfig, MLP, Transition,
+            RolloutStep, PendingStep, cartpole_sizes — rl/deep/agents/ppo.py
+            and common.py, same names and signatures
+  rollout   RolloutBuffer ([T,N] env-contiguous, on device) and VecPPO
+"""
+
+from . import _lib
+from .agent import (
+    MLP,
+    PendingStep,
+    PPOAgent,
+    PPOConfig,
+    RolloutStep,
+    TrainingConfig,
+    Transition,
+    cartpole_sizes,
+)
+from .ops import (
+    LossStats,
+    gae,
+    gae_normalize,
+    normalize_advantages,
+    ppo_loss_discrete,
+    ppo_loss_discrete_fused,
+    ppo_loss_gaussian,
+    ppo_loss_gaussian_fused,
+)
+from .rollout import RolloutBuffer, VecPPO
+
+LIB_PATH = _lib.LIB_PATH
+
+
+def load_library():
+    """Load libppo_amd.so (raises if it is not built)."""
+    return _lib.load()
+
+
+__all__ = [
+    "LIB_PATH",
+    "LossStats",
+    "MLP",
+    "PPOAgent",
+    "PPOConfig",
+    "PendingStep",
+    "RolloutBuffer",
+    "RolloutStep",
+    "TrainingConfig",
+    "Transition",
+    "VecPPO",
+    "cartpole_sizes",
+    "gae",
+    "gae_normalize",
+    "load_library",
+    "normalize_advantages",
+    "ppo_loss_discrete",
+    "ppo_loss_discrete_fused",
+    "ppo_loss_gaussian",
+    "ppo_loss_gaussian_fused",
+]

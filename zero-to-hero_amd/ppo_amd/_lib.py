@@ -1,0 +1,100 @@
+"""ctypes binding of libppo_amd.so, the C ABI declared in include/ppo_amd.h.
+
+The library is built in-tree (ppo_amd/build.py or csrc/Makefile) and loaded
+from this directory.  There is no fallback: if the library is missing or does
+not load, every op raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+LIB_NAME = "libppo_amd.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+PPO_OK = 0
+PPO_NUM_SCALARS = 6
+SCALAR_NAMES = ("loss", "policy", "value", "entropy", "approx_kl", "clipfrac")
+
+
+class LossParams(ctypes.Structure):
+    """struct ppo_loss_params (include/ppo_amd.h)."""
+
+    _fields_ = [
+        ("clip_ratio", ctypes.c_double),
+        ("vf_clip", ctypes.c_double),
+        ("value_coef", ctypes.c_double),
+        ("entropy_coef", ctypes.c_double),
+    ]
+
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f64 = ctypes.c_double
+_sz = ctypes.c_size_t
+_int = ctypes.c_int
+
+# name -> (restype, argtypes); one entry per function in include/ppo_amd.h
+SIGNATURES = {
+    "ppo_amd_version": (_int, []),
+    "ppo_amd_strerror": (ctypes.c_char_p, [_int]),
+    "ppo_gae_workspace_bytes": (_sz, [_i64, _i64]),
+    "ppo_gae_f32": (
+        _int,
+        [_vp, _vp, _vp, _vp, _i64, _i64, _f64, _f64, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "ppo_gae_norm_f32": (
+        _int,
+        [_vp, _vp, _vp, _vp, _i64, _i64, _f64, _f64, _f64, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "ppo_adv_norm_workspace_bytes": (_sz, [_i64]),
+    "ppo_adv_norm_f32": (_int, [_vp, _i64, _f64, _vp, _vp, _vp, _sz, _vp]),
+    "ppo_loss_cat_workspace_bytes": (_sz, [_i64, _i32]),
+    "ppo_loss_cat_f32": (
+        _int,
+        [_vp, _i64, _i32, _vp, _int, _vp, _vp, _vp, _vp, _vp,
+         ctypes.POINTER(LossParams), _vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "ppo_loss_gauss_workspace_bytes": (_sz, [_i64, _i32]),
+    "ppo_loss_gauss_f32": (
+        _int,
+        [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
+         ctypes.POINTER(LossParams), _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libppo_amd.so once and attach the prototypes; raise if absent."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built. Build it with `python -m ppo_amd.build` "
+                "(or __graft_entry__.build()); ppo_amd has no CPU fallback."
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+class PPOLibraryError(RuntimeError):
+    """A non-zero return code from libppo_amd."""
+
+    def __init__(self, fn: str, code: int) -> None:
+        msg = load().ppo_amd_strerror(code).decode()
+        super().__init__(f"{fn} failed with code {code}: {msg}")
+        self.code = code
+
+
+def check(fn: str, code: int) -> None:
+    if code != PPO_OK:
+        raise PPOLibraryError(fn, code)

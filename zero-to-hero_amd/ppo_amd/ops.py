@@ -1,0 +1,468 @@
+"""Torch-facing ops over libppo_amd (HIP kernels for gfx950).
+
+Each op validates its tensors on the host (device, dtype, shape, contiguity),
+allocates outputs with torch, and enqueues the HIP kernels on torch's current
+stream through the C ABI of include/ppo_amd.h.  Nothing here synchronises the
+host, and nothing falls back to a CPU implementation: a missing library or a
+non-CUDA tensor raises.
+
+Reference functions replaced (mrhooray/zero-to-hero, rl/deep/agents/ppo.py):
+  gae / gae_normalize     PPOAgent._advantages (:173-193), returns (:124),
+                          normalisation (:126-127)
+  normalize_advantages    ppo.py:126-127
+  ppo_loss_discrete       PPOAgent._update_batch loss + backward (:150-169)
+  ppo_loss_gaussian       the same loss for a Normal policy (no reference code)
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "gae",
+    "gae_normalize",
+    "normalize_advantages",
+    "ppo_loss_discrete",
+    "ppo_loss_discrete_fused",
+    "ppo_loss_gaussian",
+    "ppo_loss_gaussian_fused",
+    "LossStats",
+]
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require(t: torch.Tensor, name: str, dtypes: tuple, device=None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"{name} is on {t.device}; ppo_amd runs on the GPU only (no CPU fallback)"
+        )
+    if device is not None and t.device != device:
+        raise RuntimeError(f"{name} is on {t.device}, expected {device}")
+    if t.dtype not in dtypes:
+        names = ", ".join(str(d) for d in dtypes)
+        raise TypeError(f"{name} has dtype {t.dtype}, expected one of {names}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class _WorkspacePool:
+    """One zero-initialised scratch buffer per (device, stream).
+
+    libppo_amd needs caller-owned scratch whose first 256 bytes start at zero
+    and are left at zero by every call.  Calls on one stream are ordered, so
+    they can share a buffer; a different stream gets its own.
+    """
+
+    def __init__(self) -> None:
+        self._bufs: dict = {}
+
+    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        key = (device.index, stream)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 0 if buf is None else 2 * buf.numel(), 4096)
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+    def drop(self, device: torch.device, stream: int) -> None:
+        # after a failed launch the counters may not be back at zero
+        self._bufs.pop((device.index, stream), None)
+
+
+_WORKSPACES = _WorkspacePool()
+
+
+def _call(name: str, device: torch.device, stream: int, *args) -> None:
+    lib = _lib.load()
+    code = getattr(lib, name)(*args)
+    if code != _lib.PPO_OK:
+        _WORKSPACES.drop(device, stream)
+        _lib.check(name, code)
+
+
+def _as_2d(t: torch.Tensor) -> torch.Tensor:
+    return t.unsqueeze(1) if t.dim() == 1 else t
+
+
+def _done_bytes(dones: torch.Tensor) -> torch.Tensor:
+    if dones.dtype == torch.bool:
+        return dones.view(torch.uint8)
+    return dones
+
+
+# ---------------------------------------------------------------------------
+# GAE and normalisation
+# ---------------------------------------------------------------------------
+def _gae_inputs(rewards, values, dones, last_value):
+    _require(rewards, "rewards", (torch.float32,))
+    device = rewards.device
+    _require(values, "values", (torch.float32,), device)
+    _require(dones, "dones", (torch.uint8, torch.bool), device)
+    if rewards.dim() not in (1, 2):
+        raise ValueError(f"rewards must be [T] or [T,N], got shape {tuple(rewards.shape)}")
+    if values.shape != rewards.shape or dones.shape != rewards.shape:
+        raise ValueError(
+            "rewards, values and dones must share one shape, got "
+            f"{tuple(rewards.shape)}, {tuple(values.shape)}, {tuple(dones.shape)}"
+        )
+    r2 = _as_2d(rewards)
+    T, N = r2.shape
+    if last_value is not None:
+        _require(last_value, "last_value", (torch.float32,), device)
+        if last_value.numel() != N:
+            raise ValueError(f"last_value must hold N={N} values, got {last_value.numel()}")
+    return device, T, N
+
+
+def gae(
+    rewards: torch.Tensor,
+    values: torch.Tensor,
+    dones: torch.Tensor,
+    last_value: Optional[torch.Tensor] = None,
+    gamma: float = 0.99,
+    lam: float = 0.95,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Advantages and returns of a [T,N] (or [T]) rollout on the GPU.
+
+    Same recurrence as PPOAgent._advantages (ppo.py:173-193), per env, in fp64
+    with the reference's operation order; `dones` is terminated-or-truncated
+    (uint8 or bool); `last_value` [N] bootstraps past step T-1 (None = zeros,
+    the reference's rule).  Returns (advantages, returns) fp32, same shape as
+    rewards, with returns = advantages + values (ppo.py:124).
+    """
+    device, T, N = _gae_inputs(rewards, values, dones, last_value)
+    adv = torch.empty_like(rewards)
+    ret = torch.empty_like(rewards)
+    if T * N == 0:
+        return adv, ret
+    stream = _stream(device)
+    nbytes = _lib.load().ppo_gae_workspace_bytes(T, N)
+    ws = _WORKSPACES.get(device, stream, nbytes)
+    _call(
+        "ppo_gae_f32", device, stream,
+        rewards.data_ptr(), values.data_ptr(), _done_bytes(dones).data_ptr(),
+        _ptr(last_value), T, N, float(gamma), float(lam),
+        adv.data_ptr(), ret.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+    )
+    return adv, ret
+
+
+def gae_normalize(
+    rewards: torch.Tensor,
+    values: torch.Tensor,
+    dones: torch.Tensor,
+    last_value: Optional[torch.Tensor] = None,
+    gamma: float = 0.99,
+    lam: float = 0.95,
+    eps: float = 1e-8,
+    return_stats: bool = False,
+):
+    """gae() plus the normalised advantages of ppo.py:126-127, fused: the
+    advantage mean/std are accumulated inside the GAE pass.  Returns
+    (advantages, returns, normalized_advantages[, stats]) where stats is a
+    [2] fp32 device tensor {mean, std}."""
+    device, T, N = _gae_inputs(rewards, values, dones, last_value)
+    adv = torch.empty_like(rewards)
+    ret = torch.empty_like(rewards)
+    adv_n = torch.empty_like(rewards)
+    stats = torch.empty(2, dtype=torch.float32, device=device)
+    if T * N > 0:
+        stream = _stream(device)
+        nbytes = _lib.load().ppo_gae_workspace_bytes(T, N)
+        ws = _WORKSPACES.get(device, stream, nbytes)
+        _call(
+            "ppo_gae_norm_f32", device, stream,
+            rewards.data_ptr(), values.data_ptr(), _done_bytes(dones).data_ptr(),
+            _ptr(last_value), T, N, float(gamma), float(lam), float(eps),
+            adv.data_ptr(), ret.data_ptr(), adv_n.data_ptr(), stats.data_ptr(),
+            ws.data_ptr(), ws.numel(), stream,
+        )
+    if return_stats:
+        return adv, ret, adv_n, stats
+    return adv, ret, adv_n
+
+
+def normalize_advantages(
+    advantages: torch.Tensor, eps: float = 1e-8, out: Optional[torch.Tensor] = None
+) -> torch.Tensor:
+    """(adv - adv.mean()) / (adv.std() + eps) over all elements, unbiased std,
+    and the identity for a single element (ppo.py:126-127)."""
+    _require(advantages, "advantages", (torch.float32,))
+    device = advantages.device
+    if out is None:
+        out = torch.empty_like(advantages)
+    else:
+        _require(out, "out", (torch.float32,), device)
+        if out.shape != advantages.shape:
+            raise ValueError("out must have the shape of advantages")
+    n = advantages.numel()
+    if n == 0:
+        return out
+    stream = _stream(device)
+    nbytes = _lib.load().ppo_adv_norm_workspace_bytes(n)
+    ws = _WORKSPACES.get(device, stream, nbytes)
+    _call(
+        "ppo_adv_norm_f32", device, stream,
+        advantages.data_ptr(), n, float(eps), out.data_ptr(), None,
+        ws.data_ptr(), ws.numel(), stream,
+    )
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Fused loss
+# ---------------------------------------------------------------------------
+class LossStats(dict):
+    """Loss scalars as 0-d fp32 device tensors: loss, policy, value, entropy,
+    approx_kl, clipfrac (views of one [6] tensor; no host sync)."""
+
+
+def _stats_dict(scalars: torch.Tensor) -> LossStats:
+    s = scalars.detach()
+    return LossStats({name: s[i] for i, name in enumerate(_lib.SCALAR_NAMES)})
+
+
+def _params(clip_ratio, vf_clip, value_coef, entropy_coef) -> _lib.LossParams:
+    if not clip_ratio >= 0.0:
+        raise ValueError(f"clip_ratio must be >= 0, got {clip_ratio}")
+    vc = 0.0 if vf_clip is None else float(vf_clip)
+    if vf_clip is not None and not vc > 0.0:
+        raise ValueError(f"vf_clip must be > 0 or None, got {vf_clip}")
+    return _lib.LossParams(float(clip_ratio), vc, float(value_coef), float(entropy_coef))
+
+
+def _row_inputs(device, B, old_log_probs, advantages, returns, values, old_values, vf_clip):
+    for t, name in (
+        (old_log_probs, "old_log_probs"),
+        (advantages, "advantages"),
+        (returns, "returns"),
+        (values, "values"),
+    ):
+        _require(t, name, (torch.float32,), device)
+        if t.numel() != B or t.dim() != 1:
+            raise ValueError(f"{name} must be [B]=[{B}], got {tuple(t.shape)}")
+    if vf_clip is not None:
+        if old_values is None:
+            raise ValueError("old_values is required when vf_clip is set")
+    if old_values is not None:
+        _require(old_values, "old_values", (torch.float32,), device)
+        if old_values.numel() != B or old_values.dim() != 1:
+            raise ValueError(f"old_values must be [B]=[{B}], got {tuple(old_values.shape)}")
+
+
+def ppo_loss_discrete_fused(
+    logits: torch.Tensor,
+    actions: torch.Tensor,
+    old_log_probs: torch.Tensor,
+    advantages: torch.Tensor,
+    returns: torch.Tensor,
+    values: torch.Tensor,
+    old_values: Optional[torch.Tensor] = None,
+    clip_ratio: float = 0.2,
+    vf_clip: Optional[float] = None,
+    value_coef: float = 0.5,
+    entropy_coef: float = 0.01,
+    validate_args: bool = False,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One launch of the fused categorical PPO loss forward+backward.
+
+    Returns (scalars[6], dlogits[B,A], dvalues[B]) with scalars ordered as
+    LossStats; the gradients are d loss / d logits and d loss / d values.
+    With validate_args, out-of-range actions raise ValueError as
+    torch.distributions.Categorical's support check does (this syncs);
+    without it, such a row's log-prob is NaN.
+    """
+    _require(logits, "logits", (torch.float32,))
+    device = logits.device
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [B,A], got {tuple(logits.shape)}")
+    B, A = logits.shape
+    _require(actions, "actions", (torch.int32, torch.int64), device)
+    if actions.numel() != B or actions.dim() != 1:
+        raise ValueError(f"actions must be [B]=[{B}], got {tuple(actions.shape)}")
+    _row_inputs(device, B, old_log_probs, advantages, returns, values, old_values, vf_clip)
+    if B == 0 or A == 0:
+        raise ValueError("logits must have B > 0 rows and A > 0 actions")
+    if validate_args:
+        bad = ((actions < 0) | (actions >= A)).any()
+        if bool(bad):
+            raise ValueError(
+                "The value argument must be within the support of the categorical "
+                f"distribution (actions in [0, {A}))"
+            )
+    params = _params(clip_ratio, vf_clip, value_coef, entropy_coef)
+    dlogits = torch.empty_like(logits)
+    dvalues = torch.empty_like(values)
+    scalars = torch.empty(_lib.PPO_NUM_SCALARS, dtype=torch.float32, device=device)
+    stream = _stream(device)
+    nbytes = _lib.load().ppo_loss_cat_workspace_bytes(B, A)
+    ws = _WORKSPACES.get(device, stream, nbytes)
+    _call(
+        "ppo_loss_cat_f32", device, stream,
+        logits.data_ptr(), B, A, actions.data_ptr(), int(actions.dtype == torch.int64),
+        old_log_probs.data_ptr(), advantages.data_ptr(), returns.data_ptr(),
+        values.data_ptr(), _ptr(old_values), ctypes.byref(params),
+        dlogits.data_ptr(), dvalues.data_ptr(), scalars.data_ptr(),
+        ws.data_ptr(), ws.numel(), stream,
+    )
+    return scalars, dlogits, dvalues
+
+
+class _DiscreteLoss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits, values, actions, old_log_probs, advantages, returns,
+                old_values, clip_ratio, vf_clip, value_coef, entropy_coef, validate_args):
+        scalars, dlogits, dvalues = ppo_loss_discrete_fused(
+            logits.detach(), actions, old_log_probs, advantages, returns, values.detach(),
+            old_values, clip_ratio, vf_clip, value_coef, entropy_coef, validate_args,
+        )
+        ctx.save_for_backward(dlogits, dvalues)
+        return scalars
+
+    @staticmethod
+    def backward(ctx, grad_scalars):
+        dlogits, dvalues = ctx.saved_tensors
+        g = grad_scalars[0]
+        return (dlogits * g, dvalues * g) + (None,) * 10
+
+
+def ppo_loss_discrete(
+    logits: torch.Tensor,
+    actions: torch.Tensor,
+    old_log_probs: torch.Tensor,
+    advantages: torch.Tensor,
+    returns: torch.Tensor,
+    values: torch.Tensor,
+    old_values: Optional[torch.Tensor] = None,
+    clip_ratio: float = 0.2,
+    vf_clip: Optional[float] = None,
+    value_coef: float = 0.5,
+    entropy_coef: float = 0.01,
+    validate_args: bool = False,
+) -> tuple[torch.Tensor, LossStats]:
+    """Differentiable PPO loss of a categorical policy (ppo.py:150-167).
+
+    Returns (loss, stats): `loss` is a 0-d tensor whose backward delivers the
+    fused kernel's d loss / d logits and d loss / d values (scaled by the
+    incoming gradient); `stats` holds the component scalars, which are
+    reported values, not differentiable outputs.
+    """
+    scalars = _DiscreteLoss.apply(
+        logits, values, actions, old_log_probs, advantages, returns, old_values,
+        clip_ratio, vf_clip, value_coef, entropy_coef, validate_args,
+    )
+    return scalars[0], _stats_dict(scalars)
+
+
+def ppo_loss_gaussian_fused(
+    mu: torch.Tensor,
+    log_std: torch.Tensor,
+    actions: torch.Tensor,
+    old_log_probs: torch.Tensor,
+    advantages: torch.Tensor,
+    returns: torch.Tensor,
+    values: torch.Tensor,
+    old_values: Optional[torch.Tensor] = None,
+    clip_ratio: float = 0.2,
+    vf_clip: Optional[float] = None,
+    value_coef: float = 0.5,
+    entropy_coef: float = 0.01,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One launch of the fused Gaussian PPO loss forward+backward.
+
+    Policy Normal(mu, exp(log_std)), log_std [D] state-independent, log-prob
+    and entropy summed over D.  Returns (scalars[6], dmu[B,D], dlog_std[D],
+    dvalues[B]).
+    """
+    _require(mu, "mu", (torch.float32,))
+    device = mu.device
+    if mu.dim() != 2:
+        raise ValueError(f"mu must be [B,D], got {tuple(mu.shape)}")
+    B, D = mu.shape
+    if B == 0 or D == 0:
+        raise ValueError("mu must have B > 0 rows and D > 0 dims")
+    if D > 24:
+        raise ValueError(f"action dim D={D} exceeds the kernel's limit of 24")
+    _require(log_std, "log_std", (torch.float32,), device)
+    if log_std.numel() != D or log_std.dim() != 1:
+        raise ValueError(f"log_std must be [D]=[{D}], got {tuple(log_std.shape)}")
+    _require(actions, "actions", (torch.float32,), device)
+    if actions.shape != mu.shape:
+        raise ValueError(f"actions must be [B,D]={tuple(mu.shape)}, got {tuple(actions.shape)}")
+    _row_inputs(device, B, old_log_probs, advantages, returns, values, old_values, vf_clip)
+    params = _params(clip_ratio, vf_clip, value_coef, entropy_coef)
+    dmu = torch.empty_like(mu)
+    dlog_std = torch.empty_like(log_std)
+    dvalues = torch.empty_like(values)
+    scalars = torch.empty(_lib.PPO_NUM_SCALARS, dtype=torch.float32, device=device)
+    stream = _stream(device)
+    nbytes = _lib.load().ppo_loss_gauss_workspace_bytes(B, D)
+    ws = _WORKSPACES.get(device, stream, nbytes)
+    _call(
+        "ppo_loss_gauss_f32", device, stream,
+        mu.data_ptr(), log_std.data_ptr(), B, D, actions.data_ptr(),
+        old_log_probs.data_ptr(), advantages.data_ptr(), returns.data_ptr(),
+        values.data_ptr(), _ptr(old_values), ctypes.byref(params),
+        dmu.data_ptr(), dlog_std.data_ptr(), dvalues.data_ptr(), scalars.data_ptr(),
+        ws.data_ptr(), ws.numel(), stream,
+    )
+    return scalars, dmu, dlog_std, dvalues
+
+
+class _GaussianLoss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, mu, log_std, values, actions, old_log_probs, advantages, returns,
+                old_values, clip_ratio, vf_clip, value_coef, entropy_coef):
+        scalars, dmu, dlog_std, dvalues = ppo_loss_gaussian_fused(
+            mu.detach(), log_std.detach(), actions, old_log_probs, advantages, returns,
+            values.detach(), old_values, clip_ratio, vf_clip, value_coef, entropy_coef,
+        )
+        ctx.save_for_backward(dmu, dlog_std, dvalues)
+        return scalars
+
+    @staticmethod
+    def backward(ctx, grad_scalars):
+        dmu, dlog_std, dvalues = ctx.saved_tensors
+        g = grad_scalars[0]
+        return (dmu * g, dlog_std * g, dvalues * g) + (None,) * 9
+
+
+def ppo_loss_gaussian(
+    mu: torch.Tensor,
+    log_std: torch.Tensor,
+    actions: torch.Tensor,
+    old_log_probs: torch.Tensor,
+    advantages: torch.Tensor,
+    returns: torch.Tensor,
+    values: torch.Tensor,
+    old_values: Optional[torch.Tensor] = None,
+    clip_ratio: float = 0.2,
+    vf_clip: Optional[float] = None,
+    value_coef: float = 0.5,
+    entropy_coef: float = 0.01,
+) -> tuple[torch.Tensor, LossStats]:
+    """Differentiable PPO loss of a Normal(mu, exp(log_std)) policy; gradients
+    reach mu, log_std and values.  See ppo_loss_discrete for the contract."""
+    scalars = _GaussianLoss.apply(
+        mu, log_std, values, actions, old_log_probs, advantages, returns, old_values,
+        clip_ratio, vf_clip, value_coef, entropy_coef,
+    )
+    return scalars[0], _stats_dict(scalars)

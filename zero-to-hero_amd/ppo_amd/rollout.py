@@ -1,0 +1,167 @@
+"""Env-contiguous [T,N] rollout buffer and the vectorised PPO update.
+
+The reference stores one episode as a Python list of RolloutStep records and
+stacks them at update time (rl/deep/agents/ppo.py:93-106, :114-122).  Here the
+rollout of N parallel environments lives on the device as dense [T,N] arrays,
+row t holding step t of every env (element (t, n) at t*N + n): exactly the
+layout the GAE kernel streams.  `VecPPO.update` is PPOAgent._update
+(ppo.py:113-139) over the flattened T*N samples.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch import nn
+
+from . import ops
+from .agent import PPOConfig
+
+
+class RolloutBuffer:
+    """Device-resident [T,N] rollout storage.
+
+    Fields: observations [T,N,*obs_shape] f32, actions [T,N] int32 (discrete)
+    or [T,N,D] f32 (continuous), rewards/values/log_probs [T,N] f32,
+    dones [T,N] uint8 (terminated or truncated), last_value [N] f32 (the value
+    of the state after step T-1, used to bootstrap).
+    """
+
+    def __init__(
+        self,
+        T: int,
+        N: int,
+        obs_shape: tuple,
+        device: str | torch.device = "cuda",
+        action_dim: Optional[int] = None,
+    ) -> None:
+        if T <= 0 or N <= 0:
+            raise ValueError(f"T and N must be positive, got T={T}, N={N}")
+        dev = torch.device(device)
+        self.T, self.N, self.device = T, N, dev
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.observations = torch.zeros((T, N, *obs_shape), **f32)
+        if action_dim is None:
+            self.actions = torch.zeros((T, N), dtype=torch.int32, device=dev)
+        else:
+            self.actions = torch.zeros((T, N, action_dim), **f32)
+        self.rewards = torch.zeros((T, N), **f32)
+        self.values = torch.zeros((T, N), **f32)
+        self.log_probs = torch.zeros((T, N), **f32)
+        self.dones = torch.zeros((T, N), dtype=torch.uint8, device=dev)
+        self.last_value = torch.zeros(N, **f32)
+        self.step = 0
+
+    def add(self, observations, actions, rewards, dones, values, log_probs) -> None:
+        """Store step `self.step` for all N envs (ppo.py:93-106, batched)."""
+        if self.step >= self.T:
+            raise IndexError(f"rollout buffer is full (T={self.T})")
+        t = self.step
+        self.observations[t].copy_(observations)
+        self.actions[t].copy_(actions)
+        self.rewards[t].copy_(rewards)
+        self.dones[t].copy_(dones)
+        self.values[t].copy_(values)
+        self.log_probs[t].copy_(log_probs)
+        self.step += 1
+
+    def finish(self, last_value: Optional[torch.Tensor] = None) -> None:
+        """Set the bootstrap values (None: zeros, the reference's episode end)."""
+        if last_value is None:
+            self.last_value.zero_()
+        else:
+            self.last_value.copy_(last_value)
+
+    def reset(self) -> None:
+        self.step = 0
+
+    def compute_advantages(self, gamma: float = 0.99, lam: float = 0.95,
+                           normalize: bool = True, eps: float = 1e-8):
+        """(advantages, returns, normalized advantages) over the filled steps,
+        all [T,N] fp32 (ppo.py:123-127 generalised).  Without `normalize` the
+        third item is None."""
+        T = self.step
+        r, v, d = self.rewards[:T], self.values[:T], self.dones[:T]
+        if normalize:
+            return ops.gae_normalize(r, v, d, self.last_value, gamma, lam, eps)
+        adv, ret = ops.gae(r, v, d, self.last_value, gamma, lam)
+        return adv, ret, None
+
+
+class VecPPO:
+    """PPOAgent._update (ppo.py:113-171) for a [T,N] rollout.
+
+    `policy` maps observations to logits [B,A] (categorical) or to mu [B,D]
+    (gaussian, with the state-independent `log_std` parameter); `value` maps
+    observations to [B,1].  Minibatches come from torch.randperm on the CPU
+    generator `generator` (default: the global one, as ppo.py:130 uses).
+    """
+
+    def __init__(
+        self,
+        policy: nn.Module,
+        value: nn.Module,
+        ppo_config: PPOConfig = PPOConfig(),
+        gamma: float = 0.99,
+        lr: float = 3e-4,
+        batch_size: int = 128,
+        log_std: Optional[nn.Parameter] = None,
+        generator: Optional[torch.Generator] = None,
+    ) -> None:
+        self.policy, self.value = policy, value
+        self.ppo_config, self.gamma, self.batch_size = ppo_config, gamma, batch_size
+        self.log_std = log_std
+        self.generator = generator
+        self.parameters = list(policy.parameters()) + list(value.parameters())
+        if log_std is not None:
+            self.parameters.append(log_std)
+        self.optimizer = torch.optim.Adam(self.parameters, lr=lr)
+
+    def update(self, buffer: RolloutBuffer) -> dict:
+        """Run `epochs` passes of shuffled minibatches; returns the last
+        minibatch's loss scalars (device tensors)."""
+        cfg = self.ppo_config
+        adv, ret, adv_n = buffer.compute_advantages(self.gamma, cfg.gae_lambda, True)
+        T = buffer.step
+        n = T * buffer.N
+        if n <= 1:
+            adv_n = adv
+        obs = buffer.observations[:T].reshape(n, *buffer.observations.shape[2:])
+        acts = buffer.actions[:T].reshape(n, *buffer.actions.shape[2:])
+        old_lp = buffer.log_probs[:T].reshape(n)
+        old_v = buffer.values[:T].reshape(n)
+        adv_f, ret_f = adv_n.reshape(n), ret.reshape(n)
+        stats: dict = {}
+        for _ in range(cfg.epochs):
+            indices = torch.randperm(n, generator=self.generator)
+            for start in range(0, n, self.batch_size):
+                idx = indices[start : start + self.batch_size].to(buffer.device)
+                stats = self._update_batch(
+                    obs[idx], acts[idx], old_lp[idx], adv_f[idx], ret_f[idx], old_v[idx]
+                )
+        return stats
+
+    def _update_batch(self, observations, actions, old_log_probs, advantages, returns,
+                      old_values) -> dict:
+        cfg = self.ppo_config
+        values = self.value(observations).squeeze(1).contiguous()
+        if self.log_std is None:
+            logits = self.policy(observations).contiguous()
+            loss, stats = ops.ppo_loss_discrete(
+                logits, actions.contiguous(), old_log_probs, advantages, returns, values,
+                old_values if cfg.vf_clip is not None else None,
+                cfg.clip_ratio, cfg.vf_clip, cfg.value_coef, cfg.entropy_coef,
+            )
+        else:
+            mu = self.policy(observations).contiguous()
+            loss, stats = ops.ppo_loss_gaussian(
+                mu, self.log_std, actions.contiguous(), old_log_probs, advantages, returns,
+                values, old_values if cfg.vf_clip is not None else None,
+                cfg.clip_ratio, cfg.vf_clip, cfg.value_coef, cfg.entropy_coef,
+            )
+        self.optimizer.zero_grad()
+        loss.backward()
+        nn.utils.clip_grad_norm_(self.parameters, cfg.gradient_clip)
+        self.optimizer.step()
+        return stats
