@@ -65,11 +65,16 @@ def synthetic_rollout(torch, dev, T, N, A, seed=24):
     x["last_value"] = torch.randn(N, device=dev, generator=g)
     logits = torch.randn(B, A, device=dev, generator=g)
     old_logits = logits + 0.05 * torch.randn(B, A, device=dev, generator=g)
-    u = torch.rand(B, 1, device=dev, generator=g)
-    cdf = torch.softmax(old_logits, -1).cumsum(-1)
-    actions = (cdf < u).sum(-1).clamp_(max=A - 1)
+    # inverse-CDF sampling from softmax(old_logits), one column at a time
+    probs = torch.softmax(old_logits, -1)
+    u = torch.rand(B, device=dev, generator=g)
+    acc = torch.zeros(B, device=dev)
+    actions = torch.zeros(B, dtype=torch.int64, device=dev)
+    for j in range(A - 1):
+        acc += probs[:, j]
+        actions += (u >= acc).to(torch.int64)
     x["old_log_probs"] = torch.log_softmax(old_logits, -1).gather(1, actions[:, None]).squeeze(1)
-    del old_logits, cdf, u
+    del old_logits, probs, u, acc
     x["logits"] = logits
     x["actions"] = actions.to(torch.int32)
     x["new_values"] = x["values"].reshape(-1) + 0.1 * torch.randn(B, device=dev, generator=g)

@@ -15,10 +15,9 @@
  *     enqueues work on that stream: no host synchronisation, no device-wide
  *     synchronisation.
  *   - `workspace` is caller-owned device scratch of at least the size returned
- *     by the matching *_workspace_bytes() query.  Its first 256 bytes hold
- *     completion counters: they must be zero before the FIRST call that uses a
- *     workspace, and every call leaves them zero again.  Two calls that share
- *     one workspace must be ordered (same stream, or synchronised).
+ *     by the matching *_workspace_bytes() query; its contents on entry do not
+ *     matter.  Two calls that share one workspace must be ordered (same
+ *     stream, or synchronised).
  *   - Layouts are dense and row-major.  Rollout arrays are "[T,N]
  *     env-contiguous": element (t, n) lives at index t*N + n.
  *   - Return value: PPO_OK (0) or one of the PPO_ERR_* codes; codes

@@ -29,10 +29,20 @@ def assert_grad_close(got, expect, rtol=1e-4, floor=1e-5):
 
 
 def assert_scalars_close(scalars, o, rtol=1e-5):
+    """The reference's scalars (loss, policy, value, entropy) to rel 1e-5.
+    approx_kl = mean(old_lp - lp) is a build-only diagnostic and a
+    cancellation: each fp32 log-prob (magnitude ~log A) carries ~1e-7 of
+    rounding, so it is held to 1e-6 absolute; clipfrac counts rows and may
+    differ by a row whose ratio sits within an ulp of the clip bound."""
     s = scalars.detach().cpu()
     for i, k in enumerate(NAMES):
         e = o[k].item()
-        assert s[i].item() == pytest.approx(e, rel=rtol, abs=1e-7), k
+        if k == "approx_kl":
+            assert s[i].item() == pytest.approx(e, abs=1e-6), k
+        elif k == "clipfrac":
+            assert s[i].item() == pytest.approx(e, abs=2.0 / o["dvalues"].numel() + 1e-7), k
+        else:
+            assert s[i].item() == pytest.approx(e, rel=rtol, abs=1e-7), k
 
 
 def cat_inputs(B, A, seed, act_dtype=torch.int32):

@@ -1,8 +1,9 @@
 // Advantage normalisation (rl/deep/agents/ppo.py:126-127):
 //     if len(advantages) > 1:
 //         advantages = (advantages - advantages.mean()) / (advantages.std() + 1e-8)
-// Two kernels: a moments pass (fp64 Chan combine per thread, per block, then
-// by the last block) and an fp32 elementwise pass.
+// Three kernels: a moments pass (fp64 Chan combine per thread, then per
+// block), a one-block finaliser combining the block partials in a fixed order,
+// and an fp32 elementwise pass.
 #include <algorithm>
 
 #include "common.hpp"
@@ -29,8 +30,7 @@ __device__ __forceinline__ Moments moments4(float x0, float x1, float x2, float 
 
 template <bool kVec>
 __global__ void __launch_bounds__(kBlock) adv_moments_kernel(const float* adv, long n,
-                                                             double* partial, WsHeader* hdr,
-                                                             double eps, float* stats_out) {
+                                                             double* partial) {
   Moments m = {0.0, 0.0, 0.0};
   const long stride = (long)gridDim.x * blockDim.x;
   const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -55,10 +55,12 @@ __global__ void __launch_bounds__(kBlock) adv_moments_kernel(const float* adv, l
     partial[blockIdx.x * 4 + 2] = m.m2;
     partial[blockIdx.x * 4 + 3] = 0.0;
   }
-  if (arrive_last(&hdr->done[0], gridDim.x)) {
-    finalize_stats(partial, gridDim.x, eps, hdr, stats_out);
-    reset_counter(&hdr->done[0]);
-  }
+}
+
+__global__ void __launch_bounds__(kBlock) finalize_stats_kernel(const double* partial, long count,
+                                                                double eps, WsHeader* hdr,
+                                                                float* stats_out) {
+  finalize_stats(partial, count, eps, hdr, stats_out);
 }
 
 template <bool kVec>
@@ -88,6 +90,13 @@ __global__ void __launch_bounds__(kBlock) normalize_kernel(const float* adv, flo
 }
 
 }  // namespace
+
+int launch_finalize_stats(const double* partials, long count, double eps, WsHeader* hdr,
+                          float* stats_out, hipStream_t stream) {
+  hipLaunchKernelGGL(finalize_stats_kernel, dim3(1), dim3(kBlock), 0, stream, partials, count,
+                     eps, hdr, stats_out);
+  return last_launch_status();
+}
 
 int launch_normalize(const float* adv, float* out, long n, const WsHeader* hdr,
                      hipStream_t stream) {
@@ -127,11 +136,12 @@ extern "C" int ppo_adv_norm_f32(const float* adv, int64_t n, double eps, float* 
   const long blocks = stat_blocks(n);
   if (aligned(adv, 16))
     hipLaunchKernelGGL(adv_moments_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), 0, stream,
-                       adv, (long)n, partial, hdr, eps, stats_out);
+                       adv, (long)n, partial);
   else
     hipLaunchKernelGGL(adv_moments_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), 0,
-                       stream, adv, (long)n, partial, hdr, eps, stats_out);
+                       stream, adv, (long)n, partial);
   int st = last_launch_status();
   if (st) return st;
+  if ((st = launch_finalize_stats(partial, blocks, eps, hdr, stats_out, stream))) return st;
   return launch_normalize(adv, out, n, hdr, stream);
 }

@@ -10,12 +10,14 @@ namespace ppo {
 
 constexpr int kWave = 64;
 constexpr int kBlock = 256;              // threads per workgroup for streaming kernels
-constexpr size_t kHeaderBytes = 256;     // counters/flags at the front of every workspace
+constexpr size_t kHeaderBytes = 256;     // WsHeader at the front of every workspace
 
-// Workspace header: completion counters used by the "last workgroup finalises"
-// pattern.  Each kernel that uses a counter leaves it at zero on exit.
+// Workspace header.  Cross-workgroup results are always combined by a
+// separate one-block kernel launched after the producer on the same stream:
+// on gfx950 an in-kernel "last block finalises" handshake needs an agent-scope
+// release fence per workgroup, which compiles to a full L2 write-back
+// (buffer_wbl2) and costs far more than one extra launch.
 struct WsHeader {
-  unsigned int done[4];   // [0] stats/scalar combine of the kernel that owns it
   float stats[4];         // {mean, std, denom, 0} written by the stats finaliser
 };
 static_assert(sizeof(WsHeader) <= kHeaderBytes, "header too big");
@@ -112,29 +114,6 @@ __device__ inline void block_sum(double (&x)[K]) {
     }
   }
   __syncthreads();
-}
-
-// "Last workgroup finalises": call after thread 0 has stored this block's
-// partial result.  Returns true (in every thread) for the single block that
-// arrives last; that block then sees every other block's partials.  The
-// counter is reset by reset_counter() from the last block, so a workspace is
-// left zeroed for the next call.
-__device__ inline bool arrive_last(unsigned int* counter, unsigned int total) {
-  __shared__ int s_last;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();  // publish this block's partial before counting in
-    const unsigned int prev = atomicAdd(counter, 1u);
-    s_last = (prev == total - 1u);
-  }
-  __syncthreads();
-  const bool last = s_last != 0;
-  if (last) __threadfence();  // acquire: order the partial reads after the count
-  return last;
-}
-
-__device__ inline void reset_counter(unsigned int* counter) {
-  if (threadIdx.x == 0) atomicExch(counter, 0u);
 }
 
 // Moments of `count` partial triples (stored as 4 doubles each: n, mean, m2,

@@ -27,7 +27,8 @@
 //   3. gae_tile_kernel<.., kFinal=true>: re-reads the tile, rebuilds the
 //      segment composites, applies the tile carry, and runs the exact serial
 //      recurrence per segment, writing adv and ret (and, for the fused
-//      normaliser, per-block (n, mean, M2) of the advantages).
+//      normaliser, per-block (n, mean, M2) of the advantages, combined by a
+//      one-block finaliser before the elementwise normalise pass).
 // When the whole horizon fits in one tile (Tt == 1) steps 1-2 are skipped.
 #include <algorithm>
 
@@ -65,7 +66,7 @@ struct GaePlan {
 GaePlan make_plan(long T, long N, int vw) {
   GaePlan p;
   p.vw = vw;
-  p.L = vw == 4 ? 8 : 16;
+  p.L = vw == 4 ? 4 : 16;
   p.Q = N / vw;
   p.Qw = (int)std::min<long>(64, (long)pow2_ceil((unsigned)std::min<long>(p.Q, 64)));
   p.Sw = kBlock / p.Qw;
@@ -304,11 +305,6 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
         a.partial[bid * 4 + 2] = m.m2;
         a.partial[bid * 4 + 3] = 0.0;
       }
-      const long nblocks = a.Tt * a.Tq;
-      if (arrive_last(&a.hdr->done[0], (unsigned)nblocks)) {
-        finalize_stats(a.partial, nblocks, a.eps, a.hdr, a.stats_out);
-        reset_counter(&a.hdr->done[0]);
-      }
     }
   }
 }
@@ -410,10 +406,12 @@ int launch_gae(const GaePlan& p, GaeArgs a, bool stats, hipStream_t stream) {
   } else {
     a.carry = nullptr;
   }
-  if (stats)
+  if (stats) {
     hipLaunchKernelGGL((gae_tile_kernel<VW, L, true, true>), dim3((unsigned)blocks), dim3(kBlock),
                        0, stream, a);
-  else
+    if ((st = last_launch_status())) return st;
+    return launch_finalize_stats(a.partial, blocks, a.eps, a.hdr, a.stats_out, stream);
+  } else
     hipLaunchKernelGGL((gae_tile_kernel<VW, L, true, false>), dim3((unsigned)blocks),
                        dim3(kBlock), 0, stream, a);
   return last_launch_status();
@@ -457,7 +455,7 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
   a.stats_out = stats_out;
   a.eps = eps;
 
-  int st = vec ? launch_gae<4, 8>(p, a, norm, stream) : launch_gae<1, 16>(p, a, norm, stream);
+  int st = vec ? launch_gae<4, 4>(p, a, norm, stream) : launch_gae<1, 16>(p, a, norm, stream);
   if (st || !norm) return st;
   return launch_normalize(adv_out, adv_norm_out, T * N, a.hdr, stream);
 }

@@ -21,8 +21,8 @@
 // logits (a contiguous block of 256*A floats) through LDS with float4 loads,
 // row stride padded to an odd number of words so row-per-thread LDS reads are
 // bank-conflict-free, and writes dlogits back through the same tile.
-// Loss scalars are summed per block in fp64 and combined by the last block in
-// a fixed order (deterministic, no float atomics).
+// Loss scalars are summed per block in fp64 and combined in a fixed order by
+// a one-block finaliser kernel (deterministic, no float atomics).
 #include <float.h>
 
 #include <algorithm>
@@ -62,7 +62,6 @@ struct LossArgs {
   float* dval;
   float* scalars;
   double* partial;
-  WsHeader* hdr;
 };
 
 __device__ __forceinline__ float nan_min(float u, float w) {
@@ -186,17 +185,23 @@ __device__ __forceinline__ void stage_out(float* dst, int count, int width, int 
   }
 }
 
-// Block partial of the 5 loss sums -> partial[block*stride + 0..4]; the last
-// block combines all partials (fixed order) and writes scalars_out.
-__device__ inline void reduce_scalars(const LossArgs& a, double (&acc)[5], long block,
-                                      long nblocks, int stride, float h_const,
-                                      bool const_entropy) {
+// Block partial of the 5 loss sums -> partial[block*stride + 0..4].
+__device__ inline void store_scalar_partials(const LossArgs& a, double (&acc)[5], long block,
+                                             int stride) {
   block_sum<5>(acc);
   if (threadIdx.x == 0) {
 #pragma unroll
     for (int k = 0; k < 5; ++k) a.partial[block * stride + k] = acc[k];
   }
-  if (!arrive_last(&a.hdr->done[0], (unsigned)nblocks)) return;
+}
+
+// One-block finaliser, launched after the loss kernel on the same stream:
+// sums the per-block partials in a fixed order (deterministic), forms the
+// means and the total loss, and for the Gaussian policy (D > 0) finishes
+// dlog_std = sum over blocks of the per-block column sums - ec.
+__global__ void __launch_bounds__(kBlock) loss_finalize_kernel(LossArgs a, long nblocks, int stride,
+                                                               int D) {
+  __shared__ float s_hconst;
   double tot[5] = {0, 0, 0, 0, 0};
   const long per = (nblocks + blockDim.x - 1) / blockDim.x;
   const long lo = (long)threadIdx.x * per;
@@ -205,11 +210,38 @@ __device__ inline void reduce_scalars(const LossArgs& a, double (&acc)[5], long 
 #pragma unroll
     for (int k = 0; k < 5; ++k) tot[k] += a.partial[b * stride + k];
   block_sum<5>(tot);
+  if (D > 0) {
+    __shared__ double s_red[kBlock];
+    // column d summed over blocks by `groups` threads each, then per column
+    const int groups = kBlock / D;
+    const int t = threadIdx.x;
+    double sum = 0.0;
+    if (t < groups * D) {
+      const int d = t % D;
+      const int g = t / D;
+      for (long b = g; b < nblocks; b += groups) sum += a.partial[b * stride + kScalarSlots + d];
+    }
+    s_red[t] = sum;
+    __syncthreads();
+    if (t < D) {
+      double c = 0.0;
+      for (int g = 0; g < groups; ++g) c += s_red[g * D + t];
+      a.dlog_std[t] = (float)c - a.ec;
+    }
+    if (t == 0) {
+      // entropy of Normal(mu, scale) summed over dims, identical for every row
+      const float kEntConst = 1.41893853320467274178f;  // 0.5 + 0.5*log(2*pi)
+      float h = 0.0f;
+      for (int d = 0; d < D; ++d) h += kEntConst + logf(expf(a.log_std[d]));
+      s_hconst = h;
+    }
+    __syncthreads();
+  }
   if (threadIdx.x == 0) {
     const double nb = (double)a.B;
     const float pol = (float)(tot[0] / nb);
     const float vl = (float)(tot[1] / nb);
-    const float ent = const_entropy ? h_const : (float)(tot[2] / nb);
+    const float ent = D > 0 ? s_hconst : (float)(tot[2] / nb);
     a.scalars[PPO_SCALAR_POLICY] = pol;
     a.scalars[PPO_SCALAR_VALUE] = vl;
     a.scalars[PPO_SCALAR_ENTROPY] = ent;
@@ -217,7 +249,6 @@ __device__ inline void reduce_scalars(const LossArgs& a, double (&acc)[5], long 
     a.scalars[PPO_SCALAR_CLIPFRAC] = (float)(tot[4] / nb);
     a.scalars[PPO_SCALAR_LOSS] = (pol + a.vc * vl) - a.ec * ent;
   }
-  reset_counter(&a.hdr->done[0]);
 }
 
 // Action index of a row, or -1 when it lies outside [0, A).
@@ -273,7 +304,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_kernel(LossArgs a) {
   }
   __syncthreads();
   stage_out<kVec>(a.dx + row0 * A, nrows * A, A, AS, s_tile);
-  reduce_scalars(a, acc, blockIdx.x, gridDim.x, kScalarSlots, 0.0f, false);
+  store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
 }
 
 // ---------------------------------------------------------------------------
@@ -336,7 +367,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_wave_kernel(LossArgs a) {
       acc[4] += o.clipped;
     }
   }
-  reduce_scalars(a, acc, blockIdx.x, gridDim.x, kScalarSlots, 0.0f, false);
+  store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
 }
 
 // ---------------------------------------------------------------------------
@@ -348,7 +379,6 @@ template <bool kVec>
 __global__ void __launch_bounds__(kBlock) loss_gauss_kernel(LossArgs a) {
   extern __shared__ float s_lds[];
   __shared__ float s_2var[kMaxGaussDim], s_var[kMaxGaussDim], s_logscale[kMaxGaussDim];
-  __shared__ float s_hconst;
   const int D = a.A;
   const int DS = D | 1;
   float* s_mu = s_lds;
@@ -356,7 +386,6 @@ __global__ void __launch_bounds__(kBlock) loss_gauss_kernel(LossArgs a) {
   const long row0 = (long)blockIdx.x * kBlock;
   const int nrows = (int)std::min<long>(kBlock, a.B - row0);
   const float kLogSqrt2Pi = 0.91893853320467274178f;   // log(sqrt(2*pi))
-  const float kEntConst = 1.41893853320467274178f;     // 0.5 + 0.5*log(2*pi)
   if (threadIdx.x < D) {
     const float scale = expf(a.log_std[threadIdx.x]);
     const float var = scale * scale;
@@ -367,11 +396,6 @@ __global__ void __launch_bounds__(kBlock) loss_gauss_kernel(LossArgs a) {
   stage_in<kVec>(a.x + row0 * D, nrows * D, D, DS, s_mu);
   stage_in<kVec>(reinterpret_cast<const float*>(a.actions) + row0 * D, nrows * D, D, DS, s_act);
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float h = 0.0f;
-    for (int d = 0; d < D; ++d) h += kEntConst + s_logscale[d];
-    s_hconst = h;
-  }
 
   double acc[5] = {0, 0, 0, 0, 0};
   const int tid = threadIdx.x;
@@ -423,56 +447,7 @@ __global__ void __launch_bounds__(kBlock) loss_gauss_kernel(LossArgs a) {
       a.partial[(long)blockIdx.x * kGaussSlots + kScalarSlots + t] = c;
     }
   }
-  const float h_const = s_hconst;
-  // the last block also finishes dlog_std = sum_b partial - ec
-  block_sum<5>(acc);
-  if (threadIdx.x == 0) {
-#pragma unroll
-    for (int k = 0; k < 5; ++k) a.partial[(long)blockIdx.x * kGaussSlots + k] = acc[k];
-  }
-  const long nblocks = gridDim.x;
-  if (!arrive_last(&a.hdr->done[0], (unsigned)nblocks)) return;
-  {
-    __shared__ double s_red[kBlock];
-    // dlog_std: column d summed over blocks; `groups` threads per column.
-    const int groups = kBlock / D;
-    const int t = threadIdx.x;
-    double sum = 0.0;
-    if (t < groups * D) {
-      const int d = t % D;
-      const int g = t / D;
-      for (long b = g; b < nblocks; b += groups)
-        sum += a.partial[b * kGaussSlots + kScalarSlots + d];
-    }
-    s_red[t] = sum;
-    __syncthreads();
-    if (t < D) {
-      double c = 0.0;
-      for (int g = 0; g < groups; ++g) c += s_red[g * D + t];
-      a.dlog_std[t] = (float)c - a.ec;
-    }
-  }
-  double tot[5] = {0, 0, 0, 0, 0};
-  const long per = (nblocks + blockDim.x - 1) / blockDim.x;
-  const long lo = (long)threadIdx.x * per;
-  const long hi = lo + per < nblocks ? lo + per : nblocks;
-  for (long b = lo; b < hi; ++b)
-#pragma unroll
-    for (int k = 0; k < 5; ++k) tot[k] += a.partial[b * kGaussSlots + k];
-  block_sum<5>(tot);
-  if (threadIdx.x == 0) {
-    const double nb = (double)a.B;
-    const float pol = (float)(tot[0] / nb);
-    const float vl = (float)(tot[1] / nb);
-    const float ent = h_const;
-    a.scalars[PPO_SCALAR_POLICY] = pol;
-    a.scalars[PPO_SCALAR_VALUE] = vl;
-    a.scalars[PPO_SCALAR_ENTROPY] = ent;
-    a.scalars[PPO_SCALAR_APPROX_KL] = (float)(tot[3] / nb);
-    a.scalars[PPO_SCALAR_CLIPFRAC] = (float)(tot[4] / nb);
-    a.scalars[PPO_SCALAR_LOSS] = (pol + a.vc * vl) - a.ec * ent;
-  }
-  reset_counter(&a.hdr->done[0]);
+  store_scalar_partials(a, acc, blockIdx.x, kGaussSlots);
 }
 
 int fill_common(LossArgs& a, long B, const ppo_loss_params* p, const float* old_lp,
@@ -536,7 +511,6 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
   a.A = A;
   a.actions = actions;
   a.dx = dlogits;
-  a.hdr = reinterpret_cast<WsHeader*>(workspace);
   a.partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   const long blocks = cat_blocks(B, A);
@@ -566,6 +540,9 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
       hipLaunchKernelGGL(loss_cat_wave_kernel<int32_t>, dim3((unsigned)blocks), dim3(kBlock), 0,
                          stream, a);
   }
+  if ((st = last_launch_status())) return st;
+  hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(kBlock), 0, stream, a, blocks,
+                     kScalarSlots, 0);
   return last_launch_status();
 }
 
@@ -600,7 +577,6 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
   a.actions = actions;
   a.dx = dmu;
   a.dlog_std = dlog_std;
-  a.hdr = reinterpret_cast<WsHeader*>(workspace);
   a.partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   const long blocks = (B + kBlock - 1) / kBlock;
@@ -612,5 +588,8 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
   else
     hipLaunchKernelGGL(loss_gauss_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds,
                        stream, a);
+  if ((st = last_launch_status())) return st;
+  hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(kBlock), 0, stream, a, blocks,
+                     kGaussSlots, D);
   return last_launch_status();
 }

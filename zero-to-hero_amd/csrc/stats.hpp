@@ -6,8 +6,8 @@
 
 namespace ppo {
 
-// Called by the last block once every block has stored its (n, mean, M2)
-// partial.  Computes mean and the unbiased std in fp64, rounds both to fp32
+// One-block kernel body, run after every producer block has stored its
+// (n, mean, M2) partial (a previous launch on the same stream).  Computes mean and the unbiased std in fp64, rounds both to fp32
 // (torch returns fp32 0-d tensors for .mean() / .std()), and forms the fp32
 // denominator std + eps exactly as `advantages.std() + 1e-8` does.  For n <= 1
 // the normaliser must be the identity (the reference skips it when
@@ -37,6 +37,11 @@ __device__ inline void finalize_stats(const double* partials, long count, double
     }
   }
 }
+
+// Enqueue the one-block finaliser over `count` partials.  Defined in
+// adv_norm.hip.
+int launch_finalize_stats(const double* partials, long count, double eps, WsHeader* hdr,
+                          float* stats_out, hipStream_t stream);
 
 // Enqueue out[i] = (adv[i] - mean) / denom (fp32) where mean/denom are the
 // values finalize_stats() stored in `hdr` earlier on the same stream.

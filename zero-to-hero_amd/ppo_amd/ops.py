@@ -63,11 +63,11 @@ def _stream(device: torch.device) -> int:
 
 
 class _WorkspacePool:
-    """One zero-initialised scratch buffer per (device, stream).
+    """One scratch buffer per (device, stream), grown on demand.
 
-    libppo_amd needs caller-owned scratch whose first 256 bytes start at zero
-    and are left at zero by every call.  Calls on one stream are ordered, so
-    they can share a buffer; a different stream gets its own.
+    libppo_amd needs caller-owned scratch (partial sums, tile carries).  Calls
+    on one stream are ordered, so they can share a buffer; a different stream
+    gets its own.
     """
 
     def __init__(self) -> None:
@@ -78,12 +78,11 @@ class _WorkspacePool:
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
             size = max(nbytes, 0 if buf is None else 2 * buf.numel(), 4096)
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
             self._bufs[key] = buf
         return buf
 
     def drop(self, device: torch.device, stream: int) -> None:
-        # after a failed launch the counters may not be back at zero
         self._bufs.pop((device.index, stream), None)
 
 
