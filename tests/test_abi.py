@@ -58,7 +58,7 @@ def test_workspace_queries():
     # summary (16 B) + carry (8 B) per env per tile, tiles of >= 16 steps
     assert big < 2048 * 4096 * 24 / 16 + (1 << 20)
     assert lib.ppo_adv_norm_workspace_bytes(1 << 23) > 256
-    assert lib.ppo_loss_cat_workspace_bytes(1 << 20, 18) >= 256 + (1 << 20) // 256 * 64
+    assert lib.ppo_loss_cat_workspace_bytes(1 << 20, 18) > 256
     assert lib.ppo_loss_gauss_workspace_bytes(1 << 21, 6) > 256
 
 

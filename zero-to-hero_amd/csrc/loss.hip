@@ -17,12 +17,14 @@
 //     dvalue    = vc * 2 * (v - R) / B          (or the clipped-value form)
 // Gaussian variant: Normal(mu, exp(log_std)) summed over the action dims.
 //
-// Layout: one thread per row.  A workgroup stages its 256 rows of [B,A]
-// logits (a contiguous block of 256*A floats) through LDS with float4 loads,
-// row stride padded to an odd number of words so row-per-thread LDS reads are
-// bank-conflict-free, and writes dlogits back through the same tile.
-// Loss scalars are summed per block in fp64 and combined in a fixed order by
-// a one-block finaliser kernel (deterministic, no float atomics).
+// Layout: one thread per row.  A workgroup walks 256-row tiles of the
+// [B,A] logits (each tile a contiguous block of 256*A floats) on a grid
+// capped at a few workgroups per CU; per tile it prefetches the per-row
+// inputs into registers, stages the logits through LDS with float4 loads
+// (row stride padded to an odd number of words, so the row-per-thread LDS
+// reads are bank-conflict-free), and writes dlogits back through the same
+// tile.  Loss scalars are summed per workgroup in fp64 and combined in a fixed
+// order by a one-block finaliser kernel (deterministic, no float atomics).
 #include <float.h>
 
 #include <algorithm>
@@ -40,6 +42,10 @@ constexpr int kMaxGaussDim = 24;     // D limit of the Gaussian kernel
 constexpr int kScalarSlots = 8;      // per-block partial doubles for the loss scalars
 constexpr int kGaussSlots = kScalarSlots + kMaxGaussDim;
 constexpr long kWaveRowBlocks = 4096;  // grid cap of the wave-per-row kernel
+#ifndef PPO_LOSS_BLOCKS_PER_CU
+#define PPO_LOSS_BLOCKS_PER_CU 8
+#endif
+constexpr long kLossGridCap = 256L * PPO_LOSS_BLOCKS_PER_CU;  // 256 CUs on MI355X
 
 struct LossArgs {
   const float* x;        // logits [B,A] or mu [B,D]
@@ -79,61 +85,78 @@ __device__ __forceinline__ float clampf(float x, float lo, float hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
 
+// Per-row inputs other than the logits/mu, loaded ahead of the LDS barrier.
+struct RowIn {
+  float old_lp, adv, ret, v, vo;
+};
+
+__device__ __forceinline__ RowIn load_row(const LossArgs& a, long row) {
+  RowIn r;
+  r.old_lp = a.old_lp[row];
+  r.adv = a.adv[row];
+  r.ret = a.ret[row];
+  r.v = a.val[row];
+  r.vo = a.use_vclip ? a.old_val[row] : 0.0f;
+  return r;
+}
+
 struct RowOut {
   float g_lp;     // dloss/dlog_prob for this row
-  double pol, vl, kl, clipped;
+  float pol, vl, kl, clipped;
 };
 
 // Everything per row that does not depend on the policy family: ratio,
 // clipped surrogate, value loss, their gradients.  Writes dvalue.
-__device__ __forceinline__ RowOut ppo_row(const LossArgs& a, long row, float lp) {
+__device__ __forceinline__ RowOut ppo_row(const LossArgs& a, long row, const RowIn& in,
+                                          float lp) {
   RowOut o;
-  const float old_lp = a.old_lp[row];
-  const float A = a.adv[row];
-  const float ratio = expf(lp - old_lp);
+  const float A = in.adv;
+  const float ratio = expf(lp - in.old_lp);
   const float rc = clampf(ratio, a.lo, a.hi);
   const float u = ratio * A;
   const float w = rc * A;
-  const float pol = -nan_min(u, w);
   const float su = u < w ? 1.0f : (u == w ? 0.5f : 0.0f);
   const float sw = w < u ? 1.0f : (u == w ? 0.5f : 0.0f);
   const float inr = (ratio >= a.lo && ratio <= a.hi) ? 1.0f : 0.0f;
   // d(policy_i)/d(ratio) = -A*(su + sw*inr); times 1/B (mean) and ratio (exp').
   o.g_lp = -(A * (su + sw * inr)) * a.inv_b * ratio;
+  o.pol = -nan_min(u, w);
 
-  const float v = a.val[row];
-  const float R = a.ret[row];
-  const float d = v - R;
-  float vl, dvl;
+  const float d = in.v - in.ret;
+  float dvl;
   if (a.use_vclip) {
-    const float vo = a.old_val[row];
-    const float dv = v - vo;
-    const float vcl = vo + clampf(dv, -a.vclip, a.vclip);
-    const float d2 = vcl - R;
+    const float dv = in.v - in.vo;
+    const float vcl = in.vo + clampf(dv, -a.vclip, a.vclip);
+    const float d2 = vcl - in.ret;
     const float l1 = d * d;
     const float l2 = d2 * d2;
-    vl = nan_max(l1, l2);
+    o.vl = nan_max(l1, l2);
     const float s1 = l1 > l2 ? 1.0f : (l1 == l2 ? 0.5f : 0.0f);
     const float s2 = l2 > l1 ? 1.0f : (l1 == l2 ? 0.5f : 0.0f);
     const float in2 = (dv >= -a.vclip && dv <= a.vclip) ? 1.0f : 0.0f;
     dvl = s1 * (2.0f * d) + s2 * (2.0f * d2) * in2;
   } else {
-    vl = d * d;
+    o.vl = d * d;
     dvl = 2.0f * d;
   }
   a.dval[row] = a.vc * (dvl * a.inv_b);
-  o.pol = pol;
-  o.vl = vl;
-  o.kl = (double)old_lp - (double)lp;
-  o.clipped = fabsf(ratio - 1.0f) > a.clip ? 1.0 : 0.0;
+  o.kl = in.old_lp - lp;
+  o.clipped = fabsf(ratio - 1.0f) > a.clip ? 1.0f : 0.0f;
   return o;
+}
+
+// Row index of flat element e in a tile of `width`-float rows, without an
+// integer divide: e <= 256*64, so (e + 0.5) * (1/width) is never within
+// rounding distance of an integer boundary.
+__device__ __forceinline__ int row_of(int e, float inv_width) {
+  return (int)(((float)e + 0.5f) * inv_width);
 }
 
 // Copy `count` floats from global (contiguous) into an LDS tile of row
 // stride `ws` (count = rows * width).
 template <bool kVec>
-__device__ __forceinline__ void stage_in(const float* src, int count, int width, int ws,
-                                         float* lds) {
+__device__ __forceinline__ void stage_in(const float* src, int count, int width, float inv_width,
+                                         int ws, float* lds) {
   int start = 0;
   if constexpr (kVec) {
     const int n4 = count >> 2;
@@ -141,7 +164,7 @@ __device__ __forceinline__ void stage_in(const float* src, int count, int width,
     for (int i = threadIdx.x; i < n4; i += blockDim.x) {
       const float4 x = s4[i];
       const int e = i << 2;
-      int r = e / width;
+      int r = row_of(e, inv_width);
       int c = e - r * width;
       const float xs[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
@@ -153,21 +176,21 @@ __device__ __forceinline__ void stage_in(const float* src, int count, int width,
     start = n4 << 2;
   }
   for (int e = start + threadIdx.x; e < count; e += blockDim.x) {
-    const int r = e / width;
+    const int r = row_of(e, inv_width);
     lds[r * ws + (e - r * width)] = src[e];
   }
 }
 
 template <bool kVec>
-__device__ __forceinline__ void stage_out(float* dst, int count, int width, int ws,
-                                          const float* lds) {
+__device__ __forceinline__ void stage_out(float* dst, int count, int width, float inv_width,
+                                          int ws, const float* lds) {
   int start = 0;
   if constexpr (kVec) {
     const int n4 = count >> 2;
     float4* d4 = reinterpret_cast<float4*>(dst);
     for (int i = threadIdx.x; i < n4; i += blockDim.x) {
       const int e = i << 2;
-      int r = e / width;
+      int r = row_of(e, inv_width);
       int c = e - r * width;
       float xs[4];
 #pragma unroll
@@ -180,7 +203,7 @@ __device__ __forceinline__ void stage_out(float* dst, int count, int width, int 
     start = n4 << 2;
   }
   for (int e = start + threadIdx.x; e < count; e += blockDim.x) {
-    const int r = e / width;
+    const int r = row_of(e, inv_width);
     dst[e] = lds[r * ws + (e - r * width)];
   }
 }
@@ -193,6 +216,14 @@ __device__ inline void store_scalar_partials(const LossArgs& a, double (&acc)[5]
 #pragma unroll
     for (int k = 0; k < 5; ++k) a.partial[block * stride + k] = acc[k];
   }
+}
+
+__device__ __forceinline__ void accumulate(double (&acc)[5], const RowOut& o, float ent) {
+  acc[0] += (double)o.pol;
+  acc[1] += (double)o.vl;
+  acc[2] += (double)ent;
+  acc[3] += (double)o.kl;
+  acc[4] += (double)o.clipped;
 }
 
 // One-block finaliser, launched after the loss kernel on the same stream:
@@ -259,51 +290,68 @@ __device__ __forceinline__ int row_action(const LossArgs& a, long row) {
 }
 
 // ---------------------------------------------------------------------------
-// Categorical, A <= kMaxCatRowWidth: one thread per row, logits staged through LDS.
+// Categorical, A <= kMaxCatRowWidth: one thread per row, logits staged
+// through LDS.  Softmax statistics in two passes over the row:
+//   m = max z;  s = sum e_j, e_j = exp(z_j - m);  S = sum e_j (z_j - m)
+//   log p_j = (z_j - m) - log s;   H = log s - S / s
+// and a third pass recomputes e_j for the gradient (2 exp per logit).  The
+// per-logit exponentials use the hardware exp2 (__expf: one multiply by
+// log2(e) and v_exp_f32, relative error ~1e-6 for |z_j - m| <= 20); the
+// accurate expf sequence costs ~10 VALU ops and made this kernel VALU-bound.
+// The ratio exp(lp - old_lp) keeps the accurate expf.
 // ---------------------------------------------------------------------------
 template <typename ActT, bool kVec>
-__global__ void __launch_bounds__(kBlock) loss_cat_kernel(LossArgs a) {
+__global__ void __launch_bounds__(kBlock) loss_cat_kernel(LossArgs a, long ntiles) {
   extern __shared__ float s_tile[];
   const int A = a.A;
   const int AS = A | 1;
-  const long row0 = (long)blockIdx.x * kBlock;
-  const int nrows = (int)std::min<long>(kBlock, a.B - row0);
-  stage_in<kVec>(a.x + row0 * A, nrows * A, A, AS, s_tile);
-  __syncthreads();
-
-  double acc[5] = {0, 0, 0, 0, 0};
+  const float invA = 1.0f / (float)A;
+  const float ge = a.ec * a.inv_b;
   const int tid = threadIdx.x;
-  if (tid < nrows) {
+  double acc[5] = {0, 0, 0, 0, 0};
+
+  for (long tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const long row0 = tile * kBlock;
+    const int nrows = (int)std::min<long>(kBlock, a.B - row0);
     const long row = row0 + tid;
-    float* z = s_tile + tid * AS;
-    float m = -INFINITY;
-    for (int j = 0; j < A; ++j) m = fmaxf(m, z[j]);
-    float se = 0.0f;
-    for (int j = 0; j < A; ++j) se += expf(z[j] - m);
-    const float lse = m + logf(se);
-    float H = 0.0f;
-    for (int j = 0; j < A; ++j) {
-      const float lpj = z[j] - lse;
-      H -= fmaxf(lpj, -FLT_MAX) * expf(lpj);
+    RowIn in = {0, 0, 0, 0, 0};
+    int ai = -1;
+    if (tid < nrows) {
+      in = load_row(a, row);
+      ai = row_action<ActT>(a, row);
     }
-    const int ai = row_action<ActT>(a, row);
-    const float lp = ai >= 0 ? z[ai] - lse : __builtin_nanf("");
-    const RowOut o = ppo_row(a, row, lp);
-    const float ge = a.ec * a.inv_b;
-    for (int j = 0; j < A; ++j) {
-      const float lpj = z[j] - lse;
-      const float pj = expf(lpj);
-      const float onehot = j == ai ? 1.0f : 0.0f;
-      z[j] = o.g_lp * (onehot - pj) + ge * (pj * (fmaxf(lpj, -FLT_MAX) + H));
+    stage_in<kVec>(a.x + row0 * A, nrows * A, A, invA, AS, s_tile);
+    __syncthreads();
+
+    if (tid < nrows) {
+      float* z = s_tile + tid * AS;
+      float m = -INFINITY;
+      for (int j = 0; j < A; ++j) m = fmaxf(m, z[j]);
+      float s = 0.0f, S = 0.0f;
+      for (int j = 0; j < A; ++j) {
+        const float t = z[j] - m;
+        const float e = __expf(t);
+        s += e;
+        S += e > 0.0f ? e * t : 0.0f;
+      }
+      const float log_s = logf(s);
+      const float inv_s = 1.0f / s;
+      const float H = log_s - S * inv_s;
+      const float lp = ai >= 0 ? (z[ai] - m) - log_s : __builtin_nanf("");
+      const RowOut o = ppo_row(a, row, in, lp);
+      for (int j = 0; j < A; ++j) {
+        const float t = z[j] - m;
+        const float p = __expf(t) * inv_s;
+        const float logp = fmaxf(t - log_s, -FLT_MAX);
+        const float onehot = j == ai ? 1.0f : 0.0f;
+        z[j] = o.g_lp * (onehot - p) + ge * (p * (logp + H));
+      }
+      accumulate(acc, o, H);
     }
-    acc[0] = o.pol;
-    acc[1] = o.vl;
-    acc[2] = H;
-    acc[3] = o.kl;
-    acc[4] = o.clipped;
+    __syncthreads();
+    stage_out<kVec>(a.dx + row0 * A, nrows * A, A, invA, AS, s_tile);
+    __syncthreads();
   }
-  __syncthreads();
-  stage_out<kVec>(a.dx + row0 * A, nrows * A, A, AS, s_tile);
   store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
 }
 
@@ -327,126 +375,122 @@ __global__ void __launch_bounds__(kBlock) loss_cat_wave_kernel(LossArgs a) {
   const long wave = ((long)blockIdx.x * blockDim.x + threadIdx.x) / kWave;
   const long nwaves = (long)gridDim.x * blockDim.x / kWave;
   const int A = a.A;
+  const float ge = a.ec * a.inv_b;
   double acc[5] = {0, 0, 0, 0, 0};
   for (long row = wave; row < a.B; row += nwaves) {
     const float* z = a.x + row * A;
     float m = -INFINITY;
     for (int j = lane; j < A; j += kWave) m = fmaxf(m, z[j]);
     m = wave_max_f(m);
-    float se = 0.0f;
-    for (int j = lane; j < A; j += kWave) se += expf(z[j] - m);
-    se = wave_sum_f(se);
-    const float lse = m + logf(se);
-    float H = 0.0f;
+    float s = 0.0f, S = 0.0f;
     for (int j = lane; j < A; j += kWave) {
-      const float lpj = z[j] - lse;
-      H -= fmaxf(lpj, -FLT_MAX) * expf(lpj);
+      const float t = z[j] - m;
+      const float e = __expf(t);
+      s += e;
+      S += e > 0.0f ? e * t : 0.0f;
     }
-    H = wave_sum_f(H);
+    s = wave_sum_f(s);
+    S = wave_sum_f(S);
+    const float log_s = logf(s);
+    const float inv_s = 1.0f / s;
+    const float H = log_s - S * inv_s;
     const int ai = row_action<ActT>(a, row);
-    const float lp = ai >= 0 ? z[ai] - lse : __builtin_nanf("");
+    const float lp = ai >= 0 ? (z[ai] - m) - log_s : __builtin_nanf("");
     // every lane evaluates the row terms; only lane 0 stores dvalue and sums
-    RowOut o = {0.0f, 0.0, 0.0, 0.0, 0.0};
-    if (lane == 0) {
-      o = ppo_row(a, row, lp);
-    }
+    RowOut o = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (lane == 0) o = ppo_row(a, row, load_row(a, row), lp);
     o.g_lp = __shfl(o.g_lp, 0, kWave);
-    const float ge = a.ec * a.inv_b;
     float* dz = a.dx + row * A;
     for (int j = lane; j < A; j += kWave) {
-      const float lpj = z[j] - lse;
-      const float pj = expf(lpj);
+      const float t = z[j] - m;
+      const float p = __expf(t) * inv_s;
+      const float logp = fmaxf(t - log_s, -FLT_MAX);
       const float onehot = j == ai ? 1.0f : 0.0f;
-      dz[j] = o.g_lp * (onehot - pj) + ge * (pj * (fmaxf(lpj, -FLT_MAX) + H));
+      dz[j] = o.g_lp * (onehot - p) + ge * (p * (logp + H));
     }
-    if (lane == 0) {
-      acc[0] += o.pol;
-      acc[1] += o.vl;
-      acc[2] += H;
-      acc[3] += o.kl;
-      acc[4] += o.clipped;
-    }
+    if (lane == 0) accumulate(acc, o, H);
   }
   store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
 }
 
 // ---------------------------------------------------------------------------
-// Gaussian, D <= kMaxGaussDim: one thread per row; mu and actions staged through LDS.
-// torch Normal(loc, scale): log_prob = -(x-loc)^2/(2*scale^2) - log(scale)
-// - log(sqrt(2*pi)); entropy = 0.5 + 0.5*log(2*pi) + log(scale).
+// Gaussian, D <= kMaxGaussDim: one thread per row; mu and actions staged
+// through LDS.  torch Normal(loc, scale): log_prob = -(x-loc)^2/(2*scale^2)
+// - log(scale) - log(sqrt(2*pi)); entropy = 0.5 + 0.5*log(2*pi) + log(scale)
+// (constant over rows; the finaliser forms it).  The divisions by 2*var and
+// var are multiplications by per-dim reciprocals computed once per block
+// (<= 1 ulp from torch's quotient).
 // ---------------------------------------------------------------------------
 template <bool kVec>
-__global__ void __launch_bounds__(kBlock) loss_gauss_kernel(LossArgs a) {
+__global__ void __launch_bounds__(kBlock) loss_gauss_kernel(LossArgs a, long ntiles) {
   extern __shared__ float s_lds[];
-  __shared__ float s_2var[kMaxGaussDim], s_var[kMaxGaussDim], s_logscale[kMaxGaussDim];
+  __shared__ float s_inv2var[kMaxGaussDim], s_invvar[kMaxGaussDim], s_logscale[kMaxGaussDim];
+  __shared__ double s_col[kBlock];
   const int D = a.A;
   const int DS = D | 1;
+  const float invD = 1.0f / (float)D;
   float* s_mu = s_lds;
   float* s_act = s_lds + kBlock * DS;
-  const long row0 = (long)blockIdx.x * kBlock;
-  const int nrows = (int)std::min<long>(kBlock, a.B - row0);
   const float kLogSqrt2Pi = 0.91893853320467274178f;   // log(sqrt(2*pi))
-  if (threadIdx.x < D) {
-    const float scale = expf(a.log_std[threadIdx.x]);
-    const float var = scale * scale;
-    s_2var[threadIdx.x] = 2.0f * var;
-    s_var[threadIdx.x] = var;
-    s_logscale[threadIdx.x] = logf(scale);
-  }
-  stage_in<kVec>(a.x + row0 * D, nrows * D, D, DS, s_mu);
-  stage_in<kVec>(reinterpret_cast<const float*>(a.actions) + row0 * D, nrows * D, D, DS, s_act);
-  __syncthreads();
-
-  double acc[5] = {0, 0, 0, 0, 0};
   const int tid = threadIdx.x;
-  if (tid < nrows) {
-    const long row = row0 + tid;
-    float* mu = s_mu + tid * DS;
-    float* act = s_act + tid * DS;
-    float lp = 0.0f;
-    for (int d = 0; d < D; ++d) {
-      const float diff = act[d] - mu[d];
-      lp += ((-(diff * diff)) / s_2var[d] - s_logscale[d]) - kLogSqrt2Pi;
-    }
-    const RowOut o = ppo_row(a, row, lp);
-    for (int d = 0; d < D; ++d) {
-      const float diff = act[d] - mu[d];
-      const float z2 = (diff * diff) / s_var[d];
-      mu[d] = o.g_lp * (diff / s_var[d]);   // dmu
-      act[d] = o.g_lp * (z2 - 1.0f);           // this row's dlog_std term
-    }
-    acc[0] = o.pol;
-    acc[1] = o.vl;
-    acc[2] = 0.0;
-    acc[3] = o.kl;
-    acc[4] = o.clipped;
-  } else if (tid < kBlock) {
-    float* act = s_act + tid * DS;
-    for (int d = 0; d < D; ++d) act[d] = 0.0f;
+  if (tid < D) {
+    const float scale = expf(a.log_std[tid]);
+    const float var = scale * scale;
+    s_inv2var[tid] = 1.0f / (2.0f * var);
+    s_invvar[tid] = 1.0f / var;
+    s_logscale[tid] = logf(scale);
   }
-  __syncthreads();
-  stage_out<kVec>(a.dx + row0 * D, nrows * D, D, DS, s_mu);
+  const int groups = kBlock / D;
+  double col_acc = 0.0;  // thread t < D: this block's dlog_std[t] over its tiles
+  double acc[5] = {0, 0, 0, 0, 0};
 
-  // Column sums of the dlog_std terms over this block's rows: `groups`
-  // threads per column, then one thread per column, fixed order, fp64.
-  {
-    __shared__ double s_col[kBlock];
-    const int groups = kBlock / D;
+  for (long tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const long row0 = tile * kBlock;
+    const int nrows = (int)std::min<long>(kBlock, a.B - row0);
+    const long row = row0 + tid;
+    RowIn in = {0, 0, 0, 0, 0};
+    if (tid < nrows) in = load_row(a, row);
+    stage_in<kVec>(a.x + row0 * D, nrows * D, D, invD, DS, s_mu);
+    stage_in<kVec>(reinterpret_cast<const float*>(a.actions) + row0 * D, nrows * D, D, invD, DS,
+                   s_act);
+    __syncthreads();
+    if (tid < nrows) {
+      float* mu = s_mu + tid * DS;
+      float* act = s_act + tid * DS;
+      float lp = 0.0f;
+      for (int d = 0; d < D; ++d) {
+        const float diff = act[d] - mu[d];
+        lp += ((-(diff * diff)) * s_inv2var[d] - s_logscale[d]) - kLogSqrt2Pi;
+      }
+      const RowOut o = ppo_row(a, row, in, lp);
+      for (int d = 0; d < D; ++d) {
+        const float diff = act[d] - mu[d];
+        const float z2 = (diff * diff) * s_invvar[d];
+        mu[d] = o.g_lp * (diff * s_invvar[d]);  // dmu
+        act[d] = o.g_lp * (z2 - 1.0f);       // this row's dlog_std term
+      }
+      accumulate(acc, o, 0.0f);
+    } else {
+      float* act = s_act + tid * DS;
+      for (int d = 0; d < D; ++d) act[d] = 0.0f;
+    }
+    __syncthreads();
+    stage_out<kVec>(a.dx + row0 * D, nrows * D, D, invD, DS, s_mu);
+    // column sums of the dlog_std terms: `groups` threads per column, then
+    // one thread per column, fixed order, fp64
     double sum = 0.0;
-    const int t = threadIdx.x;
-    if (t < groups * D) {
-      const int d = t % D;
-      const int g = t / D;
+    if (tid < groups * D) {
+      const int d = tid % D;
+      const int g = tid / D;
       for (int r = g; r < kBlock; r += groups) sum += (double)s_act[r * DS + d];
     }
-    s_col[t] = sum;
+    s_col[tid] = sum;
     __syncthreads();
-    if (t < D) {
-      double c = 0.0;
-      for (int g = 0; g < groups; ++g) c += s_col[g * D + t];
-      a.partial[(long)blockIdx.x * kGaussSlots + kScalarSlots + t] = c;
-    }
+    if (tid < D)
+      for (int g = 0; g < groups; ++g) col_acc += s_col[g * D + tid];
+    __syncthreads();
   }
+  if (tid < D) a.partial[(long)blockIdx.x * kGaussSlots + kScalarSlots + tid] = col_acc;
   store_scalar_partials(a, acc, blockIdx.x, kGaussSlots);
 }
 
@@ -477,10 +521,14 @@ int fill_common(LossArgs& a, long B, const ppo_loss_params* p, const float* old_
   return PPO_OK;
 }
 
+long row_tiles(long B) { return (B + kBlock - 1) / kBlock; }
+
 long cat_blocks(long B, int A) {
-  if (A <= kMaxCatRowWidth) return (B + kBlock - 1) / kBlock;
+  if (A <= kMaxCatRowWidth) return std::min(row_tiles(B), kLossGridCap);
   return std::max(1L, std::min((B + 3) / 4, kWaveRowBlocks));
 }
+
+long gauss_blocks(long B) { return std::min(row_tiles(B), kLossGridCap); }
 
 }  // namespace
 }  // namespace ppo
@@ -501,7 +549,7 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
   using namespace ppo;
   if (B <= 0 || A <= 0) return PPO_ERR_INVALID_ARG;
   if (!logits || !actions || !dlogits) return PPO_ERR_INVALID_ARG;
-  if (B > 0x7fffffffL * (long)kBlock / 2 || (long)B * A > (1L << 50)) return PPO_ERR_TOO_LARGE;
+  if ((long)B * A > (1L << 50)) return PPO_ERR_TOO_LARGE;
   if (!workspace || workspace_bytes < ppo_loss_cat_workspace_bytes(B, A)) return PPO_ERR_WORKSPACE;
   LossArgs a = {};
   int st = fill_common(a, B, params, old_log_probs, advantages, returns, values, old_values,
@@ -514,23 +562,21 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
   a.partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   const long blocks = cat_blocks(B, A);
+  const long tiles = row_tiles(B);
   if (A <= kMaxCatRowWidth) {
     const bool vec = aligned(logits, 16) && aligned(dlogits, 16);
     const size_t lds = (size_t)kBlock * (A | 1) * sizeof(float);
+    const dim3 grid((unsigned)blocks), block(kBlock);
     if (actions_are_int64) {
       if (vec)
-        hipLaunchKernelGGL((loss_cat_kernel<int64_t, true>), dim3((unsigned)blocks), dim3(kBlock),
-                           lds, stream, a);
+        hipLaunchKernelGGL((loss_cat_kernel<int64_t, true>), grid, block, lds, stream, a, tiles);
       else
-        hipLaunchKernelGGL((loss_cat_kernel<int64_t, false>), dim3((unsigned)blocks),
-                           dim3(kBlock), lds, stream, a);
+        hipLaunchKernelGGL((loss_cat_kernel<int64_t, false>), grid, block, lds, stream, a, tiles);
     } else {
       if (vec)
-        hipLaunchKernelGGL((loss_cat_kernel<int32_t, true>), dim3((unsigned)blocks), dim3(kBlock),
-                           lds, stream, a);
+        hipLaunchKernelGGL((loss_cat_kernel<int32_t, true>), grid, block, lds, stream, a, tiles);
       else
-        hipLaunchKernelGGL((loss_cat_kernel<int32_t, false>), dim3((unsigned)blocks),
-                           dim3(kBlock), lds, stream, a);
+        hipLaunchKernelGGL((loss_cat_kernel<int32_t, false>), grid, block, lds, stream, a, tiles);
     }
   } else {
     if (actions_are_int64)
@@ -549,8 +595,7 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
 extern "C" size_t ppo_loss_gauss_workspace_bytes(int64_t B, int32_t D) {
   using namespace ppo;
   if (B <= 0 || D <= 0) return kHeaderBytes;
-  const long blocks = (B + kBlock - 1) / kBlock;
-  return kHeaderBytes + align_up((size_t)blocks * kGaussSlots * sizeof(double), 256);
+  return kHeaderBytes + align_up((size_t)gauss_blocks(B) * kGaussSlots * sizeof(double), 256);
 }
 
 extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t B, int32_t D,
@@ -564,7 +609,7 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
   if (B <= 0 || D <= 0) return PPO_ERR_INVALID_ARG;
   if (D > kMaxGaussDim) return PPO_ERR_TOO_LARGE;
   if (!mu || !log_std || !actions || !dmu || !dlog_std) return PPO_ERR_INVALID_ARG;
-  if (B > 0x7fffffffL * (long)kBlock / 2) return PPO_ERR_TOO_LARGE;
+  if ((long)B * D > (1L << 50)) return PPO_ERR_TOO_LARGE;
   if (!workspace || workspace_bytes < ppo_loss_gauss_workspace_bytes(B, D))
     return PPO_ERR_WORKSPACE;
   LossArgs a = {};
@@ -579,15 +624,16 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
   a.dlog_std = dlog_std;
   a.partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
-  const long blocks = (B + kBlock - 1) / kBlock;
+  const long blocks = gauss_blocks(B);
+  const long tiles = row_tiles(B);
   const size_t lds = (size_t)2 * kBlock * (D | 1) * sizeof(float);
   const bool vec = aligned(mu, 16) && aligned(actions, 16) && aligned(dmu, 16);
   if (vec)
     hipLaunchKernelGGL(loss_gauss_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), lds, stream,
-                       a);
+                       a, tiles);
   else
     hipLaunchKernelGGL(loss_gauss_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds,
-                       stream, a);
+                       stream, a, tiles);
   if ((st = last_launch_status())) return st;
   hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(kBlock), 0, stream, a, blocks,
                      kGaussSlots, D);
