@@ -28,6 +28,12 @@ def assert_grad_close(got, expect, rtol=1e-4, floor=1e-5):
     torch.testing.assert_close(got, expect, rtol=rtol, atol=atol)
 
 
+def assert_fixture_scalars(scalars, z):
+    o = {k: torch.tensor(float(z["scalars"][i])) for i, k in enumerate(NAMES)}
+    o["dvalues"] = torch.from_numpy(z["dvalues"])
+    assert_scalars_close(scalars, o)
+
+
 def assert_scalars_close(scalars, o, rtol=1e-5):
     """The reference's scalars (loss, policy, value, entropy) to rel 1e-5.
     approx_kl = mean(old_lp - lp) is a build-only diagnostic and a
@@ -85,7 +91,7 @@ def test_golden_fixture_cat(dev):
         t("values"), t("old_values"), float(z["clip_ratio"]), float(z["vf_clip"]),
         float(z["value_coef"]), float(z["entropy_coef"]),
     )
-    np.testing.assert_allclose(scalars.cpu().numpy(), z["scalars"], rtol=1e-5, atol=1e-7)
+    assert_fixture_scalars(scalars, z)
     assert_grad_close(dlogits, torch.from_numpy(z["dlogits"]))
     assert_grad_close(dvalues, torch.from_numpy(z["dvalues"]))
 
@@ -210,7 +216,7 @@ def test_golden_fixture_gauss(dev):
         t("returns"), t("values"), t("old_values"), float(z["clip_ratio"]),
         float(z["vf_clip"]), float(z["value_coef"]), float(z["entropy_coef"]),
     )
-    np.testing.assert_allclose(scalars.cpu().numpy(), z["scalars"], rtol=1e-5, atol=1e-7)
+    assert_fixture_scalars(scalars, z)
     assert_grad_close(dmu, torch.from_numpy(z["dmu"]))
     assert_grad_close(dls, torch.from_numpy(z["dlog_std"]))
     assert_grad_close(dv, torch.from_numpy(z["dvalues"]))

@@ -4,6 +4,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
+#include <tuple>
+
 #include "ppo_amd.h"
 
 namespace ppo {
@@ -138,5 +142,32 @@ __host__ __device__ inline unsigned int pow2_ceil(unsigned int x) {
 }
 
 inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Workgroups of `kernel` that fit on the current device at once (all CUs),
+// for persistent-style grids that loop over tiles.  Falls back to `fallback`
+// if the runtime cannot answer.
+// The answer is cached per (device, kernel, block, lds).
+inline long resident_blocks(const void* kernel, int block, size_t lds, long fallback) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, const void*, int, size_t>, long> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fallback;
+  const auto key = std::make_tuple(dev, kernel, block, lds);
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+  }
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return fallback;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess ||
+      per_cu <= 0)
+    return fallback;
+  const long n = (long)cus * per_cu;
+  std::lock_guard<std::mutex> lock(mu);
+  cache[key] = n;
+  return n;
+}
 
 }  // namespace ppo

@@ -85,6 +85,15 @@ __device__ __forceinline__ float clampf(float x, float lo, float hi) {
   return x < lo ? lo : (x > hi ? hi : x);
 }
 
+// Streamed arrays are touched once: nontemporal loads/stores keep them from
+// displacing reusable lines (measured on MI355X: a float4 copy goes from 5.5
+// to 6.3 TB/s with nontemporal accesses and 4 loads in flight per thread).
+typedef float f4 __attribute__((ext_vector_type(4)));
+template <typename T>
+__device__ __forceinline__ T ldnt(const T* p) { return __builtin_nontemporal_load(p); }
+template <typename T>
+__device__ __forceinline__ void stnt(T v, T* p) { __builtin_nontemporal_store(v, p); }
+
 // Per-row inputs other than the logits/mu, loaded ahead of the LDS barrier.
 struct RowIn {
   float old_lp, adv, ret, v, vo;
@@ -92,11 +101,11 @@ struct RowIn {
 
 __device__ __forceinline__ RowIn load_row(const LossArgs& a, long row) {
   RowIn r;
-  r.old_lp = a.old_lp[row];
-  r.adv = a.adv[row];
-  r.ret = a.ret[row];
-  r.v = a.val[row];
-  r.vo = a.use_vclip ? a.old_val[row] : 0.0f;
+  r.old_lp = ldnt(a.old_lp + row);
+  r.adv = ldnt(a.adv + row);
+  r.ret = ldnt(a.ret + row);
+  r.v = ldnt(a.val + row);
+  r.vo = a.use_vclip ? ldnt(a.old_val + row) : 0.0f;
   return r;
 }
 
@@ -139,7 +148,7 @@ __device__ __forceinline__ RowOut ppo_row(const LossArgs& a, long row, const Row
     o.vl = d * d;
     dvl = 2.0f * d;
   }
-  a.dval[row] = a.vc * (dvl * a.inv_b);
+  stnt(a.vc * (dvl * a.inv_b), a.dval + row);
   o.kl = in.old_lp - lp;
   o.clipped = fabsf(ratio - 1.0f) > a.clip ? 1.0f : 0.0f;
   return o;
@@ -356,6 +365,142 @@ __global__ void __launch_bounds__(kBlock) loss_cat_kernel(LossArgs a, long ntile
 }
 
 // ---------------------------------------------------------------------------
+// Categorical, A <= 4*PF: the same per-row math as loss_cat_kernel,
+// software-pipelined for 16-byte-aligned inputs.  Each
+// thread holds up to PF float4 of the next tile's logits plus its row
+// inputs in registers: while tile i is computed out of LDS, the loads of
+// tile i+1 are already in flight, so a workgroup never waits on HBM between
+// tiles.  All streamed accesses are nontemporal.
+// ---------------------------------------------------------------------------
+template <typename ActT, int PF>
+struct CatPrefetch {
+  f4 x[PF];
+  float tail;   // element n4*4 + tid of a tile whose size is not a multiple of 4
+  RowIn in;
+  int ai;
+  int nrows;
+};
+
+template <typename ActT, int PF>
+__device__ __forceinline__ void cat_prefetch(const LossArgs& a, long tile, CatPrefetch<ActT, PF>& p) {
+  const int tid = threadIdx.x;
+  const long row0 = tile * kBlock;
+  p.nrows = (int)std::min<long>(kBlock, a.B - row0);
+  const int count = p.nrows * a.A;
+  const int n4 = count >> 2;
+  const f4* src = reinterpret_cast<const f4*>(a.x + row0 * a.A);
+#pragma unroll
+  for (int k = 0; k < PF; ++k) {
+    const int i = k * kBlock + tid;
+    if (i < n4) p.x[k] = ldnt(src + i);
+  }
+  if (tid < count - (n4 << 2)) p.tail = ldnt(a.x + row0 * a.A + (n4 << 2) + tid);
+  p.ai = -1;
+  if (tid < p.nrows) {
+    const long row = row0 + tid;
+    p.in = load_row(a, row);
+    p.ai = row_action<ActT>(a, row);
+  }
+}
+
+template <typename ActT, int PF>
+__global__ void __launch_bounds__(kBlock) loss_cat_pipe_kernel(LossArgs a, long ntiles) {
+  extern __shared__ float s_tile[];
+  const int A = a.A;
+  const int AS = A | 1;
+  const float invA = 1.0f / (float)A;
+  const float ge = a.ec * a.inv_b;
+  const int tid = threadIdx.x;
+  double acc[5] = {0, 0, 0, 0, 0};
+  CatPrefetch<ActT, PF> pf;
+  long tile = blockIdx.x;
+  if (tile < ntiles) cat_prefetch<ActT, PF>(a, tile, pf);
+
+  for (; tile < ntiles; tile += gridDim.x) {
+    // registers -> LDS for the current tile
+    const int nrows = pf.nrows;
+    const int count = nrows * A;
+    const int n4 = count >> 2;
+#pragma unroll
+    for (int k = 0; k < PF; ++k) {
+      const int i = k * kBlock + tid;
+      if (i < n4) {
+        const int e = i << 2;
+        int r = row_of(e, invA);
+        int c = e - r * A;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          s_tile[r * AS + c] = pf.x[k][q];
+          if (++c == A) { c = 0; ++r; }
+        }
+      }
+    }
+    if (tid < count - (n4 << 2)) {
+      const int e = (n4 << 2) + tid;
+      const int r = row_of(e, invA);
+      s_tile[r * AS + (e - r * A)] = pf.tail;
+    }
+    const RowIn in = pf.in;
+    const int ai = pf.ai;
+    const long row0 = tile * kBlock;
+    __syncthreads();
+
+    // next tile's loads go out before this tile's math
+    const long next = tile + gridDim.x;
+    if (next < ntiles) cat_prefetch<ActT, PF>(a, next, pf);
+
+    if (tid < nrows) {
+      const long row = row0 + tid;
+      float* z = s_tile + tid * AS;
+      float m = -INFINITY;
+      for (int j = 0; j < A; ++j) m = fmaxf(m, z[j]);
+      float s = 0.0f, S = 0.0f;
+      for (int j = 0; j < A; ++j) {
+        const float t = z[j] - m;
+        const float e = __expf(t);
+        s += e;
+        S += e > 0.0f ? e * t : 0.0f;
+      }
+      const float log_s = logf(s);
+      const float inv_s = 1.0f / s;
+      const float H = log_s - S * inv_s;
+      const float lp = ai >= 0 ? (z[ai] - m) - log_s : __builtin_nanf("");
+      const RowOut o = ppo_row(a, row, in, lp);
+      for (int j = 0; j < A; ++j) {
+        const float t = z[j] - m;
+        const float p = __expf(t) * inv_s;
+        const float logp = fmaxf(t - log_s, -FLT_MAX);
+        const float onehot = j == ai ? 1.0f : 0.0f;
+        z[j] = o.g_lp * (onehot - p) + ge * (p * (logp + H));
+      }
+      accumulate(acc, o, H);
+    }
+    __syncthreads();
+    // LDS -> dlogits, nontemporal float4 stores
+    f4* dst = reinterpret_cast<f4*>(a.dx + row0 * A);
+    for (int i = tid; i < n4; i += kBlock) {
+      const int e = i << 2;
+      int r = row_of(e, invA);
+      int c = e - r * A;
+      f4 v;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v[q] = s_tile[r * AS + c];
+        if (++c == A) { c = 0; ++r; }
+      }
+      stnt(v, dst + i);
+    }
+    if (tid < count - (n4 << 2)) {
+      const int e = (n4 << 2) + tid;
+      const int r = row_of(e, invA);
+      a.dx[row0 * A + e] = s_tile[r * AS + (e - r * A)];
+    }
+    __syncthreads();
+  }
+  store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
+}
+
+// ---------------------------------------------------------------------------
 // Categorical, any A: one wave per row (lanes stride the actions).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_max_f(float x) {
@@ -530,6 +675,8 @@ long cat_blocks(long B, int A) {
 
 long gauss_blocks(long B) { return std::min(row_tiles(B), kLossGridCap); }
 
+dim3 grid_of(long blocks) { return dim3((unsigned)blocks); }
+
 }  // namespace
 }  // namespace ppo
 
@@ -561,23 +708,29 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
   a.dx = dlogits;
   a.partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
-  const long blocks = cat_blocks(B, A);
+  long blocks = cat_blocks(B, A);
   const long tiles = row_tiles(B);
   if (A <= kMaxCatRowWidth) {
     const bool vec = aligned(logits, 16) && aligned(dlogits, 16);
     const size_t lds = (size_t)kBlock * (A | 1) * sizeof(float);
-    const dim3 grid((unsigned)blocks), block(kBlock);
-    if (actions_are_int64) {
-      if (vec)
-        hipLaunchKernelGGL((loss_cat_kernel<int64_t, true>), grid, block, lds, stream, a, tiles);
-      else
-        hipLaunchKernelGGL((loss_cat_kernel<int64_t, false>), grid, block, lds, stream, a, tiles);
-    } else {
-      if (vec)
-        hipLaunchKernelGGL((loss_cat_kernel<int32_t, true>), grid, block, lds, stream, a, tiles);
-      else
-        hipLaunchKernelGGL((loss_cat_kernel<int32_t, false>), grid, block, lds, stream, a, tiles);
-    }
+    const void* kern;
+    if (vec && (A + 3) / 4 <= 2)
+      kern = actions_are_int64 ? (const void*)loss_cat_pipe_kernel<int64_t, 2>
+                               : (const void*)loss_cat_pipe_kernel<int32_t, 2>;
+    else if (vec && (A + 3) / 4 <= 5)
+      kern = actions_are_int64 ? (const void*)loss_cat_pipe_kernel<int64_t, 5>
+                               : (const void*)loss_cat_pipe_kernel<int32_t, 5>;
+    else if (vec)
+      kern = actions_are_int64 ? (const void*)loss_cat_kernel<int64_t, true>
+                               : (const void*)loss_cat_kernel<int32_t, true>;
+    else
+      kern = actions_are_int64 ? (const void*)loss_cat_kernel<int64_t, false>
+                               : (const void*)loss_cat_kernel<int32_t, false>;
+    // one wave of resident workgroups looping over the tiles
+    blocks = std::min(blocks, resident_blocks(kern, kBlock, lds, blocks));
+    void* args[] = {&a, const_cast<long*>(&tiles)};
+    st = hip_status(hipLaunchKernel(kern, grid_of(blocks), dim3(kBlock), args, lds, stream));
+    if (st) return st;
   } else {
     if (actions_are_int64)
       hipLaunchKernelGGL(loss_cat_wave_kernel<int64_t>, dim3((unsigned)blocks), dim3(kBlock), 0,
@@ -624,17 +777,15 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
   a.dlog_std = dlog_std;
   a.partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
-  const long blocks = gauss_blocks(B);
+  long blocks = gauss_blocks(B);
   const long tiles = row_tiles(B);
   const size_t lds = (size_t)2 * kBlock * (D | 1) * sizeof(float);
   const bool vec = aligned(mu, 16) && aligned(actions, 16) && aligned(dmu, 16);
-  if (vec)
-    hipLaunchKernelGGL(loss_gauss_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), lds, stream,
-                       a, tiles);
-  else
-    hipLaunchKernelGGL(loss_gauss_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), lds,
-                       stream, a, tiles);
-  if ((st = last_launch_status())) return st;
+  const void* kern = vec ? (const void*)loss_gauss_kernel<true> : (const void*)loss_gauss_kernel<false>;
+  blocks = std::min(blocks, resident_blocks(kern, kBlock, lds, blocks));
+  void* args[] = {&a, const_cast<long*>(&tiles)};
+  if ((st = hip_status(hipLaunchKernel(kern, grid_of(blocks), dim3(kBlock), args, lds, stream))))
+    return st;
   hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(kBlock), 0, stream, a, blocks,
                      kGaussSlots, D);
   return last_launch_status();
