@@ -103,6 +103,13 @@ def test_cat_row_kernel(dev, B, A, vf_clip):
     run_cat(dev, B, A, seed=B * 131 + A, vf_clip=vf_clip)
 
 
+@pytest.mark.parametrize("A", [2, 3, 5, 6, 7, 9, 18, 1, 10, 13, 19, 4, 8, 12, 16, 20])
+def test_cat_each_width_specialisation(dev, A):
+    """Exact-width, predicated-width and LDS-pass forms of the row kernel,
+    with a final partial tile (B not a multiple of 256)."""
+    run_cat(dev, 2 * 256 * 9 + 77, A, seed=A, vf_clip=0.2)
+
+
 @pytest.mark.parametrize("B,A", [(5, 49), (300, 64), (300, 100), (1025, 257)])
 def test_cat_wave_kernel(dev, B, A):
     """A > 64 goes through the wave-per-row kernel."""

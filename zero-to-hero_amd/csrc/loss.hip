@@ -501,6 +501,98 @@ __global__ void __launch_bounds__(kBlock) loss_cat_pipe_kernel(LossArgs a, long 
 }
 
 // ---------------------------------------------------------------------------
+// Categorical, A <= MAXA and A % 4 != 0, 16-byte-aligned inputs: the
+// register-resident form.  The tile is kept in LDS in its global layout
+// (256 dense rows of A floats), so staging is one ds_write_b128 / ds_read_b128
+// per float4 with no index arithmetic; for A % 4 != 0 a row stride of A words
+// puts the 32 lanes of a half-wave on distinct banks (A odd) or at most two
+// lanes per bank (A = 2 mod 4).  Each thread then reads its row into
+// registers once and evaluates, per logit,
+//     t_j = max(z_j - m, -FLT_MAX),  e_j = exp(t_j),  s += e_j,  S += e_j t_j
+//     dlogit_j = (e_j / s) * (ec/B * t_j + K),  K = ec/B * (H - log s) - g_lp
+// which is the gradient above rearranged (log p_j = t_j - log s); the
+// 1[j == a] * g_lp term is added by one LDS read-modify-write per row.  That
+// is ~10 VALU operations per logit against ~40 for the LDS-pass form, which
+// was VALU-bound on MI355X.
+// ---------------------------------------------------------------------------
+// KA > 0 fixes A at compile time (no per-logit predicates); KA == 0 takes
+// A from the arguments, A <= MAXA.
+template <typename ActT, int KA, int MAXA>
+__global__ void __launch_bounds__(kBlock) loss_cat_dense_kernel(LossArgs a, long ntiles) {
+  constexpr int PF = (MAXA + 3) / 4;
+  constexpr float kLog2e = 1.4426950408889634f;
+  extern __shared__ float s_tile[];
+  f4* s_tile4 = reinterpret_cast<f4*>(s_tile);
+  const int A = KA > 0 ? KA : a.A;
+  const float ge = a.ec * a.inv_b;
+  const int tid = threadIdx.x;
+  double acc[5] = {0, 0, 0, 0, 0};
+  CatPrefetch<ActT, PF> pf;
+  long tile = blockIdx.x;
+  if (tile < ntiles) cat_prefetch<ActT, PF>(a, tile, pf);
+
+  for (; tile < ntiles; tile += gridDim.x) {
+    const int nrows = pf.nrows;
+    const int count = nrows * A;
+    const int n4 = count >> 2;
+#pragma unroll
+    for (int k = 0; k < PF; ++k) {
+      const int i = k * kBlock + tid;
+      if (i < n4) s_tile4[i] = pf.x[k];
+    }
+    if (tid < count - (n4 << 2)) s_tile[(n4 << 2) + tid] = pf.tail;
+    const RowIn in = pf.in;
+    const int ai = pf.ai;
+    const long row0 = tile * kBlock;
+    __syncthreads();
+
+    const long next = tile + gridDim.x;
+    if (next < ntiles) cat_prefetch<ActT, PF>(a, next, pf);
+
+    if (tid < nrows) {
+      const long row = row0 + tid;
+      float* zr = s_tile + tid * A;
+      float t[MAXA], e[MAXA];
+      float m = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < MAXA; ++j)
+        if (j < A) {
+          t[j] = zr[j];
+          m = fmaxf(m, t[j]);
+        }
+      float s = 0.0f, S = 0.0f;
+#pragma unroll
+      for (int j = 0; j < MAXA; ++j)
+        if (j < A) {
+          const float tj = fmaxf(t[j] - m, -FLT_MAX);
+          const float ej = __builtin_amdgcn_exp2f(tj * kLog2e);
+          t[j] = tj;
+          e[j] = ej;
+          s += ej;
+          S = fmaf(ej, tj, S);
+        }
+      const float log_s = logf(s);
+      const float inv_s = 1.0f / s;
+      const float H = log_s - S * inv_s;
+      const float lp = ai >= 0 ? (zr[ai] - m) - log_s : __builtin_nanf("");
+      const RowOut o = ppo_row(a, row, in, lp);
+      const float K = ge * (H - log_s) - o.g_lp;
+#pragma unroll
+      for (int j = 0; j < MAXA; ++j)
+        if (j < A) zr[j] = (e[j] * inv_s) * fmaf(ge, t[j], K);
+      if (ai >= 0) zr[ai] += o.g_lp;
+      accumulate(acc, o, H);
+    }
+    __syncthreads();
+    f4* dst = reinterpret_cast<f4*>(a.dx + row0 * A);
+    for (int i = tid; i < n4; i += kBlock) stnt(s_tile4[i], dst + i);
+    if (tid < count - (n4 << 2)) a.dx[row0 * A + (n4 << 2) + tid] = s_tile[(n4 << 2) + tid];
+    __syncthreads();
+  }
+  store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
+}
+
+// ---------------------------------------------------------------------------
 // Categorical, any A: one wave per row (lanes stride the actions).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_max_f(float x) {
@@ -712,9 +804,36 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
   const long tiles = row_tiles(B);
   if (A <= kMaxCatRowWidth) {
     const bool vec = aligned(logits, 16) && aligned(dlogits, 16);
-    const size_t lds = (size_t)kBlock * (A | 1) * sizeof(float);
+    size_t lds = (size_t)kBlock * (A | 1) * sizeof(float);
     const void* kern;
-    if (vec && (A + 3) / 4 <= 2)
+    const bool dense = vec && (A % 4) != 0 && A <= 20;
+#define PPO_DENSE(KA, M)                                                          \
+  (actions_are_int64 ? (const void*)loss_cat_dense_kernel<int64_t, KA, M>         \
+                     : (const void*)loss_cat_dense_kernel<int32_t, KA, M>)
+    if (dense && A == 2)
+      kern = PPO_DENSE(2, 2);
+    else if (dense && A == 3)
+      kern = PPO_DENSE(3, 3);
+    else if (dense && A == 5)
+      kern = PPO_DENSE(5, 5);
+    else if (dense && A == 6)
+      kern = PPO_DENSE(6, 6);
+    else if (dense && A == 7)
+      kern = PPO_DENSE(7, 7);
+    else if (dense && A == 9)
+      kern = PPO_DENSE(9, 9);
+    else if (dense && A == 18)
+      kern = PPO_DENSE(18, 18);
+    else if (dense && A <= 4)
+      kern = PPO_DENSE(0, 4);
+    else if (dense && A <= 8)
+      kern = PPO_DENSE(0, 8);
+    else if (dense && A <= 12)
+      kern = PPO_DENSE(0, 12);
+    else if (dense)
+      kern = PPO_DENSE(0, 20);
+#undef PPO_DENSE
+    else if (vec && (A + 3) / 4 <= 2)
       kern = actions_are_int64 ? (const void*)loss_cat_pipe_kernel<int64_t, 2>
                                : (const void*)loss_cat_pipe_kernel<int32_t, 2>;
     else if (vec && (A + 3) / 4 <= 5)
@@ -726,6 +845,7 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
     else
       kern = actions_are_int64 ? (const void*)loss_cat_kernel<int64_t, false>
                                : (const void*)loss_cat_kernel<int32_t, false>;
+    if (dense) lds = (size_t)kBlock * A * sizeof(float);
     // one wave of resident workgroups looping over the tiles
     blocks = std::min(blocks, resident_blocks(kern, kBlock, lds, blocks));
     void* args[] = {&a, const_cast<long*>(&tiles)};
