@@ -50,6 +50,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB device copy (for rocprofv3 --pmc scaling)")
     return ap.parse_args()
 
 
@@ -203,59 +205,91 @@ def time_events(torch, fn, reps):
 
 
 def suite(torch, lib, dev):
-    """One line per BASELINE config kernel (2: GAE+norm, 3: long-T scan,
-    4: discrete loss, 5: Gaussian loss)."""
-    import ppo_amd
+    """One line per BASELINE config kernel chain (2: GAE+normalise, 3: long-T
+    GAE scan, 4: discrete loss, 5: Gaussian loss), each timed through the C
+    ABI with preallocated outputs (HIP events on the launch stream)."""
+    import ctypes
 
-    out = []
+    from ppo_amd import _lib
+
     g = torch.Generator(device=dev).manual_seed(24)
-    # config 2
-    T, N = 2048, 4096
-    r = torch.randn(T, N, device=dev, generator=g)
-    v = torch.randn(T, N, device=dev, generator=g)
-    d = (torch.rand(T, N, device=dev, generator=g) < 0.01).to(torch.uint8)
-    lv = torch.randn(N, device=dev, generator=g)
-    t = time_events(torch, lambda: ppo_amd.gae_normalize(r, v, d, lv), 30)
-    out.append(("config2_gae_norm", T * N, GAE_BYTES, t))
-    t = time_events(torch, lambda: ppo_amd.gae(r, v, d, lv), 30)
-    out.append(("config2_gae_only", T * N, SCAN_BYTES, t))
-    del r, v, d
-    # config 3
-    T, N = 1_048_576, 16
-    r = torch.randn(T, N, device=dev, generator=g)
-    v = torch.randn(T, N, device=dev, generator=g)
-    d = (torch.rand(T, N, device=dev, generator=g) < 0.001).to(torch.uint8)
-    lv = torch.randn(N, device=dev, generator=g)
-    t = time_events(torch, lambda: ppo_amd.gae(r, v, d, lv, 0.999, 0.95), 30)
-    out.append(("config3_long_scan", T * N, SCAN_BYTES, t))
-    del r, v, d
-    # config 4
-    B, A = 1_048_576, 18
-    x = synthetic_rollout(torch, dev, 256, 4096, A, seed=25)
-    args = (x["logits"], x["actions"], x["old_log_probs"], x["rewards"].reshape(-1),
-            x["values"].reshape(-1), x["new_values"], x["values"].reshape(-1), 0.2, 0.2)
-    t = time_events(torch, lambda: ppo_amd.ppo_loss_discrete_fused(*args), 30)
-    out.append(("config4_loss_cat", B, LOSS_CAT_BYTES, t))
-    del x, args
-    # config 5
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    f32 = dict(dtype=torch.float32, device=dev)
+    params = _lib.LossParams(0.2, 0.2, 0.5, 0.01)
+    out = []
+
+    def ws(nbytes):
+        return torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+    # config 2 and 3: GAE over [T,N]
+    for name, T, N, pd, gamma, norm in (("config2_gae_norm", 2048, 4096, 0.01, 0.99, True),
+                                        ("config3_long_scan", 1_048_576, 16, 0.001, 0.999, False)):
+        r = torch.randn(T, N, generator=g, **f32)
+        v = torch.randn(T, N, generator=g, **f32)
+        d = (torch.rand(T, N, device=dev, generator=g) < pd).to(torch.uint8)
+        lv = torch.randn(N, generator=g, **f32)
+        adv, ret, advn = (torch.empty(T, N, **f32) for _ in range(3))
+        w = ws(lib.ppo_gae_workspace_bytes(T, N))
+        if norm:
+            fn = lambda: lib.ppo_gae_norm_f32(  # noqa: E731
+                r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N, gamma, 0.95,
+                1e-8, adv.data_ptr(), ret.data_ptr(), advn.data_ptr(), None, w.data_ptr(),
+                w.numel(), stream)
+            bpu = GAE_BYTES
+        else:
+            fn = lambda: lib.ppo_gae_f32(  # noqa: E731
+                r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N, gamma, 0.95,
+                adv.data_ptr(), ret.data_ptr(), w.data_ptr(), w.numel(), stream)
+            bpu = SCAN_BYTES
+        fn()
+        out.append((name, T * N, bpu, time_events(torch, fn, 30)))
+        del r, v, d, adv, ret, advn, w
+    # config 4: discrete loss
+    x = synthetic_rollout(torch, dev, 256, 4096, 18, seed=25)
+    B, A = x["logits"].shape
+    dl, dv, sc = torch.empty(B, A, **f32), torch.empty(B, **f32), torch.empty(6, **f32)
+    w = ws(lib.ppo_loss_cat_workspace_bytes(B, A))
+    fn = lambda: lib.ppo_loss_cat_f32(  # noqa: E731
+        x["logits"].data_ptr(), B, A, x["actions"].data_ptr(), 0, x["old_log_probs"].data_ptr(),
+        x["rewards"].data_ptr(), x["values"].data_ptr(), x["new_values"].data_ptr(),
+        x["values"].data_ptr(), ctypes.byref(params), dl.data_ptr(), dv.data_ptr(),
+        sc.data_ptr(), w.data_ptr(), w.numel(), stream)
+    fn()
+    out.append(("config4_loss_cat", B, LOSS_CAT_BYTES, time_events(torch, fn, 30)))
+    del x, dl, dv, w
+    # config 5: Gaussian loss
     B, D = 2_097_152, 6
-    mu = torch.randn(B, D, device=dev, generator=g)
-    ls = torch.rand(D, device=dev, generator=g) - 1.0
-    acts = mu + 0.05 * torch.randn(B, D, device=dev, generator=g) + ls.exp() * torch.randn(
-        B, D, device=dev, generator=g)
-    olp = torch.randn(B, device=dev, generator=g) - 5.0
-    advb = torch.randn(B, device=dev, generator=g)
-    retb = torch.randn(B, device=dev, generator=g)
-    ov = torch.randn(B, device=dev, generator=g)
-    nv = ov + 0.1 * torch.randn(B, device=dev, generator=g)
-    t = time_events(torch, lambda: ppo_amd.ppo_loss_gaussian_fused(
-        mu, ls, acts, olp, advb, retb, nv, ov, 0.2, 0.2), 30)
-    out.append(("config5_loss_gauss", B, GAUSS_BYTES, t))
+    mu = torch.randn(B, D, generator=g, **f32)
+    ls = torch.rand(D, generator=g, **f32) - 1.0
+    acts = mu + 0.05 * torch.randn(B, D, generator=g, **f32) + ls.exp() * torch.randn(
+        B, D, generator=g, **f32)
+    rows = [torch.randn(B, generator=g, **f32) for _ in range(5)]
+    dmu, dls, dv = torch.empty(B, D, **f32), torch.empty(D, **f32), torch.empty(B, **f32)
+    w = ws(lib.ppo_loss_gauss_workspace_bytes(B, D))
+    fn = lambda: lib.ppo_loss_gauss_f32(  # noqa: E731
+        mu.data_ptr(), ls.data_ptr(), B, D, acts.data_ptr(), rows[0].data_ptr(),
+        rows[1].data_ptr(), rows[2].data_ptr(), rows[3].data_ptr(), rows[4].data_ptr(),
+        ctypes.byref(params), dmu.data_ptr(), dls.data_ptr(), dv.data_ptr(), sc.data_ptr(),
+        w.data_ptr(), w.numel(), stream)
+    fn()
+    out.append(("config5_loss_gauss", B, GAUSS_BYTES, time_events(torch, fn, 30)))
     for name, units, bpu, t in out:
         gbs = units * bpu / t / 1e9
         print(json.dumps({"suite": name, "units": units, "bytes_per_unit": bpu,
                           "us": round(t * 1e6, 2), "GB/s": round(gbs, 1),
                           "frac": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+
+
+def copy_calibration(torch, dev, reps=3):
+    """A plain device-to-device copy of exactly 1 GiB (torch copy_), run
+    `reps` times so that a rocprofv3 --pmc pass over this command records what
+    FETCH_SIZE / WRITE_SIZE report for 1 GiB read + 1 GiB written."""
+    a = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
 
 
 def main():
@@ -277,6 +311,8 @@ def main():
         suite(torch, lib, dev)
         torch.cuda.empty_cache()
 
+    if args.copy_calibration:
+        copy_calibration(torch, dev)
     x = synthetic_rollout(torch, dev, T_STEPS, N_ENVS, N_ACTIONS)
     step = Step(torch, lib, x, dev)
     B = step.B

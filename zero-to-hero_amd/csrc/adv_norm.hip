@@ -1,7 +1,7 @@
 // Advantage normalisation (rl/deep/agents/ppo.py:126-127):
 //     if len(advantages) > 1:
 //         advantages = (advantages - advantages.mean()) / (advantages.std() + 1e-8)
-// Three kernels: a moments pass (fp64 Chan combine per thread, then per
+// Three kernels: a moments pass (fp64 sums of x and x^2 per thread, then per
 // block), a one-block finaliser combining the block partials in a fixed order,
 // and an fp32 elementwise pass.
 #include <algorithm>
@@ -20,18 +20,11 @@ long stat_blocks(long n) {
   return std::max(1L, std::min(b, kMaxStatBlocks));
 }
 
-// Moments of 4 values as one (n, mean, M2) triple.
-__device__ __forceinline__ Moments moments4(float x0, float x1, float x2, float x3) {
-  const double a = x0, b = x1, c = x2, d = x3;
-  const double mean = (a + b + c + d) * 0.25;
-  const double da = a - mean, db = b - mean, dc = c - mean, dd = d - mean;
-  return {4.0, mean, da * da + db * db + dc * dc + dd * dd};
-}
-
+// Per-block (n, sum x, sum x^2) of the advantages, fp64 accumulation.
 template <bool kVec>
 __global__ void __launch_bounds__(kBlock) adv_moments_kernel(const float* adv, long n,
                                                              double* partial) {
-  Moments m = {0.0, 0.0, 0.0};
+  double acc[3] = {0.0, 0.0, 0.0};
   const long stride = (long)gridDim.x * blockDim.x;
   const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
   long tail_start = 0;
@@ -40,29 +33,46 @@ __global__ void __launch_bounds__(kBlock) adv_moments_kernel(const float* adv, l
     const float4* a4 = reinterpret_cast<const float4*>(adv);
     for (long i = gid; i < n4; i += stride) {
       const float4 x = a4[i];
-      m = moments_combine(m, moments4(x.x, x.y, x.z, x.w));
+      const double x0 = x.x, x1 = x.y, x2 = x.z, x3 = x.w;
+      acc[0] += 4.0;
+      acc[1] += (x0 + x1) + (x2 + x3);
+      acc[2] += (x0 * x0 + x1 * x1) + (x2 * x2 + x3 * x3);
     }
     tail_start = n4 * 4;
   }
   for (long i = tail_start + gid; i < n; i += stride) {
-    const Moments one = {1.0, (double)adv[i], 0.0};
-    m = moments_combine(m, one);
+    const double x = adv[i];
+    acc[0] += 1.0;
+    acc[1] += x;
+    acc[2] += x * x;
   }
-  m = block_moments(m);
+  block_sum<3>(acc);
   if (threadIdx.x == 0) {
-    partial[blockIdx.x * 4 + 0] = m.n;
-    partial[blockIdx.x * 4 + 1] = m.mean;
-    partial[blockIdx.x * 4 + 2] = m.m2;
+    partial[blockIdx.x * 4 + 0] = acc[0];
+    partial[blockIdx.x * 4 + 1] = acc[1];
+    partial[blockIdx.x * 4 + 2] = acc[2];
     partial[blockIdx.x * 4 + 3] = 0.0;
   }
 }
 
-__global__ void __launch_bounds__(kBlock) finalize_stats_kernel(const double* partial, long count,
+// One block: combine the partials (fixed order) and store the normaliser
+// parameters in the workspace header (and {mean, std} in stats_out).
+__global__ void __launch_bounds__(kBlock) finalize_stats_kernel(const double* partials, long count,
                                                                 double eps, WsHeader* hdr,
                                                                 float* stats_out) {
-  finalize_stats(partial, count, eps, hdr, stats_out);
+  const NormParams np = norm_params(partials, count, eps);
+  if (threadIdx.x == 0) {
+    hdr->stats[0] = np.mean_used;
+    hdr->stats[1] = np.std;
+    hdr->stats[2] = np.denom;
+    if (stats_out) {
+      stats_out[0] = np.mean;
+      stats_out[1] = np.std;
+    }
+  }
 }
 
+// Elementwise pass at full occupancy, one float4 per thread per iteration.
 template <bool kVec>
 __global__ void __launch_bounds__(kBlock) normalize_kernel(const float* adv, float* out, long n,
                                                            const WsHeader* hdr) {
@@ -72,17 +82,18 @@ __global__ void __launch_bounds__(kBlock) normalize_kernel(const float* adv, flo
   const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
   long tail_start = 0;
   if constexpr (kVec) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
     const long n4 = n / 4;
-    const float4* a4 = reinterpret_cast<const float4*>(adv);
-    float4* o4 = reinterpret_cast<float4*>(out);
+    const f4* a4 = reinterpret_cast<const f4*>(adv);
+    f4* o4 = reinterpret_cast<f4*>(out);
     for (long i = gid; i < n4; i += stride) {
-      const float4 x = a4[i];
-      float4 y;
-      y.x = (x.x - mean) / denom;
-      y.y = (x.y - mean) / denom;
-      y.z = (x.z - mean) / denom;
-      y.w = (x.w - mean) / denom;
-      o4[i] = y;
+      const f4 x = a4[i];
+      f4 y;
+      y[0] = (x[0] - mean) / denom;
+      y[1] = (x[1] - mean) / denom;
+      y[2] = (x[2] - mean) / denom;
+      y[3] = (x[3] - mean) / denom;
+      __builtin_nontemporal_store(y, o4 + i);
     }
     tail_start = n4 * 4;
   }
@@ -91,23 +102,20 @@ __global__ void __launch_bounds__(kBlock) normalize_kernel(const float* adv, flo
 
 }  // namespace
 
-int launch_finalize_stats(const double* partials, long count, double eps, WsHeader* hdr,
-                          float* stats_out, hipStream_t stream) {
-  hipLaunchKernelGGL(finalize_stats_kernel, dim3(1), dim3(kBlock), 0, stream, partials, count,
-                     eps, hdr, stats_out);
-  return last_launch_status();
-}
-
-int launch_normalize(const float* adv, float* out, long n, const WsHeader* hdr,
-                     hipStream_t stream) {
+int launch_normalize(const double* partials, long count, double eps, const float* adv, float* out,
+                     long n, WsHeader* hdr, float* stats_out, hipStream_t stream) {
   if (n <= 0) return PPO_OK;
+  hipLaunchKernelGGL(finalize_stats_kernel, dim3(1), dim3(kBlock), 0, stream, partials, count, eps,
+                     hdr, stats_out);
+  int st = last_launch_status();
+  if (st) return st;
   const bool vec = aligned(adv, 16) && aligned(out, 16);
   const long work = vec ? (n + 3) / 4 : n;
   long blocks = (work + kBlock - 1) / kBlock;
   blocks = std::max(1L, std::min(blocks, 8192L));
   if (vec)
-    hipLaunchKernelGGL(normalize_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), 0, stream,
-                       adv, out, n, hdr);
+    hipLaunchKernelGGL(normalize_kernel<true>, dim3((unsigned)blocks), dim3(kBlock), 0, stream, adv,
+                       out, n, hdr);
   else
     hipLaunchKernelGGL(normalize_kernel<false>, dim3((unsigned)blocks), dim3(kBlock), 0, stream,
                        adv, out, n, hdr);
@@ -142,6 +150,5 @@ extern "C" int ppo_adv_norm_f32(const float* adv, int64_t n, double eps, float* 
                        stream, adv, (long)n, partial);
   int st = last_launch_status();
   if (st) return st;
-  if ((st = launch_finalize_stats(partial, blocks, eps, hdr, stats_out, stream))) return st;
-  return launch_normalize(adv, out, n, hdr, stream);
+  return launch_normalize(partial, blocks, eps, adv, out, n, hdr, stats_out, stream);
 }

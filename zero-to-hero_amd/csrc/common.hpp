@@ -33,66 +33,10 @@ inline int hip_status(hipError_t e) { return e == hipSuccess ? PPO_OK : PPO_ERR_
 // Launch-error check after a hipLaunchKernelGGL.
 inline int last_launch_status() { return hip_status(hipGetLastError()); }
 
-// ---------------------------------------------------------------------------
-// Running (count, mean, M2) triple and Chan et al.'s pairwise combine (1979):
-//   n = na + nb, d = mb - ma, mean = ma + d*nb/n, M2 = M2a + M2b + d^2*na*nb/n
-// Evaluated in fp64 so that 8M fp32 advantages keep ~1e-15 relative accuracy.
-// ---------------------------------------------------------------------------
-struct Moments {
-  double n, mean, m2;
-};
-
-__device__ __forceinline__ Moments moments_combine(Moments a, Moments b) {
-  if (a.n == 0.0) return b;
-  if (b.n == 0.0) return a;
-  const double n = a.n + b.n;
-  const double d = b.mean - a.mean;
-  const double fb = b.n / n;
-  Moments r;
-  r.n = n;
-  r.mean = a.mean + d * fb;
-  r.m2 = a.m2 + b.m2 + d * d * a.n * fb;
-  return r;
-}
-
-__device__ __forceinline__ Moments moments_shfl_xor(Moments m, int lane_mask) {
-  Moments o;
-  o.n = __shfl_xor(m.n, lane_mask, kWave);
-  o.mean = __shfl_xor(m.mean, lane_mask, kWave);
-  o.m2 = __shfl_xor(m.m2, lane_mask, kWave);
-  return o;
-}
-
-// Butterfly over the 64 lanes; every lane ends with the same value.  The
-// combine order is fixed, so results are run-to-run deterministic.
-__device__ __forceinline__ Moments wave_moments(Moments m) {
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) m = moments_combine(m, moments_shfl_xor(m, off));
-  return m;
-}
-
 __device__ __forceinline__ double wave_sum(double x) {
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) x += __shfl_xor(x, off, kWave);
   return x;
-}
-
-// Block-wide moments for a 1-D block of blockDim.x (multiple of 64, <= 1024)
-// threads.  Result valid in thread 0.
-__device__ inline Moments block_moments(Moments m) {
-  __shared__ Moments s_part[16];
-  m = wave_moments(m);
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wid = threadIdx.x / kWave;
-  if (lane == 0) s_part[wid] = m;
-  __syncthreads();
-  Moments r = {0.0, 0.0, 0.0};
-  if (threadIdx.x == 0) {
-    const int nw = blockDim.x / kWave;
-    for (int w = 0; w < nw; ++w) r = moments_combine(r, s_part[w]);
-  }
-  __syncthreads();
-  return r;
 }
 
 // Block-wide sum of K doubles per thread; result valid in thread 0.
@@ -120,19 +64,21 @@ __device__ inline void block_sum(double (&x)[K]) {
   __syncthreads();
 }
 
-// Moments of `count` partial triples (stored as 4 doubles each: n, mean, m2,
-// pad) combined in a fixed order by one block.  Result valid in thread 0.
-__device__ inline Moments combine_partials(const double* part, long count) {
-  Moments acc = {0.0, 0.0, 0.0};
-  // contiguous range per thread keeps the order fixed
+// Sums of `count` partial (n, sum x, sum x^2, pad) quadruples, combined by
+// one block in a fixed order (contiguous range per thread, then the block
+// tree), so every block that calls this gets bit-identical totals.  Result
+// valid in thread 0.
+__device__ inline void sum_partials(const double* part, long count, double (&tot)[3]) {
+  tot[0] = tot[1] = tot[2] = 0.0;
   const long per = (count + blockDim.x - 1) / blockDim.x;
   const long lo = (long)threadIdx.x * per;
   const long hi = lo + per < count ? lo + per : count;
   for (long i = lo; i < hi; ++i) {
-    Moments p = {part[4 * i + 0], part[4 * i + 1], part[4 * i + 2]};
-    acc = moments_combine(acc, p);
+    tot[0] += part[4 * i + 0];
+    tot[1] += part[4 * i + 1];
+    tot[2] += part[4 * i + 2];
   }
-  return block_moments(acc);
+  block_sum<3>(tot);
 }
 
 __host__ __device__ inline unsigned int pow2_ceil(unsigned int x) {

@@ -27,8 +27,8 @@
 //   3. gae_tile_kernel<.., kFinal=true>: re-reads the tile, rebuilds the
 //      segment composites, applies the tile carry, and runs the exact serial
 //      recurrence per segment, writing adv and ret (and, for the fused
-//      normaliser, per-block (n, mean, M2) of the advantages, combined by a
-//      one-block finaliser before the elementwise normalise pass).
+//      normaliser, per-block (n, sum, sum of squares) of the advantages,
+//      combined by a one-block finaliser before the elementwise pass).
 // When the whole horizon fits in one tile (Tt == 1) steps 1-2 are skipped.
 #include <algorithm>
 
@@ -49,7 +49,7 @@ struct GaeArgs {
   float* ret;          // may be null
   double2* summary;    // [Tt][N] (a, P)
   const double* carry; // [Tt][N] or null (all-zero carries)
-  double* partial;     // [blocks][4] moments, fused-normalise only
+  double* partial;     // [blocks][4] (n, sum, sum sq), fused-normalise only
   WsHeader* hdr;
   float* stats_out;
   double eps;
@@ -99,22 +99,43 @@ __device__ __forceinline__ double mul(double a, double b) { return __dmul_rn(a, 
 __device__ __forceinline__ double add(double a, double b) { return __dadd_rn(a, b); }
 __device__ __forceinline__ double sub(double a, double b) { return __dsub_rn(a, b); }
 
+// Rollout arrays are streamed: nontemporal loads and stores.
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+#ifndef PPO_GAE_NT_LOAD
+#define PPO_GAE_NT_LOAD 0
+#endif
+#ifndef PPO_GAE_NT_STORE
+#define PPO_GAE_NT_STORE 1
+#endif
+template <typename T>
+__device__ __forceinline__ T ld(const T* p) {
+  if constexpr (PPO_GAE_NT_LOAD) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <typename T>
+__device__ __forceinline__ void st(T v, T* p) {
+  if constexpr (PPO_GAE_NT_STORE) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
+
 template <int VW>
 __device__ __forceinline__ void load_f(const float* p, float (&x)[VW]) {
   if constexpr (VW == 4) {
-    const float4 t = *reinterpret_cast<const float4*>(p);
-    x[0] = t.x; x[1] = t.y; x[2] = t.z; x[3] = t.w;
+    const f4 t = ld(reinterpret_cast<const f4*>(p));
+    x[0] = t[0]; x[1] = t[1]; x[2] = t[2]; x[3] = t[3];
   } else {
-    x[0] = *p;
+    x[0] = ld(p);
   }
 }
 
 template <int VW>
 __device__ __forceinline__ void store_f(float* p, const float (&x)[VW]) {
   if constexpr (VW == 4) {
-    *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    const f4 t = {x[0], x[1], x[2], x[3]};
+    st(t, reinterpret_cast<f4*>(p));
   } else {
-    *p = x[0];
+    st(x[0], p);
   }
 }
 
@@ -122,11 +143,11 @@ __device__ __forceinline__ void store_f(float* p, const float (&x)[VW]) {
 template <int VW>
 __device__ __forceinline__ unsigned load_done(const uint8_t* p) {
   if constexpr (VW == 4) {
-    const unsigned w = *reinterpret_cast<const unsigned*>(p);
+    const unsigned w = ld(reinterpret_cast<const unsigned*>(p));
     return ((w & 0xffu) != 0u) | (((w >> 8) & 0xffu) != 0u) << 1 |
            (((w >> 16) & 0xffu) != 0u) << 2 | ((w >> 24) != 0u) << 3;
   } else {
-    return *p != 0;
+    return ld(p) != 0;
   }
 }
 
@@ -198,7 +219,7 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
   // Reverse inclusive scan over the Sw segments of the tile:
   // (a_s, P_s) <- (a_s + P_s*a_{s+off}, P_s*P_{s+off}).
 #pragma unroll
-  for (int k = 0; k < VW; ++k) { s_a[tid * VW + k] = ia[k]; s_p[tid * VW + k] = ip[k]; }
+  for (int k = 0; k < VW; ++k) { s_a[k * kBlock + tid] = ia[k]; s_p[k * kBlock + tid] = ip[k]; }
   for (int off = 1; off < a.Sw; off <<= 1) {
     __syncthreads();
     const bool has = s + off < a.Sw;
@@ -206,8 +227,8 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
     if (has) {
 #pragma unroll
       for (int k = 0; k < VW; ++k) {
-        pa[k] = s_a[(tid + off * a.Qw) * VW + k];
-        pp[k] = s_p[(tid + off * a.Qw) * VW + k];
+        pa[k] = s_a[k * kBlock + tid + off * a.Qw];
+        pp[k] = s_p[k * kBlock + tid + off * a.Qw];
       }
     }
     __syncthreads();
@@ -216,8 +237,8 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
       for (int k = 0; k < VW; ++k) {
         ia[k] = ia[k] + ip[k] * pa[k];
         ip[k] = ip[k] * pp[k];
-        s_a[tid * VW + k] = ia[k];
-        s_p[tid * VW + k] = ip[k];
+        s_a[k * kBlock + tid] = ia[k];
+        s_p[k * kBlock + tid] = ip[k];
       }
     }
   }
@@ -237,7 +258,7 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
     for (int k = 0; k < VW; ++k) {
       const double C = (a.carry && col_ok) ? a.carry[tile_t * a.N + env0 + k] : 0.0;
       if (s + 1 < a.Sw)
-        cin[k] = s_a[(tid + a.Qw) * VW + k] + s_p[(tid + a.Qw) * VW + k] * C;
+        cin[k] = s_a[k * kBlock + tid + a.Qw] + s_p[k * kBlock + tid + a.Qw] * C;
       else
         cin[k] = C;
     }
@@ -277,32 +298,21 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
     }
 
     if constexpr (kStats) {
-      Moments m = {0.0, 0.0, 0.0};
-      if (nvalid > 0) {
-        double sum = 0.0;
+      double acc[3] = {(double)(nvalid * VW), 0.0, 0.0};
 #pragma unroll
-        for (int i = 0; i < L; ++i)
-          if (i < nvalid)
+      for (int i = 0; i < L; ++i)
+        if (i < nvalid)
 #pragma unroll
-            for (int k = 0; k < VW; ++k) sum += (double)r[i][k];
-        m.n = (double)(nvalid * VW);
-        m.mean = sum / m.n;
-        double m2 = 0.0;
-#pragma unroll
-        for (int i = 0; i < L; ++i)
-          if (i < nvalid)
-#pragma unroll
-            for (int k = 0; k < VW; ++k) {
-              const double dv = (double)r[i][k] - m.mean;
-              m2 += dv * dv;
-            }
-        m.m2 = m2;
-      }
-      m = block_moments(m);
+          for (int k = 0; k < VW; ++k) {
+            const double x = (double)r[i][k];
+            acc[1] += x;
+            acc[2] += x * x;
+          }
+      block_sum<3>(acc);
       if (tid == 0) {
-        a.partial[bid * 4 + 0] = m.n;
-        a.partial[bid * 4 + 1] = m.mean;
-        a.partial[bid * 4 + 2] = m.m2;
+        a.partial[bid * 4 + 0] = acc[0];
+        a.partial[bid * 4 + 1] = acc[1];
+        a.partial[bid * 4 + 2] = acc[2];
         a.partial[bid * 4 + 3] = 0.0;
       }
     }
@@ -406,12 +416,10 @@ int launch_gae(const GaePlan& p, GaeArgs a, bool stats, hipStream_t stream) {
   } else {
     a.carry = nullptr;
   }
-  if (stats) {
+  if (stats)
     hipLaunchKernelGGL((gae_tile_kernel<VW, L, true, true>), dim3((unsigned)blocks), dim3(kBlock),
                        0, stream, a);
-    if ((st = last_launch_status())) return st;
-    return launch_finalize_stats(a.partial, blocks, a.eps, a.hdr, a.stats_out, stream);
-  } else
+  else
     hipLaunchKernelGGL((gae_tile_kernel<VW, L, true, false>), dim3((unsigned)blocks),
                        dim3(kBlock), 0, stream, a);
   return last_launch_status();
@@ -457,7 +465,8 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
 
   int st = vec ? launch_gae<4, 4>(p, a, norm, stream) : launch_gae<1, 16>(p, a, norm, stream);
   if (st || !norm) return st;
-  return launch_normalize(adv_out, adv_norm_out, T * N, a.hdr, stream);
+  return launch_normalize(a.partial, p.blocks(), eps, adv_out, adv_norm_out, T * N, a.hdr,
+                          stats_out, stream);
 }
 
 }  // namespace

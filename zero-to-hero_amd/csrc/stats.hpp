@@ -6,47 +6,47 @@
 
 namespace ppo {
 
-// One-block kernel body, run after every producer block has stored its
-// (n, mean, M2) partial (a previous launch on the same stream).  Computes mean and the unbiased std in fp64, rounds both to fp32
-// (torch returns fp32 0-d tensors for .mean() / .std()), and forms the fp32
-// denominator std + eps exactly as `advantages.std() + 1e-8` does.  For n <= 1
-// the normaliser must be the identity (the reference skips it when
-// len(advantages) <= 1), so mean = 0 and denom = 1 are stored instead.
-__device__ inline void finalize_stats(const double* partials, long count, double eps,
-                                      WsHeader* hdr, float* stats_out) {
-  Moments m = combine_partials(partials, count);
-  if (threadIdx.x == 0) {
-    float mean_f, std_f, denom;
-    if (m.n > 1.0) {
-      const double var = m.m2 / (m.n - 1.0);
-      mean_f = (float)m.mean;
-      std_f = (float)sqrt(var);
-      denom = std_f + (float)eps;
-      hdr->stats[0] = mean_f;
-      hdr->stats[2] = denom;
-    } else {
-      mean_f = (float)m.mean;
-      std_f = __builtin_nanf("");
-      hdr->stats[0] = 0.0f;
-      hdr->stats[2] = 1.0f;
-    }
-    hdr->stats[1] = std_f;
-    if (stats_out) {
-      stats_out[0] = mean_f;
-      stats_out[1] = std_f;
-    }
+// Normaliser parameters from the block partials (n, sum x, sum x^2 in fp64),
+// combined in a fixed order by one block (the same order in every block that
+// calls this, so every block derives bit-identical values).  mean and the
+// unbiased std, var = (sum x^2 - (sum x)^2 / n) / (n - 1), are formed in fp64
+// (relative error ~1e-16 * (1 + mean^2/var), i.e. exact to fp32 unless
+// |mean|/std exceeds ~1e4) and rounded to fp32 (torch returns fp32 0-d tensors for .mean() /
+// .std()), and the denominator is the fp32 sum std + eps exactly as
+// `advantages.std() + 1e-8` forms it.  For n <= 1 the normaliser must be the
+// identity (the reference skips it when len(advantages) <= 1): mean 0 and
+// denominator 1 are returned instead.  Result valid in thread 0.
+struct NormParams {
+  float mean_used, denom;  // what the elementwise pass applies
+  float mean, std;         // what is reported
+};
+
+__device__ inline NormParams norm_params(const double* partials, long count, double eps) {
+  double tot[3];
+  sum_partials(partials, count, tot);
+  const double n = tot[0];
+  const double mean = tot[1] / n;
+  NormParams r;
+  r.mean = (float)mean;
+  if (n > 1.0) {
+    const double m2 = tot[2] - tot[1] * mean;
+    r.std = (float)sqrt((m2 > 0.0 ? m2 : 0.0) / (n - 1.0));
+    r.mean_used = r.mean;
+    r.denom = r.std + (float)eps;
+  } else {
+    r.std = __builtin_nanf("");
+    r.mean_used = 0.0f;
+    r.denom = 1.0f;
   }
+  return r;
 }
 
-// Enqueue the one-block finaliser over `count` partials.  Defined in
-// adv_norm.hip.
-int launch_finalize_stats(const double* partials, long count, double eps, WsHeader* hdr,
-                          float* stats_out, hipStream_t stream);
-
-// Enqueue out[i] = (adv[i] - mean) / denom (fp32) where mean/denom are the
-// values finalize_stats() stored in `hdr` earlier on the same stream.
+// Enqueue the normaliser: a one-block kernel derives mean/denom from the
+// `count` (n, sum, sum of squares) partials left in the workspace by the
+// previous kernel on the same stream (and stores {mean, std} in stats_out if
+// not null), then out[i] = (adv[i] - mean) / denom in fp32 over n elements.
 // Defined in adv_norm.hip.
-int launch_normalize(const float* adv, float* out, long n, const WsHeader* hdr,
-                     hipStream_t stream);
+int launch_normalize(const double* partials, long count, double eps, const float* adv, float* out,
+                     long n, WsHeader* hdr, float* stats_out, hipStream_t stream);
 
 }  // namespace ppo
