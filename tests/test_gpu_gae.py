@@ -152,6 +152,13 @@ def test_gae_config3_full_size(dev):
     assert exact > 0.99
 
 
+def test_gae_multi_round_chunk_fold(dev):
+    """T=262144, N=64: 4096 tiles in 32 carry chunks, more than one block's
+    rows, so the later-chunk fold takes two rounds."""
+    exact = _run(dev, 262_144, 64, 0.002, seed=31, gamma=0.997, lam=0.97)
+    assert exact > 0.99
+
+
 def test_gae_repeatable(dev):
     r, v, d, lv = _inputs(1024, 64, 0.01, seed=12)
     args = (r.to(dev), v.to(dev), d.to(dev), lv.to(dev))

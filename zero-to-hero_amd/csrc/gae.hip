@@ -23,7 +23,8 @@
 //   1. gae_tile_kernel<.., kFinal=false>: per tile and env, the composite
 //      (a, P) of all its steps -> workspace `summary` [Tt][N].
 //   2. gae_carry_kernel: per env, a reverse scan over the tiles' (a, P) ->
-//      `carry` [Tt][N], the advantage entering each tile from the right.
+//      `carry` [Tt][N], the advantage entering each tile from the right
+//      (two levels, via per-chunk composites, for long horizons).
 //   3. gae_tile_kernel<.., kFinal=true>: re-reads the tile, rebuilds the
 //      segment composites, applies the tile carry, and runs the exact serial
 //      recurrence per segment, writing adv and ret (and, for the fused
@@ -48,6 +49,7 @@ struct GaeArgs {
   float* adv;
   float* ret;          // may be null
   double2* summary;    // [Tt][N] (a, P)
+  double2* chunk_sum;  // [nchunks][N] (a, P) of each carry-scan chunk
   const double* carry; // [Tt][N] or null (all-zero carries)
   double* partial;     // [blocks][4] (n, sum, sum sq), fused-normalise only
   WsHeader* hdr;
@@ -76,8 +78,28 @@ GaePlan make_plan(long T, long N, int vw) {
   return p;
 }
 
+// Carry-scan geometry (see gae_carry_kernel): 1024-thread blocks of Ew envs x
+// Rw rows, 8 tile composites per thread, so a chunk spans Rw*8 tiles.
+constexpr int kCarryBlock = 1024;
+constexpr int kCarryG = 8;
+
+struct CarryPlan {
+  int Ew, Rw;
+  long groups, nchunks;
+};
+
+CarryPlan make_carry_plan(long Tt, long N) {
+  CarryPlan c;
+  c.Ew = (int)std::min<long>(64, (long)pow2_ceil((unsigned)std::min<long>(N, 64)));
+  c.Rw = kCarryBlock / c.Ew;
+  c.groups = (N + c.Ew - 1) / c.Ew;
+  const long chunk_tiles = (long)c.Rw * kCarryG;
+  c.nchunks = (Tt + chunk_tiles - 1) / chunk_tiles;
+  return c;
+}
+
 struct GaeLayout {
-  size_t summary, carry, partial, total;
+  size_t summary, carry, chunk_sum, partial, total;
 };
 
 GaeLayout make_layout(const GaePlan& p, long N) {
@@ -87,6 +109,8 @@ GaeLayout make_layout(const GaePlan& p, long N) {
   off += align_up((size_t)p.Tt * N * sizeof(double2), 256);
   l.carry = off;
   off += align_up((size_t)p.Tt * N * sizeof(double), 256);
+  l.chunk_sum = off;
+  off += align_up((size_t)make_carry_plan(p.Tt, N).nchunks * N * sizeof(double2), 256);
   l.partial = off;
   off += align_up((size_t)p.blocks() * 4 * sizeof(double), 256);
   l.total = off;
@@ -319,15 +343,47 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
   }
 }
 
-// Reverse scan of tile composites into per-tile carries.  One block covers Ew
-// envs; its Rw thread-rows split each round of Rw*G tiles into contiguous
-// groups of G held in registers.  Rounds run from the last tile backwards.
-constexpr int kCarryBlock = 1024;
-constexpr int kCarryG = 8;
+// Reverse scan of tile composites into per-tile carries, two levels.
+// A "chunk" is kCarryChunk = Rw*G consecutive tiles of Ew envs, owned by one
+// 1024-thread block: its Rw thread-rows hold G tile composites each in
+// registers and are combined with a Kogge-Stone scan in LDS.
+//   kCompose: each chunk's composite -> chunk_sum[c][env]        (many chunks only)
+//   kCarry:   fold the composites of all later chunks (Rw at a time, scanned in
+//             LDS) into the advantage entering this chunk, then scan the chunk
+//             and write carry[k][env] for each of its tiles.
+// Horizons of up to Rw*G tiles are one chunk and need only the kCarry launch.
 
+// Reverse inclusive scan over the Rw thread-rows of (ga, gp) in LDS; returns
+// with s_a/s_p holding, for row g, the composite of rows g..Rw-1.
+__device__ __forceinline__ void carry_row_scan(double* s_a, double* s_p, int tid, int g, int Ew,
+                                               int Rw, double ga, double gp) {
+  s_a[tid] = ga;
+  s_p[tid] = gp;
+  for (int off = 1; off < Rw; off <<= 1) {
+    __syncthreads();
+    const bool has = g + off < Rw;
+    double pa = 0.0, pp = 1.0;
+    if (has) {
+      pa = s_a[tid + off * Ew];
+      pp = s_p[tid + off * Ew];
+    }
+    __syncthreads();
+    if (has) {
+      ga = ga + gp * pa;
+      gp = gp * pp;
+      s_a[tid] = ga;
+      s_p[tid] = gp;
+    }
+  }
+  __syncthreads();
+}
+
+template <bool kCompose>
 __global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* __restrict__ summary,
-                                                                 double* __restrict__ carry, long Tt,
-                                                                 long N, int Ew, int Rw) {
+                                                                 double* __restrict__ carry,
+                                                                 double2* __restrict__ chunk_sum,
+                                                                 long Tt, long N, int Ew, int Rw,
+                                                                 long nchunks) {
   __shared__ double s_a[kCarryBlock];
   __shared__ double s_p[kCarryBlock];
   const int tid = threadIdx.x;
@@ -335,62 +391,62 @@ __global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* _
   const int g = tid / Ew;
   const long env = (long)blockIdx.x * Ew + e;
   const bool ok = env < N;
-  const long round_tiles = (long)Rw * kCarryG;
+  const long c = blockIdx.y;
+  const long chunk_tiles = (long)Rw * kCarryG;
+  const long lo = c * chunk_tiles;
+  const long hi = lo + chunk_tiles < Tt ? lo + chunk_tiles : Tt;
 
-  double C = 0.0;  // advantage entering the current round from the right
-  for (long hi = Tt; hi > 0; hi -= round_tiles) {
-    const long lo = hi - round_tiles > 0 ? hi - round_tiles : 0;
-    const long k0 = lo + (long)g * kCarryG;
-    double ta[kCarryG], tp[kCarryG];
-#pragma unroll
-    for (int j = 0; j < kCarryG; ++j) {
-      const long k = k0 + j;
-      if (ok && k < hi) {
-        const double2 t = summary[k * N + env];
-        ta[j] = t.x;
-        tp[j] = t.y;
-      } else {
-        ta[j] = 0.0;
-        tp[j] = 1.0;
+  // advantage entering this chunk from the right
+  double C = 0.0;
+  if constexpr (!kCompose) {
+    for (long top = nchunks; top > c + 1; top -= Rw) {
+      const long bot = top - Rw > c + 1 ? top - Rw : c + 1;
+      const long j = bot + g;
+      double ga = 0.0, gp = 1.0;
+      if (ok && j < top) {
+        const double2 t = chunk_sum[j * N + env];
+        ga = t.x;
+        gp = t.y;
       }
+      carry_row_scan(s_a, s_p, tid, g, Ew, Rw, ga, gp);
+      C = s_a[e] + s_p[e] * C;
+      __syncthreads();
     }
-    double ga = 0.0, gp = 1.0;
+  }
+
+  const long k0 = lo + (long)g * kCarryG;
+  double ta[kCarryG], tp[kCarryG];
+#pragma unroll
+  for (int j = 0; j < kCarryG; ++j) {
+    const long k = k0 + j;
+    if (ok && k < hi) {
+      const double2 t = summary[k * N + env];
+      ta[j] = t.x;
+      tp[j] = t.y;
+    } else {
+      ta[j] = 0.0;
+      tp[j] = 1.0;
+    }
+  }
+  double ga = 0.0, gp = 1.0;
+#pragma unroll
+  for (int j = kCarryG - 1; j >= 0; --j) {
+    ga = ta[j] + tp[j] * ga;
+    gp = tp[j] * gp;
+  }
+  carry_row_scan(s_a, s_p, tid, g, Ew, Rw, ga, gp);
+  if constexpr (kCompose) {
+    if (g == 0 && ok) chunk_sum[c * N + env] = make_double2(s_a[e], s_p[e]);
+  } else {
+    double cc = (g + 1 < Rw) ? s_a[tid + Ew] + s_p[tid + Ew] * C : C;
 #pragma unroll
     for (int j = kCarryG - 1; j >= 0; --j) {
-      ga = ta[j] + tp[j] * ga;
-      gp = tp[j] * gp;
-    }
-    s_a[tid] = ga;
-    s_p[tid] = gp;
-    for (int off = 1; off < Rw; off <<= 1) {
-      __syncthreads();
-      const bool has = g + off < Rw;
-      double pa = 0.0, pp = 1.0;
-      if (has) {
-        pa = s_a[tid + off * Ew];
-        pp = s_p[tid + off * Ew];
-      }
-      __syncthreads();
-      if (has) {
-        ga = ga + gp * pa;
-        gp = gp * pp;
-        s_a[tid] = ga;
-        s_p[tid] = gp;
-      }
-    }
-    __syncthreads();
-    double c = (g + 1 < Rw) ? s_a[tid + Ew] + s_p[tid + Ew] * C : C;
-    const double c_next = s_a[e] + s_p[e] * C;
-#pragma unroll
-    for (int j = kCarryG - 1; j >= 0; --j) {
       const long k = k0 + j;
       if (ok && k < hi) {
-        carry[k * N + env] = c;
-        c = ta[j] + tp[j] * c;
+        carry[k * N + env] = cc;
+        cc = ta[j] + tp[j] * cc;
       }
     }
-    C = c_next;
-    __syncthreads();
   }
 }
 
@@ -407,11 +463,16 @@ int launch_gae(const GaePlan& p, GaeArgs a, bool stats, hipStream_t stream) {
     hipLaunchKernelGGL((gae_tile_kernel<VW, L, false, false>), dim3((unsigned)blocks),
                        dim3(kBlock), 0, stream, a);
     if ((st = last_launch_status())) return st;
-    const int Ew = (int)std::min<long>(64, (long)pow2_ceil((unsigned)std::min<long>(a.N, 64)));
-    const int Rw = kCarryBlock / Ew;
-    const long cblocks = (a.N + Ew - 1) / Ew;
-    hipLaunchKernelGGL(gae_carry_kernel, dim3((unsigned)cblocks), dim3(kCarryBlock), 0, stream,
-                       a.summary, const_cast<double*>(a.carry), p.Tt, a.N, Ew, Rw);
+    const CarryPlan cp = make_carry_plan(p.Tt, a.N);
+    if (cp.nchunks > 1) {
+      hipLaunchKernelGGL(gae_carry_kernel<true>, dim3((unsigned)cp.groups, (unsigned)cp.nchunks),
+                         dim3(kCarryBlock), 0, stream, a.summary, const_cast<double*>(a.carry),
+                         a.chunk_sum, p.Tt, a.N, cp.Ew, cp.Rw, cp.nchunks);
+      if ((st = last_launch_status())) return st;
+    }
+    hipLaunchKernelGGL(gae_carry_kernel<false>, dim3((unsigned)cp.groups, (unsigned)cp.nchunks),
+                       dim3(kCarryBlock), 0, stream, a.summary, const_cast<double*>(a.carry),
+                       a.chunk_sum, p.Tt, a.N, cp.Ew, cp.Rw, cp.nchunks);
     if ((st = last_launch_status())) return st;
   } else {
     a.carry = nullptr;
@@ -441,7 +502,8 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
                    aligned(adv_out, 16) && (!ret_out || aligned(ret_out, 16)) &&
                    aligned(dones, 4) && (!last_value || aligned(last_value, 16));
   const GaePlan p = make_plan(T, N, vec ? 4 : 1);
-  if (p.blocks() > 0x7fffffffL) return PPO_ERR_TOO_LARGE;
+  if (p.blocks() > 0x7fffffffL || make_carry_plan(p.Tt, N).nchunks > 65535)
+    return PPO_ERR_TOO_LARGE;
   const GaeLayout l = make_layout(p, N);
   char* ws = static_cast<char*>(workspace);
 
@@ -458,6 +520,7 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
   a.ret = ret_out;
   a.summary = reinterpret_cast<double2*>(ws + l.summary);
   a.carry = reinterpret_cast<double*>(ws + l.carry);
+  a.chunk_sum = reinterpret_cast<double2*>(ws + l.chunk_sum);
   a.partial = reinterpret_cast<double*>(ws + l.partial);
   a.hdr = reinterpret_cast<WsHeader*>(ws);
   a.stats_out = stats_out;
