@@ -235,6 +235,26 @@ def test_gauss(dev, B, D, vf_clip):
     run_gauss(dev, B, D, seed=B * 7 + D, vf_clip=vf_clip)
 
 
+@pytest.mark.parametrize("D", [1, 2, 3, 4, 5, 6, 7, 8, 9, 13, 16, 17, 24])
+def test_gauss_each_width_specialisation(dev, D):
+    """Exact-width and predicated-width register kernels, final partial tile."""
+    run_gauss(dev, 2 * 256 * 9 + 77, D, seed=100 + D)
+
+
+def test_gauss_misaligned_mu(dev):
+    B, D = 700, 6
+    inp = gauss_inputs(B, D, seed=12)
+    mu = inp[0]
+    buf = torch.empty(B * D + 1, device=dev)
+    buf[1:] = mu.reshape(-1).to(dev)
+    args = [buf[1:].view(B, D)] + [x.to(dev) for x in inp[1:]]
+    scalars, dmu, dls, dv = ppo_amd.ppo_loss_gaussian_fused(*args, 0.2, 0.2, 0.5, 0.01)
+    o = ref.loss_gaussian_reference(*inp, 0.2, 0.2, 0.5, 0.01)
+    assert_scalars_close(scalars, o)
+    assert_grad_close(dmu, o["dmu"])
+    assert_grad_close(dls, o["dlog_std"])
+
+
 def test_gauss_config5_full_size(dev):
     """B=2,097,152, D=6, vf_clip=0.2."""
     run_gauss(dev, 2_097_152, 6, seed=24)

@@ -731,6 +731,138 @@ __global__ void __launch_bounds__(kBlock) loss_gauss_kernel(LossArgs a, long nti
   store_scalar_partials(a, acc, blockIdx.x, kGaussSlots);
 }
 
+// ---------------------------------------------------------------------------
+// Gaussian, register-resident form for 16-byte-aligned mu/actions/dmu (any
+// D <= MAXD; KD > 0 fixes D at compile time).  mu and action tiles are staged
+// in LDS in their global layout (ds_write_b128, no index arithmetic), each
+// thread reads its row of both into registers, and this block's dlog_std
+// column sums accumulate in per-thread fp64 registers across all its tiles
+// (one block reduction per dim at the end) instead of an LDS column pass per
+// tile.  Per element: diff, diff^2, an FMA into log_prob, dmu and the
+// dlog_std term.
+// ---------------------------------------------------------------------------
+template <int PF>
+struct GaussPrefetch {
+  f4 mu[PF], act[PF];
+  float mu_tail, act_tail;
+  RowIn in;
+  int nrows;
+};
+
+template <int PF>
+__device__ __forceinline__ void gauss_prefetch(const LossArgs& a, long tile, int D,
+                                               GaussPrefetch<PF>& p) {
+  const int tid = threadIdx.x;
+  const long row0 = tile * kBlock;
+  p.nrows = (int)std::min<long>(kBlock, a.B - row0);
+  const int count = p.nrows * D;
+  const int n4 = count >> 2;
+  const f4* m4 = reinterpret_cast<const f4*>(a.x + row0 * D);
+  const f4* a4 = reinterpret_cast<const f4*>(reinterpret_cast<const float*>(a.actions) + row0 * D);
+#pragma unroll
+  for (int k = 0; k < PF; ++k) {
+    const int i = k * kBlock + tid;
+    if (i < n4) {
+      p.mu[k] = ldnt(m4 + i);
+      p.act[k] = ldnt(a4 + i);
+    }
+  }
+  if (tid < count - (n4 << 2)) {
+    p.mu_tail = ldnt(a.x + row0 * D + (n4 << 2) + tid);
+    p.act_tail = ldnt(reinterpret_cast<const float*>(a.actions) + row0 * D + (n4 << 2) + tid);
+  }
+  if (tid < p.nrows) p.in = load_row(a, row0 + tid);
+}
+
+template <int KD, int MAXD>
+__global__ void __launch_bounds__(kBlock) loss_gauss_dense_kernel(LossArgs a, long ntiles) {
+  constexpr int PF = (MAXD + 3) / 4;
+  extern __shared__ float s_lds[];
+  __shared__ float s_inv2var[kMaxGaussDim], s_invvar[kMaxGaussDim], s_logscale[kMaxGaussDim];
+  const int D = KD > 0 ? KD : a.A;
+  float* s_mu = s_lds;
+  float* s_act = s_lds + kBlock * D;
+  f4* s_mu4 = reinterpret_cast<f4*>(s_mu);
+  f4* s_act4 = reinterpret_cast<f4*>(s_act);
+  const float kLogSqrt2Pi = 0.91893853320467274178f;  // log(sqrt(2*pi))
+  const int tid = threadIdx.x;
+  if (tid < D) {
+    const float scale = expf(a.log_std[tid]);
+    const float var = scale * scale;
+    s_inv2var[tid] = 1.0f / (2.0f * var);
+    s_invvar[tid] = 1.0f / var;
+    s_logscale[tid] = logf(scale);
+  }
+  double col[MAXD];
+#pragma unroll
+  for (int d = 0; d < MAXD; ++d) col[d] = 0.0;
+  double acc[5] = {0, 0, 0, 0, 0};
+  GaussPrefetch<PF> pf;
+  long tile = blockIdx.x;
+  if (tile < ntiles) gauss_prefetch<PF>(a, tile, D, pf);
+
+  for (; tile < ntiles; tile += gridDim.x) {
+    const int nrows = pf.nrows;
+    const int count = nrows * D;
+    const int n4 = count >> 2;
+#pragma unroll
+    for (int k = 0; k < PF; ++k) {
+      const int i = k * kBlock + tid;
+      if (i < n4) {
+        s_mu4[i] = pf.mu[k];
+        s_act4[i] = pf.act[k];
+      }
+    }
+    if (tid < count - (n4 << 2)) {
+      s_mu[(n4 << 2) + tid] = pf.mu_tail;
+      s_act[(n4 << 2) + tid] = pf.act_tail;
+    }
+    const RowIn in = pf.in;
+    const long row0 = tile * kBlock;
+    __syncthreads();
+
+    const long next = tile + gridDim.x;
+    if (next < ntiles) gauss_prefetch<PF>(a, next, D, pf);
+
+    if (tid < nrows) {
+      float* mu = s_mu + tid * D;
+      const float* act = s_act + tid * D;
+      float diff[MAXD];
+      float lp = 0.0f;
+#pragma unroll
+      for (int d = 0; d < MAXD; ++d)
+        if (d < D) {
+          diff[d] = act[d] - mu[d];
+          lp += ((-(diff[d] * diff[d])) * s_inv2var[d] - s_logscale[d]) - kLogSqrt2Pi;
+        }
+      const RowOut o = ppo_row(a, row0 + tid, in, lp);
+#pragma unroll
+      for (int d = 0; d < MAXD; ++d)
+        if (d < D) {
+          const float z = diff[d] * s_invvar[d];
+          mu[d] = o.g_lp * z;                                        // dmu
+          col[d] += (double)(o.g_lp * (diff[d] * z - 1.0f));         // dlog_std term
+        }
+      accumulate(acc, o, 0.0f);
+    }
+    __syncthreads();
+    f4* dst = reinterpret_cast<f4*>(a.dx + row0 * D);
+    for (int i = tid; i < n4; i += kBlock) stnt(s_mu4[i], dst + i);
+    if (tid < count - (n4 << 2)) a.dx[row0 * D + (n4 << 2) + tid] = s_mu[(n4 << 2) + tid];
+    __syncthreads();
+  }
+  // this block's dlog_std partials: one block reduction per dim
+#pragma unroll
+  for (int d = 0; d < MAXD; ++d) {
+    if (d < D) {
+      double v[1] = {col[d]};
+      block_sum<1>(v);
+      if (tid == 0) a.partial[(long)blockIdx.x * kGaussSlots + kScalarSlots + d] = v[0];
+    }
+  }
+  store_scalar_partials(a, acc, blockIdx.x, kGaussSlots);
+}
+
 int fill_common(LossArgs& a, long B, const ppo_loss_params* p, const float* old_lp,
                 const float* adv, const float* ret, const float* val, const float* old_val,
                 float* dval, float* scalars) {
@@ -901,10 +1033,28 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
   const long tiles = row_tiles(B);
   const size_t lds = (size_t)2 * kBlock * (D | 1) * sizeof(float);
   const bool vec = aligned(mu, 16) && aligned(actions, 16) && aligned(dmu, 16);
-  const void* kern = vec ? (const void*)loss_gauss_kernel<true> : (const void*)loss_gauss_kernel<false>;
-  blocks = std::min(blocks, resident_blocks(kern, kBlock, lds, blocks));
+  const void* kern;
+  size_t lds_used = lds;
+  if (vec) {
+    // dense layout: two 256 x D tiles, no padding
+    lds_used = (size_t)2 * kBlock * D * sizeof(float);
+    if (D == 6)
+      kern = (const void*)loss_gauss_dense_kernel<6, 6>;
+    else if (D <= 4)
+      kern = (const void*)loss_gauss_dense_kernel<0, 4>;
+    else if (D <= 8)
+      kern = (const void*)loss_gauss_dense_kernel<0, 8>;
+    else if (D <= 16)
+      kern = (const void*)loss_gauss_dense_kernel<0, 16>;
+    else
+      kern = (const void*)loss_gauss_dense_kernel<0, 24>;
+  } else {
+    kern = (const void*)loss_gauss_kernel<false>;
+  }
+  blocks = std::min(blocks, resident_blocks(kern, kBlock, lds_used, blocks));
   void* args[] = {&a, const_cast<long*>(&tiles)};
-  if ((st = hip_status(hipLaunchKernel(kern, grid_of(blocks), dim3(kBlock), args, lds, stream))))
+  if ((st = hip_status(
+           hipLaunchKernel(kern, grid_of(blocks), dim3(kBlock), args, lds_used, stream))))
     return st;
   hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(kBlock), 0, stream, a, blocks,
                      kGaussSlots, D);
