@@ -55,8 +55,9 @@ def test_workspace_queries():
     small = lib.ppo_gae_workspace_bytes(128, 8)
     big = lib.ppo_gae_workspace_bytes(2048, 4096)
     assert 256 < small < big
-    # summary (16 B) + carry (8 B) per env per tile, tiles of >= 16 steps
-    assert big < 2048 * 4096 * 24 / 16 + (1 << 20)
+    # summary (16 B) + carry (8 B) + five fp32 tile sums (20 B) per env per
+    # tile, tiles of >= 16 steps
+    assert big < 2048 * 4096 * 44 / 16 + (1 << 20)
     assert lib.ppo_adv_norm_workspace_bytes(1 << 23) > 256
     assert lib.ppo_loss_cat_workspace_bytes(1 << 20, 18) > 256
     assert lib.ppo_loss_gauss_workspace_bytes(1 << 21, 6) > 256

@@ -102,12 +102,17 @@ __global__ void __launch_bounds__(kBlock) normalize_kernel(const float* adv, flo
 
 }  // namespace
 
+int launch_finalize_stats(const double* partials, long count, double eps, WsHeader* hdr,
+                          float* stats_out, hipStream_t stream) {
+  hipLaunchKernelGGL(finalize_stats_kernel, dim3(1), dim3(kBlock), 0, stream, partials, count, eps,
+                     hdr, stats_out);
+  return last_launch_status();
+}
+
 int launch_normalize(const double* partials, long count, double eps, const float* adv, float* out,
                      long n, WsHeader* hdr, float* stats_out, hipStream_t stream) {
   if (n <= 0) return PPO_OK;
-  hipLaunchKernelGGL(finalize_stats_kernel, dim3(1), dim3(kBlock), 0, stream, partials, count, eps,
-                     hdr, stats_out);
-  int st = last_launch_status();
+  int st = launch_finalize_stats(partials, count, eps, hdr, stats_out, stream);
   if (st) return st;
   const bool vec = aligned(adv, 16) && aligned(out, 16);
   const long work = vec ? (n + 3) / 4 : n;

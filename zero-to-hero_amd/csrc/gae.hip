@@ -11,7 +11,7 @@
 // order and no fused multiply-adds, so an element whose carry is exact is
 // bit-identical to the reference after the final fp32 cast.
 //
-// Parallel structure (three kernels, all HBM-streaming):
+// Parallel structure (HBM-streaming kernels):
 //   The recurrence is affine in the carried advantage: adv_t = delta_t +
 //   c_t*adv_{t+1} with c_t = gamma*lambda*mask_t.  A run of steps therefore
 //   maps the advantage entering it from the right, x, to a + P*x.
@@ -20,17 +20,23 @@
 //   * A "tile" is Sw consecutive segments x Qw adjacent env-groups owned by
 //     one 256-thread workgroup; segments are composed with a Kogge-Stone scan
 //     in LDS.
-//   1. gae_tile_kernel<.., kFinal=false>: per tile and env, the composite
-//      (a, P) of all its steps -> workspace `summary` [Tt][N].
+//   1. gae_tile_kernel<kSummary>: per tile and env, the composite (a, P) of
+//      all its steps -> workspace `summary` [Tt][N].
 //   2. gae_carry_kernel: per env, a reverse scan over the tiles' (a, P) ->
 //      `carry` [Tt][N], the advantage entering each tile from the right
 //      (two levels, via per-chunk composites, for long horizons).
-//   3. gae_tile_kernel<.., kFinal=true>: re-reads the tile, rebuilds the
+//   3. gae_tile_kernel<kFinal>: re-reads the tile, rebuilds the
 //      segment composites, applies the tile carry, and runs the exact serial
-//      recurrence per segment, writing adv and ret (and, for the fused
-//      normaliser, per-block (n, sum, sum of squares) of the advantages,
-//      combined by a one-block finaliser before the elementwise pass).
-// When the whole horizon fits in one tile (Tt == 1) steps 1-2 are skipped.
+//      recurrence per segment, writing adv and ret.
+// Fused normalisation (ppo_gae_norm_f32): pass 1 also stores, per tile and
+// env, five sums that make the tile's sum of advantages and of their squares
+// closed-form functions of its carry; the carry scan evaluates them as it
+// produces the carries, a one-block finaliser turns the totals into mean and
+// std, and pass 3 writes the normalised advantages beside adv and ret.  The
+// statistics are those of the fp64 advantages before their fp32 rounding
+// (relative difference ~1e-8 from the rounded values' statistics).
+// When the whole horizon fits in one tile (Tt == 1) steps 1-2 are skipped and
+// the final pass emits per-block sums for a separate normalise pass instead.
 #include <algorithm>
 
 #include "common.hpp"
@@ -51,12 +57,24 @@ struct GaeArgs {
   double2* summary;    // [Tt][N] (a, P)
   double2* chunk_sum;  // [nchunks][N] (a, P) of each carry-scan chunk
   const double* carry; // [Tt][N] or null (all-zero carries)
-  double* partial;     // [blocks][4] (n, sum, sum sq), fused-normalise only
+  double* partial;     // [.][4] (n, sum, sum sq) partials of the advantages
+  float* tstat;        // [5][Tt][N] per tile and env: sums over the tile's steps of
+                       // a, P, a*a, a*P, P*P (a, P: composite from the step to the tile end)
+  float* adv_n;        // normalised advantages (fused-normalise, multi-tile path)
   WsHeader* hdr;
   float* stats_out;
   double eps;
-  long Q, Tq, Tt;
+  long Q, Tq, Tt, span;
   int Qw, Sw;
+};
+
+// What a gae_tile_kernel launch computes.
+enum GaeMode {
+  kSummary = 0,       // pass 1: tile composites
+  kSummaryStats = 1,  // pass 1: tile composites + tile sums for the normaliser
+  kFinal = 2,         // pass 2: adv, ret
+  kFinalPartials = 3, // pass 2: adv, ret + per-block (n, sum, sum sq) (single-tile horizon)
+  kFinalNorm = 4,     // pass 2: adv, ret, adv_n with mean/denom from the workspace header
 };
 
 struct GaePlan {
@@ -88,10 +106,18 @@ struct CarryPlan {
   long groups, nchunks;
 };
 
+// Ew envs per block (16-64, for 128-512-byte coalesced summary rows), halved
+// down to 16 until the envs alone give >= 256 blocks; Rw rows, no more than
+// the horizon needs (G tiles per row), no more than fit 1024 threads, and at
+// least one full wave per block.
 CarryPlan make_carry_plan(long Tt, long N) {
   CarryPlan c;
   c.Ew = (int)std::min<long>(64, (long)pow2_ceil((unsigned)std::min<long>(N, 64)));
-  c.Rw = kCarryBlock / c.Ew;
+  while (c.Ew > 16 && (N + c.Ew - 1) / c.Ew < 256) c.Ew >>= 1;
+  const long rows_needed = (Tt + kCarryG - 1) / kCarryG;
+  c.Rw = (int)std::min<long>(kCarryBlock / c.Ew,
+                             (long)pow2_ceil((unsigned)std::min<long>(rows_needed, 1024)));
+  c.Rw = std::max(c.Rw, kWave / c.Ew);  // whole waves: block reductions assume them
   c.groups = (N + c.Ew - 1) / c.Ew;
   const long chunk_tiles = (long)c.Rw * kCarryG;
   c.nchunks = (Tt + chunk_tiles - 1) / chunk_tiles;
@@ -99,7 +125,7 @@ CarryPlan make_carry_plan(long Tt, long N) {
 }
 
 struct GaeLayout {
-  size_t summary, carry, chunk_sum, partial, total;
+  size_t summary, carry, chunk_sum, tstat, partial, total;
 };
 
 GaeLayout make_layout(const GaePlan& p, long N) {
@@ -111,8 +137,14 @@ GaeLayout make_layout(const GaePlan& p, long N) {
   off += align_up((size_t)p.Tt * N * sizeof(double), 256);
   l.chunk_sum = off;
   off += align_up((size_t)make_carry_plan(p.Tt, N).nchunks * N * sizeof(double2), 256);
+  l.tstat = off;
+  off += align_up((size_t)5 * p.Tt * N * sizeof(float), 256);
   l.partial = off;
-  off += align_up((size_t)p.blocks() * 4 * sizeof(double), 256);
+  {
+    const CarryPlan cp = make_carry_plan(p.Tt, N);
+    const long parts = std::max<long>(p.blocks(), cp.groups * cp.nchunks);
+    off += align_up((size_t)parts * 4 * sizeof(double), 256);
+  }
   l.total = off;
   return l;
 }
@@ -175,8 +207,10 @@ __device__ __forceinline__ unsigned load_done(const uint8_t* p) {
   }
 }
 
-template <int VW, int L, bool kFinal, bool kStats>
+template <int VW, int L, int kMode>
 __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
+  constexpr bool kIsFinal = kMode >= kFinal;
+  constexpr bool kTileStats = kMode == kSummaryStats;
   static_assert(L * VW <= 32, "done bits must fit one word");
   __shared__ double s_a[kBlock * VW];
   __shared__ double s_p[kBlock * VW];
@@ -217,12 +251,19 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
       load_f<VW>(a.lastv + env0, nv);
   }
 
-  // Composite (a, P) of this segment with a zero carry.
+  // Composite (a, P) of this segment with a zero carry.  With kTileStats also
+  // the sums over the segment's steps of a_t, P_t, a_t^2, a_t P_t, P_t^2, where
+  // (a_t, P_t) is the composite from step t to the segment end, so that the
+  // advantage is adv_t = a_t + P_t * carry.
   double ia[VW], ip[VW];
+  float sa[VW], sP[VW], saa[VW], saP[VW], sPP[VW];  // fp32: at most 16 terms each
   {
     double nvd[VW];
 #pragma unroll
-    for (int k = 0; k < VW; ++k) { ia[k] = 0.0; ip[k] = 1.0; nvd[k] = nv[k]; }
+    for (int k = 0; k < VW; ++k) {
+      ia[k] = 0.0; ip[k] = 1.0; nvd[k] = nv[k];
+      sa[k] = sP[k] = saa[k] = saP[k] = sPP[k] = 0.0f;
+    }
 #pragma unroll
     for (int i = L - 1; i >= 0; --i) {
       if (i < nvalid) {
@@ -235,6 +276,14 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
           ia[k] = add(delta, mul(c, ia[k]));
           ip[k] = mul(ip[k], c);
           nvd[k] = vd;
+          if constexpr (kTileStats) {
+            const float fa = (float)ia[k], fp = (float)ip[k];
+            sa[k] += fa;
+            sP[k] += fp;
+            saa[k] += fa * fa;
+            saP[k] += fa * fp;
+            sPP[k] += fp * fp;
+          }
         }
       }
     }
@@ -268,11 +317,51 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
   }
   __syncthreads();
 
-  if constexpr (!kFinal) {
+  if constexpr (!kIsFinal) {
     if (s == 0 && col_ok) {
 #pragma unroll
       for (int k = 0; k < VW; ++k)
         a.summary[tile_t * a.N + env0 + k] = make_double2(ia[k], ip[k]);
+    }
+    if constexpr (kTileStats) {
+      // Re-base the segment sums on the tile end: with (An, Pn) the composite
+      // of the later segments of the tile, a' = a + An P and P' = Pn P.
+      float q5[5][VW];
+#pragma unroll
+      for (int k = 0; k < VW; ++k) {
+        float An = 0.0f, Pn = 1.0f;
+        if (s + 1 < a.Sw) {
+          An = (float)s_a[k * kBlock + tid + a.Qw];
+          Pn = (float)s_p[k * kBlock + tid + a.Qw];
+        }
+        q5[0][k] = sa[k] + An * sP[k];
+        q5[1][k] = Pn * sP[k];
+        q5[2][k] = saa[k] + 2.0f * An * saP[k] + An * An * sPP[k];
+        q5[3][k] = Pn * (saP[k] + An * sPP[k]);
+        q5[4][k] = Pn * Pn * sPP[k];
+      }
+      // tree-sum of all five sums over the Sw segments of the tile at once
+      __shared__ float s_q[kTileStats ? 5 * VW * kBlock : 1];
+      const long plane = a.Tt * a.N;
+#pragma unroll
+      for (int j = 0; j < 5; ++j)
+#pragma unroll
+        for (int k = 0; k < VW; ++k) s_q[(j * VW + k) * kBlock + tid] = q5[j][k];
+      for (int h = a.Sw >> 1; h > 0; h >>= 1) {
+        __syncthreads();
+        if (s < h) {
+#pragma unroll
+          for (int j = 0; j < 5 * VW; ++j) s_q[j * kBlock + tid] += s_q[j * kBlock + tid + h * a.Qw];
+        }
+      }
+      __syncthreads();
+      if (s == 0 && col_ok) {
+#pragma unroll
+        for (int j = 0; j < 5; ++j)
+#pragma unroll
+          for (int k = 0; k < VW; ++k)
+            a.tstat[j * plane + tile_t * a.N + env0 + k] = s_q[(j * VW + k) * kBlock + tid];
+      }
     }
     return;
   } else {
@@ -307,6 +396,11 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
         }
       }
     }
+    float mean = 0.0f, denom = 1.0f;
+    if constexpr (kMode == kFinalNorm) {
+      mean = a.hdr->stats[0];
+      denom = a.hdr->stats[2];
+    }
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       if (i < nvalid) {
@@ -318,10 +412,16 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
           for (int k = 0; k < VW; ++k) rt[k] = r[i][k] + v[i][k];
           store_f<VW>(a.ret + off, rt);
         }
+        if constexpr (kMode == kFinalNorm) {
+          float an[VW];
+#pragma unroll
+          for (int k = 0; k < VW; ++k) an[k] = (r[i][k] - mean) / denom;
+          store_f<VW>(a.adv_n + off, an);
+        }
       }
     }
 
-    if constexpr (kStats) {
+    if constexpr (kMode == kFinalPartials) {
       double acc[3] = {(double)(nvalid * VW), 0.0, 0.0};
 #pragma unroll
       for (int i = 0; i < L; ++i)
@@ -378,12 +478,21 @@ __device__ __forceinline__ void carry_row_scan(double* s_a, double* s_p, int tid
   __syncthreads();
 }
 
+// With tstat (the kCarry launch of the fused-normalise path), each thread also
+// accumulates, for every tile k it writes with carry c_k, the tile's sums of
+// the advantages adv_t = a_t + P_t c_k and of their squares,
+//     sum adv   = S_a + c_k S_P
+//     sum adv^2 = S_aa + 2 c_k S_aP + c_k^2 S_PP,
+// and the block stores (n, sum, sum of squares) in stat_part.
 template <bool kCompose>
 __global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* __restrict__ summary,
                                                                  double* __restrict__ carry,
                                                                  double2* __restrict__ chunk_sum,
                                                                  long Tt, long N, int Ew, int Rw,
-                                                                 long nchunks) {
+                                                                 long nchunks,
+                                                                 const float* __restrict__ tstat,
+                                                                 double* __restrict__ stat_part,
+                                                                 long T, long span) {
   __shared__ double s_a[kCarryBlock];
   __shared__ double s_p[kCarryBlock];
   const int tid = threadIdx.x;
@@ -439,51 +548,87 @@ __global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* _
     if (g == 0 && ok) chunk_sum[c * N + env] = make_double2(s_a[e], s_p[e]);
   } else {
     double cc = (g + 1 < Rw) ? s_a[tid + Ew] + s_p[tid + Ew] * C : C;
+    double st[3] = {0.0, 0.0, 0.0};
+    const long plane = Tt * N;
 #pragma unroll
     for (int j = kCarryG - 1; j >= 0; --j) {
       const long k = k0 + j;
       if (ok && k < hi) {
         carry[k * N + env] = cc;
+        if (tstat) {
+          const long i = k * N + env;
+          const long len = T - k * span < span ? T - k * span : span;
+          st[0] += (double)len;
+          st[1] += (double)tstat[i] + cc * (double)tstat[plane + i];
+          st[2] += (double)tstat[2 * plane + i] + 2.0 * cc * (double)tstat[3 * plane + i] +
+                   cc * cc * (double)tstat[4 * plane + i];
+        }
         cc = ta[j] + tp[j] * cc;
+      }
+    }
+    if (tstat) {
+      block_sum<3>(st);
+      if (tid == 0) {
+        const long b = c * gridDim.x + blockIdx.x;
+        stat_part[b * 4 + 0] = st[0];
+        stat_part[b * 4 + 1] = st[1];
+        stat_part[b * 4 + 2] = st[2];
+        stat_part[b * 4 + 3] = 0.0;
       }
     }
   }
 }
 
 template <int VW, int L>
-int launch_gae(const GaePlan& p, GaeArgs a, bool stats, hipStream_t stream) {
+int launch_gae(const GaePlan& p, GaeArgs a, bool norm, hipStream_t stream) {
   const long blocks = p.blocks();
   a.Q = p.Q;
   a.Tq = p.Tq;
   a.Tt = p.Tt;
   a.Qw = p.Qw;
   a.Sw = p.Sw;
+  a.span = p.span;
   int st;
+  const dim3 grid((unsigned)blocks), block(kBlock);
   if (p.Tt > 1) {
-    hipLaunchKernelGGL((gae_tile_kernel<VW, L, false, false>), dim3((unsigned)blocks),
-                       dim3(kBlock), 0, stream, a);
+    if (norm)
+      hipLaunchKernelGGL((gae_tile_kernel<VW, L, kSummaryStats>), grid, block, 0, stream, a);
+    else
+      hipLaunchKernelGGL((gae_tile_kernel<VW, L, kSummary>), grid, block, 0, stream, a);
     if ((st = last_launch_status())) return st;
     const CarryPlan cp = make_carry_plan(p.Tt, a.N);
+    const dim3 cgrid((unsigned)cp.groups, (unsigned)cp.nchunks);
     if (cp.nchunks > 1) {
-      hipLaunchKernelGGL(gae_carry_kernel<true>, dim3((unsigned)cp.groups, (unsigned)cp.nchunks),
-                         dim3(kCarryBlock), 0, stream, a.summary, const_cast<double*>(a.carry),
-                         a.chunk_sum, p.Tt, a.N, cp.Ew, cp.Rw, cp.nchunks);
+      hipLaunchKernelGGL(gae_carry_kernel<true>, cgrid, dim3(cp.Ew * cp.Rw), 0, stream, a.summary,
+                         const_cast<double*>(a.carry), a.chunk_sum, p.Tt, a.N, cp.Ew, cp.Rw,
+                         cp.nchunks, nullptr, nullptr, a.T, p.span);
       if ((st = last_launch_status())) return st;
     }
-    hipLaunchKernelGGL(gae_carry_kernel<false>, dim3((unsigned)cp.groups, (unsigned)cp.nchunks),
-                       dim3(kCarryBlock), 0, stream, a.summary, const_cast<double*>(a.carry),
-                       a.chunk_sum, p.Tt, a.N, cp.Ew, cp.Rw, cp.nchunks);
+    hipLaunchKernelGGL(gae_carry_kernel<false>, cgrid, dim3(cp.Ew * cp.Rw), 0, stream, a.summary,
+                       const_cast<double*>(a.carry), a.chunk_sum, p.Tt, a.N, cp.Ew, cp.Rw,
+                       cp.nchunks, norm ? a.tstat : nullptr, a.partial, a.T, p.span);
     if ((st = last_launch_status())) return st;
-  } else {
-    a.carry = nullptr;
+    if (!norm) {
+      hipLaunchKernelGGL((gae_tile_kernel<VW, L, kFinal>), grid, block, 0, stream, a);
+      return last_launch_status();
+    }
+    // mean/std from the carry-scan partials, then one pass writes adv, ret, adv_n
+    if ((st = launch_finalize_stats(a.partial, cp.groups * cp.nchunks, a.eps, a.hdr, a.stats_out,
+                                    stream)))
+      return st;
+    hipLaunchKernelGGL((gae_tile_kernel<VW, L, kFinalNorm>), grid, block, 0, stream, a);
+    return last_launch_status();
   }
-  if (stats)
-    hipLaunchKernelGGL((gae_tile_kernel<VW, L, true, true>), dim3((unsigned)blocks), dim3(kBlock),
-                       0, stream, a);
-  else
-    hipLaunchKernelGGL((gae_tile_kernel<VW, L, true, false>), dim3((unsigned)blocks),
-                       dim3(kBlock), 0, stream, a);
-  return last_launch_status();
+  a.carry = nullptr;
+  if (!norm) {
+    hipLaunchKernelGGL((gae_tile_kernel<VW, L, kFinal>), grid, block, 0, stream, a);
+    return last_launch_status();
+  }
+  // single-tile horizon: partials from the final pass, then the elementwise normaliser
+  hipLaunchKernelGGL((gae_tile_kernel<VW, L, kFinalPartials>), grid, block, 0, stream, a);
+  if ((st = last_launch_status())) return st;
+  return launch_normalize(a.partial, blocks, a.eps, a.adv, a.adv_n, a.T * a.N, a.hdr, a.stats_out,
+                          stream);
 }
 
 int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
@@ -525,11 +670,10 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
   a.hdr = reinterpret_cast<WsHeader*>(ws);
   a.stats_out = stats_out;
   a.eps = eps;
+  a.adv_n = adv_norm_out;
+  a.tstat = reinterpret_cast<float*>(ws + l.tstat);
 
-  int st = vec ? launch_gae<4, 4>(p, a, norm, stream) : launch_gae<1, 16>(p, a, norm, stream);
-  if (st || !norm) return st;
-  return launch_normalize(a.partial, p.blocks(), eps, adv_out, adv_norm_out, T * N, a.hdr,
-                          stats_out, stream);
+  return vec ? launch_gae<4, 4>(p, a, norm, stream) : launch_gae<1, 16>(p, a, norm, stream);
 }
 
 }  // namespace

@@ -41,6 +41,13 @@ __device__ inline NormParams norm_params(const double* partials, long count, dou
   return r;
 }
 
+// Enqueue the one-block kernel that turns `count` (n, sum, sum of squares)
+// partials into the normaliser parameters in hdr->stats ({mean used, std,
+// denominator}) and {mean, std} in stats_out (if not null).  Defined in
+// adv_norm.hip.
+int launch_finalize_stats(const double* partials, long count, double eps, WsHeader* hdr,
+                          float* stats_out, hipStream_t stream);
+
 // Enqueue the normaliser: a one-block kernel derives mean/denom from the
 // `count` (n, sum, sum of squares) partials left in the workspace by the
 // previous kernel on the same stream (and stores {mean, std} in stats_out if
