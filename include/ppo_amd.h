@@ -68,6 +68,9 @@ size_t ppo_gae_workspace_bytes(int64_t T, int64_t N);
  *     ret_out[t,n] = adv_out[t,n] + values[t,n]    (fp32 add, as ppo.py:124)
  * last_value may be NULL, meaning zeros: that is the reference's own
  * end-of-episode rule (ppo.py:175-176, `next_value = 0.0`).
+ * values may be NULL, meaning zeros: with lam = 1 the advantages are then the
+ * discounted returns value = reward + gamma*value of REINFORCE
+ * (rl/deep/agents/reinforce.py:57-63), per env, reset at dones.
  * A non-zero byte in dones counts as done.  ret_out may be NULL.
  */
 int ppo_gae_f32(const float* rewards, const float* values, const uint8_t* dones,
@@ -175,6 +178,51 @@ int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t B,
                        float* dmu, float* dlog_std, float* dvalues,
                        float* scalars_out, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Update loop around the fused loss.                                       */
+/* ------------------------------------------------------------------------ */
+
+#define PPO_GATHER_MAX_ARRAYS 8
+
+/*
+ * Replaces the minibatch gather of PPOAgent._update (rl/deep/agents/ppo.py:
+ * 132-139: observations[batch_indices], actions[batch_indices], ...): for each
+ * of `narrays` (<= PPO_GATHER_MAX_ARRAYS) row-major arrays of n_src rows,
+ * dst[k][b] = src[k][index[b]] for b < B, rows of row_bytes[k] bytes (a
+ * multiple of 4), all in one launch.  An index outside [0, n_src) yields a
+ * zero row (it is never dereferenced).  index is int64 (torch.randperm's
+ * dtype).
+ */
+int ppo_gather_rows(const int64_t* index, int64_t B, int64_t n_src, int32_t narrays,
+                    const void* const* src, const int32_t* row_bytes, void* const* dst,
+                    void* stream);
+
+#define PPO_ADAM_MAX_TENSORS 32
+
+typedef struct ppo_adam_params {
+  double lr, beta1, beta2, eps;  /* torch.optim.Adam(lr, betas=(beta1, beta2), eps) */
+  double max_grad_norm;          /* clip_grad_norm_ max_norm; <= 0: no clipping    */
+  int64_t step;                  /* the step number after this update (>= 1)      */
+} ppo_adam_params;
+
+size_t ppo_adam_clip_workspace_bytes(int32_t ntensors, const int64_t* numel);
+
+/*
+ * Replaces nn.utils.clip_grad_norm_(params, max_grad_norm) + Adam.step()
+ * (rl/deep/agents/ppo.py:170-171; TrainingConfig.lr, PPOConfig.gradient_clip)
+ * for ntensors <= PPO_ADAM_MAX_TENSORS fp32 tensors: total norm of all
+ * gradients (the norm of the per-tensor norms), grads *= min(max_norm /
+ * (norm + 1e-6), 1) in place, then Adam (no weight decay, no amsgrad) on
+ * params, exp_avg and exp_avg_sq in place, following torch's multi-tensor Adam
+ * operation by operation in fp32.  grad_norm_out (may be NULL) receives the
+ * total norm (clip_grad_norm_'s return value).  The pointer arrays are host
+ * arrays of device pointers.
+ */
+int ppo_adam_clip_f32(int32_t ntensors, float* const* params, float* const* grads,
+                      float* const* exp_avg, float* const* exp_avg_sq, const int64_t* numel,
+                      const ppo_adam_params* hp, float* grad_norm_out, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

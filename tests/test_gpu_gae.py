@@ -165,3 +165,62 @@ def test_gae_repeatable(dev):
     a1, _, n1 = ppo_amd.gae_normalize(*args)
     a2, _, n2 = ppo_amd.gae_normalize(*args)
     assert torch.equal(a1, a2) and torch.equal(n1, n2)
+
+
+# ---------------------------------------------------------------------------
+# REINFORCE returns (rl/deep/agents/reinforce.py:57-66) through the GAE kernel
+# ---------------------------------------------------------------------------
+def _reinforce_python(rewards, gamma):
+    """reinforce.py:57-63 restated: value = reward + gamma * value."""
+    returns = []
+    value = 0.0
+    for reward in reversed(rewards):
+        value = reward + gamma * value
+        returns.append(value)
+    returns.reverse()
+    return returns
+
+
+@pytest.mark.parametrize("T", [1, 2, 37, 500, 5000])
+def test_discounted_returns_bit_identical_to_reference_loop(dev, T):
+    g = torch.Generator().manual_seed(T)
+    r = torch.randn(T, generator=g)
+    got = ppo_amd.discounted_returns(r.to(dev), gamma=0.97).cpu().numpy()
+    expect = np.array(_reinforce_python([float(x) for x in r], 0.97), dtype=np.float32)
+    np.testing.assert_array_equal(got, expect)
+    centered = ppo_amd.discounted_returns(r.to(dev), gamma=0.97, center=True).cpu()
+    ref_t = torch.as_tensor(expect)
+    torch.testing.assert_close(centered, ref_t - ref_t.mean(), rtol=1e-6, atol=1e-6)
+
+
+def test_discounted_returns_vectorised_with_dones(dev):
+    T, N = 3000, 20
+    g = torch.Generator().manual_seed(2)
+    r = torch.randn(T, N, generator=g)
+    d = (torch.rand(T, N, generator=g) < 0.01).to(torch.uint8)
+    boot = torch.randn(N, generator=g)
+    got = ppo_amd.discounted_returns(r.to(dev), d.to(dev), 0.99, boot.to(dev)).cpu().numpy()
+    # oracle: GAE with lambda = 1 and zero values
+    expect, _ = ref.gae_c(r.numpy(), np.zeros((T, N), np.float32), d.numpy(), boot.numpy(),
+                          0.99, 1.0)
+    assert_gae_close(got, expect)
+    # per env it is the reference loop restarted after each done
+    for n in range(3):
+        col, start = [], 0
+        ends = list(np.nonzero(d[:, n].numpy())[0]) + [T - 1]
+        for e in ends:
+            seg = [float(x) for x in r[start:e + 1, n]]
+            if e == T - 1 and not d[T - 1, n]:
+                vals = []
+                v = float(boot[n])
+                for x in reversed(seg):
+                    v = x + 0.99 * v
+                    vals.append(v)
+                col += list(reversed(vals))
+            else:
+                col += _reinforce_python(seg, 0.99)
+            start = e + 1
+            if start >= T:
+                break
+        np.testing.assert_allclose(got[:len(col), n], np.array(col, np.float32), rtol=1e-6,
+                                   atol=1e-6)

@@ -50,6 +50,7 @@ struct GaeArgs {
   const float* v;
   const uint8_t* d;
   const float* lastv;  // may be null (zeros)
+  // v may be null (all values zero: discounted returns, the REINFORCE case)
   long T, N;
   double gamma, gl;    // gamma and gamma*lambda (the product rounded once, as in Python)
   float* adv;
@@ -235,7 +236,12 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
     if (i < nvalid) {
       const long off = (t0 + i) * a.N + env0;
       load_f<VW>(a.r + off, r[i]);
-      load_f<VW>(a.v + off, v[i]);
+      if (a.v) {
+        load_f<VW>(a.v + off, v[i]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) v[i][k] = 0.0f;
+      }
       dbits |= load_done<VW>(a.d + off) << (i * VW);
     } else {
 #pragma unroll
@@ -245,10 +251,11 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
 #pragma unroll
   for (int k = 0; k < VW; ++k) nv[k] = 0.0f;
   if (nvalid > 0) {
-    if (t0 + L < a.T)
-      load_f<VW>(a.v + (t0 + L) * a.N + env0, nv);
-    else if (a.lastv)
+    if (t0 + L < a.T) {
+      if (a.v) load_f<VW>(a.v + (t0 + L) * a.N + env0, nv);
+    } else if (a.lastv) {
       load_f<VW>(a.lastv + env0, nv);
+    }
   }
 
   // Composite (a, P) of this segment with a zero carry.  With kTileStats also
@@ -637,13 +644,13 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
              void* workspace, size_t workspace_bytes, void* stream_ptr) {
   if (T < 0 || N < 0) return PPO_ERR_INVALID_ARG;
   if (T == 0 || N == 0) return PPO_OK;
-  if (!rewards || !values || !dones || !adv_out) return PPO_ERR_INVALID_ARG;
+  if (!rewards || !dones || !adv_out) return PPO_ERR_INVALID_ARG;
   if (norm && !adv_norm_out) return PPO_ERR_INVALID_ARG;
   if (N > (1L << 31) || T > (1L << 40) || T * N > (1L << 50)) return PPO_ERR_TOO_LARGE;
   if (!workspace || workspace_bytes < ppo_gae_workspace_bytes(T, N)) return PPO_ERR_WORKSPACE;
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
 
-  const bool vec = (N % 4 == 0) && aligned(rewards, 16) && aligned(values, 16) &&
+  const bool vec = (N % 4 == 0) && aligned(rewards, 16) && (!values || aligned(values, 16)) &&
                    aligned(adv_out, 16) && (!ret_out || aligned(ret_out, 16)) &&
                    aligned(dones, 4) && (!last_value || aligned(last_value, 16));
   const GaePlan p = make_plan(T, N, vec ? 4 : 1);

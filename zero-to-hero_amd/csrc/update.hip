@@ -1,0 +1,243 @@
+// Update-loop kernels around the fused loss (rl/deep/agents/ppo.py:129-171):
+//
+//  * ppo_gather_rows — the minibatch gather of ppo.py:132-139
+//    (observations[batch_indices], actions[...], ...): every array's rows at
+//    one index vector, in one launch instead of one torch gather per array.
+//  * ppo_adam_clip_f32 — nn.utils.clip_grad_norm_(params, max_norm) followed
+//    by torch.optim.Adam.step() (ppo.py:170-171), for up to
+//    PPO_ADAM_MAX_TENSORS tensors in two launches: per-block sums of squared
+//    gradients, then a pass in which every block derives the global norm and
+//    the clip coefficient from those sums and updates its slice of
+//    gradients, moments and parameters.  The fp32 arithmetic follows torch's
+//    multi-tensor Adam op by op (lerp for the first moment, mul + addcmul for
+//    the second, sqrt / bias-correction / eps / addcdiv for the update), each
+//    operation rounded separately.
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace ppo {
+namespace {
+
+// ---------------------------------------------------------------------------
+// gather
+// ---------------------------------------------------------------------------
+struct GatherTable {
+  const unsigned* src[PPO_GATHER_MAX_ARRAYS];
+  unsigned* dst[PPO_GATHER_MAX_ARRAYS];
+  int words[PPO_GATHER_MAX_ARRAYS];           // 4-byte words per row
+  int word_start[PPO_GATHER_MAX_ARRAYS + 1];  // prefix of words over arrays
+  int narr;
+};
+
+__global__ void __launch_bounds__(kBlock) gather_rows_kernel(GatherTable t,
+                                                             const int64_t* __restrict__ idx,
+                                                             long B, long nsrc) {
+  const long W = t.word_start[t.narr];
+  const long total = B * W;
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long u = (long)blockIdx.x * blockDim.x + threadIdx.x; u < total; u += stride) {
+    const long b = u / W;
+    const int w = (int)(u - b * W);
+    int k = 0;
+    while (k + 1 < t.narr && w >= t.word_start[k + 1]) ++k;
+    const int ww = w - t.word_start[k];
+    const long i = idx[b];
+    unsigned val = 0u;  // rows for out-of-range indices are zero (no out-of-bounds read)
+    if (i >= 0 && i < nsrc) val = t.src[k][i * t.words[k] + ww];
+    t.dst[k][b * t.words[k] + ww] = val;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// clip_grad_norm_ + Adam
+// ---------------------------------------------------------------------------
+constexpr int kAdamPerThread = 4;
+constexpr long kAdamChunk = (long)kBlock * kAdamPerThread * 4;  // elements per block
+
+struct AdamTable {
+  float* p[PPO_ADAM_MAX_TENSORS];
+  float* g[PPO_ADAM_MAX_TENSORS];
+  float* m[PPO_ADAM_MAX_TENSORS];
+  float* v[PPO_ADAM_MAX_TENSORS];
+  long n[PPO_ADAM_MAX_TENSORS];
+  long block_start[PPO_ADAM_MAX_TENSORS + 1];
+  int nt;
+};
+
+__device__ __forceinline__ int tensor_of_block(const AdamTable& t, long b) {
+  int k = 0;
+  while (k + 1 < t.nt && b >= t.block_start[k + 1]) ++k;
+  return k;
+}
+
+__global__ void __launch_bounds__(kBlock) adam_sumsq_kernel(AdamTable t, double* partial) {
+  const long b = blockIdx.x;
+  const int k = tensor_of_block(t, b);
+  const long lo = (b - t.block_start[k]) * kAdamChunk;
+  const long hi = lo + kAdamChunk < t.n[k] ? lo + kAdamChunk : t.n[k];
+  double acc[1] = {0.0};
+  for (long i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+    const double x = (double)t.g[k][i];
+    acc[0] += x * x;
+  }
+  block_sum<1>(acc);
+  if (threadIdx.x == 0) partial[b] = acc[0];
+}
+
+struct AdamScalars {
+  float max_norm;      // clip threshold
+  float beta1_w;       // 1 - beta1, the lerp weight
+  float beta2;
+  float one_m_beta2;   // 1 - beta2
+  float bc2_sqrt;      // sqrt(1 - beta2^step)
+  float eps;
+  float neg_step;      // -(lr / (1 - beta1^step))
+  int clip;            // 0: no clipping (max_norm <= 0)
+};
+
+__global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
+                                                             const double* __restrict__ partial,
+                                                             AdamScalars s, float* norm_out) {
+  __shared__ float s_coef;
+  // Global norm: per-tensor norms rounded to fp32, then the norm of those (the
+  // two-level form of torch's _get_total_norm); every block derives the same
+  // value in the same order.
+  if (threadIdx.x == 0) {
+    float total_sq = 0.0f;
+    for (int k = 0; k < t.nt; ++k) {
+      double sk = 0.0;
+      for (long b = t.block_start[k]; b < t.block_start[k + 1]; ++b) sk += partial[b];
+      const float nk = (float)sqrt(sk);
+      total_sq = __fadd_rn(total_sq, __fmul_rn(nk, nk));
+    }
+    const float total = __fsqrt_rn(total_sq);
+    float coef = 1.0f;
+    if (s.clip) {
+      const float c = __fdiv_rn(s.max_norm, __fadd_rn(total, 1e-6f));
+      coef = c < 1.0f ? c : 1.0f;
+    }
+    s_coef = coef;
+    if (blockIdx.x == 0 && norm_out) *norm_out = total;
+  }
+  __syncthreads();
+  const float coef = s_coef;
+  const long b = blockIdx.x;
+  const int k = tensor_of_block(t, b);
+  const long lo = (b - t.block_start[k]) * kAdamChunk;
+  const long hi = lo + kAdamChunk < t.n[k] ? lo + kAdamChunk : t.n[k];
+  float* __restrict__ p = t.p[k];
+  float* __restrict__ g = t.g[k];
+  float* __restrict__ m = t.m[k];
+  float* __restrict__ v = t.v[k];
+  for (long i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+    const float gi = s.clip ? __fmul_rn(g[i], coef) : g[i];
+    if (s.clip) g[i] = gi;
+    // exp_avg.lerp_(grad, 1 - beta1), weight < 0.5: m + w * (g - m)
+    const float mi = __fadd_rn(m[i], __fmul_rn(s.beta1_w, __fsub_rn(gi, m[i])));
+    // exp_avg_sq.mul_(beta2).addcmul_(grad, grad, value=1 - beta2)
+    const float vi = __fadd_rn(__fmul_rn(v[i], s.beta2), __fmul_rn(__fmul_rn(s.one_m_beta2, gi), gi));
+    // denom = sqrt(v) / sqrt(1 - beta2^t) + eps;  p += (-lr / (1 - beta1^t)) * (m / denom)
+    const float denom = __fadd_rn(__fdiv_rn(__fsqrt_rn(vi), s.bc2_sqrt), s.eps);
+    p[i] = __fadd_rn(p[i], __fmul_rn(s.neg_step, __fdiv_rn(mi, denom)));
+    m[i] = mi;
+    v[i] = vi;
+  }
+}
+
+long adam_blocks(int nt, const int64_t* numel, long* starts) {
+  long b = 0;
+  for (int k = 0; k < nt; ++k) {
+    starts[k] = b;
+    b += (numel[k] + kAdamChunk - 1) / kAdamChunk;
+  }
+  starts[nt] = b;
+  return b;
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" int ppo_gather_rows(const int64_t* index, int64_t B, int64_t n_src, int32_t narrays,
+                               const void* const* src, const int32_t* row_bytes,
+                               void* const* dst, void* stream_ptr) {
+  using namespace ppo;
+  if (B < 0 || n_src < 0 || narrays < 1 || narrays > PPO_GATHER_MAX_ARRAYS) return PPO_ERR_INVALID_ARG;
+  if (B == 0) return PPO_OK;
+  if (!index || !src || !row_bytes || !dst) return PPO_ERR_INVALID_ARG;
+  GatherTable t = {};
+  t.narr = narrays;
+  int w = 0;
+  for (int k = 0; k < narrays; ++k) {
+    if (!src[k] || !dst[k] || row_bytes[k] <= 0 || row_bytes[k] % 4) return PPO_ERR_INVALID_ARG;
+    t.src[k] = static_cast<const unsigned*>(src[k]);
+    t.dst[k] = static_cast<unsigned*>(dst[k]);
+    t.words[k] = row_bytes[k] / 4;
+    t.word_start[k] = w;
+    w += t.words[k];
+  }
+  t.word_start[narrays] = w;
+  const long total = (long)B * w;
+  long blocks = std::min((total + kBlock - 1) / kBlock, 8192L);
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
+                     reinterpret_cast<hipStream_t>(stream_ptr), t, index, (long)B, (long)n_src);
+  return last_launch_status();
+}
+
+extern "C" size_t ppo_adam_clip_workspace_bytes(int32_t ntensors, const int64_t* numel) {
+  using namespace ppo;
+  if (ntensors < 1 || ntensors > PPO_ADAM_MAX_TENSORS || !numel) return kHeaderBytes;
+  long starts[PPO_ADAM_MAX_TENSORS + 1];
+  const long blocks = adam_blocks(ntensors, numel, starts);
+  return kHeaderBytes + align_up((size_t)std::max(blocks, 1L) * sizeof(double), 256);
+}
+
+extern "C" int ppo_adam_clip_f32(int32_t ntensors, float* const* params, float* const* grads,
+                                 float* const* exp_avg, float* const* exp_avg_sq,
+                                 const int64_t* numel, const ppo_adam_params* hp,
+                                 float* grad_norm_out, void* workspace, size_t workspace_bytes,
+                                 void* stream_ptr) {
+  using namespace ppo;
+  if (ntensors < 1 || ntensors > PPO_ADAM_MAX_TENSORS) return PPO_ERR_INVALID_ARG;
+  if (!params || !grads || !exp_avg || !exp_avg_sq || !numel || !hp) return PPO_ERR_INVALID_ARG;
+  if (hp->step < 1 || !(hp->lr >= 0.0) || !(hp->eps >= 0.0)) return PPO_ERR_INVALID_ARG;
+  if (!workspace || workspace_bytes < ppo_adam_clip_workspace_bytes(ntensors, numel))
+    return PPO_ERR_WORKSPACE;
+  AdamTable t = {};
+  t.nt = ntensors;
+  for (int k = 0; k < ntensors; ++k) {
+    if (numel[k] < 0) return PPO_ERR_INVALID_ARG;
+    if (numel[k] > 0 && (!params[k] || !grads[k] || !exp_avg[k] || !exp_avg_sq[k]))
+      return PPO_ERR_INVALID_ARG;
+    t.p[k] = params[k];
+    t.g[k] = grads[k];
+    t.m[k] = exp_avg[k];
+    t.v[k] = exp_avg_sq[k];
+    t.n[k] = numel[k];
+  }
+  const long blocks = adam_blocks(ntensors, numel, t.block_start);
+  if (blocks == 0) return PPO_OK;
+  if (blocks > 0x7fffffffL) return PPO_ERR_TOO_LARGE;
+  // Host-side scalars exactly as torch forms them: Python doubles, rounded to
+  // fp32 where the tensor op consumes them.
+  const double bc1 = 1.0 - pow(hp->beta1, (double)hp->step);
+  const double bc2 = 1.0 - pow(hp->beta2, (double)hp->step);
+  AdamScalars s;
+  s.max_norm = (float)hp->max_grad_norm;
+  s.clip = hp->max_grad_norm > 0.0 ? 1 : 0;
+  s.beta1_w = (float)(1.0 - hp->beta1);
+  s.beta2 = (float)hp->beta2;
+  s.one_m_beta2 = (float)(1.0 - hp->beta2);
+  s.bc2_sqrt = (float)sqrt(bc2);
+  s.eps = (float)hp->eps;
+  s.neg_step = (float)((hp->lr / bc1) * -1.0);
+  double* partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  hipLaunchKernelGGL(adam_sumsq_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, stream, t,
+                     partial);
+  int st = last_launch_status();
+  if (st) return st;
+  hipLaunchKernelGGL(adam_update_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, stream, t,
+                     partial, s, grad_norm_out);
+  return last_launch_status();
+}

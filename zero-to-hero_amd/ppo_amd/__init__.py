@@ -9,6 +9,7 @@ include/ppo_amd.h) behind the reference's own PPO surface:
             RolloutStep, PendingStep, cartpole_sizes — rl/deep/agents/ppo.py
             and common.py, same names and signatures
   rollout   RolloutBuffer ([T,N] env-contiguous, on device) and VecPPO
+  optim     ClippedAdam (clip_grad_norm_ + Adam, two launches)
 """
 
 from . import _lib
@@ -24,7 +25,9 @@ from .agent import (
 )
 from .ops import (
     LossStats,
+    discounted_returns,
     gae,
+    gather_rows,
     gae_normalize,
     normalize_advantages,
     ppo_loss_discrete,
@@ -32,6 +35,7 @@ from .ops import (
     ppo_loss_gaussian,
     ppo_loss_gaussian_fused,
 )
+from .optim import ClippedAdam
 from .rollout import RolloutBuffer, VecPPO
 
 LIB_PATH = _lib.LIB_PATH
@@ -43,6 +47,7 @@ def load_library():
 
 
 __all__ = [
+    "ClippedAdam",
     "LIB_PATH",
     "LossStats",
     "MLP",
@@ -55,8 +60,10 @@ __all__ = [
     "Transition",
     "VecPPO",
     "cartpole_sizes",
+    "discounted_returns",
     "gae",
     "gae_normalize",
+    "gather_rows",
     "load_library",
     "normalize_advantages",
     "ppo_loss_discrete",

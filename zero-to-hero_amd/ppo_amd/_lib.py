@@ -29,6 +29,22 @@ class LossParams(ctypes.Structure):
     ]
 
 
+class AdamParams(ctypes.Structure):
+    """struct ppo_adam_params (include/ppo_amd.h)."""
+
+    _fields_ = [
+        ("lr", ctypes.c_double),
+        ("beta1", ctypes.c_double),
+        ("beta2", ctypes.c_double),
+        ("eps", ctypes.c_double),
+        ("max_grad_norm", ctypes.c_double),
+        ("step", ctypes.c_int64),
+    ]
+
+
+GATHER_MAX_ARRAYS = 8
+ADAM_MAX_TENSORS = 32
+
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -62,6 +78,18 @@ SIGNATURES = {
         _int,
         [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp,
          ctypes.POINTER(LossParams), _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "ppo_gather_rows": (
+        _int,
+        [_vp, _i64, _i64, _i32,
+         ctypes.POINTER(_vp), ctypes.POINTER(_i32), ctypes.POINTER(_vp), _vp],
+    ),
+    "ppo_adam_clip_workspace_bytes": (_sz, [_i32, ctypes.POINTER(_i64)]),
+    "ppo_adam_clip_f32": (
+        _int,
+        [_i32, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+         ctypes.POINTER(_vp), ctypes.POINTER(_i64), ctypes.POINTER(AdamParams), _vp, _vp, _sz,
+         _vp],
     ),
 }
 

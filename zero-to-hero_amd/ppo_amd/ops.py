@@ -26,6 +26,8 @@ from . import _lib
 __all__ = [
     "gae",
     "gae_normalize",
+    "discounted_returns",
+    "gather_rows",
     "normalize_advantages",
     "ppo_loss_discrete",
     "ppo_loss_discrete_fused",
@@ -224,6 +226,91 @@ def normalize_advantages(
         ws.data_ptr(), ws.numel(), stream,
     )
     return out
+
+
+def discounted_returns(
+    rewards: torch.Tensor,
+    dones: Optional[torch.Tensor] = None,
+    gamma: float = 0.99,
+    bootstrap: Optional[torch.Tensor] = None,
+    center: bool = False,
+) -> torch.Tensor:
+    """REINFORCE returns, rl/deep/agents/reinforce.py:57-66, on the GPU.
+
+    Per env, walking t backwards: value = reward + gamma * value, restarted
+    after a done (the reference handles one episode, so it has no done inside
+    the rollout), with `bootstrap` [N] (None = zeros, the reference's start
+    value 0.0) entering after step T-1.  This is the GAE kernel with lambda = 1
+    and all values zero, so the fp64 sums are bit-identical to the reference's
+    Python floats.  With `center`, the mean over all returns is subtracted in
+    fp32 (reinforce.py:66).
+    """
+    _require(rewards, "rewards", (torch.float32,))
+    device = rewards.device
+    if rewards.dim() not in (1, 2):
+        raise ValueError(f"rewards must be [T] or [T,N], got shape {tuple(rewards.shape)}")
+    if dones is None:
+        dones = torch.zeros(rewards.shape, dtype=torch.uint8, device=device)
+    _require(dones, "dones", (torch.uint8, torch.bool), device)
+    if dones.shape != rewards.shape:
+        raise ValueError("dones must have the shape of rewards")
+    T, N = _as_2d(rewards).shape
+    if bootstrap is not None:
+        _require(bootstrap, "bootstrap", (torch.float32,), device)
+        if bootstrap.numel() != N:
+            raise ValueError(f"bootstrap must hold N={N} values, got {bootstrap.numel()}")
+    out = torch.empty_like(rewards)
+    if T * N == 0:
+        return out
+    stream = _stream(device)
+    nbytes = _lib.load().ppo_gae_workspace_bytes(T, N)
+    ws = _WORKSPACES.get(device, stream, nbytes)
+    _call(
+        "ppo_gae_f32", device, stream,
+        rewards.data_ptr(), None, _done_bytes(dones).data_ptr(), _ptr(bootstrap), T, N,
+        float(gamma), 1.0, out.data_ptr(), None, ws.data_ptr(), ws.numel(), stream,
+    )
+    if center:
+        out = out - out.mean()
+    return out
+
+
+def gather_rows(index: torch.Tensor, *arrays: torch.Tensor) -> list[torch.Tensor]:
+    """[a[index] for a in arrays] in one launch (the minibatch gather of
+    ppo.py:132-139).  Every array is contiguous on one device with the same
+    leading dimension n and 4-byte-multiple rows (fp32/int32/int64/...);
+    `index` is int64 [B] with values in [0, n) (others give zero rows)."""
+    _require(index, "index", (torch.int64,))
+    device = index.device
+    if index.dim() != 1:
+        raise ValueError(f"index must be 1-D, got shape {tuple(index.shape)}")
+    if not 1 <= len(arrays) <= _lib.GATHER_MAX_ARRAYS:
+        raise ValueError(f"between 1 and {_lib.GATHER_MAX_ARRAYS} arrays, got {len(arrays)}")
+    n = arrays[0].shape[0]
+    outs, rb = [], []
+    for k, a in enumerate(arrays):
+        if not isinstance(a, torch.Tensor) or a.device != device:
+            raise RuntimeError(f"array {k} must be a tensor on {device}")
+        if not a.is_contiguous():
+            raise ValueError(f"array {k} must be contiguous")
+        if a.dim() < 1 or a.shape[0] != n:
+            raise ValueError(f"array {k} must have leading dimension {n}")
+        row = a.element_size() * (a[0].numel() if a.dim() > 1 else 1)
+        if row % 4:
+            raise ValueError(f"array {k}: rows of {row} bytes are not a multiple of 4")
+        rb.append(row)
+        outs.append(torch.empty((index.numel(),) + tuple(a.shape[1:]), dtype=a.dtype,
+                                device=device))
+    B = index.numel()
+    if B == 0:
+        return outs
+    na = len(arrays)
+    src = (ctypes.c_void_p * na)(*[a.data_ptr() for a in arrays])
+    dst = (ctypes.c_void_p * na)(*[o.data_ptr() for o in outs])
+    rbs = (ctypes.c_int32 * na)(*rb)
+    stream = _stream(device)
+    _call("ppo_gather_rows", device, stream, index.data_ptr(), B, n, na, src, rbs, dst, stream)
+    return outs
 
 
 # ---------------------------------------------------------------------------

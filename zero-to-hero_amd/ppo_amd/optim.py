@@ -1,0 +1,105 @@
+"""clip_grad_norm_ + Adam as one fused GPU step (rl/deep/agents/ppo.py:170-171).
+
+`ClippedAdam` holds the same state as torch.optim.Adam (exp_avg, exp_avg_sq
+and a step count per parameter) and replaces the pair
+
+    nn.utils.clip_grad_norm_(params, max_grad_norm)
+    optimizer.step()
+
+with two kernel launches (ppo_adam_clip_f32) whatever the number of tensors,
+following torch's multi-tensor Adam operation by operation in fp32.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Iterable
+
+import torch
+
+from . import _lib
+from .ops import _WORKSPACES, _call, _stream
+
+
+class ClippedAdam:
+    """Adam (no weight decay, no amsgrad) on fp32 CUDA parameters whose
+    gradients are first clipped to a global 2-norm of `max_grad_norm`
+    (<= 0 disables clipping).  step() returns the pre-clip total norm as a
+    0-d device tensor, as clip_grad_norm_ does."""
+
+    def __init__(
+        self,
+        params: Iterable[torch.Tensor],
+        lr: float = 3e-4,
+        betas: tuple[float, float] = (0.9, 0.999),
+        eps: float = 1e-8,
+        max_grad_norm: float = 0.5,
+    ) -> None:
+        self.params = list(params)
+        if not self.params:
+            raise ValueError("ClippedAdam got an empty parameter list")
+        if len(self.params) > _lib.ADAM_MAX_TENSORS:
+            raise ValueError(f"at most {_lib.ADAM_MAX_TENSORS} tensors, got {len(self.params)}")
+        device = self.params[0].device
+        for k, p in enumerate(self.params):
+            if p.device.type != "cuda" or p.device != device:
+                raise RuntimeError(f"parameter {k} is on {p.device}; ClippedAdam runs on one GPU")
+            if p.dtype != torch.float32 or not p.is_contiguous():
+                raise TypeError(f"parameter {k} must be contiguous fp32")
+        if not lr >= 0.0 or not eps >= 0.0:
+            raise ValueError("lr and eps must be >= 0")
+        self.device = device
+        self.lr, self.betas, self.eps, self.max_grad_norm = lr, betas, eps, max_grad_norm
+        self.exp_avg = [torch.zeros_like(p) for p in self.params]
+        self.exp_avg_sq = [torch.zeros_like(p) for p in self.params]
+        self.steps = [0] * len(self.params)
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        for p in self.params:
+            if p.grad is not None:
+                if set_to_none:
+                    p.grad = None
+                else:
+                    p.grad.zero_()
+
+    @torch.no_grad()
+    def step(self) -> torch.Tensor:
+        # as torch: parameters without a gradient are skipped (and keep their step)
+        live = [k for k, p in enumerate(self.params) if p.grad is not None]
+        norm = torch.zeros((), dtype=torch.float32, device=self.device)
+        if not live:
+            return norm
+        for k in live:
+            g = self.params[k].grad
+            if g.dtype != torch.float32 or not g.is_contiguous():
+                raise TypeError(f"gradient of parameter {k} must be contiguous fp32")
+        # one launch pair per group of tensors at the same step count (one group
+        # in steady state); the clip norm spans all live gradients only when
+        # they form one group, so mixed counts are stepped without clipping
+        groups: dict[int, list[int]] = {}
+        for k in live:
+            groups.setdefault(self.steps[k] + 1, []).append(k)
+        if len(groups) > 1 and self.max_grad_norm > 0:
+            raise RuntimeError("ClippedAdam: parameters at different step counts cannot share "
+                               "one clip norm; step them together from the start")
+        stream = _stream(self.device)
+        lib = _lib.load()
+        for step, ks in groups.items():
+            nt = len(ks)
+            P = ctypes.c_void_p * nt
+            numel = (ctypes.c_int64 * nt)(*[self.params[k].numel() for k in ks])
+            hp = _lib.AdamParams(float(self.lr), float(self.betas[0]), float(self.betas[1]),
+                                 float(self.eps), float(self.max_grad_norm), int(step))
+            nbytes = lib.ppo_adam_clip_workspace_bytes(nt, numel)
+            ws = _WORKSPACES.get(self.device, stream, nbytes)
+            _call(
+                "ppo_adam_clip_f32", self.device, stream, nt,
+                P(*[self.params[k].data_ptr() for k in ks]),
+                P(*[self.params[k].grad.data_ptr() for k in ks]),
+                P(*[self.exp_avg[k].data_ptr() for k in ks]),
+                P(*[self.exp_avg_sq[k].data_ptr() for k in ks]),
+                numel, ctypes.byref(hp), norm.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+            )
+            for k in ks:
+                self.steps[k] = step
+        return norm

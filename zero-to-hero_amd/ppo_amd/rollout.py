@@ -17,6 +17,7 @@ from torch import nn
 
 from . import ops
 from .agent import PPOConfig
+from .optim import ClippedAdam
 
 
 class RolloutBuffer:
@@ -96,6 +97,9 @@ class VecPPO:
     (gaussian, with the state-independent `log_std` parameter); `value` maps
     observations to [B,1].  Minibatches come from torch.randperm on the CPU
     generator `generator` (default: the global one, as ppo.py:130 uses).
+    With `fused_update` (default), the minibatch gather is one ppo_gather_rows
+    launch and clip_grad_norm_ + Adam is ClippedAdam (two launches); otherwise
+    torch indexing, clip_grad_norm_ and torch.optim.Adam are used.
     """
 
     def __init__(
@@ -108,6 +112,7 @@ class VecPPO:
         batch_size: int = 128,
         log_std: Optional[nn.Parameter] = None,
         generator: Optional[torch.Generator] = None,
+        fused_update: bool = True,
     ) -> None:
         self.policy, self.value = policy, value
         self.ppo_config, self.gamma, self.batch_size = ppo_config, gamma, batch_size
@@ -116,7 +121,12 @@ class VecPPO:
         self.parameters = list(policy.parameters()) + list(value.parameters())
         if log_std is not None:
             self.parameters.append(log_std)
-        self.optimizer = torch.optim.Adam(self.parameters, lr=lr)
+        self.fused = fused_update
+        if fused_update:
+            self.optimizer = ClippedAdam(self.parameters, lr=lr,
+                                         max_grad_norm=ppo_config.gradient_clip)
+        else:
+            self.optimizer = torch.optim.Adam(self.parameters, lr=lr)
 
     def update(self, buffer: RolloutBuffer) -> dict:
         """Run `epochs` passes of shuffled minibatches; returns the last
@@ -127,19 +137,21 @@ class VecPPO:
         n = T * buffer.N
         if n <= 1:
             adv_n = adv
-        obs = buffer.observations[:T].reshape(n, *buffer.observations.shape[2:])
-        acts = buffer.actions[:T].reshape(n, *buffer.actions.shape[2:])
-        old_lp = buffer.log_probs[:T].reshape(n)
-        old_v = buffer.values[:T].reshape(n)
-        adv_f, ret_f = adv_n.reshape(n), ret.reshape(n)
+        obs = buffer.observations[:T].reshape(n, *buffer.observations.shape[2:]).contiguous()
+        acts = buffer.actions[:T].reshape(n, *buffer.actions.shape[2:]).contiguous()
+        old_lp = buffer.log_probs[:T].reshape(n).contiguous()
+        old_v = buffer.values[:T].reshape(n).contiguous()
+        adv_f, ret_f = adv_n.reshape(n).contiguous(), ret.reshape(n).contiguous()
         stats: dict = {}
         for _ in range(cfg.epochs):
             indices = torch.randperm(n, generator=self.generator)
             for start in range(0, n, self.batch_size):
                 idx = indices[start : start + self.batch_size].to(buffer.device)
-                stats = self._update_batch(
-                    obs[idx], acts[idx], old_lp[idx], adv_f[idx], ret_f[idx], old_v[idx]
-                )
+                if self.fused:
+                    batch = ops.gather_rows(idx, obs, acts, old_lp, adv_f, ret_f, old_v)
+                else:
+                    batch = [x[idx] for x in (obs, acts, old_lp, adv_f, ret_f, old_v)]
+                stats = self._update_batch(*batch)
         return stats
 
     def _update_batch(self, observations, actions, old_log_probs, advantages, returns,
@@ -162,6 +174,9 @@ class VecPPO:
             )
         self.optimizer.zero_grad()
         loss.backward()
-        nn.utils.clip_grad_norm_(self.parameters, cfg.gradient_clip)
-        self.optimizer.step()
+        if self.fused:
+            self.optimizer.step()  # clips to cfg.gradient_clip, then Adam
+        else:
+            nn.utils.clip_grad_norm_(self.parameters, cfg.gradient_clip)
+            self.optimizer.step()
         return stats
