@@ -16,7 +16,8 @@ launched on.  `cpu_baseline` times the CPU restatement of the same path
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--suite]
 
 --suite additionally prints one line per BASELINE config (2-5) kernel, for
-the roofline table; the driver's contract line is always the last line.
+the roofline table; --update-suite times the whole minibatch update loop;
+the driver's contract line is always the last line.
 """
 
 from __future__ import annotations
@@ -47,6 +48,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--suite", action="store_true")
+    ap.add_argument("--update-suite", action="store_true",
+                    help="also time the whole minibatch update loop (VecPPO) vs the CPU oracle")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -280,6 +283,70 @@ def suite(torch, lib, dev):
                           "frac": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
 
 
+def update_suite(torch, dev, reps=10):
+    """The whole update loop (ppo.py:113-171 generalised to [T,N]): GAE +
+    normalisation + `epochs` x shuffled minibatches of MLP forward, fused loss,
+    backward and optimizer step.  BASELINE config 1 (T=128, N=8, MLP 4-64-64
+    tanh, A=2, 4 epochs x 4 minibatches of 256) and a larger T=2048, N=64 case
+    (minibatches of 4096).  Times VecPPO with the fused gather + ClippedAdam
+    replayed from graphs, the same eagerly, VecPPO with torch indexing + clip_grad_norm_ + Adam, and the CPU oracle
+    (numpy GAE, torch CPU loss/backward/Adam)."""
+    import copy
+
+    import ppo_amd
+    from oracle import ppo_oracle as ref
+    from ppo_amd.agent import MLP, PPOConfig
+
+    for name, T, N, mb in (("config1", 128, 8, 256), ("T2048_N64", 2048, 64, 4096)):
+        g = torch.Generator().manual_seed(24)
+        obs = (torch.rand(T, N, 4, generator=g) - 0.5) * 0.1
+        torch.manual_seed(24)
+        policy, value = MLP(4, 64, 2, "tanh"), MLP(4, 64, 1, "tanh")
+        with torch.no_grad():
+            logits = policy(obs)
+            acts = torch.multinomial(torch.softmax(logits.reshape(-1, 2), -1), 1,
+                                     generator=g).reshape(T, N)
+            lps = torch.log_softmax(logits, -1).gather(2, acts[..., None]).squeeze(2)
+            vals = value(obs).squeeze(2)
+        rewards = torch.ones(T, N)
+        dones = (torch.rand(T, N, generator=g) < 1 / 200).to(torch.uint8)
+        buf = ppo_amd.RolloutBuffer(T, N, (4,), device=dev)
+        for t in range(T):
+            buf.add(obs[t].to(dev), acts[t].to(torch.int32).to(dev), rewards[t].to(dev),
+                    dones[t].to(dev), vals[t].to(dev), lps[t].to(dev))
+        buf.finish(None)
+        out = {"update_suite": name, "T": T, "N": N, "minibatch": mb, "epochs": 4}
+        for label, fused, graphs in (("gpu_graphs_ms", True, True),
+                                     ("gpu_fused_ms", True, False),
+                                     ("gpu_torch_ms", False, False)):
+            vec = ppo_amd.VecPPO(copy.deepcopy(policy).to(dev), copy.deepcopy(value).to(dev),
+                                 PPOConfig(), batch_size=mb, fused_update=fused,
+                                 generator=torch.Generator().manual_seed(7), graphs=graphs)
+            vec.update(buf)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                vec.update(buf)
+            torch.cuda.synchronize()
+            out[label] = round((time.perf_counter() - t0) / reps * 1e3, 3)
+        cpol, cval = copy.deepcopy(policy), copy.deepcopy(value)
+        opt = torch.optim.Adam(list(cpol.parameters()) + list(cval.parameters()), lr=3e-4)
+        cfg = ref.OracleConfig(batch_size=mb)
+        gen = torch.Generator().manual_seed(7)
+        t0 = time.perf_counter()
+        creps = max(1, reps // 2)
+        for _ in range(creps):
+            adv, ret = ref.gae_numpy(rewards.numpy(), vals.numpy(), dones.numpy(), None,
+                                     0.99, 0.95)
+            adv_n = ref.normalize_reference(torch.from_numpy(adv).reshape(-1))
+            ref.reference_epochs(cpol, cval, opt, obs.reshape(-1, 4), acts.reshape(-1),
+                                 lps.reshape(-1), adv_n, torch.from_numpy(ret).reshape(-1), cfg,
+                                 generator=gen)
+        out["cpu_ms"] = round((time.perf_counter() - t0) / creps * 1e3, 3)
+        out["cpu_threads"] = torch.get_num_threads()
+        print(json.dumps(out), flush=True)
+
+
 def copy_calibration(torch, dev, reps=3):
     """A plain device-to-device copy of exactly 1 GiB (torch copy_), run
     `reps` times so that a rocprofv3 --pmc pass over this command records what
@@ -310,6 +377,8 @@ def main():
     if args.suite:
         suite(torch, lib, dev)
         torch.cuda.empty_cache()
+    if args.update_suite:
+        update_suite(torch, dev)
 
     if args.copy_calibration:
         copy_calibration(torch, dev)

@@ -204,6 +204,11 @@ typedef struct ppo_adam_params {
   double lr, beta1, beta2, eps;  /* torch.optim.Adam(lr, betas=(beta1, beta2), eps) */
   double max_grad_norm;          /* clip_grad_norm_ max_norm; <= 0: no clipping    */
   int64_t step;                  /* the step number after this update (>= 1)      */
+  /* Optional device counter (NULL: use `step`).  When set, the first kernel
+     increments *step_counter and the second derives the bias corrections from
+     it on the device, so the call can be captured once in a graph and
+     replayed for every step. */
+  int64_t* step_counter;
 } ppo_adam_params;
 
 size_t ppo_adam_clip_workspace_bytes(int32_t ntensors, const int64_t* numel);

@@ -44,13 +44,15 @@ def _make_params(dev, seed, shapes):
     return [torch.randn(*s, generator=g).to(dev).requires_grad_(True) for s in shapes]
 
 
+@pytest.mark.parametrize("capturable", [False, True])
 @pytest.mark.parametrize("max_norm", [0.5, 1e6, 0.0])
-def test_clipped_adam_matches_torch(dev, max_norm):
+def test_clipped_adam_matches_torch(dev, max_norm, capturable):
     shapes = [(64, 4), (64,), (64, 64), (64,), (2, 64), (2,), (10_000,), (3, 5, 7)]
     p_ref = _make_params(dev, 1, shapes)
     p_got = [p.detach().clone().requires_grad_(True) for p in p_ref]
     opt_ref = torch.optim.Adam(p_ref, lr=3e-4)
-    opt_got = ppo_amd.ClippedAdam(p_got, lr=3e-4, max_grad_norm=max_norm)
+    opt_got = ppo_amd.ClippedAdam(p_got, lr=3e-4, max_grad_norm=max_norm,
+                                 capturable=capturable)
     g = torch.Generator().manual_seed(2)
     for step in range(5):
         grads = [torch.randn(*s, generator=g).to(dev) * (0.1 + step) for s in shapes]

@@ -91,3 +91,13 @@ def test_rollout_buffer_validation():
     with pytest.raises(IndexError):
         buf.add(torch.zeros(3, 4), torch.zeros(3, dtype=torch.int32), z, z.to(torch.uint8), z, z)
     assert buf.observations.shape == (2, 3, 4) and buf.dones.dtype == torch.uint8
+
+
+def test_vecppo_graph_options_validated():
+    from ppo_amd.agent import MLP
+
+    pol, val = MLP(4, 8, 2), MLP(4, 8, 1)
+    with pytest.raises(ValueError, match="fused_update"):
+        ppo_amd.VecPPO(pol, val, graphs=True, fused_update=False)
+    with pytest.raises(ValueError, match="graph_chunk"):
+        ppo_amd.VecPPO(pol, val, graphs=True, graph_chunk=0)

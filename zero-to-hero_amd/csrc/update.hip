@@ -71,8 +71,10 @@ __device__ __forceinline__ int tensor_of_block(const AdamTable& t, long b) {
   return k;
 }
 
-__global__ void __launch_bounds__(kBlock) adam_sumsq_kernel(AdamTable t, double* partial) {
+__global__ void __launch_bounds__(kBlock) adam_sumsq_kernel(AdamTable t, double* partial,
+                                                            int64_t* step_counter) {
   const long b = blockIdx.x;
+  if (step_counter && b == 0 && threadIdx.x == 0) *step_counter += 1;
   const int k = tensor_of_block(t, b);
   const long lo = (b - t.block_start[k]) * kAdamChunk;
   const long hi = lo + kAdamChunk < t.n[k] ? lo + kAdamChunk : t.n[k];
@@ -86,6 +88,7 @@ __global__ void __launch_bounds__(kBlock) adam_sumsq_kernel(AdamTable t, double*
 }
 
 struct AdamScalars {
+  // host-formed scalars (used when no device step counter is given)
   float max_norm;      // clip threshold
   float beta1_w;       // 1 - beta1, the lerp weight
   float beta2;
@@ -94,12 +97,27 @@ struct AdamScalars {
   float eps;
   float neg_step;      // -(lr / (1 - beta1^step))
   int clip;            // 0: no clipping (max_norm <= 0)
+  // for the device step counter: the Python doubles the bias corrections
+  // are formed from
+  double lr_d, beta1_d, beta2_d;
 };
+
+// Bias-correction scalars for `step`, formed as torch forms them in Python
+// doubles (1 - beta^t, lr / bc1 * -1, bc2 ** 0.5) and rounded to fp32.
+__device__ inline void adam_step_scalars(AdamScalars& s, const int64_t* step_counter) {
+  const double step = (double)*step_counter;
+  const double bc1 = 1.0 - pow(s.beta1_d, step);
+  const double bc2 = 1.0 - pow(s.beta2_d, step);
+  s.neg_step = (float)((s.lr_d / bc1) * -1.0);
+  s.bc2_sqrt = (float)sqrt(bc2);
+}
 
 __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
                                                              const double* __restrict__ partial,
-                                                             AdamScalars s, float* norm_out) {
+                                                             AdamScalars s, float* norm_out,
+                                                             const int64_t* step_counter) {
   __shared__ float s_coef;
+  if (step_counter) adam_step_scalars(s, step_counter);
   // Global norm: per-tensor norms rounded to fp32, then the norm of those (the
   // two-level form of torch's _get_total_norm); every block derives the same
   // value in the same order.
@@ -200,7 +218,8 @@ extern "C" int ppo_adam_clip_f32(int32_t ntensors, float* const* params, float* 
   using namespace ppo;
   if (ntensors < 1 || ntensors > PPO_ADAM_MAX_TENSORS) return PPO_ERR_INVALID_ARG;
   if (!params || !grads || !exp_avg || !exp_avg_sq || !numel || !hp) return PPO_ERR_INVALID_ARG;
-  if (hp->step < 1 || !(hp->lr >= 0.0) || !(hp->eps >= 0.0)) return PPO_ERR_INVALID_ARG;
+  if ((!hp->step_counter && hp->step < 1) || !(hp->lr >= 0.0) || !(hp->eps >= 0.0))
+    return PPO_ERR_INVALID_ARG;
   if (!workspace || workspace_bytes < ppo_adam_clip_workspace_bytes(ntensors, numel))
     return PPO_ERR_WORKSPACE;
   AdamTable t = {};
@@ -220,8 +239,9 @@ extern "C" int ppo_adam_clip_f32(int32_t ntensors, float* const* params, float* 
   if (blocks > 0x7fffffffL) return PPO_ERR_TOO_LARGE;
   // Host-side scalars exactly as torch forms them: Python doubles, rounded to
   // fp32 where the tensor op consumes them.
-  const double bc1 = 1.0 - pow(hp->beta1, (double)hp->step);
-  const double bc2 = 1.0 - pow(hp->beta2, (double)hp->step);
+  const double step = hp->step_counter ? 1.0 : (double)hp->step;  // device path recomputes
+  const double bc1 = 1.0 - pow(hp->beta1, step);
+  const double bc2 = 1.0 - pow(hp->beta2, step);
   AdamScalars s;
   s.max_norm = (float)hp->max_grad_norm;
   s.clip = hp->max_grad_norm > 0.0 ? 1 : 0;
@@ -231,13 +251,16 @@ extern "C" int ppo_adam_clip_f32(int32_t ntensors, float* const* params, float* 
   s.bc2_sqrt = (float)sqrt(bc2);
   s.eps = (float)hp->eps;
   s.neg_step = (float)((hp->lr / bc1) * -1.0);
+  s.lr_d = hp->lr;
+  s.beta1_d = hp->beta1;
+  s.beta2_d = hp->beta2;
   double* partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   hipLaunchKernelGGL(adam_sumsq_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, stream, t,
-                     partial);
+                     partial, hp->step_counter);
   int st = last_launch_status();
   if (st) return st;
   hipLaunchKernelGGL(adam_update_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, stream, t,
-                     partial, s, grad_norm_out);
+                     partial, s, grad_norm_out, hp->step_counter);
   return last_launch_status();
 }

@@ -39,6 +39,7 @@ class AdamParams(ctypes.Structure):
         ("eps", ctypes.c_double),
         ("max_grad_norm", ctypes.c_double),
         ("step", ctypes.c_int64),
+        ("step_counter", ctypes.c_void_p),
     ]
 
 

@@ -74,6 +74,10 @@ class _WorkspacePool:
 
     def __init__(self) -> None:
         self._bufs: dict = {}
+        # while a graph is being captured: every buffer handed out is appended
+        # here, so the graph keeps its scratch alive even if the pool later
+        # replaces that buffer with a larger one
+        self.capture_refs: Optional[list] = None
 
     def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
         key = (device.index, stream)
@@ -82,6 +86,8 @@ class _WorkspacePool:
             size = max(nbytes, 0 if buf is None else 2 * buf.numel(), 4096)
             buf = torch.empty(size, dtype=torch.uint8, device=device)
             self._bufs[key] = buf
+        if self.capture_refs is not None:
+            self.capture_refs.append(buf)
         return buf
 
     def drop(self, device: torch.device, stream: int) -> None:

@@ -8,6 +8,11 @@ and a step count per parameter) and replaces the pair
 
 with two kernel launches (ppo_adam_clip_f32) whatever the number of tensors,
 following torch's multi-tensor Adam operation by operation in fp32.
+
+With `capturable=True` the step count lives in a device int64 counter that the
+first kernel increments and the second turns into the bias corrections, so a
+step() recorded in a CUDA/HIP graph advances the count on every replay (the
+role of torch.optim.Adam(capturable=True)).
 """
 
 from __future__ import annotations
@@ -34,6 +39,7 @@ class ClippedAdam:
         betas: tuple[float, float] = (0.9, 0.999),
         eps: float = 1e-8,
         max_grad_norm: float = 0.5,
+        capturable: bool = False,
     ) -> None:
         self.params = list(params)
         if not self.params:
@@ -53,6 +59,17 @@ class ClippedAdam:
         self.exp_avg = [torch.zeros_like(p) for p in self.params]
         self.exp_avg_sq = [torch.zeros_like(p) for p in self.params]
         self.steps = [0] * len(self.params)
+        self.capturable = capturable
+        # device step counter (capturable mode): one count shared by all tensors
+        self.step_t = (torch.zeros((), dtype=torch.int64, device=device)
+                       if capturable else None)
+
+    def step_count(self) -> int:
+        """The number of steps taken (reads the device counter in capturable
+        mode, which synchronises)."""
+        if self.capturable:
+            return int(self.step_t.item())
+        return max(self.steps)
 
     def zero_grad(self, set_to_none: bool = True) -> None:
         for p in self.params:
@@ -69,6 +86,9 @@ class ClippedAdam:
         norm = torch.zeros((), dtype=torch.float32, device=self.device)
         if not live:
             return norm
+        if self.capturable and len(live) != len(self.params):
+            raise RuntimeError("ClippedAdam(capturable=True) steps all parameters together; "
+                               "every parameter needs a gradient")
         for k in live:
             g = self.params[k].grad
             if g.dtype != torch.float32 or not g.is_contiguous():
@@ -89,7 +109,8 @@ class ClippedAdam:
             P = ctypes.c_void_p * nt
             numel = (ctypes.c_int64 * nt)(*[self.params[k].numel() for k in ks])
             hp = _lib.AdamParams(float(self.lr), float(self.betas[0]), float(self.betas[1]),
-                                 float(self.eps), float(self.max_grad_norm), int(step))
+                                 float(self.eps), float(self.max_grad_norm), int(step),
+                                 self.step_t.data_ptr() if self.capturable else None)
             nbytes = lib.ppo_adam_clip_workspace_bytes(nt, numel)
             ws = _WORKSPACES.get(self.device, stream, nbytes)
             _call(
@@ -100,6 +121,7 @@ class ClippedAdam:
                 P(*[self.exp_avg_sq[k].data_ptr() for k in ks]),
                 numel, ctypes.byref(hp), norm.data_ptr(), ws.data_ptr(), ws.numel(), stream,
             )
-            for k in ks:
-                self.steps[k] = step
+            if not self.capturable:
+                for k in ks:
+                    self.steps[k] = step
         return norm

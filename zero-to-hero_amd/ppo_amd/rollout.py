@@ -100,6 +100,15 @@ class VecPPO:
     With `fused_update` (default), the minibatch gather is one ppo_gather_rows
     launch and clip_grad_norm_ + Adam is ClippedAdam (two launches); otherwise
     torch indexing, clip_grad_norm_ and torch.optim.Adam are used.
+
+    With `graphs=True` (requires `fused_update`) the minibatch loop is replayed
+    from CUDA/HIP graphs: the whole update runs on a private stream, the
+    flattened rollout and each epoch's permutation are copied into static
+    device buffers, the first epoch after a change of shape runs eagerly (the
+    warm-up that initialises library handles and autograd state), and the
+    minibatch sequence is then captured as graphs of `graph_chunk`
+    minibatches each and replayed for every later epoch.  The results equal
+    the eager fused path's: the same kernels run on the same data.
     """
 
     def __init__(
@@ -113,6 +122,8 @@ class VecPPO:
         log_std: Optional[nn.Parameter] = None,
         generator: Optional[torch.Generator] = None,
         fused_update: bool = True,
+        graphs: bool = False,
+        graph_chunk: int = 64,
     ) -> None:
         self.policy, self.value = policy, value
         self.ppo_config, self.gamma, self.batch_size = ppo_config, gamma, batch_size
@@ -122,9 +133,17 @@ class VecPPO:
         if log_std is not None:
             self.parameters.append(log_std)
         self.fused = fused_update
+        if graphs and not fused_update:
+            raise ValueError("graphs=True needs fused_update=True")
+        if graph_chunk < 1:
+            raise ValueError(f"graph_chunk must be >= 1, got {graph_chunk}")
+        self.graphs, self.graph_chunk = graphs, graph_chunk
+        self._plan: Optional[_GraphPlan] = None
+        self._side_stream: Optional[torch.cuda.Stream] = None
         if fused_update:
             self.optimizer = ClippedAdam(self.parameters, lr=lr,
-                                         max_grad_norm=ppo_config.gradient_clip)
+                                         max_grad_norm=ppo_config.gradient_clip,
+                                         capturable=graphs)
         else:
             self.optimizer = torch.optim.Adam(self.parameters, lr=lr)
 
@@ -142,6 +161,8 @@ class VecPPO:
         old_lp = buffer.log_probs[:T].reshape(n).contiguous()
         old_v = buffer.values[:T].reshape(n).contiguous()
         adv_f, ret_f = adv_n.reshape(n).contiguous(), ret.reshape(n).contiguous()
+        if self.graphs:
+            return self._update_graphed(buffer.device, (obs, acts, old_lp, adv_f, ret_f, old_v))
         stats: dict = {}
         for _ in range(cfg.epochs):
             indices = torch.randperm(n, generator=self.generator)
@@ -153,6 +174,70 @@ class VecPPO:
                     batch = [x[idx] for x in (obs, acts, old_lp, adv_f, ret_f, old_v)]
                 stats = self._update_batch(*batch)
         return stats
+
+    def update_graphed_ready(self) -> bool:
+        """True once graphs are captured for the current rollout shape."""
+        return self._plan is not None and bool(self._plan.graphs)
+
+    def _update_graphed(self, device: torch.device, arrays: tuple) -> dict:
+        cfg = self.ppo_config
+        n, B = arrays[0].shape[0], self.batch_size
+        key = (n, B, cfg.epochs) + tuple((a.dtype, tuple(a.shape[1:])) for a in arrays)
+        if self._side_stream is None:
+            self._side_stream = torch.cuda.Stream(device=device)
+        s = self._side_stream
+        caller = torch.cuda.current_stream(device)
+        s.wait_stream(caller)
+        with torch.cuda.stream(s):
+            plan = self._plan
+            if plan is None or plan.key != key:
+                plan = self._plan = _GraphPlan(key, arrays, n, B, cfg.epochs, device)
+            for st, a in zip(plan.static, arrays):
+                st.copy_(a)
+            perms = torch.stack([torch.randperm(n, generator=self.generator)
+                                 for _ in range(cfg.epochs)])
+            plan.perms.copy_(perms.pin_memory(), non_blocking=True)
+            stats: dict = {}
+            for e in range(cfg.epochs):
+                plan.perm.copy_(plan.perms[e])
+                if plan.graphs:
+                    for g in plan.graphs:
+                        g.replay()
+                    stats = plan.stats
+                elif not plan.warm:
+                    for j in range(plan.nmb):
+                        stats = self._graph_minibatch(plan, j)
+                    plan.warm = True
+                else:
+                    self._capture(plan, s)
+                    for g in plan.graphs:
+                        g.replay()
+                    stats = plan.stats
+        caller.wait_stream(s)
+        return stats
+
+    def _graph_minibatch(self, plan: "_GraphPlan", j: int) -> dict:
+        idx = plan.perm[j * plan.B : (j + 1) * plan.B]
+        return self._update_batch(*ops.gather_rows(idx, *plan.static))
+
+    def _capture(self, plan: "_GraphPlan", stream: torch.cuda.Stream) -> None:
+        pool = torch.cuda.graph_pool_handle()
+        refs: list = []
+        ops._WORKSPACES.capture_refs = refs
+        try:
+            stats: dict = {}
+            for c in range(0, plan.nmb, self.graph_chunk):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, pool=pool, stream=stream):
+                    for j in range(c, min(c + self.graph_chunk, plan.nmb)):
+                        stats = self._graph_minibatch(plan, j)
+                plan.graphs.append(g)
+        except BaseException:
+            plan.graphs.clear()
+            raise
+        finally:
+            ops._WORKSPACES.capture_refs = None
+        plan.stats, plan.refs = stats, refs
 
     def _update_batch(self, observations, actions, old_log_probs, advantages, returns,
                       old_values) -> dict:
@@ -180,3 +265,21 @@ class VecPPO:
             nn.utils.clip_grad_norm_(self.parameters, cfg.gradient_clip)
             self.optimizer.step()
         return stats
+
+
+class _GraphPlan:
+    """Static buffers and captured graphs of VecPPO's minibatch loop for one
+    rollout shape: `static` holds the flattened arrays the graphs gather from,
+    `perm` the current epoch's permutation (its slices are the minibatch
+    indices), `perms` every epoch's permutation for one update."""
+
+    def __init__(self, key, arrays, n: int, B: int, epochs: int, device) -> None:
+        self.key, self.n, self.B = key, n, B
+        self.nmb = (n + B - 1) // B
+        self.static = [torch.empty_like(a) for a in arrays]
+        self.perm = torch.empty(n, dtype=torch.int64, device=device)
+        self.perms = torch.empty((epochs, n), dtype=torch.int64, device=device)
+        self.warm = False
+        self.graphs: list = []
+        self.stats: dict = {}
+        self.refs: list = []
