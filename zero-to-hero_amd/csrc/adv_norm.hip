@@ -57,7 +57,7 @@ __global__ void __launch_bounds__(kBlock) adv_moments_kernel(const float* adv, l
 
 // One block: combine the partials (fixed order) and store the normaliser
 // parameters in the workspace header (and {mean, std} in stats_out).
-__global__ void __launch_bounds__(kBlock) finalize_stats_kernel(const double* partials, long count,
+__global__ void __launch_bounds__(kFinalBlock) finalize_stats_kernel(const double* partials, long count,
                                                                 double eps, WsHeader* hdr,
                                                                 float* stats_out) {
   const NormParams np = norm_params(partials, count, eps);
@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(kBlock) normalize_kernel(const float* adv, flo
 
 int launch_finalize_stats(const double* partials, long count, double eps, WsHeader* hdr,
                           float* stats_out, hipStream_t stream) {
-  hipLaunchKernelGGL(finalize_stats_kernel, dim3(1), dim3(kBlock), 0, stream, partials, count, eps,
+  hipLaunchKernelGGL(finalize_stats_kernel, dim3(1), dim3(kFinalBlock), 0, stream, partials, count, eps,
                      hdr, stats_out);
   return last_launch_status();
 }

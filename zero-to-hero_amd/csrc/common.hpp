@@ -33,13 +33,43 @@ inline int hip_status(hipError_t e) { return e == hipSuccess ? PPO_OK : PPO_ERR_
 // Launch-error check after a hipLaunchKernelGGL.
 inline int last_launch_status() { return hip_status(hipGetLastError()); }
 
-__device__ __forceinline__ double wave_sum(double x) {
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) x += __shfl_xor(x, off, kWave);
-  return x;
+// DPP lane move of a double (two 32-bit halves), every lane and bank enabled.
+template <int kCtrl>
+__device__ __forceinline__ double dpp_move(double x) {
+  const int2 v = __builtin_bit_cast(int2, x);
+  int2 r;
+  r.x = __builtin_amdgcn_update_dpp(0, v.x, kCtrl, 0xF, 0xF, false);
+  r.y = __builtin_amdgcn_update_dpp(0, v.y, kCtrl, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, r);
 }
 
-// Block-wide sum of K doubles per thread; result valid in thread 0.
+__device__ __forceinline__ double read_lane(double x, int lane) {
+  const int2 v = __builtin_bit_cast(int2, x);
+  int2 r;
+  r.x = __builtin_amdgcn_readlane(v.x, lane);
+  r.y = __builtin_amdgcn_readlane(v.y, lane);
+  return __builtin_bit_cast(double, r);
+}
+
+// Wave-wide sum, the same value in every lane.  Within each 16-lane row, DPP
+// moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
+// row_mirror) leave the row's sum in every lane of the row; the four row sums
+// are then read out with readlane and added as (r0 + r1) + (r2 + r3).  DPP
+// moves are VALU operations; a __shfl_xor butterfly goes through the LDS
+// crossbar (ds_bpermute, twice per double) at LDS latency per step.  The
+// summation order is fixed, so results are deterministic.
+__device__ __forceinline__ double wave_sum(double x) {
+  x += dpp_move<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_move<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp_move<0x141>(x);  // row_half_mirror
+  x += dpp_move<0x140>(x);  // row_mirror
+  return (read_lane(x, 0) + read_lane(x, 16)) + (read_lane(x, 32) + read_lane(x, 48));
+}
+
+// Block-wide sum of K doubles per thread (whole waves, at most 16); result
+// valid in every lane of wave 0.  Each wave reduces its values with wave_sum, and wave 0
+// then reduces the per-wave sums the same way (lanes past the last wave add
+// zeros), so the order is fixed and no thread loops over the waves.
 template <int K>
 __device__ inline void block_sum(double (&x)[K]) {
   __shared__ double s_part[16][K];
@@ -52,34 +82,42 @@ __device__ inline void block_sum(double (&x)[K]) {
     for (int k = 0; k < K; ++k) s_part[wid][k] = x[k];
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (wid == 0) {
     const int nw = blockDim.x / kWave;
+    double v[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      double s = 0.0;
-      for (int w = 0; w < nw; ++w) s += s_part[w][k];
-      x[k] = s;
-    }
+    for (int k = 0; k < K; ++k) v[k] = lane < nw ? s_part[lane < 16 ? lane : 0][k] : 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) x[k] = wave_sum(v[k]);
   }
   __syncthreads();
 }
 
 // Sums of `count` partial (n, sum x, sum x^2, pad) quadruples, combined by
-// one block in a fixed order (contiguous range per thread, then the block
-// tree), so every block that calls this gets bit-identical totals.  Result
+// one block in a fixed order (thread t takes partials t, t + blockDim, ...,
+// then the block tree), so every call gets bit-identical totals.  Result
 // valid in thread 0.
 __device__ inline void sum_partials(const double* part, long count, double (&tot)[3]) {
   tot[0] = tot[1] = tot[2] = 0.0;
-  const long per = (count + blockDim.x - 1) / blockDim.x;
-  const long lo = (long)threadIdx.x * per;
-  const long hi = lo + per < count ? lo + per : count;
-  for (long i = lo; i < hi; ++i) {
-    tot[0] += part[4 * i + 0];
-    tot[1] += part[4 * i + 1];
-    tot[2] += part[4 * i + 2];
+  // two partials per thread per round, all loads in flight together
+  for (long i = threadIdx.x; i < count; i += 2 * blockDim.x) {
+    const long j = i + blockDim.x < count ? i + blockDim.x : i;
+    const double a0 = part[4 * i + 0], a1 = part[4 * i + 1], a2 = part[4 * i + 2];
+    const double b0 = part[4 * j + 0], b1 = part[4 * j + 1], b2 = part[4 * j + 2];
+    const bool second = j != i;
+    tot[0] += a0;
+    tot[1] += a1;
+    tot[2] += a2;
+    tot[0] += second ? b0 : 0.0;
+    tot[1] += second ? b1 : 0.0;
+    tot[2] += second ? b2 : 0.0;
   }
   block_sum<3>(tot);
 }
+
+// Threads of the one-block finaliser kernels: a whole CU's worth of waves, so
+// that the partial loads and the wave reductions run 16 waves wide.
+constexpr int kFinalBlock = 1024;
 
 __host__ __device__ inline unsigned int pow2_ceil(unsigned int x) {
   unsigned int p = 1;

@@ -39,7 +39,7 @@ namespace {
 // the static reduction arrays stay under the 64 KiB a workgroup may address.
 constexpr int kMaxCatRowWidth = 48;  // A above this uses the wave-per-row kernel
 constexpr int kMaxGaussDim = 24;     // D limit of the Gaussian kernel
-constexpr int kScalarSlots = 8;      // per-block partial doubles for the loss scalars
+constexpr int kScalarSlots = 8;      // per-block partial doubles reserved for the loss scalars
 constexpr int kGaussSlots = kScalarSlots + kMaxGaussDim;
 constexpr long kWaveRowBlocks = 4096;  // grid cap of the wave-per-row kernel
 #ifndef PPO_LOSS_BLOCKS_PER_CU
@@ -217,13 +217,21 @@ __device__ __forceinline__ void stage_out(float* dst, int count, int width, floa
   }
 }
 
-// Block partial of the 5 loss sums -> partial[block*stride + 0..4].
-__device__ inline void store_scalar_partials(const LossArgs& a, double (&acc)[5], long block,
-                                             int stride) {
+// Per-block partials are stored slot-major, partial[slot * gridDim.x + block]
+// (slots 0-4: the loss sums; slots 5..5+D-1: the Gaussian dlog_std column
+// sums), so the finaliser's loads of one slot are contiguous.
+constexpr int kLossSums = 5;
+
+__device__ inline void store_partial(const LossArgs& a, int slot, double v) {
+  a.partial[(long)slot * gridDim.x + blockIdx.x] = v;
+}
+
+// Block partial of the 5 loss sums.
+__device__ inline void store_scalar_partials(const LossArgs& a, double (&acc)[5]) {
   block_sum<5>(acc);
   if (threadIdx.x == 0) {
 #pragma unroll
-    for (int k = 0; k < 5; ++k) a.partial[block * stride + k] = acc[k];
+    for (int k = 0; k < 5; ++k) store_partial(a, k, acc[k]);
   }
 }
 
@@ -236,52 +244,62 @@ __device__ __forceinline__ void accumulate(double (&acc)[5], const RowOut& o, fl
 }
 
 // One-block finaliser, launched after the loss kernel on the same stream:
-// sums the per-block partials in a fixed order (deterministic), forms the
-// means and the total loss, and for the Gaussian policy (D > 0) finishes
-// dlog_std = sum over blocks of the per-block column sums - ec.
-__global__ void __launch_bounds__(kBlock) loss_finalize_kernel(LossArgs a, long nblocks, int stride,
-                                                               int D) {
-  __shared__ float s_hconst;
-  double tot[5] = {0, 0, 0, 0, 0};
-  const long per = (nblocks + blockDim.x - 1) / blockDim.x;
-  const long lo = (long)threadIdx.x * per;
-  const long hi = lo + per < nblocks ? lo + per : nblocks;
-  for (long b = lo; b < hi; ++b)
+// sums the per-block partials in a fixed order (thread t takes blocks t,
+// t + kFinalBlock, ...; then the block tree), so results are deterministic;
+// forms the means and the total loss, and for the Gaussian policy (D > 0,
+// D <= MAXD) finishes dlog_std = sum over blocks of the column sums - ec.
+template <int MAXD>
+__global__ void __launch_bounds__(kFinalBlock) loss_finalize_kernel(LossArgs a, long nblocks, int D) {
+  constexpr int K = kLossSums + MAXD;
+  // Gaussian: lane d of wave 0 loads log_std[d] now (overlapping the partial
+  // loads) and forms its entropy term, summed in dim order below
+  __shared__ float s_hterm[MAXD > 0 ? MAXD : 1];
+  if (MAXD > 0 && threadIdx.x < D) {
+    const float kEntConst = 1.41893853320467274178f;  // 0.5 + 0.5*log(2*pi)
+    s_hterm[threadIdx.x] = kEntConst + logf(expf(a.log_std[threadIdx.x]));
+  }
+  double tot[K];
 #pragma unroll
-    for (int k = 0; k < 5; ++k) tot[k] += a.partial[b * stride + k];
-  block_sum<5>(tot);
-  if (D > 0) {
-    __shared__ double s_red[kBlock];
-    // column d summed over blocks by `groups` threads each, then per column
-    const int groups = kBlock / D;
-    const int t = threadIdx.x;
-    double sum = 0.0;
-    if (t < groups * D) {
-      const int d = t % D;
-      const int g = t / D;
-      for (long b = g; b < nblocks; b += groups) sum += a.partial[b * stride + kScalarSlots + d];
+  for (int k = 0; k < K; ++k) tot[k] = 0.0;
+  // every slot's load is issued before any is consumed: slots past the last
+  // used one re-read that slot (valid memory) and are masked out by a select,
+  // so no load sits behind a branch and its own wait
+  const int used = kLossSums + D;
+  // two blocks per thread per round, all loads in flight together
+  for (long b0 = threadIdx.x; b0 < nblocks; b0 += 2 * kFinalBlock) {
+    double v[2][K];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const long b = b0 + h * kFinalBlock < nblocks ? b0 + h * kFinalBlock : b0;
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        v[h][k] = a.partial[(long)(k < used ? k : used - 1) * nblocks + b];
     }
-    s_red[t] = sum;
-    __syncthreads();
-    if (t < D) {
-      double c = 0.0;
-      for (int g = 0; g < groups; ++g) c += s_red[g * D + t];
-      a.dlog_std[t] = (float)c - a.ec;
-    }
-    if (t == 0) {
-      // entropy of Normal(mu, scale) summed over dims, identical for every row
-      const float kEntConst = 1.41893853320467274178f;  // 0.5 + 0.5*log(2*pi)
-      float h = 0.0f;
-      for (int d = 0; d < D; ++d) h += kEntConst + logf(expf(a.log_std[d]));
-      s_hconst = h;
-    }
-    __syncthreads();
+    const bool second = b0 + kFinalBlock < nblocks;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int k = 0; k < K; ++k) tot[k] += (k < used && (h == 0 || second)) ? v[h][k] : 0.0;
+  }
+  block_sum<K>(tot);  // also leaves the totals in every lane of wave 0
+  if (MAXD > 0 && threadIdx.x < kWave) {
+#pragma unroll
+    for (int d = 0; d < MAXD; ++d)
+      if (d < D && (int)threadIdx.x == d) a.dlog_std[d] = (float)tot[kLossSums + d] - a.ec;
   }
   if (threadIdx.x == 0) {
+    float ent;
+    if (MAXD > 0) {
+      // entropy of Normal(mu, scale) summed over dims, identical for every row
+      float h = 0.0f;
+      for (int d = 0; d < D; ++d) h += s_hterm[d];
+      ent = h;
+    } else {
+      ent = (float)(tot[2] / (double)a.B);
+    }
     const double nb = (double)a.B;
     const float pol = (float)(tot[0] / nb);
     const float vl = (float)(tot[1] / nb);
-    const float ent = D > 0 ? s_hconst : (float)(tot[2] / nb);
     a.scalars[PPO_SCALAR_POLICY] = pol;
     a.scalars[PPO_SCALAR_VALUE] = vl;
     a.scalars[PPO_SCALAR_ENTROPY] = ent;
@@ -361,7 +379,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_kernel(LossArgs a, long ntile
     stage_out<kVec>(a.dx + row0 * A, nrows * A, A, invA, AS, s_tile);
     __syncthreads();
   }
-  store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
+  store_scalar_partials(a, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -497,7 +515,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_pipe_kernel(LossArgs a, long 
     }
     __syncthreads();
   }
-  store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
+  store_scalar_partials(a, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -589,7 +607,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_dense_kernel(LossArgs a, long
     if (tid < count - (n4 << 2)) a.dx[row0 * A + (n4 << 2) + tid] = s_tile[(n4 << 2) + tid];
     __syncthreads();
   }
-  store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
+  store_scalar_partials(a, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -647,7 +665,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_wave_kernel(LossArgs a) {
     }
     if (lane == 0) accumulate(acc, o, H);
   }
-  store_scalar_partials(a, acc, blockIdx.x, kScalarSlots);
+  store_scalar_partials(a, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -727,8 +745,8 @@ __global__ void __launch_bounds__(kBlock) loss_gauss_kernel(LossArgs a, long nti
       for (int g = 0; g < groups; ++g) col_acc += s_col[g * D + tid];
     __syncthreads();
   }
-  if (tid < D) a.partial[(long)blockIdx.x * kGaussSlots + kScalarSlots + tid] = col_acc;
-  store_scalar_partials(a, acc, blockIdx.x, kGaussSlots);
+  if (tid < D) store_partial(a, kLossSums + tid, col_acc);
+  store_scalar_partials(a, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -851,16 +869,18 @@ __global__ void __launch_bounds__(kBlock) loss_gauss_dense_kernel(LossArgs a, lo
     if (tid < count - (n4 << 2)) a.dx[row0 * D + (n4 << 2) + tid] = s_mu[(n4 << 2) + tid];
     __syncthreads();
   }
-  // this block's dlog_std partials: one block reduction per dim
+  // this block's loss sums and dlog_std column sums: one block reduction
+  double all[kLossSums + MAXD];
 #pragma unroll
-  for (int d = 0; d < MAXD; ++d) {
-    if (d < D) {
-      double v[1] = {col[d]};
-      block_sum<1>(v);
-      if (tid == 0) a.partial[(long)blockIdx.x * kGaussSlots + kScalarSlots + d] = v[0];
-    }
+  for (int k = 0; k < kLossSums; ++k) all[k] = acc[k];
+#pragma unroll
+  for (int d = 0; d < MAXD; ++d) all[kLossSums + d] = col[d];
+  block_sum<kLossSums + MAXD>(all);
+  if (tid == 0) {
+#pragma unroll
+    for (int k = 0; k < kLossSums + MAXD; ++k)
+      if (k < kLossSums + D) store_partial(a, k, all[k]);
   }
-  store_scalar_partials(a, acc, blockIdx.x, kGaussSlots);
 }
 
 int fill_common(LossArgs& a, long B, const ppo_loss_params* p, const float* old_lp,
@@ -992,8 +1012,7 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
                          stream, a);
   }
   if ((st = last_launch_status())) return st;
-  hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(kBlock), 0, stream, a, blocks,
-                     kScalarSlots, 0);
+  hipLaunchKernelGGL(loss_finalize_kernel<0>, dim3(1), dim3(kFinalBlock), 0, stream, a, blocks, 0);
   return last_launch_status();
 }
 
@@ -1056,7 +1075,13 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
   if ((st = hip_status(
            hipLaunchKernel(kern, grid_of(blocks), dim3(kBlock), args, lds_used, stream))))
     return st;
-  hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(kBlock), 0, stream, a, blocks,
-                     kGaussSlots, D);
+  // the finaliser reads exactly `blocks` partials per slot: the launched grid
+  if (D == 6)
+    hipLaunchKernelGGL(loss_finalize_kernel<6>, dim3(1), dim3(kFinalBlock), 0, stream, a, blocks, D);
+  else if (D <= 8)
+    hipLaunchKernelGGL(loss_finalize_kernel<8>, dim3(1), dim3(kFinalBlock), 0, stream, a, blocks, D);
+  else
+    hipLaunchKernelGGL(loss_finalize_kernel<kMaxGaussDim>, dim3(1), dim3(kFinalBlock), 0, stream,
+                       a, blocks, D);
   return last_launch_status();
 }
