@@ -38,6 +38,7 @@
 // When the whole horizon fits in one tile (Tt == 1) steps 1-2 are skipped and
 // the final pass emits per-block sums for a separate normalise pass instead.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "stats.hpp"
@@ -78,22 +79,67 @@ enum GaeMode {
   kFinalNorm = 4,     // pass 2: adv, ret, adv_n with mean/denom from the workspace header
 };
 
-struct GaePlan {
-  int vw, L, Qw, Sw;
-  long Q, Tq, Tt, span;
-  long blocks() const { return Tt * Tq; }
+// Geometry of one tile pass: L steps x VW envs per thread, Sw segments x Qw
+// env-groups per 256-thread tile (Sw * L steps), Tq tiles across the envs.
+struct PassGeom {
+  int L, Qw, Sw;
+  long Tq;
+  bool solo;  // Sw == 1: the thread's segment is the tile, no LDS scan
+  bool quad;  // Sw == 4, Qw == 64: segments of a tile in adjacent lanes
 };
 
+struct GaePlan {
+  int vw;
+  long Q, Tt, span;
+  PassGeom scan, fin;  // pass 1 (tile composites) and the final pass
+  PassGeom fin_solo;   // final pass without the normaliser (wide rollouts only)
+  long blocks() const { return Tt * std::max(std::max(scan.Tq, fin.Tq), fin_solo.Tq); }
+  // the final pass's geometry: solo tiles where they exist and no normaliser
+  const PassGeom& final_geom(bool norm) const { return !norm && fin_solo.Tq > 0 ? fin_solo : fin; }
+};
+
+PassGeom make_geom(long Q, int L, int Qw) {
+  PassGeom g;
+  g.L = L;
+  g.Qw = Qw;
+  g.Sw = kBlock / Qw;
+  g.Tq = (Q + Qw - 1) / Qw;
+  g.solo = g.Sw == 1;
+  g.quad = false;
+  return g;
+}
+
+
+// Tiles span 16 steps for VW = 4 and 256/Qw * 16 steps for VW = 1.  Narrow
+// rollouts stack Sw = 256/Qw segments per tile (Qw <= 64 env-groups) and
+// compose them with an LDS scan, keeping a workgroup's rows wide enough to
+// coalesce.  Wide rollouts (VW = 4, >= 256 env-groups) have 4 segments of 4
+// steps x 64 env-groups per tile, with two more layouts chosen per pass by
+// measurement at T=2048, N=4096 (kernel us, stacked / quad / solo):
+//   pass 1 with the normaliser's tile sums: 24.3 / 22.1 / 33.1 -> quad
+//   pass 1 without:                          17.9 / 19.3 / -    -> stacked
+//   final pass writing adv, ret, adv_n:      30.5 / 33.6 / 31.7 -> stacked
+//   final pass writing adv, ret:             26.6 / 30.4 / 23.0 -> solo
+// (solo tiles are 16 steps x 4 envs per thread, 256 env-groups per tile: the
+// same tile boundaries in T, so their carries are interchangeable.)
 GaePlan make_plan(long T, long N, int vw) {
   GaePlan p;
   p.vw = vw;
-  p.L = vw == 4 ? 4 : 16;
   p.Q = N / vw;
-  p.Qw = (int)std::min<long>(64, (long)pow2_ceil((unsigned)std::min<long>(p.Q, 64)));
-  p.Sw = kBlock / p.Qw;
-  p.span = (long)p.Sw * p.L;
+  p.fin_solo.Tq = 0;
+  if (vw == 1) {
+    const int Qw = (int)std::min<long>(64, (long)pow2_ceil((unsigned)std::min<long>(p.Q, 64)));
+    p.scan = p.fin = make_geom(p.Q, 16, Qw);
+  } else if (p.Q < kBlock) {
+    const int Qw = (int)std::min<long>(64, (long)pow2_ceil((unsigned)std::min<long>(p.Q, 64)));
+    p.scan = p.fin = make_geom(p.Q, 4, Qw);
+  } else {
+    p.scan = make_geom(p.Q, 4, 64);
+    p.fin = make_geom(p.Q, 4, 64);
+    p.fin_solo = make_geom(p.Q, 16, kBlock);
+  }
+  p.span = (long)p.fin.Sw * p.fin.L;
   p.Tt = (T + p.span - 1) / p.span;
-  p.Tq = (p.Q + p.Qw - 1) / p.Qw;
   return p;
 }
 
@@ -208,20 +254,50 @@ __device__ __forceinline__ unsigned load_done(const uint8_t* p) {
   }
 }
 
-template <int VW, int L, int kMode>
+// Tile layouts: how a tile's Sw segments map to the workgroup's threads.
+enum TileLayout {
+  kStacked = 0,  // segment s of env-group q is thread s*Qw + q; LDS scan across waves
+  kSoloTile = 1, // Sw == 1: the thread's segment is the tile
+  kQuadTile = 2, // Sw == 4: segment s of env-group q is thread 4q + s; the scan and
+                 // the tile sums are DPP moves inside each quad of lanes, no LDS
+};
+
+// Lane i of each quad takes lane min(i + off, 3): quad_perm [1,2,3,3] for
+// off = 1, [2,3,3,3] for off = 2.
+template <int kOff>
+struct QuadCtrl {
+  static_assert(kOff == 1 || kOff == 2, "quad offsets 1 and 2");
+  static constexpr int value = kOff == 1 ? 0xF9 : 0xFE;
+};
+template <int kOff>
+__device__ __forceinline__ double quad_down(double x) {
+  return dpp_move<QuadCtrl<kOff>::value>(x);
+}
+template <int kOff>
+__device__ __forceinline__ float quad_down(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                               QuadCtrl<kOff>::value, 0xF, 0xF,
+                                                               false));
+}
+
+template <int VW, int L, int kLayout, int kMode>
 __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
+  constexpr bool kSolo = kLayout == kSoloTile;
+  constexpr bool kQuad = kLayout == kQuadTile;
+  constexpr bool kLds = kLayout == kStacked;
   constexpr bool kIsFinal = kMode >= kFinal;
   constexpr bool kTileStats = kMode == kSummaryStats;
-  static_assert(L * VW <= 32, "done bits must fit one word");
-  __shared__ double s_a[kBlock * VW];
-  __shared__ double s_p[kBlock * VW];
+  static_assert(L * VW <= 64, "done bits must fit two words");
+  using DoneBits = typename std::conditional<(L * VW > 32), unsigned long long, unsigned>::type;
+  __shared__ double s_a[kLds ? kBlock * VW : 1];
+  __shared__ double s_p[kLds ? kBlock * VW : 1];
 
   const long bid = blockIdx.x;
   const long tile_t = bid / a.Tq;
   const long tile_q = bid - tile_t * a.Tq;
   const int tid = threadIdx.x;
-  const int q = tid % a.Qw;
-  const int s = tid / a.Qw;
+  const int q = kQuad ? tid >> 2 : tid % a.Qw;
+  const int s = kQuad ? tid & 3 : tid / a.Qw;
   const long col = tile_q * a.Qw + q;
   const bool col_ok = col < a.Q;
   const long env0 = col * VW;
@@ -230,7 +306,7 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
   const int nvalid = col_ok ? (int)(remain <= 0 ? 0 : (remain < L ? remain : L)) : 0;
 
   float r[L][VW], v[L][VW], nv[VW];
-  unsigned dbits = 0;
+  DoneBits dbits = 0;
 #pragma unroll
   for (int i = 0; i < L; ++i) {
     if (i < nvalid) {
@@ -242,7 +318,7 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
 #pragma unroll
         for (int k = 0; k < VW; ++k) v[i][k] = 0.0f;
       }
-      dbits |= load_done<VW>(a.d + off) << (i * VW);
+      dbits |= (DoneBits)load_done<VW>(a.d + off) << (i * VW);
     } else {
 #pragma unroll
       for (int k = 0; k < VW; ++k) r[i][k] = v[i][k] = 0.0f;
@@ -297,7 +373,22 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
   }
 
   // Reverse inclusive scan over the Sw segments of the tile:
-  // (a_s, P_s) <- (a_s + P_s*a_{s+off}, P_s*P_{s+off}).
+  // (a_s, P_s) <- (a_s + P_s*a_{s+off}, P_s*P_{s+off}).  (Solo tiles: the
+  // segment is the tile; quad tiles scan with DPP moves.)
+  if constexpr (kQuad) {
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      {
+        const double pa = quad_down<1>(ia[k]), pp = quad_down<1>(ip[k]);
+        if (s + 1 < 4) { ia[k] = ia[k] + ip[k] * pa; ip[k] = ip[k] * pp; }
+      }
+      {
+        const double pa = quad_down<2>(ia[k]), pp = quad_down<2>(ip[k]);
+        if (s + 2 < 4) { ia[k] = ia[k] + ip[k] * pa; ip[k] = ip[k] * pp; }
+      }
+    }
+  }
+  if constexpr (kLds) {
 #pragma unroll
   for (int k = 0; k < VW; ++k) { s_a[k * kBlock + tid] = ia[k]; s_p[k * kBlock + tid] = ip[k]; }
   for (int off = 1; off < a.Sw; off <<= 1) {
@@ -323,6 +414,7 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
     }
   }
   __syncthreads();
+  }
 
   if constexpr (!kIsFinal) {
     if (s == 0 && col_ok) {
@@ -330,7 +422,50 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
       for (int k = 0; k < VW; ++k)
         a.summary[tile_t * a.N + env0 + k] = make_double2(ia[k], ip[k]);
     }
-    if constexpr (kTileStats) {
+    if constexpr (kTileStats && kQuad) {
+      // Re-base on the tile end with the composite (An, Pn) of the later
+      // segments (the scanned value of lane s+1), then sum the four lanes:
+      // (x0 + x2) + (x1 + x3), in lane 0 of the quad.
+      float q5[5][VW];
+#pragma unroll
+      for (int k = 0; k < VW; ++k) {
+        const double na = quad_down<1>(ia[k]), np = quad_down<1>(ip[k]);
+        const float An = s + 1 < 4 ? (float)na : 0.0f;
+        const float Pn = s + 1 < 4 ? (float)np : 1.0f;
+        q5[0][k] = sa[k] + An * sP[k];
+        q5[1][k] = Pn * sP[k];
+        q5[2][k] = saa[k] + 2.0f * An * saP[k] + An * An * sPP[k];
+        q5[3][k] = Pn * (saP[k] + An * sPP[k]);
+        q5[4][k] = Pn * Pn * sPP[k];
+      }
+#pragma unroll
+      for (int j = 0; j < 5; ++j)
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          q5[j][k] += quad_down<2>(q5[j][k]);
+          q5[j][k] += quad_down<1>(q5[j][k]);
+        }
+      if (s == 0 && col_ok) {
+        const long plane = a.Tt * a.N;
+#pragma unroll
+        for (int j = 0; j < 5; ++j) store_f<VW>(a.tstat + j * plane + tile_t * a.N + env0, q5[j]);
+      }
+    } else if constexpr (kTileStats && kSolo) {
+      if (col_ok) {
+        const long plane = a.Tt * a.N;
+        float q5[5][VW];
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          q5[0][k] = sa[k];
+          q5[1][k] = sP[k];
+          q5[2][k] = saa[k];
+          q5[3][k] = saP[k];
+          q5[4][k] = sPP[k];
+        }
+#pragma unroll
+        for (int j = 0; j < 5; ++j) store_f<VW>(a.tstat + j * plane + tile_t * a.N + env0, q5[j]);
+      }
+    } else if constexpr (kTileStats) {
       // Re-base the segment sums on the tile end: with (An, Pn) the composite
       // of the later segments of the tile, a' = a + An P and P' = Pn P.
       float q5[5][VW];
@@ -377,7 +512,14 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
 #pragma unroll
     for (int k = 0; k < VW; ++k) {
       const double C = (a.carry && col_ok) ? a.carry[tile_t * a.N + env0 + k] : 0.0;
-      if (s + 1 < a.Sw)
+      double na = 0.0, np = 1.0;
+      if constexpr (kQuad) {
+        na = quad_down<1>(ia[k]);
+        np = quad_down<1>(ip[k]);
+      }
+      if (kQuad && s + 1 < 4)
+        cin[k] = na + np * C;
+      else if (kLds && s + 1 < a.Sw)
         cin[k] = s_a[k * kBlock + tid + a.Qw] + s_p[k * kBlock + tid + a.Qw] * C;
       else
         cin[k] = C;
@@ -586,23 +728,38 @@ __global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* _
   }
 }
 
-template <int VW, int L>
+// Pass kernels by (VW, L, solo) geometry.
+template <int kMode>
+const void* tile_kernel(int vw, const PassGeom& g) {
+  if (vw == 1) return (const void*)gae_tile_kernel<1, 16, kStacked, kMode>;
+  if (g.solo) return (const void*)gae_tile_kernel<4, 16, kSoloTile, kMode>;
+  if (g.quad) return (const void*)gae_tile_kernel<4, 4, kQuadTile, kMode>;
+  return (const void*)gae_tile_kernel<4, 4, kStacked, kMode>;
+}
+
+int launch_tile(const void* kern, const PassGeom& g, GaeArgs a, long Tt, hipStream_t stream) {
+  a.Tq = g.Tq;
+  a.Qw = g.Qw;
+  a.Sw = g.Sw;
+  void* args[] = {&a};
+  return hip_status(hipLaunchKernel(kern, dim3((unsigned)(Tt * g.Tq)), dim3(kBlock), args, 0,
+                                    stream));
+}
+
 int launch_gae(const GaePlan& p, GaeArgs a, bool norm, hipStream_t stream) {
-  const long blocks = p.blocks();
   a.Q = p.Q;
-  a.Tq = p.Tq;
   a.Tt = p.Tt;
-  a.Qw = p.Qw;
-  a.Sw = p.Sw;
   a.span = p.span;
   int st;
-  const dim3 grid((unsigned)blocks), block(kBlock);
   if (p.Tt > 1) {
-    if (norm)
-      hipLaunchKernelGGL((gae_tile_kernel<VW, L, kSummaryStats>), grid, block, 0, stream, a);
-    else
-      hipLaunchKernelGGL((gae_tile_kernel<VW, L, kSummary>), grid, block, 0, stream, a);
-    if ((st = last_launch_status())) return st;
+    // pass 1: quad tiles when the tile sums are needed (their DPP tree beats
+    // the LDS tree), stacked tiles otherwise (measured faster without sums)
+    PassGeom g1 = p.scan;
+    g1.quad = norm && p.vw == 4 && g1.Qw == 64 && g1.Sw == 4 && p.fin_solo.Tq > 0;
+    if ((st = launch_tile(norm ? tile_kernel<kSummaryStats>(p.vw, g1)
+                               : tile_kernel<kSummary>(p.vw, g1),
+                          g1, a, p.Tt, stream)))
+      return st;
     const CarryPlan cp = make_carry_plan(p.Tt, a.N);
     const dim3 cgrid((unsigned)cp.groups, (unsigned)cp.nchunks);
     if (cp.nchunks > 1) {
@@ -616,26 +773,25 @@ int launch_gae(const GaePlan& p, GaeArgs a, bool norm, hipStream_t stream) {
                        cp.nchunks, norm ? a.tstat : nullptr, a.partial, a.T, p.span);
     if ((st = last_launch_status())) return st;
     if (!norm) {
-      hipLaunchKernelGGL((gae_tile_kernel<VW, L, kFinal>), grid, block, 0, stream, a);
-      return last_launch_status();
+      const PassGeom& gf = p.final_geom(false);
+      return launch_tile(tile_kernel<kFinal>(p.vw, gf), gf, a, p.Tt, stream);
     }
     // mean/std from the carry-scan partials, then one pass writes adv, ret, adv_n
     if ((st = launch_finalize_stats(a.partial, cp.groups * cp.nchunks, a.eps, a.hdr, a.stats_out,
                                     stream)))
       return st;
-    hipLaunchKernelGGL((gae_tile_kernel<VW, L, kFinalNorm>), grid, block, 0, stream, a);
-    return last_launch_status();
+    return launch_tile(tile_kernel<kFinalNorm>(p.vw, p.fin), p.fin, a, p.Tt, stream);
   }
   a.carry = nullptr;
   if (!norm) {
-    hipLaunchKernelGGL((gae_tile_kernel<VW, L, kFinal>), grid, block, 0, stream, a);
-    return last_launch_status();
+    const PassGeom& gf = p.final_geom(false);
+    return launch_tile(tile_kernel<kFinal>(p.vw, gf), gf, a, p.Tt, stream);
   }
   // single-tile horizon: partials from the final pass, then the elementwise normaliser
-  hipLaunchKernelGGL((gae_tile_kernel<VW, L, kFinalPartials>), grid, block, 0, stream, a);
-  if ((st = last_launch_status())) return st;
-  return launch_normalize(a.partial, blocks, a.eps, a.adv, a.adv_n, a.T * a.N, a.hdr, a.stats_out,
-                          stream);
+  if ((st = launch_tile(tile_kernel<kFinalPartials>(p.vw, p.fin), p.fin, a, p.Tt, stream)))
+    return st;
+  return launch_normalize(a.partial, p.Tt * p.fin.Tq, a.eps, a.adv, a.adv_n, a.T * a.N, a.hdr,
+                          a.stats_out, stream);
 }
 
 int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
@@ -680,7 +836,7 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
   a.adv_n = adv_norm_out;
   a.tstat = reinterpret_cast<float*>(ws + l.tstat);
 
-  return vec ? launch_gae<4, 4>(p, a, norm, stream) : launch_gae<1, 16>(p, a, norm, stream);
+  return launch_gae(p, a, norm, stream);
 }
 
 }  // namespace
