@@ -311,9 +311,22 @@ __global__ void __launch_bounds__(kFinalBlock) loss_finalize_kernel(LossArgs a, 
 
 // Action index of a row, or -1 when it lies outside [0, A).
 template <typename ActT>
-__device__ __forceinline__ int row_action(const LossArgs& a, long row) {
-  const long act = (long)reinterpret_cast<const ActT*>(a.actions)[row];
+__device__ __forceinline__ int action_index(const LossArgs& a, ActT raw) {
+  const long act = (long)raw;
   return (act >= 0 && act < a.A) ? (int)act : -1;
+}
+
+template <typename ActT>
+__device__ __forceinline__ int row_action(const LossArgs& a, long row) {
+  return action_index<ActT>(a, reinterpret_cast<const ActT*>(a.actions)[row]);
+}
+
+// The raw action of a row, loaded without inspecting it: a prefetch that
+// validated it on the spot would make the compiler wait for every load in
+// flight, the prefetched tile included.
+template <typename ActT>
+__device__ __forceinline__ ActT row_action_raw(const LossArgs& a, long row) {
+  return __builtin_nontemporal_load(reinterpret_cast<const ActT*>(a.actions) + row);
 }
 
 // ---------------------------------------------------------------------------
@@ -395,7 +408,7 @@ struct CatPrefetch {
   f4 x[PF];
   float tail;   // element n4*4 + tid of a tile whose size is not a multiple of 4
   RowIn in;
-  int ai;
+  ActT act;     // raw action (validated when the tile is processed)
   int nrows;
 };
 
@@ -413,11 +426,10 @@ __device__ __forceinline__ void cat_prefetch(const LossArgs& a, long tile, CatPr
     if (i < n4) p.x[k] = ldnt(src + i);
   }
   if (tid < count - (n4 << 2)) p.tail = ldnt(a.x + row0 * a.A + (n4 << 2) + tid);
-  p.ai = -1;
   if (tid < p.nrows) {
     const long row = row0 + tid;
     p.in = load_row(a, row);
-    p.ai = row_action<ActT>(a, row);
+    p.act = row_action_raw<ActT>(a, row);
   }
 }
 
@@ -459,7 +471,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_pipe_kernel(LossArgs a, long 
       s_tile[r * AS + (e - r * A)] = pf.tail;
     }
     const RowIn in = pf.in;
-    const int ai = pf.ai;
+    const int ai = tid < nrows ? action_index<ActT>(a, pf.act) : -1;
     const long row0 = tile * kBlock;
     __syncthreads();
 
@@ -519,93 +531,172 @@ __global__ void __launch_bounds__(kBlock) loss_cat_pipe_kernel(LossArgs a, long 
 }
 
 // ---------------------------------------------------------------------------
-// Categorical, A <= MAXA and A % 4 != 0, 16-byte-aligned inputs: the
-// register-resident form.  The tile is kept in LDS in its global layout
-// (256 dense rows of A floats), so staging is one ds_write_b128 / ds_read_b128
-// per float4 with no index arithmetic; for A % 4 != 0 a row stride of A words
-// puts the 32 lanes of a half-wave on distinct banks (A odd) or at most two
-// lanes per bank (A = 2 mod 4).  Each thread then reads its row into
-// registers once and evaluates, per logit,
+// Categorical, A <= MAXA and A % 4 != 0, 16-byte-aligned inputs: wave tiles,
+// the register-resident form.  Each wave owns a tile of 64 consecutive rows
+// (one contiguous span of 64*A floats, 16*A float4) and stages it through its
+// own slice of LDS in its global layout (one ds_write_b128 / ds_read_b128 per
+// float4, no index arithmetic), so the transposition between the coalesced
+// float4 layout and one-row-per-lane needs no workgroup barrier: a wave's LDS
+// operations execute in issue order, and a wave-level compiler barrier keeps
+// the compiler from moving LDS accesses across the hand-offs.  Waves stream
+// independently, each with the next tile's loads in flight during the
+// current tile's math.  Each lane reads its row into registers once and
+// evaluates, per logit,
 //     t_j = max(z_j - m, -FLT_MAX),  e_j = exp(t_j),  s += e_j,  S += e_j t_j
 //     dlogit_j = (e_j / s) * (ec/B * t_j + K),  K = ec/B * (H - log s) - g_lp
-// which is the gradient above rearranged (log p_j = t_j - log s); the
-// 1[j == a] * g_lp term is added by one LDS read-modify-write per row.  That
-// is ~10 VALU operations per logit against ~40 for the LDS-pass form, which
-// was VALU-bound on MI355X.
+// which is the gradient of the LDS-pass form rearranged (log p_j = t_j -
+// log s); the 1[j == a] * g_lp term is added by one LDS read-modify-write per
+// row.  That is ~10 VALU operations per logit against ~40 for the LDS-pass
+// form, which was VALU-bound on MI355X.  KA > 0 fixes A at compile time (no
+// per-logit predicates); KA == 0 takes A from the arguments, A <= MAXA.
+//
+// Full tiles run branch-free: lane l moves float4 min(64k + l, 16A - 1) for
+// k < ceil(A/4) (lanes past the end repeat the last float4: same address,
+// same value), the action is validated only when used, and vf_clip is a
+// template parameter.  With no data-dependent branch between a tile's
+// prefetch and the next tile's staging, the compiler waits only for the
+// prefetched loads there, not for the previous tile's stores (on gfx9 the
+// vector memory counter counts stores too).  The last, partial tile
+// (B mod 64 rows) is processed after the loop with predicated accesses.
 // ---------------------------------------------------------------------------
-// KA > 0 fixes A at compile time (no per-logit predicates); KA == 0 takes
-// A from the arguments, A <= MAXA.
-template <typename ActT, int KA, int MAXA>
-__global__ void __launch_bounds__(kBlock) loss_cat_dense_kernel(LossArgs a, long ntiles) {
-  constexpr int PF = (MAXA + 3) / 4;
-  constexpr float kLog2e = 1.4426950408889634f;
-  extern __shared__ float s_tile[];
-  f4* s_tile4 = reinterpret_cast<f4*>(s_tile);
-  const int A = KA > 0 ? KA : a.A;
-  const float ge = a.ec * a.inv_b;
-  const int tid = threadIdx.x;
-  double acc[5] = {0, 0, 0, 0, 0};
-  CatPrefetch<ActT, PF> pf;
-  long tile = blockIdx.x;
-  if (tile < ntiles) cat_prefetch<ActT, PF>(a, tile, pf);
+template <bool kVclip>
+__device__ __forceinline__ RowIn load_row_t(const LossArgs& a, long row) {
+  RowIn r;
+  r.old_lp = ldnt(a.old_lp + row);
+  r.adv = ldnt(a.adv + row);
+  r.ret = ldnt(a.ret + row);
+  r.v = ldnt(a.val + row);
+  r.vo = kVclip ? ldnt(a.old_val + row) : 0.0f;
+  return r;
+}
 
-  for (; tile < ntiles; tile += gridDim.x) {
-    const int nrows = pf.nrows;
-    const int count = nrows * A;
-    const int n4 = count >> 2;
+template <typename ActT, int PF>
+struct WavePrefetch {
+  f4 x[PF];
+  RowIn in;
+  ActT act;  // raw action (validated when the tile is processed)
+};
+
+template <typename ActT, int PF, bool kVclip>
+__device__ __forceinline__ void wave_prefetch(const LossArgs& a, long wt, int lane, int n4,
+                                              WavePrefetch<ActT, PF>& p) {
+  const long row0 = wt * kWave;
+  const f4* src = reinterpret_cast<const f4*>(a.x + row0 * a.A);
+#pragma unroll
+  for (int k = 0; k < PF; ++k) p.x[k] = ldnt(src + std::min(k * kWave + lane, n4 - 1));
+  // keep the logits loads ahead of the row loads in every copy of this
+  // prefetch, so the staging wait can leave the row loads (and any later
+  // stores) outstanding on every path into the loop
+  __builtin_amdgcn_sched_barrier(0);
+  p.in = load_row_t<kVclip>(a, row0 + lane);
+  p.act = row_action_raw<ActT>(a, row0 + lane);
+}
+
+// Orders this wave's LDS accesses before and after a cross-lane hand-off.
+__device__ __forceinline__ void wave_lds_handoff() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One row from LDS (zr: A logits) to its gradient in place; accumulates the
+// row's loss terms (the formulas above).
+template <int KA, int MAXA>
+__device__ __forceinline__ void cat_row_math(const LossArgs& a, float* zr, int A, long row,
+                                             const RowIn& in, int ai, float ge,
+                                             double (&acc)[5]) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  float t[MAXA], e[MAXA];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < MAXA; ++j)
+    if (j < A) {
+      t[j] = zr[j];
+      m = fmaxf(m, t[j]);
+    }
+  float s = 0.0f, S = 0.0f;
+#pragma unroll
+  for (int j = 0; j < MAXA; ++j)
+    if (j < A) {
+      const float tj = fmaxf(t[j] - m, -FLT_MAX);
+      const float ej = __builtin_amdgcn_exp2f(tj * kLog2e);
+      t[j] = tj;
+      e[j] = ej;
+      s += ej;
+      S = fmaf(ej, tj, S);
+    }
+  const float log_s = logf(s);
+  const float inv_s = 1.0f / s;
+  const float H = log_s - S * inv_s;
+  const float lp = ai >= 0 ? (zr[ai] - m) - log_s : __builtin_nanf("");
+  const RowOut o = ppo_row(a, row, in, lp);
+  const float K = ge * (H - log_s) - o.g_lp;
+#pragma unroll
+  for (int j = 0; j < MAXA; ++j)
+    if (j < A) zr[j] = (e[j] * inv_s) * fmaf(ge, t[j], K);
+  if (ai >= 0) zr[ai] += o.g_lp;
+  accumulate(acc, o, H);
+}
+
+template <typename ActT, int KA, int MAXA, bool kVclip>
+__global__ void __launch_bounds__(kBlock) loss_cat_wtile_kernel(LossArgs a, long nfull) {
+  constexpr int PF = (MAXA + 3) / 4;
+  constexpr int kWavesPerBlock = kBlock / kWave;
+  extern __shared__ float s_lds[];
+  const int A = KA > 0 ? KA : a.A;
+  const int n4 = (kWave / 4) * A;  // float4 per full tile
+  const float ge = a.ec * a.inv_b;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  float* s_tile = s_lds + wid * kWave * A;  // 256*A bytes: 16-byte aligned
+  f4* s_tile4 = reinterpret_cast<f4*>(s_tile);
+  double acc[5] = {0, 0, 0, 0, 0};
+  WavePrefetch<ActT, PF> pf;
+  const long wstride = (long)gridDim.x * kWavesPerBlock;
+  long wt = (long)blockIdx.x * kWavesPerBlock + wid;
+  if (wt < nfull) wave_prefetch<ActT, PF, kVclip>(a, wt, lane, n4, pf);
+
+  for (; wt < nfull; wt += wstride) {
+#pragma unroll
+    for (int k = 0; k < PF; ++k) s_tile4[std::min(k * kWave + lane, n4 - 1)] = pf.x[k];
+    const RowIn in = pf.in;
+    const int ai = action_index<ActT>(a, pf.act);
+    const long row0 = wt * kWave;
+    wave_lds_handoff();
+
+    const long next = wt + wstride;
+    if (next < nfull) wave_prefetch<ActT, PF, kVclip>(a, next, lane, n4, pf);
+
+    cat_row_math<KA, MAXA>(a, s_tile + lane * A, A, row0 + lane, in, ai, ge, acc);
+    wave_lds_handoff();
+    f4* dst = reinterpret_cast<f4*>(a.dx + row0 * A);
 #pragma unroll
     for (int k = 0; k < PF; ++k) {
-      const int i = k * kBlock + tid;
-      if (i < n4) s_tile4[i] = pf.x[k];
+      const int i = std::min(k * kWave + lane, n4 - 1);
+      stnt(s_tile4[i], dst + i);
     }
-    if (tid < count - (n4 << 2)) s_tile[(n4 << 2) + tid] = pf.tail;
-    const RowIn in = pf.in;
-    const int ai = pf.ai;
-    const long row0 = tile * kBlock;
-    __syncthreads();
+    wave_lds_handoff();
+  }
 
-    const long next = tile + gridDim.x;
-    if (next < ntiles) cat_prefetch<ActT, PF>(a, next, pf);
-
-    if (tid < nrows) {
-      const long row = row0 + tid;
-      float* zr = s_tile + tid * A;
-      float t[MAXA], e[MAXA];
-      float m = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < MAXA; ++j)
-        if (j < A) {
-          t[j] = zr[j];
-          m = fmaxf(m, t[j]);
-        }
-      float s = 0.0f, S = 0.0f;
-#pragma unroll
-      for (int j = 0; j < MAXA; ++j)
-        if (j < A) {
-          const float tj = fmaxf(t[j] - m, -FLT_MAX);
-          const float ej = __builtin_amdgcn_exp2f(tj * kLog2e);
-          t[j] = tj;
-          e[j] = ej;
-          s += ej;
-          S = fmaf(ej, tj, S);
-        }
-      const float log_s = logf(s);
-      const float inv_s = 1.0f / s;
-      const float H = log_s - S * inv_s;
-      const float lp = ai >= 0 ? (zr[ai] - m) - log_s : __builtin_nanf("");
-      const RowOut o = ppo_row(a, row, in, lp);
-      const float K = ge * (H - log_s) - o.g_lp;
-#pragma unroll
-      for (int j = 0; j < MAXA; ++j)
-        if (j < A) zr[j] = (e[j] * inv_s) * fmaf(ge, t[j], K);
-      if (ai >= 0) zr[ai] += o.g_lp;
-      accumulate(acc, o, H);
+  // the partial last tile, by the one wave whose sequence reaches it
+  const long row0 = wt * kWave;
+  if (wt == nfull && row0 < a.B) {
+    const int nrows = (int)(a.B - row0);
+    const int count = nrows * A;
+    const int m4 = count >> 2;
+    const f4* src = reinterpret_cast<const f4*>(a.x + row0 * A);
+    for (int i = lane; i < m4; i += kWave) s_tile4[i] = ldnt(src + i);
+    if (lane < count - (m4 << 2)) s_tile[(m4 << 2) + lane] = ldnt(a.x + row0 * A + (m4 << 2) + lane);
+    wave_lds_handoff();
+    if (lane < nrows) {
+      const long row = row0 + lane;
+      cat_row_math<KA, MAXA>(a, s_tile + lane * A, A, row, load_row_t<kVclip>(a, row),
+                             row_action<ActT>(a, row), ge, acc);
     }
-    __syncthreads();
+    wave_lds_handoff();
     f4* dst = reinterpret_cast<f4*>(a.dx + row0 * A);
-    for (int i = tid; i < n4; i += kBlock) stnt(s_tile4[i], dst + i);
-    if (tid < count - (n4 << 2)) a.dx[row0 * A + (n4 << 2) + tid] = s_tile[(n4 << 2) + tid];
-    __syncthreads();
+    for (int i = lane; i < m4; i += kWave) stnt(s_tile4[i], dst + i);
+    if (lane < count - (m4 << 2)) a.dx[row0 * A + (m4 << 2) + lane] = s_tile[(m4 << 2) + lane];
   }
   store_scalar_partials(a, acc);
 }
@@ -959,9 +1050,13 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
     size_t lds = (size_t)kBlock * (A | 1) * sizeof(float);
     const void* kern;
     const bool dense = vec && (A % 4) != 0 && A <= 20;
-#define PPO_DENSE(KA, M)                                                          \
-  (actions_are_int64 ? (const void*)loss_cat_dense_kernel<int64_t, KA, M>         \
-                     : (const void*)loss_cat_dense_kernel<int32_t, KA, M>)
+    const bool vclip = a.use_vclip != 0;
+#define PPO_DENSE(KA, M)                                                                 \
+  (actions_are_int64                                                                     \
+       ? (vclip ? (const void*)loss_cat_wtile_kernel<int64_t, KA, M, true>               \
+                : (const void*)loss_cat_wtile_kernel<int64_t, KA, M, false>)             \
+       : (vclip ? (const void*)loss_cat_wtile_kernel<int32_t, KA, M, true>               \
+                : (const void*)loss_cat_wtile_kernel<int32_t, KA, M, false>))
     if (dense && A == 2)
       kern = PPO_DENSE(2, 2);
     else if (dense && A == 3)
@@ -1000,7 +1095,8 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
     if (dense) lds = (size_t)kBlock * A * sizeof(float);
     // one wave of resident workgroups looping over the tiles
     blocks = std::min(blocks, resident_blocks(kern, kBlock, lds, blocks));
-    void* args[] = {&a, const_cast<long*>(&tiles)};
+    const long wfull = B / kWave;  // full wave tiles
+    void* args[] = {&a, const_cast<long*>(dense ? &wfull : &tiles)};
     st = hip_status(hipLaunchKernel(kern, grid_of(blocks), dim3(kBlock), args, lds, stream));
     if (st) return st;
   } else {
