@@ -40,6 +40,7 @@ GAE_BYTES = 21       # r 4 + V 4 + done 1 in; adv 4 + ret 4 + adv_n 4 out
 LOSS_CAT_BYTES = 172  # logits 72 + 6 x 4 per-row inputs in; dlogits 72 + dvalue 4 out
 GAUSS_BYTES = 96     # mu 24 + actions 24 + 5 x 4 in; dmu 24 + dvalue 4 out
 SCAN_BYTES = 17      # r, V, done in; adv, ret out
+LOSS_CAT_A2_BYTES = 44  # A = 2: logits 8 + 6 x 4 in; dlogits 8 + dvalue 4 out
 
 
 def parse_args():
@@ -181,6 +182,19 @@ def cpu_baseline(torch, x, budget_s):
         if time.perf_counter() - t0 >= budget_s:
             break
     dt = time.perf_counter() - t0
+    # the reference's own scalar loop (ppo.py:177-190 semantics) at config 1's
+    # shape: one T=128 episode per env column, N=8 columns, ~1 s of repeats
+    g = np.random.default_rng(24)
+    r1 = np.ones((128, 8))
+    v1 = g.standard_normal((128, 8))
+    d1 = g.random((128, 8)) < 1 / 200
+    n1, t1 = 0, time.perf_counter()
+    while time.perf_counter() - t1 < 1.0:
+        for col in range(8):
+            ref.advantages_python(r1[:, col].tolist(), d1[:, col].tolist(), v1[:, col].tolist(),
+                                  0.99, 0.95)
+        n1 += 128 * 8
+    scalar_rate = n1 / (time.perf_counter() - t1)
     return {
         "value": done_samples / dt,
         "unit": "samples/s",
@@ -189,6 +203,8 @@ def cpu_baseline(torch, x, budget_s):
         "sample": f"{reps} x (T={T} x {n_env} envs = {B} samples: GAE+norm+loss fwd/bwd, A=18)",
         "os_cpu_count": os.cpu_count(),
         "affinity_cores": len(os.sched_getaffinity(0)),
+        "python_scalar_gae": {"value": round(scalar_rate), "unit": "elements/s", "cores": 1,
+                              "sample": "oracle.advantages_python, T=128 x N=8 (config 1)"},
     }
 
 
@@ -276,6 +292,15 @@ def suite(torch, lib, dev):
         w.data_ptr(), w.numel(), stream)
     fn()
     out.append(("config5_loss_gauss", B, GAUSS_BYTES, time_events(torch, fn, 30)))
+    del mu, acts, rows, dmu, dls, dv, w
+    # the north-star step with A = 2 (CartPole's action count): GAE+norm + loss
+    x = synthetic_rollout(torch, dev, T_STEPS, N_ENVS, 2, seed=26)
+    st = Step(torch, lib, x, dev)
+    st.gae()
+    st.loss()
+    out.append(("north_star_A2_loss", st.B, LOSS_CAT_A2_BYTES, time_events(torch, st.loss, 30)))
+    out.append(("north_star_A2_step", st.B, GAE_BYTES + LOSS_CAT_A2_BYTES,
+                time_events(torch, lambda: (st.gae(), st.loss()), 30)))
     for name, units, bpu, t in out:
         gbs = units * bpu / t / 1e9
         print(json.dumps({"suite": name, "units": units, "bytes_per_unit": bpu,

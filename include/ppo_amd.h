@@ -198,6 +198,37 @@ int ppo_gather_rows(const int64_t* index, int64_t B, int64_t n_src, int32_t narr
                     const void* const* src, const int32_t* row_bytes, void* const* dst,
                     void* stream);
 
+/*
+ * Batched action selection of PPOAgent.select_action (rl/deep/agents/ppo.py:
+ * 65-79: Categorical(logits=policy(obs)).sample(), .log_prob(action),
+ * value(obs)) for N environments at once, written straight into row t of a
+ * [T,N] rollout buffer by passing pointers to that row.  For row n of
+ * logits [N,A] and the caller's uniform u_n in [0,1):
+ *   actions_out[n] = min{ j : u_n < sum_{k<=j} softmax(logits[n])_k }
+ *                    (inverse CDF; A-1 if rounding leaves u_n above the total)
+ *   logp_out[n]    = log softmax(logits[n])[actions_out[n]]
+ *   values_out[n]  = values[n]            (skipped when either is NULL)
+ * actions_out is int32.  Uniforms come from the caller (e.g. torch.rand on
+ * the device with a seeded generator), so a rollout is reproducible.  No
+ * workspace; no host synchronisation.
+ */
+int ppo_sample_cat_f32(const float* logits, int64_t N, int32_t A, const float* uniforms,
+                       int32_t* actions_out, float* logp_out, const float* values,
+                       float* values_out, void* stream);
+
+/*
+ * The continuous counterpart (Normal(mu, exp(log_std)).sample() and
+ * .log_prob(action).sum(-1)) for the Gaussian policy: with the caller's
+ * standard normals eps [N,D],
+ *   actions_out[n,d] = mu[n,d] + exp(log_std[d]) * eps[n,d]
+ *   logp_out[n]      = sum_d -(a-mu)^2/(2 sigma_d^2) - log sigma_d - log sqrt(2 pi)
+ *   values_out[n]    = values[n]          (skipped when either is NULL)
+ * D <= 24.
+ */
+int ppo_sample_gauss_f32(const float* mu, const float* log_std, int64_t N, int32_t D,
+                         const float* normals, float* actions_out, float* logp_out,
+                         const float* values, float* values_out, void* stream);
+
 #define PPO_ADAM_MAX_TENSORS 32
 
 typedef struct ppo_adam_params {

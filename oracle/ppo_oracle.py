@@ -330,6 +330,38 @@ def loss_gaussian_reference(
 # ---------------------------------------------------------------------------
 # The whole update, for end-to-end parity of the host driver
 # ---------------------------------------------------------------------------
+
+
+# ---------------------------------------------------------------------------
+# Action selection
+# ---------------------------------------------------------------------------
+def sample_categorical_reference(logits: np.ndarray, uniforms: np.ndarray):
+    """Inverse-CDF sampling of Categorical(logits=...) at given uniforms, fp64.
+
+    PPOAgent.select_action (ppo.py:65-79) draws `Categorical(logits).sample()`
+    and keeps `.log_prob(action)`; the batched kernel draws the same
+    distribution by inverting the CDF at a caller-supplied uniform, which this
+    restates: action = min{ j : u < cumsum(softmax(z))_j } (A-1 if none), and
+    log_prob = log_softmax(z)[action].  Returns (actions int64 [N], log_probs
+    float64 [N], margin [N]) where margin is the distance from u to the
+    nearest CDF boundary (rows with a tiny margin may round differently in
+    fp32).  Pinned in tests/test_oracle.py by known answers, by the empirical
+    frequencies matching softmax, and by the log-probs matching
+    torch.distributions.Categorical in fp64.
+    """
+    z = np.asarray(logits, dtype=np.float64)
+    u = np.asarray(uniforms, dtype=np.float64)
+    zs = z - z.max(axis=1, keepdims=True)
+    p = np.exp(zs)
+    p /= p.sum(axis=1, keepdims=True)
+    cdf = np.cumsum(p, axis=1)
+    actions = (u[:, None] >= cdf).sum(axis=1)
+    actions = np.minimum(actions, z.shape[1] - 1)
+    logp = zs - np.log(np.exp(zs).sum(axis=1, keepdims=True))
+    margin = np.abs(cdf - u[:, None]).min(axis=1)
+    return actions, logp[np.arange(z.shape[0]), actions], margin
+
+
 @dataclass(frozen=True)
 class OracleConfig:
     """Defaults of TrainingConfig (rl/deep/type.py:30-41) and PPOConfig

@@ -24,7 +24,7 @@ def declared_functions():
 def test_header_declares_expected_functions():
     names = declared_functions()
     assert "ppo_gae_f32" in names and "ppo_loss_cat_f32" in names
-    assert len(names) == 14
+    assert len(names) == 16
 
 
 def test_library_exports_every_declared_symbol():
@@ -83,6 +83,11 @@ def test_host_side_errors_before_launch():
                                 ctypes.byref(params), None, None, None, None, 0, None) == 1
     assert lib.ppo_loss_gauss_f32(p, p, 10, 25, p, p, p, p, p, None, ctypes.byref(params),
                                   p, p, p, p, p, 1 << 20, None) == 3
+    # sampling: A <= 0 / null outputs / D above the limit; N == 0 is a no-op
+    assert lib.ppo_sample_cat_f32(p, 4, 0, p, p, p, None, None, None) == 1
+    assert lib.ppo_sample_cat_f32(p, 4, 3, p, None, p, None, None, None) == 1
+    assert lib.ppo_sample_cat_f32(None, 0, 3, None, None, None, None, None, None) == 0
+    assert lib.ppo_sample_gauss_f32(p, p, 4, 25, p, p, p, None, None, None) == 3
 
 
 def test_error_mapping():

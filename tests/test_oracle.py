@@ -342,3 +342,39 @@ def test_golden_loss_gauss():
     np.testing.assert_allclose(o["dmu"].numpy(), z["dmu"], rtol=1e-6, atol=1e-9)
     np.testing.assert_allclose(o["dlog_std"].numpy(), z["dlog_std"], rtol=1e-6, atol=1e-9)
     np.testing.assert_allclose(o["loss"].item(), z["scalars"][0], rtol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# action selection (ppo.py:65-79)
+# ---------------------------------------------------------------------------
+def test_sample_reference_known_answers():
+    # two equal logits: p = (0.5, 0.5); u < 0.5 -> 0, u >= 0.5 -> 1
+    z = np.zeros((4, 2))
+    a, lp, _ = ref.sample_categorical_reference(z, np.array([0.0, 0.25, 0.5, 0.999]))
+    assert a.tolist() == [0, 0, 1, 1]
+    assert np.allclose(lp, np.log(0.5))
+    # a dominant logit takes (almost) every draw
+    z = np.array([[0.0, 50.0, 0.0]])
+    a, _, _ = ref.sample_categorical_reference(np.repeat(z, 3, 0), np.array([1e-9, 0.5, 0.9999]))
+    assert a.tolist() == [1, 1, 1]
+
+
+def test_sample_reference_frequencies_match_softmax():
+    g = np.random.default_rng(7)
+    z = g.standard_normal(5) * 1.5
+    n = 200_000
+    a, _, _ = ref.sample_categorical_reference(np.repeat(z[None], n, 0), g.random(n))
+    p = np.exp(z - z.max())
+    p /= p.sum()
+    freq = np.bincount(a, minlength=5) / n
+    # five binomial standard deviations
+    assert np.all(np.abs(freq - p) < 5 * np.sqrt(p * (1 - p) / n))
+
+
+def test_sample_reference_log_prob_matches_torch_categorical():
+    g = torch.Generator().manual_seed(3)
+    z = torch.randn(64, 18, generator=g, dtype=torch.float64)
+    u = torch.rand(64, generator=g, dtype=torch.float64)
+    a, lp, _ = ref.sample_categorical_reference(z.numpy(), u.numpy())
+    want = torch.distributions.Categorical(logits=z).log_prob(torch.from_numpy(a))
+    assert np.allclose(lp, want.numpy(), rtol=0, atol=1e-12)

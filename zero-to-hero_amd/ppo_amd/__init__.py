@@ -3,8 +3,9 @@
 Hand-written HIP kernels for gfx950 (libppo_amd.so, C ABI in
 include/ppo_amd.h) behind the reference's own PPO surface:
 
-  ops       gae, gae_normalize, normalize_advantages, ppo_loss_discrete,
-            ppo_loss_gaussian (+ *_fused functional forms)
+  ops       gae, gae_normalize, normalize_advantages, discounted_returns,
+            gather_rows, sample_categorical, sample_gaussian,
+            ppo_loss_discrete, ppo_loss_gaussian (+ *_fused functional forms)
   agent     PPOAgent, PPOConfig, TrainingConfig, MLP, Transition,
             RolloutStep, PendingStep, cartpole_sizes — rl/deep/agents/ppo.py
             and common.py, same names and signatures
@@ -34,6 +35,8 @@ from .ops import (
     ppo_loss_discrete_fused,
     ppo_loss_gaussian,
     ppo_loss_gaussian_fused,
+    sample_categorical,
+    sample_gaussian,
 )
 from .optim import ClippedAdam
 from .rollout import RolloutBuffer, VecPPO
@@ -70,4 +73,6 @@ __all__ = [
     "ppo_loss_discrete_fused",
     "ppo_loss_gaussian",
     "ppo_loss_gaussian_fused",
+    "sample_categorical",
+    "sample_gaussian",
 ]

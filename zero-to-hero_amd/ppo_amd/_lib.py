@@ -85,6 +85,8 @@ SIGNATURES = {
         [_vp, _i64, _i64, _i32,
          ctypes.POINTER(_vp), ctypes.POINTER(_i32), ctypes.POINTER(_vp), _vp],
     ),
+    "ppo_sample_cat_f32": (_int, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ppo_sample_gauss_f32": (_int, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ppo_adam_clip_workspace_bytes": (_sz, [_i32, ctypes.POINTER(_i64)]),
     "ppo_adam_clip_f32": (
         _int,

@@ -29,6 +29,8 @@ __all__ = [
     "discounted_returns",
     "gather_rows",
     "normalize_advantages",
+    "sample_categorical",
+    "sample_gaussian",
     "ppo_loss_discrete",
     "ppo_loss_discrete_fused",
     "ppo_loss_gaussian",
@@ -317,6 +319,106 @@ def gather_rows(index: torch.Tensor, *arrays: torch.Tensor) -> list[torch.Tensor
     stream = _stream(device)
     _call("ppo_gather_rows", device, stream, index.data_ptr(), B, n, na, src, rbs, dst, stream)
     return outs
+
+
+# ---------------------------------------------------------------------------
+# Batched action selection
+# ---------------------------------------------------------------------------
+def _out(t, name, shape, dtype, device):
+    if t is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    _require(t, name, (dtype,), device)
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must be {tuple(shape)}, got {tuple(t.shape)}")
+    return t
+
+
+def sample_categorical(
+    logits: torch.Tensor,
+    uniforms: Optional[torch.Tensor] = None,
+    generator: Optional[torch.Generator] = None,
+    values: Optional[torch.Tensor] = None,
+    actions_out: Optional[torch.Tensor] = None,
+    log_probs_out: Optional[torch.Tensor] = None,
+    values_out: Optional[torch.Tensor] = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Categorical(logits=logits).sample() and .log_prob() for N rows in one
+    launch (PPOAgent.select_action, ppo.py:65-79, batched over envs).
+
+    The draw is the inverse CDF of softmax(logits[n]) at uniforms[n] (drawn
+    with torch.rand on the device from `generator` when not given), so the
+    sample is a deterministic function of (logits, uniforms).  Returns
+    (actions int32 [N], log_probs [N]); the *_out tensors, if given, are
+    written in place (e.g. row t of a [T,N] rollout buffer), and `values`
+    is copied to `values_out` in the same launch.
+    """
+    _require(logits, "logits", (torch.float32,))
+    device = logits.device
+    if logits.dim() != 2 or logits.shape[1] == 0:
+        raise ValueError(f"logits must be [N,A] with A > 0, got {tuple(logits.shape)}")
+    N, A = logits.shape
+    if uniforms is None:
+        uniforms = torch.rand(N, device=device, generator=generator)
+    _require(uniforms, "uniforms", (torch.float32,), device)
+    if uniforms.shape != (N,):
+        raise ValueError(f"uniforms must be [N]=[{N}], got {tuple(uniforms.shape)}")
+    actions_out = _out(actions_out, "actions_out", (N,), torch.int32, device)
+    log_probs_out = _out(log_probs_out, "log_probs_out", (N,), torch.float32, device)
+    if (values is None) != (values_out is None):
+        raise ValueError("values and values_out go together")
+    if values is not None:
+        _require(values, "values", (torch.float32,), device)
+        values_out = _out(values_out, "values_out", (N,), torch.float32, device)
+        if values.numel() != N:
+            raise ValueError(f"values must have N={N} elements, got {values.numel()}")
+    stream = _stream(device)
+    _call("ppo_sample_cat_f32", device, stream, logits.data_ptr(), N, A, uniforms.data_ptr(),
+          actions_out.data_ptr(), log_probs_out.data_ptr(), _ptr(values), _ptr(values_out),
+          stream)
+    return actions_out, log_probs_out
+
+
+def sample_gaussian(
+    mu: torch.Tensor,
+    log_std: torch.Tensor,
+    normals: Optional[torch.Tensor] = None,
+    generator: Optional[torch.Generator] = None,
+    values: Optional[torch.Tensor] = None,
+    actions_out: Optional[torch.Tensor] = None,
+    log_probs_out: Optional[torch.Tensor] = None,
+    values_out: Optional[torch.Tensor] = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Normal(mu, exp(log_std)).sample() and .log_prob(a).sum(-1) for N rows
+    in one launch: actions = mu + exp(log_std) * normals (normals drawn with
+    torch.randn from `generator` when not given).  Returns (actions [N,D],
+    log_probs [N]); *_out tensors are written in place when given."""
+    _require(mu, "mu", (torch.float32,))
+    device = mu.device
+    if mu.dim() != 2 or mu.shape[1] == 0:
+        raise ValueError(f"mu must be [N,D] with D > 0, got {tuple(mu.shape)}")
+    N, D = mu.shape
+    _require(log_std, "log_std", (torch.float32,), device)
+    if log_std.numel() != D:
+        raise ValueError(f"log_std must have D={D} elements, got {log_std.numel()}")
+    if normals is None:
+        normals = torch.randn(N, D, device=device, generator=generator)
+    _require(normals, "normals", (torch.float32,), device)
+    if normals.shape != (N, D):
+        raise ValueError(f"normals must be [N,D]=[{N},{D}], got {tuple(normals.shape)}")
+    actions_out = _out(actions_out, "actions_out", (N, D), torch.float32, device)
+    log_probs_out = _out(log_probs_out, "log_probs_out", (N,), torch.float32, device)
+    if (values is None) != (values_out is None):
+        raise ValueError("values and values_out go together")
+    if values is not None:
+        _require(values, "values", (torch.float32,), device)
+        values_out = _out(values_out, "values_out", (N,), torch.float32, device)
+        if values.numel() != N:
+            raise ValueError(f"values must have N={N} elements, got {values.numel()}")
+    stream = _stream(device)
+    _call("ppo_sample_gauss_f32", device, stream, mu.data_ptr(), log_std.contiguous().data_ptr(),
+          N, D, normals.data_ptr(), actions_out.data_ptr(), log_probs_out.data_ptr(),
+          _ptr(values), _ptr(values_out), stream)
+    return actions_out, log_probs_out
 
 
 # ---------------------------------------------------------------------------

@@ -67,6 +67,16 @@ class RolloutBuffer:
         self.log_probs[t].copy_(log_probs)
         self.step += 1
 
+    def add_outcome(self, rewards, dones) -> None:
+        """Complete step `self.step` after VecPPO.act(obs, buffer=self) has
+        written its observations, actions, log-probs and values: store the
+        environment's rewards and dones and advance."""
+        if self.step >= self.T:
+            raise IndexError(f"rollout buffer is full (T={self.T})")
+        self.rewards[self.step].copy_(rewards)
+        self.dones[self.step].copy_(dones)
+        self.step += 1
+
     def finish(self, last_value: Optional[torch.Tensor] = None) -> None:
         """Set the bootstrap values (None: zeros, the reference's episode end)."""
         if last_value is None:
@@ -146,6 +156,39 @@ class VecPPO:
                                          capturable=graphs)
         else:
             self.optimizer = torch.optim.Adam(self.parameters, lr=lr)
+
+    @torch.no_grad()
+    def act(self, observations: torch.Tensor, buffer: Optional[RolloutBuffer] = None,
+            generator: Optional[torch.Generator] = None):
+        """PPOAgent.select_action (ppo.py:65-79) for all N envs at once.
+
+        Runs the policy and value networks on observations [N, *obs_shape],
+        then one sampling launch draws every env's action (from uniforms /
+        normals drawn on the device with `generator`) and its log-prob.  With
+        `buffer`, the observations, actions, log-probs and values are written
+        straight into row `buffer.step` (complete it with
+        buffer.add_outcome(rewards, dones)).  Returns (actions, log_probs,
+        values), views of that row when a buffer is given.
+        """
+        values = self.value(observations).reshape(-1).contiguous()
+        if buffer is not None:
+            if buffer.step >= buffer.T:
+                raise IndexError(f"rollout buffer is full (T={buffer.T})")
+            t = buffer.step
+            buffer.observations[t].copy_(observations)
+            outs = dict(actions_out=buffer.actions[t], log_probs_out=buffer.log_probs[t],
+                        values_out=buffer.values[t])
+        else:
+            outs = dict(values_out=torch.empty_like(values))
+        if self.log_std is None:
+            logits = self.policy(observations).contiguous()
+            acts, logp = ops.sample_categorical(logits, generator=generator, values=values,
+                                                **outs)
+        else:
+            mu = self.policy(observations).contiguous()
+            acts, logp = ops.sample_gaussian(mu, self.log_std.detach(), generator=generator,
+                                             values=values, **outs)
+        return acts, logp, outs["values_out"]
 
     def update(self, buffer: RolloutBuffer) -> dict:
         """Run `epochs` passes of shuffled minibatches; returns the last
