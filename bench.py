@@ -208,13 +208,34 @@ def cpu_baseline(torch, x, budget_s):
     }
 
 
-def time_events(torch, fn, reps):
+def time_step_events(torch, step, reps):
+    """Average durations (s) of step.gae() and step.loss() within `reps`
+    back-to-back steps: HIP events before the GAE call, between the calls and
+    after the loss call, on the current stream."""
+    s = torch.cuda.current_stream()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
+    for e in ev:
+        e[0].record(s)
+        step.gae()
+        e[1].record(s)
+        step.loss()
+        e[2].record(s)
+    torch.cuda.synchronize()
+    g = sum(e[0].elapsed_time(e[1]) for e in ev) / reps / 1e3
+    loss = sum(e[1].elapsed_time(e[2]) for e in ev) / reps / 1e3
+    return g, loss
+
+
+def time_events(torch, fn, reps, flush=None):
     """Average duration (s) of fn over `reps` launches, HIP events on the
-    current stream (the stream the kernels are enqueued on)."""
+    current stream (the stream the kernels are enqueued on).  `flush`, if
+    given, runs before each launch, outside the events."""
     s = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
     for i in range(reps):
+        if flush is not None:
+            flush()
         starts[i].record(s)
         fn()
         ends[i].record(s)
@@ -226,7 +247,9 @@ def time_events(torch, fn, reps):
 def suite(torch, lib, dev):
     """One line per BASELINE config kernel chain (2: GAE+normalise, 3: long-T
     GAE scan, 4: discrete loss, 5: Gaussian loss), each timed through the C
-    ABI with preallocated outputs (HIP events on the launch stream)."""
+    ABI with preallocated outputs (HIP events on the launch stream).  Each
+    timed call follows a read of a 512 MiB buffer, so its inputs come from HBM
+    rather than the 256 MB Infinity Cache (configs 2, 4 and 5 fit in it)."""
     import ctypes
 
     from ppo_amd import _lib
@@ -236,6 +259,11 @@ def suite(torch, lib, dev):
     f32 = dict(dtype=torch.float32, device=dev)
     params = _lib.LossParams(0.2, 0.2, 0.5, 0.01)
     out = []
+    evict = torch.empty(128 * 1024 * 1024, **f32)
+    evict_sum = torch.empty((), **f32)
+
+    def flush():
+        torch.sum(evict, dim=0, out=evict_sum)
 
     def ws(nbytes):
         return torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -261,7 +289,7 @@ def suite(torch, lib, dev):
                 adv.data_ptr(), ret.data_ptr(), w.data_ptr(), w.numel(), stream)
             bpu = SCAN_BYTES
         fn()
-        out.append((name, T * N, bpu, time_events(torch, fn, 30)))
+        out.append((name, T * N, bpu, time_events(torch, fn, 30, flush)))
         del r, v, d, adv, ret, advn, w
     # config 4: discrete loss
     x = synthetic_rollout(torch, dev, 256, 4096, 18, seed=25)
@@ -274,7 +302,7 @@ def suite(torch, lib, dev):
         x["values"].data_ptr(), ctypes.byref(params), dl.data_ptr(), dv.data_ptr(),
         sc.data_ptr(), w.data_ptr(), w.numel(), stream)
     fn()
-    out.append(("config4_loss_cat", B, LOSS_CAT_BYTES, time_events(torch, fn, 30)))
+    out.append(("config4_loss_cat", B, LOSS_CAT_BYTES, time_events(torch, fn, 30, flush)))
     del x, dl, dv, w
     # config 5: Gaussian loss
     B, D = 2_097_152, 6
@@ -291,16 +319,16 @@ def suite(torch, lib, dev):
         ctypes.byref(params), dmu.data_ptr(), dls.data_ptr(), dv.data_ptr(), sc.data_ptr(),
         w.data_ptr(), w.numel(), stream)
     fn()
-    out.append(("config5_loss_gauss", B, GAUSS_BYTES, time_events(torch, fn, 30)))
+    out.append(("config5_loss_gauss", B, GAUSS_BYTES, time_events(torch, fn, 30, flush)))
     del mu, acts, rows, dmu, dls, dv, w
     # the north-star step with A = 2 (CartPole's action count): GAE+norm + loss
     x = synthetic_rollout(torch, dev, T_STEPS, N_ENVS, 2, seed=26)
     st = Step(torch, lib, x, dev)
     st.gae()
     st.loss()
-    out.append(("north_star_A2_loss", st.B, LOSS_CAT_A2_BYTES, time_events(torch, st.loss, 30)))
+    out.append(("north_star_A2_loss", st.B, LOSS_CAT_A2_BYTES, time_events(torch, st.loss, 30, flush)))
     out.append(("north_star_A2_step", st.B, GAE_BYTES + LOSS_CAT_A2_BYTES,
-                time_events(torch, lambda: (st.gae(), st.loss()), 30)))
+                time_events(torch, lambda: (st.gae(), st.loss()), 30, flush)))
     for name, units, bpu, t in out:
         gbs = units * bpu / t / 1e9
         print(json.dumps({"suite": name, "units": units, "bytes_per_unit": bpu,
@@ -425,9 +453,10 @@ def main():
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
 
-    # per-kernel HIP-event timing on the launch stream
-    t_loss = time_events(torch, step.loss, max(args.steps, 20))
-    t_gae = time_events(torch, step.gae, max(args.steps, 20))
+    # per-call HIP-event timing on the launch stream, inside the step sequence:
+    # each GAE call follows a loss call, so its rollout comes from HBM (back-to-
+    # back GAE calls would find the 75 MB rollout in the 256 MB Infinity Cache)
+    t_gae, t_loss = time_step_events(torch, step, max(args.steps, 20))
     achieved = LOSS_CAT_BYTES * B / t_loss / 1e9
     traffic = read_traffic("loss_cat_north_star")
 

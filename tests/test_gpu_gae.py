@@ -224,3 +224,64 @@ def test_discounted_returns_vectorised_with_dones(dev):
                 break
         np.testing.assert_allclose(got[:len(col), n], np.array(col, np.float32), rtol=1e-6,
                                    atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Strip walk (wide rollouts, N >= 2048 aligned): one workgroup per strip of
+# 8/16/32 envs walks the horizon backwards in chunks of 1024/512/256 steps.
+# Shapes cover each strip width, horizons shorter than, equal to and not a
+# multiple of a chunk, odd and even chunk counts, a partial last strip (N not
+# a multiple of the strip width), and short horizons that stay on the tile
+# passes (T < a quarter of a chunk).
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize(
+    "T,N,p",
+    [
+        (1, 2048, 0.1), (3, 4096, 0.1), (100, 2048, 0.02),    # tile passes
+        (300, 2048, 0.02), (1024, 2048, 0.01), (2048, 2048, 0.01),  # E=8: <1, 1, 2 chunks
+        (1500, 2052, 0.01),                                    # E=8, partial strip
+        (200, 4096, 0.01), (512, 4096, 0.01), (1536, 4096, 0.01),  # E=16: <1, 1, 3 chunks
+        (1000, 4100, 0.02),                                    # E=16, partial strip
+        (129, 8192, 0.05), (640, 8196, 0.01),                  # E=32
+    ],
+)
+def test_gae_strip_walk_matches_oracle(dev, T, N, p):
+    exact = _run(dev, T, N, p, seed=T * 31 + N)
+    assert exact > 0.99
+
+
+def test_gae_strip_walk_without_bootstrap(dev):
+    _run(dev, 700, 4096, 0.01, seed=41, last=False)
+
+
+def test_gae_strip_walk_all_or_no_dones(dev):
+    _run(dev, 300, 2048, 1.0, seed=42)
+    _run(dev, 300, 2048, 0.0, seed=43)
+
+
+def test_discounted_returns_strip_walk(dev):
+    """values = None (REINFORCE returns) on the strip walk."""
+    T, N = 600, 4096
+    g = torch.Generator().manual_seed(44)
+    r = torch.randn(T, N, generator=g)
+    d = (torch.rand(T, N, generator=g) < 0.01).to(torch.uint8)
+    boot = torch.randn(N, generator=g)
+    got = ppo_amd.discounted_returns(r.to(dev), d.to(dev), 0.99, boot.to(dev)).cpu().numpy()
+    expect, _ = ref.gae_c(r.numpy(), np.zeros((T, N), np.float32), d.numpy(), boot.numpy(),
+                          0.99, 1.0)
+    assert_gae_close(got, expect)
+
+
+def test_gae_normalize_strip_walk_matches_separate_ops(dev):
+    g = torch.Generator().manual_seed(45)
+    T, N = 777, 2056
+    r = torch.randn(T, N, generator=g).to(dev)
+    v = torch.randn(T, N, generator=g).to(dev)
+    d = (torch.rand(T, N, generator=g) < 0.02).to(torch.uint8).to(dev)
+    lv = torch.randn(N, generator=g).to(dev)
+    adv, ret, adv_n = ppo_amd.gae_normalize(r, v, d, lv)
+    adv2, ret2 = ppo_amd.gae(r, v, d, lv)
+    assert torch.equal(adv, adv2) and torch.equal(ret, ret2)
+    torch.testing.assert_close(adv_n, ppo_amd.normalize_advantages(adv2), rtol=1e-6, atol=1e-7)
+    n_ref = ref.normalize_reference(adv2.cpu().reshape(-1)).reshape(T, N)
+    torch.testing.assert_close(adv_n.cpu(), n_ref, rtol=1e-5, atol=1e-6)

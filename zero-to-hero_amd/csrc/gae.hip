@@ -37,6 +37,12 @@
 // (relative difference ~1e-8 from the rounded values' statistics).
 // When the whole horizon fits in one tile (Tt == 1) steps 1-2 are skipped and
 // the final pass emits per-block sums for a separate normalise pass instead.
+//
+// Wide rollouts (N >= 2048, aligned) take a single-pass "strip walk" instead
+// (gae_strip_kernel): a workgroup owns 8-32 adjacent envs for the whole
+// horizon and walks it backwards in chunks, carrying the advantage from chunk
+// to chunk, so the rollout is read once; the normaliser then needs one
+// elementwise pass over the advantages.
 #include <algorithm>
 #include <type_traits>
 
@@ -89,6 +95,7 @@ struct PassGeom {
 };
 
 struct GaePlan {
+  long T;
   int vw;
   long Q, Tt, span;
   PassGeom scan, fin;  // pass 1 (tile composites) and the final pass
@@ -124,6 +131,7 @@ PassGeom make_geom(long Q, int L, int Qw) {
 // same tile boundaries in T, so their carries are interchangeable.)
 GaePlan make_plan(long T, long N, int vw) {
   GaePlan p;
+  p.T = T;
   p.vw = vw;
   p.Q = N / vw;
   p.fin_solo.Tq = 0;
@@ -171,6 +179,52 @@ CarryPlan make_carry_plan(long Tt, long N) {
   return c;
 }
 
+// Strip-walk geometry (gae_strip_kernel): 1024-thread workgroups, each
+// owning a strip of E envs (one env and kStripL consecutive steps per thread)
+// for the whole horizon, in chunks of (1024/E)*kStripL steps.  E is the widest
+// of 32, 16, 8 that still gives every CU a strip (kStripMinBlocks) and keeps
+// at least a quarter of a chunk's threads busy; narrower rollouts, very short
+// horizons, misaligned buffers and rollouts of >= 2^30 elements take the tile
+// passes (measured: T=16, N=65536 runs 12 us tiled, 36 us as strips).
+#ifndef PPO_GAE_STRIP_BLOCK
+#define PPO_GAE_STRIP_BLOCK 1024
+#endif
+#ifndef PPO_GAE_STRIP_EMAX
+#define PPO_GAE_STRIP_EMAX 32
+#endif
+#ifndef PPO_GAE_STRIP_L
+#define PPO_GAE_STRIP_L 8
+#endif
+constexpr int kStripBlock = PPO_GAE_STRIP_BLOCK;
+constexpr int kStripL = PPO_GAE_STRIP_L;
+// (PPO_GAE_STRIP_MIN: build-time override, e.g. to time the tile passes alone)
+#ifndef PPO_GAE_STRIP_MIN
+#define PPO_GAE_STRIP_MIN 256
+#endif
+constexpr long kStripMinBlocks = PPO_GAE_STRIP_MIN;
+
+struct StripPlan {
+  int E;        // envs per strip (0: use the tile passes)
+  long strips;  // workgroups
+};
+
+StripPlan strip_plan(const GaePlan& p) {
+  const long T = p.T;
+  StripPlan sp = {0, 0};
+  const long N = p.Q * p.vw;
+  if (p.vw != 4 || T * N >= (1L << 30)) return sp;
+  for (int E = PPO_GAE_STRIP_EMAX; E >= 8; E >>= 1) {
+    const long strips = (N + E - 1) / E;
+    const long chunk = (long)(kStripBlock / E) * kStripL;
+    if (strips >= kStripMinBlocks && 4 * T >= chunk) {
+      sp.E = E;
+      sp.strips = strips;
+      return sp;
+    }
+  }
+  return sp;
+}
+
 struct GaeLayout {
   size_t summary, carry, chunk_sum, tstat, partial, total;
 };
@@ -189,7 +243,8 @@ GaeLayout make_layout(const GaePlan& p, long N) {
   l.partial = off;
   {
     const CarryPlan cp = make_carry_plan(p.Tt, N);
-    const long parts = std::max<long>(p.blocks(), cp.groups * cp.nchunks);
+    const long parts = std::max<long>(std::max<long>(p.blocks(), cp.groups * cp.nchunks),
+                                      strip_plan(p).strips);
     off += align_up((size_t)parts * 4 * sizeof(double), 256);
   }
   l.total = off;
@@ -239,6 +294,30 @@ __device__ __forceinline__ void store_f(float* p, const float (&x)[VW]) {
     st(t, reinterpret_cast<f4*>(p));
   } else {
     st(x[0], p);
+  }
+}
+
+typedef float f2 __attribute__((ext_vector_type(2)));
+template <int VW>
+__device__ __forceinline__ void load_vec(const float* p, float (&x)[VW]) {
+  if constexpr (VW == 2) {
+    const f2 t = ld(reinterpret_cast<const f2*>(p));
+    x[0] = t[0]; x[1] = t[1];
+  } else {
+    load_f<VW>(p, x);
+  }
+}
+// Plain (temporal) stores: the strip walk writes half cache lines from two
+// workgroups on the same XCD, which the L2 merges only if it holds them
+// (with nontemporal stores the HBM writes measured 1.33x the bytes).
+template <int VW>
+__device__ __forceinline__ void store_vec(float* p, const float (&x)[VW]) {
+  if constexpr (VW == 4) {
+    *reinterpret_cast<f4*>(p) = f4{x[0], x[1], x[2], x[3]};
+  } else if constexpr (VW == 2) {
+    *reinterpret_cast<f2*>(p) = f2{x[0], x[1]};
+  } else {
+    *p = x[0];
   }
 }
 
@@ -728,6 +807,277 @@ __global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* _
   }
 }
 
+// Strip walk (wide rollouts): one workgroup owns a strip of E adjacent envs
+// for the whole horizon and walks it backwards in chunks of S*L steps: a
+// thread owns a segment of L steps x VW envs, G = E/VW threads cover a row of
+// the strip and S = kStripBlock/G segments make a chunk.  The advantage
+// entering a chunk from the right is known when the chunk starts, so one pass
+// over the rollout suffices: per chunk each thread forms its segment
+// composite (a, P) with a zero carry, a reverse scan composes the segments
+// (lane moves inside a wave, then a fold over the waves' composites staged in
+// LDS), every thread applies its carry and runs the exact serial recurrence,
+// and the chunk's composite applied to the incoming carry is the carry of the
+// next chunk to the left.  The next chunk's rows are loaded before the
+// current one's arithmetic.  With kStats each block also leaves (n, sum, sum
+// of squares) of its fp32 advantages in `partial` for the normaliser.
+constexpr int kStripWaves = kStripBlock / kWave;
+constexpr int kXcds = 8;
+
+template <int L, int VW>
+struct StripRows {
+  float r[L][VW], v[L][VW];
+  unsigned d[L];  // the row's done bytes as loaded (byte k: env k)
+  __device__ __forceinline__ bool done(int i, int k) const {
+    if constexpr (VW == 1) return d[i] != 0u;
+    else return ((d[i] >> (8 * k)) & 0xffu) != 0u;
+  }
+};
+
+template <int VW>
+__device__ __forceinline__ unsigned load_done_raw(const uint8_t* p) {
+  if constexpr (VW == 4) return ld(reinterpret_cast<const unsigned*>(p));
+  else if constexpr (VW == 2) return ld(reinterpret_cast<const unsigned short*>(p));
+  else return ld(p);
+}
+
+// Element offsets in the strip walk are 32-bit (rollouts of < 2^30
+// elements).  Loads are unconditional (rows past the horizon or the last env
+// re-read element 0 and are never used), so a chunk's loads stay in flight
+// until its arithmetic needs them.
+template <typename T>
+__device__ __forceinline__ T* at_byte(T* base, unsigned byte_off) {
+  using C = typename std::conditional<std::is_const<T>::value, const char, char>::type;
+  return reinterpret_cast<T*>(reinterpret_cast<C*>(base) + byte_off);
+}
+
+template <int L, int VW, bool kHasV>
+__device__ __forceinline__ void strip_load(const GaeArgs& a, long t0, unsigned e0, bool ok,
+                                           StripRows<L, VW>& x) {
+  const unsigned n = (unsigned)a.N;
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    const unsigned off = (ok && t0 + i < a.T) ? e0 + (unsigned)i * n : 0u;
+    load_vec<VW>(at_byte(a.r, off * 4u), x.r[i]);
+    if constexpr (kHasV) {
+      load_vec<VW>(at_byte(a.v, off * 4u), x.v[i]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) x.v[i][k] = 0.0f;
+    }
+    x.d[i] = load_done_raw<VW>(at_byte(a.d, off));
+  }
+}
+
+// Shared-memory staging of one strip walk (double-buffered by chunk parity).
+template <int S, int E>
+struct StripShared {
+  float v0[2][S][E];                   // first value row of each segment
+  double2 wc[2][kStripWaves][E];       // wave composites (a, P) per env
+};
+
+// One chunk of the strip walk: rows `x` of chunk c, carry C in and out.
+template <int L, int VW, int E, bool kStats>
+__device__ __forceinline__ void strip_chunk(const GaeArgs& a, StripShared<kStripBlock / (E / VW), E>& sh,
+                                            long c, long env0, bool ok,
+                                            const StripRows<L, VW>& cur, const float (&lastv)[VW],
+                                            double (&C)[VW],
+                                            double (&acc)[3]) {
+  constexpr int G = E / VW;           // threads per strip row
+  constexpr int S = kStripBlock / G;  // segments per chunk
+  constexpr int SW = kWave / G;       // segments per wave
+  constexpr long CS = (long)S * L;    // steps per chunk
+  const int tid = threadIdx.x;
+  const int g = tid % G;
+  const int s = tid / G;
+  const int w = tid / kWave;
+  const int j = (tid % kWave) / G;  // segment index inside the wave
+  const unsigned n32 = (unsigned)a.N;
+  const int par = (int)(c & 1);
+  const long t0 = c * CS + (long)s * L;
+  const unsigned e0 = (unsigned)t0 * n32 + (unsigned)env0;
+#pragma unroll
+  for (int k = 0; k < VW; ++k) sh.v0[par][s][g * VW + k] = cur.v[0][k];
+  __syncthreads();
+  // value of the step after this segment (the bootstrap past the horizon)
+  float nv[VW];
+  {
+    const bool past = t0 + L >= a.T;
+    const int row = s + 1 < S ? s + 1 : 0;
+    const int bank = s + 1 < S ? par : par ^ 1;
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      const float x = sh.v0[bank][row][g * VW + k];
+      nv[k] = past ? lastv[k] : x;
+    }
+  }
+  const int nvalid = t0 >= a.T ? 0 : (a.T - t0 < L ? (int)(a.T - t0) : L);
+
+  // segment composite with a zero carry, then a reverse inclusive scan over
+  // the wave's segments (lane + G*off holds the segment `off` to the right)
+  // Each step's delta is formed once (fp64, reference order) and kept for the
+  // final pass; gamma*lambda*mask is gl or gl*0, chosen by the done bit.
+  const double gl0 = mul(a.gl, 0.0);
+  double na[VW], np[VW];
+  double dl[L][VW];
+#pragma unroll
+  for (int k = 0; k < VW; ++k) {
+    double ia = 0.0, ip = 1.0;
+    double nvd = nv[k];
+#pragma unroll
+    for (int i = L - 1; i >= 0; --i) {
+      if (i < nvalid) {
+        const bool done = cur.done(i, k);
+        const double vd = (double)cur.v[i][k];
+        dl[i][k] = sub(add((double)cur.r[i][k], mul(mul(a.gamma, nvd), done ? 0.0 : 1.0)), vd);
+        const double cc = done ? gl0 : a.gl;
+        ia = add(dl[i][k], mul(cc, ia));
+        ip = mul(ip, cc);
+        nvd = vd;
+      } else {
+        dl[i][k] = 0.0;
+      }
+    }
+#pragma unroll
+    for (int off = 1; off < SW; off <<= 1) {
+      const double pa = __shfl_down(ia, G * off);
+      const double pp = __shfl_down(ip, G * off);
+      if (j + off < SW) {
+        ia = ia + ip * pa;
+        ip = ip * pp;
+      }
+    }
+    na[k] = __shfl_down(ia, G);
+    np[k] = __shfl_down(ip, G);
+    if (j + 1 >= SW) {
+      na[k] = 0.0;
+      np[k] = 1.0;
+    }
+    if (j == 0) sh.wc[par][w][g * VW + k] = make_double2(ia, ip);
+  }
+  __syncthreads();
+  // fold the wave composites from the right: Cw enters this wave, C then
+  // enters the chunk to the left
+  double Cw[VW];
+#pragma unroll
+  for (int k = 0; k < VW; ++k) Cw[k] = C[k];
+#pragma unroll 4
+  for (int ww = kStripWaves - 1; ww >= 0; --ww) {
+    if (ww == w) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) Cw[k] = C[k];
+    }
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      const double2 t = sh.wc[par][ww][g * VW + k];
+      C[k] = t.x + t.y * C[k];
+    }
+  }
+
+  // exact serial recurrence over the segment from its incoming advantage
+  float adv[L][VW];
+#pragma unroll
+  for (int k = 0; k < VW; ++k) {
+    double x = na[k] + np[k] * Cw[k];
+#pragma unroll
+    for (int i = L - 1; i >= 0; --i) {
+      if (i < nvalid) {
+        const bool done = cur.done(i, k);
+        x = add(dl[i][k], mul(done ? gl0 : a.gl, x));
+      }
+      adv[i][k] = (float)x;
+    }
+  }
+  float s1 = 0.0f, s2 = 0.0f;  // this chunk's sums: few terms, fp32
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+    if (ok && i < nvalid) {
+      const unsigned off = (e0 + (unsigned)i * n32) * 4u;
+      store_vec<VW>(at_byte(a.adv, off), adv[i]);
+      if (a.ret) {
+        float rt[VW];
+#pragma unroll
+        for (int k = 0; k < VW; ++k) rt[k] = adv[i][k] + cur.v[i][k];
+        store_vec<VW>(at_byte(a.ret, off), rt);
+      }
+      if constexpr (kStats) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          s1 += adv[i][k];
+          s2 += adv[i][k] * adv[i][k];
+        }
+      }
+    }
+  }
+  if constexpr (kStats) {
+    if (ok) {
+      acc[0] += (double)(nvalid * VW);
+      acc[1] += (double)s1;
+      acc[2] += (double)s2;
+    }
+  }
+}
+
+template <int L, int VW, int E, bool kStats, bool kHasV>
+__global__ void __launch_bounds__(kStripBlock) gae_strip_kernel(GaeArgs a) {
+  constexpr int G = E / VW;           // threads per strip row
+  static_assert(E % VW == 0 && kWave % G == 0 && L * VW <= 32, "strip geometry");
+  constexpr int S = kStripBlock / G;  // segments per chunk
+  constexpr long CS = (long)S * L;    // steps per chunk
+  __shared__ StripShared<S, E> sh;
+
+  const int s = threadIdx.x / G;
+  // Workgroups are dispatched to the 8 XCDs round-robin; strips are handed
+  // out so that each XCD owns a contiguous run of them, and strips that share
+  // a 128-byte line of a row share that XCD's L2.
+  long strip = blockIdx.x;
+  if (gridDim.x % kXcds == 0)
+    strip = (long)(blockIdx.x % kXcds) * (gridDim.x / kXcds) + blockIdx.x / kXcds;
+  const long env0 = strip * E + (long)(threadIdx.x % G) * VW;
+  const bool ok = env0 < a.N;
+  const long nch = (a.T + CS - 1) / CS;
+  // element offset of this thread's first row in chunk c
+  auto row0 = [&](long c) { return (unsigned)((c * CS + (long)s * L) * a.N + env0); };
+  auto load = [&](long c, StripRows<L, VW>& x) {
+    strip_load<L, VW, kHasV>(a, c * CS + (long)s * L, row0(c), ok && c >= 0, x);
+  };
+
+  double C[VW];  // advantage entering the chunk from the right
+  float lastv[VW];  // bootstrap value past the horizon
+#pragma unroll
+  for (int k = 0; k < VW; ++k) {
+    C[k] = 0.0;
+    lastv[k] = 0.0f;
+  }
+  if (a.lastv && ok) load_vec<VW>(a.lastv + env0, lastv);
+  double acc[3] = {0.0, 0.0, 0.0};
+
+  // The next chunk's rows are in flight while a chunk is processed (two row
+  // buffers, the loop unrolled over them).  Every load is unconditional (the
+  // chunk before the first one reads element 0 in every lane, one cache
+  // line), so the compiler's wait counts stay exact: a load under a branch
+  // makes the next join wait for every load in flight.  (Measured: prefetching
+  // two chunks ahead is no faster.)
+  StripRows<L, VW> b0, b1;
+  load(nch - 1, b0);
+  for (long c = nch - 1;;) {
+    load(c - 1, b1);
+    strip_chunk<L, VW, E, kStats>(a, sh, c, env0, ok, b0, lastv, C, acc);
+    if (--c < 0) break;
+    load(c - 1, b0);
+    strip_chunk<L, VW, E, kStats>(a, sh, c, env0, ok, b1, lastv, C, acc);
+    if (--c < 0) break;
+  }
+  if constexpr (kStats) {
+    block_sum<3>(acc);
+    if (threadIdx.x == 0) {
+      a.partial[blockIdx.x * 4 + 0] = acc[0];
+      a.partial[blockIdx.x * 4 + 1] = acc[1];
+      a.partial[blockIdx.x * 4 + 2] = acc[2];
+      a.partial[blockIdx.x * 4 + 3] = 0.0;
+    }
+  }
+}
+
 // Pass kernels by (VW, L, solo) geometry.
 template <int kMode>
 const void* tile_kernel(int vw, const PassGeom& g) {
@@ -735,6 +1085,22 @@ const void* tile_kernel(int vw, const PassGeom& g) {
   if (g.solo) return (const void*)gae_tile_kernel<4, 16, kSoloTile, kMode>;
   if (g.quad) return (const void*)gae_tile_kernel<4, 4, kQuadTile, kMode>;
   return (const void*)gae_tile_kernel<4, 4, kStacked, kMode>;
+}
+
+// Strip-walk kernel for strips of E envs.
+template <int E>
+const void* strip_kernel_e(bool norm, bool has_v) {
+  if (norm)
+    return has_v ? (const void*)gae_strip_kernel<kStripL, 1, E, true, true>
+                 : (const void*)gae_strip_kernel<kStripL, 1, E, true, false>;
+  return has_v ? (const void*)gae_strip_kernel<kStripL, 1, E, false, true>
+               : (const void*)gae_strip_kernel<kStripL, 1, E, false, false>;
+}
+
+const void* strip_kernel(int E, bool norm, bool has_v) {
+  if (E == 32) return strip_kernel_e<32>(norm, has_v);
+  if (E == 16) return strip_kernel_e<16>(norm, has_v);
+  return strip_kernel_e<8>(norm, has_v);
 }
 
 int launch_tile(const void* kern, const PassGeom& g, GaeArgs a, long Tt, hipStream_t stream) {
@@ -751,6 +1117,17 @@ int launch_gae(const GaePlan& p, GaeArgs a, bool norm, hipStream_t stream) {
   a.Tt = p.Tt;
   a.span = p.span;
   int st;
+  const StripPlan sp = strip_plan(p);
+  if (sp.E > 0) {
+    void* args[] = {&a};
+    const void* kern = strip_kernel(sp.E, norm, a.v != nullptr);
+    if ((st = hip_status(hipLaunchKernel(kern, dim3((unsigned)sp.strips), dim3(kStripBlock), args,
+                                         0, stream))))
+      return st;
+    if (!norm) return PPO_OK;
+    return launch_normalize(a.partial, sp.strips, a.eps, a.adv, a.adv_n, a.T * a.N, a.hdr,
+                            a.stats_out, stream);
+  }
   if (p.Tt > 1) {
     // pass 1: quad tiles when the tile sums are needed (their DPP tree beats
     // the LDS tree), stacked tiles otherwise (measured faster without sums)
