@@ -341,9 +341,11 @@ def update_suite(torch, dev, reps=10):
     normalisation + `epochs` x shuffled minibatches of MLP forward, fused loss,
     backward and optimizer step.  BASELINE config 1 (T=128, N=8, MLP 4-64-64
     tanh, A=2, 4 epochs x 4 minibatches of 256) and a larger T=2048, N=64 case
-    (minibatches of 4096).  Times VecPPO with the fused gather + ClippedAdam
-    replayed from graphs, the same eagerly, VecPPO with torch indexing + clip_grad_norm_ + Adam, and the CPU oracle
-    (numpy GAE, torch CPU loss/backward/Adam)."""
+    (minibatches of 4096).  Times VecPPO with the fused MLP minibatch kernel +
+    ClippedAdam replayed from graphs, the same eagerly, graph replay with
+    torch's MLPs + the fused loss + gather, VecPPO with torch indexing +
+    clip_grad_norm_ + Adam, and the CPU oracle (numpy GAE, torch CPU
+    loss/backward/Adam)."""
     import copy
 
     import ppo_amd
@@ -369,12 +371,14 @@ def update_suite(torch, dev, reps=10):
                     dones[t].to(dev), vals[t].to(dev), lps[t].to(dev))
         buf.finish(None)
         out = {"update_suite": name, "T": T, "N": N, "minibatch": mb, "epochs": 4}
-        for label, fused, graphs in (("gpu_graphs_ms", True, True),
-                                     ("gpu_fused_ms", True, False),
-                                     ("gpu_torch_ms", False, False)):
+        for label, fused, graphs, fmlp in (("gpu_graphs_ms", True, True, True),
+                                           ("gpu_fused_ms", True, False, True),
+                                           ("gpu_graphs_torch_mlp_ms", True, True, False),
+                                           ("gpu_torch_ms", False, False, False)):
             vec = ppo_amd.VecPPO(copy.deepcopy(policy).to(dev), copy.deepcopy(value).to(dev),
                                  PPOConfig(), batch_size=mb, fused_update=fused,
-                                 generator=torch.Generator().manual_seed(7), graphs=graphs)
+                                 generator=torch.Generator().manual_seed(7), graphs=graphs,
+                                 fused_mlp=fmlp)
             vec.update(buf)
             torch.cuda.synchronize()
             t0 = time.perf_counter()

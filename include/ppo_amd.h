@@ -38,6 +38,7 @@ extern "C" {
 #define PPO_ERR_INVALID_ARG 1     /* null pointer, negative size, bad coefficient */
 #define PPO_ERR_WORKSPACE 2       /* workspace missing or smaller than required */
 #define PPO_ERR_TOO_LARGE 3       /* size beyond what the kernels index (2^31 rows) */
+#define PPO_ERR_UNSUPPORTED 4     /* shape or option the kernels do not implement   */
 #define PPO_ERR_HIP_BASE 1000     /* + hipError_t */
 
 /* Library version, as MAJOR*10000 + MINOR*100 + PATCH. */
@@ -259,6 +260,54 @@ int ppo_adam_clip_f32(int32_t ntensors, float* const* params, float* const* grad
                       float* const* exp_avg, float* const* exp_avg_sq, const int64_t* numel,
                       const ppo_adam_params* hp, float* grad_norm_out, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Fused minibatch gradient through the actor and critic MLPs.              */
+/* ------------------------------------------------------------------------ */
+
+#define PPO_ACT_RELU 0  /* nn.ReLU (the reference's MLP, common.py:21-24)     */
+#define PPO_ACT_TANH 1  /* nn.Tanh                                           */
+
+/*
+ * One MLP of rl/deep/agents/common.py:16-28, Linear(in,H)-act-Linear(H,H)-
+ * act-Linear(H,out): weight[l] and bias[l] are the nn.Linear parameters of
+ * layer l ([out,in] row-major fp32, 16-byte aligned weights); weight_grad[l]
+ * and bias_grad[l] receive their gradients (same shapes, overwritten).
+ */
+typedef struct ppo_mlp3_f32 {
+  const float* weight[3];
+  const float* bias[3];
+  float* weight_grad[3];
+  float* bias_grad[3];
+} ppo_mlp3_f32;
+
+size_t ppo_mlp_cat_grad_workspace_bytes(int64_t B, int32_t obs_dim, int32_t hidden, int32_t A);
+
+/*
+ * Replaces the forward and backward of PPOAgent._update_batch (rl/deep/agents/
+ * ppo.py:141-169) for one minibatch, from the observation rows to the
+ * parameter gradients, together with the minibatch gather of ppo.py:132-139:
+ *   rows      = index[0..B) (NULL: rows 0..B-1) of the [n, ...] arrays
+ *   values    = critic(observations[rows]).squeeze(1)          (ppo.py:147)
+ *   logits    = actor(observations[rows])                      (ppo.py:149)
+ *   loss      = ppo_loss_cat_f32's loss over the B rows        (ppo.py:150-167)
+ *   loss.backward()                                             (ppo.py:169)
+ * writing the gradient of every actor and critic weight and bias (actor
+ * output A logits, critic output 1; both hidden size `hidden`, one activation)
+ * and scalars_out[PPO_NUM_SCALARS].  Requires obs_dim <= 64, A <= 32 and
+ * hidden in {16, 32, 64, 128} (else PPO_ERR_UNSUPPORTED).  Gradients are
+ * summed over the minibatch per 16-row workgroup and then across workgroups in
+ * a fixed order (deterministic).  Follow with ppo_adam_clip_f32 for
+ * clip_grad_norm_ + Adam (ppo.py:170-171).
+ */
+int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
+                         int32_t obs_dim, int32_t hidden, int32_t A, int32_t activation,
+                         const float* observations, int64_t n, const int64_t* index, int64_t B,
+                         const void* actions, int actions_are_int64,
+                         const float* old_log_probs, const float* advantages,
+                         const float* returns, const float* old_values,
+                         const ppo_loss_params* params, float* scalars_out, void* workspace,
+                         size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

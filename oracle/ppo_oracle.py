@@ -445,6 +445,64 @@ def reference_epochs(
             optimizer.step()                                        # :171
 
 
+def update_batch_grads_reference(
+    policy: nn.Module,
+    value: nn.Module,
+    observations: torch.Tensor,
+    actions: torch.Tensor,
+    old_log_probs: torch.Tensor,
+    advantages: torch.Tensor,
+    returns: torch.Tensor,
+    old_values: torch.Tensor | None = None,
+    clip_ratio: float = 0.2,
+    vf_clip: float | None = None,
+    value_coef: float = 0.5,
+    entropy_coef: float = 0.01,
+) -> dict:
+    """The forward and backward of PPOAgent._update_batch, ppo.py:141-169, on
+    CPU modules for one (already gathered) minibatch: the parameter gradients
+    of `policy` then `value` (in .parameters() order) and the loss scalars.
+    Computes in the modules' dtype; the modules' .grad are left untouched."""
+    with torch.enable_grad():
+        return _update_batch_grads(policy, value, observations, actions, old_log_probs,
+                                   advantages, returns, old_values, clip_ratio, vf_clip,
+                                   value_coef, entropy_coef)
+
+
+def _update_batch_grads(policy, value, observations, actions, old_log_probs, advantages,
+                        returns, old_values, clip_ratio, vf_clip, value_coef, entropy_coef):
+    params = list(policy.parameters()) + list(value.parameters())
+    dt = params[0].dtype
+    obs = observations.detach().cpu().to(dt)
+    logits = policy(obs)                                            # :149
+    values = value(obs).squeeze(1)                                  # :152
+    distribution = Categorical(logits=logits)                       # :150
+    log_probs = distribution.log_prob(actions.detach().cpu().long())  # :151
+    ratio, policy_loss = _policy_terms(log_probs, old_log_probs.detach().cpu().to(dt),
+                                       advantages.detach().cpu().to(dt), clip_ratio)
+    ov = None if old_values is None else old_values.detach().cpu().to(dt)
+    value_loss = _value_loss(values, returns.detach().cpu().to(dt), ov, vf_clip)  # :160
+    entropy_bonus = distribution.entropy()                          # :161
+    loss = (                                                        # :163-167
+        policy_loss.mean()
+        + value_coef * value_loss
+        - entropy_coef * entropy_bonus.mean()
+    )
+    grads = torch.autograd.grad(loss, params)                       # :169
+    with torch.no_grad():
+        approx_kl = (old_log_probs.detach().cpu().to(dt) - log_probs).mean()
+        clipfrac = ((ratio - 1.0).abs() > clip_ratio).to(dt).mean()
+    return {
+        "grads": [g.detach() for g in grads],
+        "loss": loss.detach(),
+        "policy": policy_loss.mean().detach(),
+        "value": value_loss.detach(),
+        "entropy": entropy_bonus.mean().detach(),
+        "approx_kl": approx_kl,
+        "clipfrac": clipfrac,
+    }
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline step (bench.py's cpu_baseline leg)
 # ---------------------------------------------------------------------------

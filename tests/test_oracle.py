@@ -191,6 +191,60 @@ def test_cat_loss_finite_differences(vf_clip):
     torch.testing.assert_close(o["dvalues"], fdv, rtol=1e-6, atol=1e-8)
 
 
+def _tiny_nets(D, H, A, act, seed):
+    from ppo_amd.agent import MLP
+
+    torch.manual_seed(seed)
+    return MLP(D, H, A, act).double(), MLP(D, H, 1, act).double()
+
+
+@pytest.mark.parametrize("act,vf_clip", [("tanh", None), ("relu", 0.2)])
+def test_update_batch_grads_finite_differences(act, vf_clip):
+    """update_batch_grads_reference (ppo.py:141-169 through the MLPs) against
+    central differences of its own loss in fp64, every parameter element."""
+    D, H, A, B = 3, 5, 4, 6
+    pol, val = _tiny_nets(D, H, A, act, seed=3)
+    g = torch.Generator().manual_seed(5)
+    obs = torch.randn(B, D, generator=g, dtype=torch.float64)
+    _, actions, old_lp, adv, ret, _, old_v = _cat_inputs(B, A, seed=13)
+    args = (obs, actions, old_lp, adv, ret, old_v, 0.2, vf_clip, 0.5, 0.01)
+    o = ref.update_batch_grads_reference(pol, val, *args)
+    params = list(pol.parameters()) + list(val.parameters())
+    h = 1e-6
+    with torch.no_grad():
+        for p, gp in zip(params, o["grads"]):
+            flat, gflat = p.view(-1), gp.reshape(-1)
+            for k in range(flat.numel()):
+                x0 = flat[k].item()
+                flat[k] = x0 + h
+                lp_ = ref.update_batch_grads_reference(pol, val, *args)["loss"].item()
+                flat[k] = x0 - h
+                lm_ = ref.update_batch_grads_reference(pol, val, *args)["loss"].item()
+                flat[k] = x0
+                assert gflat[k].item() == pytest.approx((lp_ - lm_) / (2 * h), rel=1e-5,
+                                                        abs=1e-8)
+
+
+def test_update_batch_grads_chain_rule_matches_loss_oracle():
+    """The MLP oracle's loss and scalars equal loss_categorical_reference on
+    the networks' outputs, and its gradients equal the chain rule applied to
+    that oracle's d loss / d logits and d loss / d values."""
+    D, H, A, B = 4, 8, 3, 9
+    pol, val = _tiny_nets(D, H, A, "tanh", seed=7)
+    g = torch.Generator().manual_seed(8)
+    obs = torch.randn(B, D, generator=g, dtype=torch.float64)
+    _, actions, old_lp, adv, ret, _, old_v = _cat_inputs(B, A, seed=14)
+    o = ref.update_batch_grads_reference(pol, val, obs, actions, old_lp, adv, ret)
+    logits, values = pol(obs), val(obs).squeeze(1)
+    lo = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, values)
+    for k in ("loss", "policy", "value", "entropy", "approx_kl", "clipfrac"):
+        torch.testing.assert_close(o[k], lo[k], rtol=1e-12, atol=1e-14)
+    params = list(pol.parameters()) + list(val.parameters())
+    chain = torch.autograd.grad([logits, values], params, [lo["dlogits"], lo["dvalues"]])
+    for a, b in zip(o["grads"], chain):
+        torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-14)
+
+
 def test_cat_loss_invariants():
     B, A = 64, 7
     logits, actions, old_lp, adv, ret, val, old_v = _cat_inputs(B, A, seed=12)

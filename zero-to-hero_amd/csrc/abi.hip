@@ -15,6 +15,8 @@ extern "C" const char* ppo_amd_strerror(int code) {
       return "workspace missing or smaller than the *_workspace_bytes() query";
     case PPO_ERR_TOO_LARGE:
       return "problem size beyond what the kernels index";
+    case PPO_ERR_UNSUPPORTED:
+      return "shape or option outside what the kernels implement";
     default:
       break;
   }

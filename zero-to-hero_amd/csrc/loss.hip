@@ -30,6 +30,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "row_math.hpp"
 
 namespace ppo {
 namespace {
@@ -70,21 +71,6 @@ struct LossArgs {
   double* partial;
 };
 
-__device__ __forceinline__ float nan_min(float u, float w) {
-  if (u != u) return u;
-  if (w != w) return w;
-  return u < w ? u : w;
-}
-__device__ __forceinline__ float nan_max(float u, float w) {
-  if (u != u) return u;
-  if (w != w) return w;
-  return u > w ? u : w;
-}
-// torch.clamp(x, lo, hi): NaN stays NaN.
-__device__ __forceinline__ float clampf(float x, float lo, float hi) {
-  return x < lo ? lo : (x > hi ? hi : x);
-}
-
 // Streamed arrays are touched once: nontemporal loads/stores keep them from
 // displacing reusable lines (measured on MI355X: a float4 copy goes from 5.5
 // to 6.3 TB/s with nontemporal accesses and 4 loads in flight per thread).
@@ -94,11 +80,7 @@ __device__ __forceinline__ T ldnt(const T* p) { return __builtin_nontemporal_loa
 template <typename T>
 __device__ __forceinline__ void stnt(T v, T* p) { __builtin_nontemporal_store(v, p); }
 
-// Per-row inputs other than the logits/mu, loaded ahead of the LDS barrier.
-struct RowIn {
-  float old_lp, adv, ret, v, vo;
-};
-
+// Per-row inputs other than the logits/mu are loaded ahead of the LDS barrier.
 __device__ __forceinline__ RowIn load_row(const LossArgs& a, long row) {
   RowIn r;
   r.old_lp = ldnt(a.old_lp + row);
@@ -109,48 +91,12 @@ __device__ __forceinline__ RowIn load_row(const LossArgs& a, long row) {
   return r;
 }
 
-struct RowOut {
-  float g_lp;     // dloss/dlog_prob for this row
-  float pol, vl, kl, clipped;
-};
-
-// Everything per row that does not depend on the policy family: ratio,
-// clipped surrogate, value loss, their gradients.  Writes dvalue.
+// Everything per row that does not depend on the policy family (row_math.hpp);
+// stores dvalue.
 __device__ __forceinline__ RowOut ppo_row(const LossArgs& a, long row, const RowIn& in,
                                           float lp) {
-  RowOut o;
-  const float A = in.adv;
-  const float ratio = expf(lp - in.old_lp);
-  const float rc = clampf(ratio, a.lo, a.hi);
-  const float u = ratio * A;
-  const float w = rc * A;
-  const float su = u < w ? 1.0f : (u == w ? 0.5f : 0.0f);
-  const float sw = w < u ? 1.0f : (u == w ? 0.5f : 0.0f);
-  const float inr = (ratio >= a.lo && ratio <= a.hi) ? 1.0f : 0.0f;
-  // d(policy_i)/d(ratio) = -A*(su + sw*inr); times 1/B (mean) and ratio (exp').
-  o.g_lp = -(A * (su + sw * inr)) * a.inv_b * ratio;
-  o.pol = -nan_min(u, w);
-
-  const float d = in.v - in.ret;
-  float dvl;
-  if (a.use_vclip) {
-    const float dv = in.v - in.vo;
-    const float vcl = in.vo + clampf(dv, -a.vclip, a.vclip);
-    const float d2 = vcl - in.ret;
-    const float l1 = d * d;
-    const float l2 = d2 * d2;
-    o.vl = nan_max(l1, l2);
-    const float s1 = l1 > l2 ? 1.0f : (l1 == l2 ? 0.5f : 0.0f);
-    const float s2 = l2 > l1 ? 1.0f : (l1 == l2 ? 0.5f : 0.0f);
-    const float in2 = (dv >= -a.vclip && dv <= a.vclip) ? 1.0f : 0.0f;
-    dvl = s1 * (2.0f * d) + s2 * (2.0f * d2) * in2;
-  } else {
-    o.vl = d * d;
-    dvl = 2.0f * d;
-  }
-  stnt(a.vc * (dvl * a.inv_b), a.dval + row);
-  o.kl = in.old_lp - lp;
-  o.clipped = fabsf(ratio - 1.0f) > a.clip ? 1.0f : 0.0f;
+  const RowOut o = ppo_row_math(a, in, lp);
+  stnt(o.dval, a.dval + row);
   return o;
 }
 
@@ -605,36 +551,9 @@ template <int KA, int MAXA>
 __device__ __forceinline__ void cat_row_math(const LossArgs& a, float* zr, int A, long row,
                                              const RowIn& in, int ai, float ge,
                                              double (&acc)[5]) {
-  constexpr float kLog2e = 1.4426950408889634f;
-  float t[MAXA], e[MAXA];
-  float m = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < MAXA; ++j)
-    if (j < A) {
-      t[j] = zr[j];
-      m = fmaxf(m, t[j]);
-    }
-  float s = 0.0f, S = 0.0f;
-#pragma unroll
-  for (int j = 0; j < MAXA; ++j)
-    if (j < A) {
-      const float tj = fmaxf(t[j] - m, -FLT_MAX);
-      const float ej = __builtin_amdgcn_exp2f(tj * kLog2e);
-      t[j] = tj;
-      e[j] = ej;
-      s += ej;
-      S = fmaf(ej, tj, S);
-    }
-  const float log_s = logf(s);
-  const float inv_s = 1.0f / s;
-  const float H = log_s - S * inv_s;
-  const float lp = ai >= 0 ? (zr[ai] - m) - log_s : __builtin_nanf("");
-  const RowOut o = ppo_row(a, row, in, lp);
-  const float K = ge * (H - log_s) - o.g_lp;
-#pragma unroll
-  for (int j = 0; j < MAXA; ++j)
-    if (j < A) zr[j] = (e[j] * inv_s) * fmaf(ge, t[j], K);
-  if (ai >= 0) zr[ai] += o.g_lp;
+  float H;
+  const RowOut o = cat_row_grad<MAXA>(a, zr, A, ai, ge, in, H);
+  stnt(o.dval, a.dval + row);
   accumulate(acc, o, H);
 }
 
@@ -985,17 +904,16 @@ int fill_common(LossArgs& a, long B, const ppo_loss_params* p, const float* old_
   a.ret = ret;
   a.val = val;
   a.old_val = old_val;
-  // torch: ratio.clamp(1.0 - clip, 1.0 + clip) takes Python-double bounds
-  // and compares in fp32.
-  a.lo = (float)(1.0 - p->clip_ratio);
-  a.hi = (float)(1.0 + p->clip_ratio);
-  a.clip = (float)p->clip_ratio;
-  a.use_vclip = (p->vf_clip > 0.0 && p->vf_clip < INFINITY) ? 1 : 0;
+  const RowParams rp = make_row_params(p, B);
+  a.lo = rp.lo;
+  a.hi = rp.hi;
+  a.clip = rp.clip;
+  a.use_vclip = rp.use_vclip;
   if (a.use_vclip && !old_val) return PPO_ERR_INVALID_ARG;
-  a.vclip = (float)p->vf_clip;
-  a.vc = (float)p->value_coef;
-  a.ec = (float)p->entropy_coef;
-  a.inv_b = 1.0f / (float)B;
+  a.vclip = rp.vclip;
+  a.vc = rp.vc;
+  a.ec = rp.ec;
+  a.inv_b = rp.inv_b;
   a.dval = dval;
   a.scalars = scalars;
   return PPO_OK;

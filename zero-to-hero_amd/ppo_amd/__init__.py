@@ -30,11 +30,13 @@ from .ops import (
     gae,
     gather_rows,
     gae_normalize,
+    mlp_fusable,
     normalize_advantages,
     ppo_loss_discrete,
     ppo_loss_discrete_fused,
     ppo_loss_gaussian,
     ppo_loss_gaussian_fused,
+    ppo_mlp_cat_grads,
     sample_categorical,
     sample_gaussian,
 )
@@ -68,11 +70,13 @@ __all__ = [
     "gae_normalize",
     "gather_rows",
     "load_library",
+    "mlp_fusable",
     "normalize_advantages",
     "ppo_loss_discrete",
     "ppo_loss_discrete_fused",
     "ppo_loss_gaussian",
     "ppo_loss_gaussian_fused",
+    "ppo_mlp_cat_grads",
     "sample_categorical",
     "sample_gaussian",
 ]

@@ -43,6 +43,22 @@ class AdamParams(ctypes.Structure):
     ]
 
 
+class Mlp3(ctypes.Structure):
+    """struct ppo_mlp3_f32 (include/ppo_amd.h): the three nn.Linear layers of
+    an MLP and their gradient buffers, as device pointers."""
+
+    _fields_ = [
+        ("weight", ctypes.c_void_p * 3),
+        ("bias", ctypes.c_void_p * 3),
+        ("weight_grad", ctypes.c_void_p * 3),
+        ("bias_grad", ctypes.c_void_p * 3),
+    ]
+
+
+PPO_ACT_RELU = 0
+PPO_ACT_TANH = 1
+PPO_ERR_UNSUPPORTED = 4
+
 GATHER_MAX_ARRAYS = 8
 ADAM_MAX_TENSORS = 32
 
@@ -87,6 +103,12 @@ SIGNATURES = {
     ),
     "ppo_sample_cat_f32": (_int, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ppo_sample_gauss_f32": (_int, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ppo_mlp_cat_grad_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32]),
+    "ppo_mlp_cat_grad_f32": (
+        _int,
+        [ctypes.POINTER(Mlp3), ctypes.POINTER(Mlp3), _i32, _i32, _i32, _i32, _vp, _i64, _vp,
+         _i64, _vp, _int, _vp, _vp, _vp, _vp, ctypes.POINTER(LossParams), _vp, _vp, _sz, _vp],
+    ),
     "ppo_adam_clip_workspace_bytes": (_sz, [_i32, ctypes.POINTER(_i64)]),
     "ppo_adam_clip_f32": (
         _int,

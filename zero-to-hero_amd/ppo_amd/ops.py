@@ -12,6 +12,8 @@ Reference functions replaced (mrhooray/zero-to-hero, rl/deep/agents/ppo.py):
   normalize_advantages    ppo.py:126-127
   ppo_loss_discrete       PPOAgent._update_batch loss + backward (:150-169)
   ppo_loss_gaussian       the same loss for a Normal policy (no reference code)
+  ppo_mlp_cat_grads       PPOAgent._update_batch forward + backward through the
+                          actor/critic MLPs (:141-169, common.py:16-28)
 """
 
 from __future__ import annotations
@@ -35,6 +37,8 @@ __all__ = [
     "ppo_loss_discrete_fused",
     "ppo_loss_gaussian",
     "ppo_loss_gaussian_fused",
+    "ppo_mlp_cat_grads",
+    "mlp_fusable",
     "LossStats",
 ]
 
@@ -660,3 +664,143 @@ def ppo_loss_gaussian(
         clip_ratio, vf_clip, value_coef, entropy_coef,
     )
     return scalars[0], _stats_dict(scalars)
+
+
+# ---------------------------------------------------------------------------
+# Fused minibatch gradient through the actor and critic MLPs
+# ---------------------------------------------------------------------------
+MLP_HIDDEN_SIZES = (16, 32, 64, 128)
+MLP_MAX_IN = 64
+MLP_MAX_ACTIONS = 32
+
+
+def mlp_structure(net: torch.nn.Module) -> Optional[tuple[list, str]]:
+    """The three nn.Linear layers and the activation ("relu" / "tanh") of a
+    network shaped like rl/deep/agents/common.py:16-28's MLP (an `.net`
+    nn.Sequential, or the Sequential itself, of Linear-act-Linear-act-Linear
+    with one activation), or None for any other network."""
+    seq = getattr(net, "net", net)
+    if not isinstance(seq, torch.nn.Sequential) or len(seq) != 5:
+        return None
+    lin = [seq[0], seq[2], seq[4]]
+    if not all(type(m) is torch.nn.Linear and m.bias is not None for m in lin):
+        return None
+    kinds = {type(seq[1]), type(seq[3])}
+    if kinds == {torch.nn.ReLU}:
+        act = "relu"
+    elif kinds == {torch.nn.Tanh}:
+        act = "tanh"
+    else:
+        return None
+    return lin, act
+
+
+def mlp_fusable(policy: torch.nn.Module, value: torch.nn.Module) -> bool:
+    """True when ppo_mlp_cat_grads supports this actor/critic pair: both
+    MLP-shaped with the same input size, hidden size (16/32/64/128) and
+    activation, the critic with one output, <= 64 inputs, <= 32 actions, fp32
+    contiguous parameters on one GPU."""
+    sp, sv = mlp_structure(policy), mlp_structure(value)
+    if sp is None or sv is None or sp[1] != sv[1]:
+        return False
+    lp, lv = sp[0], sv[0]
+    D, H, A = lp[0].in_features, lp[0].out_features, lp[2].out_features
+    if lv[0].in_features != D or lv[0].out_features != H or lv[2].out_features != 1:
+        return False
+    if lp[1].in_features != H or lp[1].out_features != H or lv[1].out_features != H:
+        return False
+    if H not in MLP_HIDDEN_SIZES or D > MLP_MAX_IN or A > MLP_MAX_ACTIONS:
+        return False
+    params = [p for m in lp + lv for p in (m.weight, m.bias)]
+    dev = params[0].device
+    return all(p.device == dev and p.device.type == "cuda" and p.dtype == torch.float32
+               and p.is_contiguous() for p in params)
+
+
+def _mlp_struct(layers: list) -> _lib.Mlp3:
+    s = _lib.Mlp3()
+    for i, m in enumerate(layers):
+        for p in (m.weight, m.bias):
+            if p.grad is None:
+                p.grad = torch.zeros_like(p)
+            elif p.grad.shape != p.shape or p.grad.dtype != p.dtype or not p.grad.is_contiguous():
+                raise ValueError("parameter gradients must be contiguous fp32 of the parameter's shape")
+        s.weight[i] = m.weight.data_ptr()
+        s.bias[i] = m.bias.data_ptr()
+        s.weight_grad[i] = m.weight.grad.data_ptr()
+        s.bias_grad[i] = m.bias.grad.data_ptr()
+    return s
+
+
+def ppo_mlp_cat_grads(
+    policy: torch.nn.Module,
+    value: torch.nn.Module,
+    observations: torch.Tensor,
+    actions: torch.Tensor,
+    old_log_probs: torch.Tensor,
+    advantages: torch.Tensor,
+    returns: torch.Tensor,
+    old_values: Optional[torch.Tensor] = None,
+    index: Optional[torch.Tensor] = None,
+    clip_ratio: float = 0.2,
+    vf_clip: Optional[float] = None,
+    value_coef: float = 0.5,
+    entropy_coef: float = 0.01,
+    scalars_out: Optional[torch.Tensor] = None,
+) -> LossStats:
+    """Forward and backward of PPOAgent._update_batch (ppo.py:141-169) for one
+    minibatch in two launches: the rows `index` (int64 [B]; None: all n rows)
+    of the rollout arrays (observations [n,D], actions [n] int32/int64,
+    old_log_probs / advantages / returns / old_values [n]) go through both
+    MLPs, the categorical PPO loss and its backward, and every parameter's
+    `.grad` is overwritten with d loss / d parameter (allocated if None).
+    Returns the loss scalars (0-d device tensors).  Both networks must satisfy
+    mlp_fusable(); follow with ClippedAdam.step()."""
+    if not mlp_fusable(policy, value):
+        raise ValueError("policy/value are not MLPs the fused kernel supports (see mlp_fusable)")
+    lp, act = mlp_structure(policy)
+    lv, _ = mlp_structure(value)
+    D, H, A = lp[0].in_features, lp[0].out_features, lp[2].out_features
+    device = lp[0].weight.device
+    _require(observations, "observations", (torch.float32,), device)
+    if observations.dim() != 2 or observations.shape[1] != D:
+        raise ValueError(f"observations must be [n,{D}], got {tuple(observations.shape)}")
+    n = observations.shape[0]
+    _require(actions, "actions", (torch.int32, torch.int64), device)
+    if actions.shape != (n,):
+        raise ValueError(f"actions must be [n]=[{n}], got {tuple(actions.shape)}")
+    for t, name in ((old_log_probs, "old_log_probs"), (advantages, "advantages"),
+                    (returns, "returns")):
+        _require(t, name, (torch.float32,), device)
+        if t.shape != (n,):
+            raise ValueError(f"{name} must be [n]=[{n}], got {tuple(t.shape)}")
+    params = _params(clip_ratio, vf_clip, value_coef, entropy_coef)
+    if vf_clip is not None:
+        if old_values is None:
+            raise ValueError("vf_clip needs old_values")
+        _require(old_values, "old_values", (torch.float32,), device)
+        if old_values.shape != (n,):
+            raise ValueError(f"old_values must be [n]=[{n}], got {tuple(old_values.shape)}")
+    if index is not None:
+        _require(index, "index", (torch.int64,), device)
+        if index.dim() != 1:
+            raise ValueError(f"index must be 1-D, got {tuple(index.shape)}")
+        B = index.numel()
+    else:
+        B = n
+    if B == 0:
+        raise ValueError("the minibatch is empty")
+    scalars = _out(scalars_out, "scalars_out", (_lib.PPO_NUM_SCALARS,), torch.float32, device)
+    actor, critic = _mlp_struct(lp), _mlp_struct(lv)
+    stream = _stream(device)
+    lib = _lib.load()
+    nbytes = lib.ppo_mlp_cat_grad_workspace_bytes(B, D, H, A)
+    ws = _WORKSPACES.get(device, stream, nbytes)
+    _call("ppo_mlp_cat_grad_f32", device, stream, ctypes.byref(actor), ctypes.byref(critic),
+          D, H, A, _lib.PPO_ACT_TANH if act == "tanh" else _lib.PPO_ACT_RELU,
+          observations.data_ptr(), n, _ptr(index), B, actions.data_ptr(),
+          1 if actions.dtype == torch.int64 else 0, old_log_probs.data_ptr(),
+          advantages.data_ptr(), returns.data_ptr(),
+          _ptr(old_values) if vf_clip is not None else None, ctypes.byref(params),
+          scalars.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    return _stats_dict(scalars)

@@ -111,6 +111,11 @@ class VecPPO:
     launch and clip_grad_norm_ + Adam is ClippedAdam (two launches); otherwise
     torch indexing, clip_grad_norm_ and torch.optim.Adam are used.
 
+    With `fused_mlp` (default: whenever `fused_update` is on, the policy is
+    categorical and both networks are MLPs that ops.mlp_fusable accepts) each
+    minibatch's gather, MLP forwards, loss and backward are the two launches
+    of ops.ppo_mlp_cat_grads, which write the parameters' gradients directly.
+
     With `graphs=True` (requires `fused_update`) the minibatch loop is replayed
     from CUDA/HIP graphs: the whole update runs on a private stream, the
     flattened rollout and each epoch's permutation are copied into static
@@ -134,6 +139,7 @@ class VecPPO:
         fused_update: bool = True,
         graphs: bool = False,
         graph_chunk: int = 64,
+        fused_mlp: Optional[bool] = None,
     ) -> None:
         self.policy, self.value = policy, value
         self.ppo_config, self.gamma, self.batch_size = ppo_config, gamma, batch_size
@@ -150,6 +156,18 @@ class VecPPO:
         self.graphs, self.graph_chunk = graphs, graph_chunk
         self._plan: Optional[_GraphPlan] = None
         self._side_stream: Optional[torch.cuda.Stream] = None
+        can_fuse = fused_update and log_std is None and ops.mlp_fusable(policy, value)
+        if fused_mlp and not can_fuse:
+            raise ValueError("fused_mlp needs fused_update, a categorical policy and MLPs that "
+                             "ops.mlp_fusable accepts")
+        self.fused_mlp = can_fuse if fused_mlp is None else bool(fused_mlp)
+        self._scalars: Optional[torch.Tensor] = None
+        if self.fused_mlp:
+            # gradients exist before any graph capture; the kernel overwrites them
+            for p in self.parameters:
+                if p.grad is None:
+                    p.grad = torch.zeros_like(p)
+            self._scalars = torch.zeros(6, dtype=torch.float32, device=self.parameters[0].device)
         if fused_update:
             self.optimizer = ClippedAdam(self.parameters, lr=lr,
                                          max_grad_norm=ppo_config.gradient_clip,
@@ -204,19 +222,34 @@ class VecPPO:
         old_lp = buffer.log_probs[:T].reshape(n).contiguous()
         old_v = buffer.values[:T].reshape(n).contiguous()
         adv_f, ret_f = adv_n.reshape(n).contiguous(), ret.reshape(n).contiguous()
+        arrays = (obs, acts, old_lp, adv_f, ret_f, old_v)
         if self.graphs:
-            return self._update_graphed(buffer.device, (obs, acts, old_lp, adv_f, ret_f, old_v))
+            return self._update_graphed(buffer.device, arrays)
         stats: dict = {}
         for _ in range(cfg.epochs):
             indices = torch.randperm(n, generator=self.generator)
             for start in range(0, n, self.batch_size):
                 idx = indices[start : start + self.batch_size].to(buffer.device)
-                if self.fused:
-                    batch = ops.gather_rows(idx, obs, acts, old_lp, adv_f, ret_f, old_v)
-                else:
-                    batch = [x[idx] for x in (obs, acts, old_lp, adv_f, ret_f, old_v)]
-                stats = self._update_batch(*batch)
+                stats = self._minibatch(idx, arrays)
         return stats
+
+    def _minibatch(self, idx: torch.Tensor, arrays: tuple) -> dict:
+        """One minibatch (rows idx of the flattened rollout arrays): forward,
+        loss, backward and optimizer step."""
+        if self.fused_mlp and arrays[0].dim() == 2:
+            cfg = self.ppo_config
+            obs, acts, old_lp, adv, ret, old_v = arrays
+            stats = ops.ppo_mlp_cat_grads(
+                self.policy, self.value, obs, acts, old_lp, adv, ret,
+                old_v if cfg.vf_clip is not None else None, idx, cfg.clip_ratio, cfg.vf_clip,
+                cfg.value_coef, cfg.entropy_coef, scalars_out=self._scalars)
+            self.optimizer.step()  # clips to cfg.gradient_clip, then Adam
+            return stats
+        if self.fused:
+            batch = ops.gather_rows(idx, *arrays)
+        else:
+            batch = [x[idx] for x in arrays]
+        return self._update_batch(*batch)
 
     def update_graphed_ready(self) -> bool:
         """True once graphs are captured for the current rollout shape."""
@@ -261,7 +294,7 @@ class VecPPO:
 
     def _graph_minibatch(self, plan: "_GraphPlan", j: int) -> dict:
         idx = plan.perm[j * plan.B : (j + 1) * plan.B]
-        return self._update_batch(*ops.gather_rows(idx, *plan.static))
+        return self._minibatch(idx, tuple(plan.static))
 
     def _capture(self, plan: "_GraphPlan", stream: torch.cuda.Stream) -> None:
         pool = torch.cuda.graph_pool_handle()
