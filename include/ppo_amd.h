@@ -200,6 +200,19 @@ int ppo_gather_rows(const int64_t* index, int64_t B, int64_t n_src, int32_t narr
                     void* stream);
 
 /*
+ * Host-to-device copy of nbytes (a multiple of 4, < 2 GiB) from pinned host
+ * memory (hipHostMalloc / torch pin_memory) as one kernel launch on `stream`
+ * that reads the pinned pages over the bus; no counterpart in the reference.
+ * For the minibatch permutations of ppo.py:130, drawn on the CPU generator:
+ * a small hipMemcpyAsync from the host can wait for the stream's earlier work
+ * and stall the host, this launch does not.  The caller must keep src_host
+ * unchanged until the stream has passed the launch.  Returns
+ * PPO_ERR_INVALID_ARG (launching nothing) for memory that is not pinned and
+ * mapped for the device.
+ */
+int ppo_copy_from_pinned(void* dst, const void* src_host, int64_t nbytes, void* stream);
+
+/*
  * Batched action selection of PPOAgent.select_action (rl/deep/agents/ppo.py:
  * 65-79: Categorical(logits=policy(obs)).sample(), .log_prob(action),
  * value(obs)) for N environments at once, written straight into row t of a

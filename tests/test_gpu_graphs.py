@@ -71,8 +71,9 @@ def test_vecppo_graphs_match_eager_categorical(dev, graph_chunk):
         torch.cuda.synchronize()
         assert graphed.update_graphed_ready()
         _check(eager, graphed, s_e, s_g)
-    n_graphs = len(graphed._plan.graphs)
-    assert n_graphs == -(-5 // graph_chunk)
+    # one graph sequence per epoch, each of ceil(5 minibatches / chunk) graphs
+    assert len(graphed._plan.graphs) == 3
+    assert all(len(seq) == -(-5 // graph_chunk) for seq in graphed._plan.graphs)
     assert graphed.optimizer.step_count() == 3 * 3 * 5
 
 

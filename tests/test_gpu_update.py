@@ -86,3 +86,26 @@ def test_clipped_adam_skips_missing_grads(dev):
     opt.step()
     assert torch.equal(p[1].detach(), before)
     assert opt.steps == [1, 0]
+
+
+def test_copy_from_pinned(dev):
+    """ppo_copy_from_pinned: pinned host -> device by a kernel launch; memory
+    that is not pinned is refused before any launch."""
+    import ctypes
+
+    import numpy as np
+
+    from ppo_amd import _lib, ops
+
+    src = torch.randperm(10_000, generator=torch.Generator().manual_seed(3)).reshape(4, 2500)
+    pinned = src.pin_memory()
+    dst = torch.empty(4, 2500, dtype=torch.int64, device=dev)
+    ops.copy_pinned_to_device(dst, pinned)
+    assert torch.equal(dst.cpu(), src)
+    with pytest.raises(ValueError):
+        ops.copy_pinned_to_device(dst, src)  # not pinned: refused on the host side
+    plain = np.arange(16, dtype=np.int32)
+    rc = _lib.load().ppo_copy_from_pinned(dst.data_ptr(), plain.ctypes.data_as(ctypes.c_void_p),
+                                          64, torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.PPO_OK + 1  # PPO_ERR_INVALID_ARG: not pinned, nothing launched
+    assert torch.equal(dst.cpu(), src)

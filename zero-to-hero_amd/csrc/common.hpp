@@ -51,6 +51,16 @@ __device__ __forceinline__ double read_lane(double x, int lane) {
   return __builtin_bit_cast(double, r);
 }
 
+// Workgroup barrier that orders LDS only: waits for this wave's LDS
+// operations (lgkmcnt) but leaves its global loads and stores in flight,
+// where __syncthreads() would wait for all of them.  For phases that
+// communicate through LDS alone.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Wave-wide sum, the same value in every lane.  Within each 16-lane row, DPP
 // moves (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror,
 // row_mirror) leave the row's sum in every lane of the row; the four row sums

@@ -88,165 +88,251 @@ __device__ __forceinline__ float act_grad(float g, float y) {
   else return y > 0.0f ? g : 0.0f;
 }
 
-// Hidden layer forward: out[r][m] = act(b[m] + sum_k W[m][k] in[r][k]),
-// M = H outputs, K inputs (K % 4 == 0 when kVecK).
-template <int H, int kAct, bool kVecK>
-__device__ __forceinline__ void fwd_hidden(const float* __restrict__ W, const float* __restrict__ b,
-                                           const float* in, int K, float* out) {
-  constexpr int G = kMlpBlock / H;
-  constexpr int RPT = kMlpRows / G;
-  const int m = threadIdx.x % H;
-  const int g = threadIdx.x / H;
-  float acc[RPT];
-  const float bm = b[m];
+// ---------------------------------------------------------------------------
+// 16x16 MFMA tiles (v_mfma_f32_16x16x4f32, fp32 in and out).  Per step of 4
+// along the contraction, lane l supplies A(l % 16, k0 + l / 16) and
+// B(k0 + l / 16, l % 16); the result C(4 * (l / 16) + r, l % 16) is element r.
+// Every GEMM here has one 16-row side (the workgroup's minibatch rows) and
+// is cut into such tiles, spread over the workgroup's 4 waves.
+// ---------------------------------------------------------------------------
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4f mfma4(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// LDS row stride of a [16][H] activation buffer: H + 2 floats, so a half-
+// wave's operand reads (16 rows x 2 columns) fall in 32 distinct banks.
+template <int H>
+constexpr int act_ld() { return H + 2; }
+constexpr int kXld = kMlpMaxIn + 2;   // observations [16][kXld]
+constexpr int kZld = kMlpMaxA + 2;    // logits / dlogits [16][kZld]
+
+// Forward tile: out[r][n] = f(b[n] + sum_{k<K} in[r][k] W[n][k]) for the 16
+// columns n in [16 tj, 16 tj + 16) below N (f = the activation, or identity
+// for kAct < 0).  KC = K at compile time (0: runtime K): the lane's weight
+// values are then loaded in one batch.
+template <int KC, int kAct>
+__device__ __forceinline__ void fwd_tile(const float* in, int ldin, int K,
+                                         const float* __restrict__ W,
+                                         const float* __restrict__ b, int N, float* out,
+                                         int ldout, int tj) {
+  const int l = threadIdx.x % kWave, i = l % 16, kk = l / 16;
+  const int n = 16 * tj + i;
+  const bool nok = n < N;
+  const float* wrow = W + (long)(nok ? n : 0) * K;
+  v4f c = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (KC > 0) {
+    // contraction order permuted so that each lane's weights are contiguous:
+    // in step (q, e) lane (i, kk) contributes k = 16 q + 4 kk + e, its weight
+    // row read as one float4 per q
+    static_assert(KC % 16 == 0, "compile-time K must be a multiple of 16");
+    float4 bw[KC / 16];
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) acc[i] = bm;
-  const float* wr = W + (long)m * K;
-  if constexpr (kVecK) {
-    for (int k = 0; k < K; k += 4) {
-      const float4 w = *reinterpret_cast<const float4*>(wr + k);
+    for (int q = 0; q < KC / 16; ++q)
+      bw[q] = nok ? *reinterpret_cast<const float4*>(wrow + 16 * q + 4 * kk)
+                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-      for (int i = 0; i < RPT; ++i) {
-        const float4 x = *reinterpret_cast<const float4*>(in + (g + G * i) * K + k);
-        acc[i] = fmaf(w.x, x.x, acc[i]);
-        acc[i] = fmaf(w.y, x.y, acc[i]);
-        acc[i] = fmaf(w.z, x.z, acc[i]);
-        acc[i] = fmaf(w.w, x.w, acc[i]);
-      }
+    for (int q = 0; q < KC / 16; ++q) {
+      const float* ir = in + i * ldin + 16 * q + 4 * kk;
+      c = mfma4(ir[0], bw[q].x, c);
+      c = mfma4(ir[1], bw[q].y, c);
+      c = mfma4(ir[2], bw[q].z, c);
+      c = mfma4(ir[3], bw[q].w, c);
     }
   } else {
-    for (int k = 0; k < K; ++k) {
-      const float w = wr[k];
-#pragma unroll
-      for (int i = 0; i < RPT; ++i) acc[i] = fmaf(w, in[(g + G * i) * K + k], acc[i]);
+    for (int k0 = 0; k0 < K; k0 += 4) {
+      const int k = k0 + kk;
+      const float av = k < K ? in[i * ldin + k] : 0.0f;
+      const float bv = (k < K && nok) ? wrow[k] : 0.0f;
+      c = mfma4(av, bv, c);
     }
   }
+  if (nok) {
+    const float bias = b[n];
 #pragma unroll
-  for (int i = 0; i < RPT; ++i) out[(g + G * i) * H + m] = act_fwd<kAct>(acc[i]);
-}
-
-// Output layer forward: out[r][m] = b[m] + sum_k W[m][k] h[r][k], M <= 32.
-template <int H>
-__device__ __forceinline__ void fwd_out(const float* __restrict__ W, const float* __restrict__ b,
-                                        const float* h, int M, float* out) {
-  for (int o = threadIdx.x; o < kMlpRows * M; o += kMlpBlock) {
-    const int r = o / M, m = o - (o / M) * M;
-    const float* wr = W + (long)m * H;
-    float acc = b[m];
-#pragma unroll 4
-    for (int k = 0; k < H; k += 4) {
-      const float4 w = *reinterpret_cast<const float4*>(wr + k);
-      const float4 x = *reinterpret_cast<const float4*>(h + r * H + k);
-      acc = fmaf(w.x, x.x, acc);
-      acc = fmaf(w.y, x.y, acc);
-      acc = fmaf(w.z, x.z, acc);
-      acc = fmaf(w.w, x.w, acc);
+    for (int r = 0; r < 4; ++r) {
+      const float v = c[r] + bias;
+      if constexpr (kAct >= 0) out[(4 * kk + r) * ldout + n] = act_fwd<kAct>(v);
+      else out[(4 * kk + r) * ldout + n] = v;
     }
-    out[r * M + m] = acc;
   }
 }
 
-// Weight and bias gradient partials of one layer: gW[m][k] = sum_r d[r][m]
-// in[r][k], gb[m] = sum_r d[r][m] over the workgroup's rows.
-__device__ __forceinline__ void grad_wb(const float* d, int M, const float* in, int K,
-                                        float* __restrict__ gw, float* __restrict__ gb) {
-  for (int o = threadIdx.x; o < M * K; o += kMlpBlock) {
-    const int m = o / K, k = o - (o / K) * K;
-    float s = 0.0f;
+// Input-gradient tile of a layer with H inputs: gin[r][k] = act'(h[r][k]) *
+// sum_{m<M} d[r][m] W[m][k] for k in [16 tj, 16 tj + 16).  MC = M at compile
+// time (0: runtime M).  W rows are read along k: coalesced.
+template <int H, int MC, int kAct>
+__device__ __forceinline__ void back_tile(const float* d, int ldd, int M,
+                                          const float* __restrict__ W, const float* h,
+                                          float* gin, int tj) {
+  constexpr int ld = act_ld<H>();
+  const int l = threadIdx.x % kWave, i = l % 16, kk = l / 16;
+  const int col = 16 * tj + i;
+  v4f c = {0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (MC > 0) {
+    float bw[MC / 4];
 #pragma unroll
-    for (int r = 0; r < kMlpRows; ++r) s = fmaf(d[r * M + m], in[r * K + k], s);
-    gw[o] = s;
+    for (int q = 0; q < MC / 4; ++q) bw[q] = W[(long)(4 * q + kk) * H + col];
+#pragma unroll
+    for (int q = 0; q < MC / 4; ++q) c = mfma4(d[i * ldd + 4 * q + kk], bw[q], c);
+  } else {
+    for (int m0 = 0; m0 < M; m0 += 4) {
+      const int m = m0 + kk;
+      const float av = m < M ? d[i * ldd + m] : 0.0f;
+      const float bv = m < M ? W[(long)m * H + col] : 0.0f;
+      c = mfma4(av, bv, c);
+    }
   }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 4 * kk + r;
+    gin[row * ld + col] = act_grad<kAct>(c[r], h[row * ld + col]);
+  }
+}
+
+// Weight-gradient tile: gw[m][k] = sum over the 16 rows r of d[r][m] in[r][k]
+// for m in [16 ti, 16 ti + 16) below M and k in [16 tj, 16 tj + 16) below K,
+// written to the workgroup's partial (row-major [M][K]).
+__device__ __forceinline__ void wgrad_tile(const float* d, int ldd, int M, const float* in,
+                                           int ldin, int K, float* __restrict__ gw, int ti,
+                                           int tj) {
+  const int l = threadIdx.x % kWave, i = l % 16, kk = l / 16;
+  const int m = 16 * ti + i, k = 16 * tj + i;
+  v4f c = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = 4 * q + kk;
+    const float av = m < M ? d[r * ldd + m] : 0.0f;
+    const float bv = k < K ? in[r * ldin + k] : 0.0f;
+    c = mfma4(av, bv, c);
+  }
+  if (k < K) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int mo = 16 * ti + 4 * kk + r;
+      if (mo < M) gw[(long)mo * K + k] = c[r];
+    }
+  }
+}
+
+// Bias gradient: gb[m] = sum over the 16 rows of d[r][m], threads t < M.
+__device__ __forceinline__ void bgrad(const float* d, int ldd, int M, float* __restrict__ gb) {
   for (int m = threadIdx.x; m < M; m += kMlpBlock) {
     float s = 0.0f;
 #pragma unroll
-    for (int r = 0; r < kMlpRows; ++r) s += d[r * M + m];
+    for (int r = 0; r < kMlpRows; ++r) s += d[r * ldd + m];
     gb[m] = s;
   }
 }
 
-// Gradient into a hidden layer's output: din[r][k] = act'(h[r][k]) *
-// sum_m d[r][m] W[m][k], K = H units, M outputs of the next layer.
+// One network's backward from the gradient d3 [16][M3] at its output:
+// phase 1 (dW3, db3, gradient into the second hidden layer), phase 2 (dW2,
+// db2, gradient into the first), phase 3 (dW1, db1).  LDS-only barriers
+// between the phases (the gradient partials go to global memory and are read
+// by the next kernel); phase 3 leaves without one (the caller's next phase
+// must not write g1 before a barrier).
 template <int H, int kAct>
-__device__ __forceinline__ void back_hidden(const float* d, int M, const float* __restrict__ W,
-                                            const float* h, float* din) {
-  constexpr int G = kMlpBlock / H;
-  constexpr int RPT = kMlpRows / G;
-  const int k = threadIdx.x % H;
-  const int g = threadIdx.x / H;
-  float acc[RPT];
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) acc[i] = 0.0f;
-  for (int m = 0; m < M; ++m) {
-    const float w = W[(long)m * H + k];
-#pragma unroll
-    for (int i = 0; i < RPT; ++i) acc[i] = fmaf(d[(g + G * i) * M + m], w, acc[i]);
+__device__ __forceinline__ void net_backward(const MlpNet& net, const NetOffsets& o, float* gp,
+                                             const float* d3, int ld3, int M3, const float* x,
+                                             int D, const float* h1, const float* h2, float* g1,
+                                             float* g2) {
+  constexpr int ld = act_ld<H>();
+  constexpr int NT = H / 16;
+  const int w = threadIdx.x / kWave;
+  constexpr int kWaves = kMlpBlock / kWave;
+  const int MT3 = (M3 + 15) / 16;
+  // phase 1
+  for (int t = w; t < MT3 * NT + NT; t += kWaves) {
+    if (t < MT3 * NT) wgrad_tile(d3, ld3, M3, h2, ld, H, gp + o.w[2], t / NT, t % NT);
+    else back_tile<H, 0, kAct>(d3, ld3, M3, net.w[2], h2, g2, t - MT3 * NT);
   }
-#pragma unroll
-  for (int i = 0; i < RPT; ++i) {
-    const int r = g + G * i;
-    din[r * H + k] = act_grad<kAct>(acc[i], h[r * H + k]);
+  bgrad(d3, ld3, M3, gp + o.b[2]);
+  lds_barrier();
+  // phase 2
+  for (int t = w; t < NT * NT + NT; t += kWaves) {
+    if (t < NT * NT) wgrad_tile(g2, ld, H, h1, ld, H, gp + o.w[1], t / NT, t % NT);
+    else back_tile<H, H, kAct>(g2, ld, H, net.w[1], h1, g1, t - NT * NT);
   }
+  bgrad(g2, ld, H, gp + o.b[1]);
+  lds_barrier();
+  // phase 3
+  const int DT = (D + 15) / 16;
+  for (int t = w; t < NT * DT; t += kWaves)
+    wgrad_tile(g1, ld, H, x, kXld, D, gp + o.w[0], t / DT, t % DT);
+  bgrad(g1, ld, H, gp + o.b[0]);
 }
 
-template <int H, int kAct, typename ActT>
+template <int H, int kAct>
 __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   constexpr int R = kMlpRows;
-  // (16-byte aligned: the layers read them as float4)
-  __shared__ __align__(16) float s_x[R * kMlpMaxIn];
-  __shared__ __align__(16) float s_a1[R * H], s_a2[R * H], s_c1[R * H], s_c2[R * H];
-  __shared__ __align__(16) float s_g1[R * H], s_g2[R * H];
-  __shared__ __align__(16) float s_z[R * kMlpMaxA];
-  __shared__ __align__(16) float s_v[R];
+  constexpr int ld = act_ld<H>();
+  constexpr int NT = H / 16;
+  constexpr int kWaves = kMlpBlock / kWave;
+  __shared__ float s_x[R * kXld];
+  __shared__ float s_a1[R * ld], s_a2[R * ld], s_c1[R * ld], s_c2[R * ld];
+  __shared__ float s_g1[R * ld], s_g2[R * ld];
+  __shared__ float s_z[R * kZld];
+  __shared__ float s_v[R];
   __shared__ long s_row[R];
 
   const int tid = threadIdx.x;
+  const int w = tid / kWave;
   const long row0 = (long)blockIdx.x * R;
   const int D = a.D, A = a.A;
+  // the loss inputs of row `tid` (tid < R) are loaded now, ahead of the
+  // forward pass that precedes their use
+  RowIn rin = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  long raw_act = 0;
   if (tid < R) {
     const long i = row0 + tid;
-    s_row[tid] = i < a.B ? (a.idx ? (long)a.idx[i] : i) : -1;
+    const long src = i < a.B ? (a.idx ? (long)a.idx[i] : i) : -1;
+    s_row[tid] = src;
+    const long sc = src >= 0 ? src : 0;
+    rin.old_lp = a.old_lp[sc];
+    rin.adv = a.adv[sc];
+    rin.ret = a.ret[sc];
+    rin.vo = a.use_vclip ? a.old_val[sc] : 0.0f;
+    raw_act = a.act64 ? (long)reinterpret_cast<const int64_t*>(a.actions)[sc]
+                      : (long)reinterpret_cast<const int32_t*>(a.actions)[sc];
   }
-  __syncthreads();
+  lds_barrier();
   // gather the observation rows (padding rows past B are zeros)
   for (int e = tid; e < R * D; e += kMlpBlock) {
     const int r = e / D, c = e - (e / D) * D;
     const long src = s_row[r];
-    s_x[e] = (src >= 0 && src < a.n) ? a.obs[src * D + c] : 0.0f;
+    s_x[r * kXld + c] = (src >= 0 && src < a.n) ? a.obs[src * D + c] : 0.0f;
   }
-  __syncthreads();
+  lds_barrier();
 
-  // forward: both networks
-  if (D % 4 == 0) {
-    fwd_hidden<H, kAct, true>(a.actor.w[0], a.actor.b[0], s_x, D, s_a1);
-    fwd_hidden<H, kAct, true>(a.critic.w[0], a.critic.b[0], s_x, D, s_c1);
-  } else {
-    fwd_hidden<H, kAct, false>(a.actor.w[0], a.actor.b[0], s_x, D, s_a1);
-    fwd_hidden<H, kAct, false>(a.critic.w[0], a.critic.b[0], s_x, D, s_c1);
+  // forward, both networks: tiles (network, column tile) over the waves
+  for (int t = w; t < 2 * NT; t += kWaves) {
+    const MlpNet& net = t < NT ? a.actor : a.critic;
+    fwd_tile<0, kAct>(s_x, kXld, D, net.w[0], net.b[0], H, t < NT ? s_a1 : s_c1, ld, t % NT);
   }
-  __syncthreads();
-  fwd_hidden<H, kAct, true>(a.actor.w[1], a.actor.b[1], s_a1, H, s_a2);
-  fwd_hidden<H, kAct, true>(a.critic.w[1], a.critic.b[1], s_c1, H, s_c2);
-  __syncthreads();
-  fwd_out<H>(a.actor.w[2], a.actor.b[2], s_a2, A, s_z);
-  fwd_out<H>(a.critic.w[2], a.critic.b[2], s_c2, 1, s_v);
-  __syncthreads();
+  lds_barrier();
+  for (int t = w; t < 2 * NT; t += kWaves) {
+    const MlpNet& net = t < NT ? a.actor : a.critic;
+    fwd_tile<H, kAct>(t < NT ? s_a1 : s_c1, ld, H, net.w[1], net.b[1], H, t < NT ? s_a2 : s_c2,
+                      ld, t % NT);
+  }
+  lds_barrier();
+  const int AT = (A + 15) / 16;
+  for (int t = w; t < AT + 1; t += kWaves) {
+    if (t < AT) fwd_tile<H, -1>(s_a2, ld, H, a.actor.w[2], a.actor.b[2], A, s_z, kZld, t);
+    else fwd_tile<H, -1>(s_c2, ld, H, a.critic.w[2], a.critic.b[2], 1, s_v, 1, 0);
+  }
+  lds_barrier();
 
   // loss rows: logits -> dlogits in place, value -> dvalue in place
   double acc[kMlpSums] = {0.0, 0.0, 0.0, 0.0, 0.0};
   if (tid < R) {
     const long src = s_row[tid];
-    float* zr = s_z + tid * A;
+    float* zr = s_z + tid * kZld;
     if (src >= 0) {
-      RowIn in;
-      in.old_lp = a.old_lp[src];
-      in.adv = a.adv[src];
-      in.ret = a.ret[src];
+      RowIn in = rin;
       in.v = s_v[tid];
-      in.vo = a.use_vclip ? a.old_val[src] : 0.0f;
-      const long raw = a.act64 ? (long)reinterpret_cast<const int64_t*>(a.actions)[src]
-                               : (long)reinterpret_cast<const int32_t*>(a.actions)[src];
-      const int ai = (raw >= 0 && raw < A) ? (int)raw : -1;
+      const int ai = (raw_act >= 0 && raw_act < A) ? (int)raw_act : -1;
       float H_ent;
       const RowOut o = cat_row_grad<kMlpMaxA>(a, zr, A, ai, a.ec * a.inv_b, in, H_ent);
       s_v[tid] = o.dval;
@@ -267,45 +353,59 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   }
 
   float* gp = a.gpart + (long)blockIdx.x * a.P;
-  // actor backward
-  grad_wb(s_z, A, s_a2, H, gp + a.oa.w[2], gp + a.oa.b[2]);
-  back_hidden<H, kAct>(s_z, A, a.actor.w[2], s_a2, s_g2);
-  __syncthreads();
-  grad_wb(s_g2, H, s_a1, H, gp + a.oa.w[1], gp + a.oa.b[1]);
-  back_hidden<H, kAct>(s_g2, H, a.actor.w[1], s_a1, s_g1);
-  __syncthreads();
-  grad_wb(s_g1, H, s_x, D, gp + a.oa.w[0], gp + a.oa.b[0]);
-  __syncthreads();
-  // critic backward
-  grad_wb(s_v, 1, s_c2, H, gp + a.oc.w[2], gp + a.oc.b[2]);
-  back_hidden<H, kAct>(s_v, 1, a.critic.w[2], s_c2, s_g2);
-  __syncthreads();
-  grad_wb(s_g2, H, s_c1, H, gp + a.oc.w[1], gp + a.oc.b[1]);
-  back_hidden<H, kAct>(s_g2, H, a.critic.w[1], s_c1, s_g1);
-  __syncthreads();
-  grad_wb(s_g1, H, s_x, D, gp + a.oc.w[0], gp + a.oc.b[0]);
+  net_backward<H, kAct>(a.actor, a.oa, gp, s_z, kZld, A, s_x, D, s_a1, s_a2, s_g1, s_g2);
+  lds_barrier();
+  net_backward<H, kAct>(a.critic, a.oc, gp, s_v, 1, 1, s_x, D, s_c1, s_c2, s_g1, s_g2);
 }
 
-// Sum the per-workgroup gradient partials (fixed order, fp64) into the
-// parameters' gradient tensors; workgroup 0 also forms the loss scalars.
+// Sum the per-workgroup gradient partials into the parameters' gradient
+// tensors: a workgroup owns 64 consecutive parameters; wave w sums partials
+// w, w + 4, w + 8, ... (fp64, 8 loads in flight per step) and the four wave
+// sums are added in wave order, so the order is fixed (deterministic).
+// Workgroup 0 also forms the loss scalars.
+constexpr int kRedCols = 64;
+
+__device__ __forceinline__ float* grad_slot(const MlpArgs& a, long p) {
+  const MlpNet* nets[2] = {&a.actor, &a.critic};
+  const NetOffsets* offs[2] = {&a.oa, &a.oc};
+  float* dst = nullptr;
+#pragma unroll
+  for (int n = 0; n < 2; ++n)
+#pragma unroll
+    for (int l = 0; l < 3; ++l) {
+      if (p >= offs[n]->w[l] && p < offs[n]->b[l]) dst = nets[n]->gw[l] + (p - offs[n]->w[l]);
+      const long bend = (l < 2) ? offs[n]->w[l + 1] : (n == 0 ? a.oc.w[0] : a.P);
+      if (p >= offs[n]->b[l] && p < bend) dst = nets[n]->gb[l] + (p - offs[n]->b[l]);
+    }
+  return dst;
+}
+
 __global__ void __launch_bounds__(kMlpBlock) mlp_grad_reduce_kernel(MlpArgs a) {
-  const long p = (long)blockIdx.x * kMlpBlock + threadIdx.x;
-  if (p < a.P) {
-    double s = 0.0;
-    for (long b = 0; b < a.nblocks; ++b) s += (double)a.gpart[b * a.P + p];
-    // which tensor p falls in: offsets ascend actor w0 b0 w1 b1 w2 b2, critic ...
-    const MlpNet* nets[2] = {&a.actor, &a.critic};
-    const NetOffsets* offs[2] = {&a.oa, &a.oc};
-    float* dst = nullptr;
+  constexpr int kWaves = kMlpBlock / kWave;
+  __shared__ double s_sum[kWaves][kRedCols];
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  const long p = (long)blockIdx.x * kRedCols + lane;
+  const long pc = p < a.P ? p : a.P - 1;
+  double s = 0.0;
+  for (long b0 = w; b0 < a.nblocks; b0 += 8 * kWaves) {
+    float v[8];
 #pragma unroll
-    for (int n = 0; n < 2; ++n)
+    for (int j = 0; j < 8; ++j) {
+      const long b = b0 + (long)j * kWaves;
+      v[j] = a.gpart[(b < a.nblocks ? b : 0) * a.P + pc];
+    }
 #pragma unroll
-      for (int l = 0; l < 3; ++l) {
-        if (p >= offs[n]->w[l] && p < offs[n]->b[l]) dst = nets[n]->gw[l] + (p - offs[n]->w[l]);
-        const long bend = (l < 2) ? offs[n]->w[l + 1] : (n == 0 ? a.oc.w[0] : a.P);
-        if (p >= offs[n]->b[l] && p < bend) dst = nets[n]->gb[l] + (p - offs[n]->b[l]);
-      }
-    *dst = (float)s;
+    for (int j = 0; j < 8; ++j)
+      if (b0 + (long)j * kWaves < a.nblocks) s += (double)v[j];
+  }
+  s_sum[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && p < a.P) {
+    double t = s_sum[0][lane];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) t += s_sum[k][lane];
+    *grad_slot(a, p) = (float)t;
   }
   if (blockIdx.x == 0) {
     double tot[kMlpSums];
@@ -356,19 +456,13 @@ MlpLayout mlp_layout(long B, int D, int H, int A) {
   return l;
 }
 
-template <int H, int kAct>
-const void* mlp_kernel_h(bool i64) {
-  return i64 ? (const void*)mlp_cat_grad_kernel<H, kAct, int64_t>
-             : (const void*)mlp_cat_grad_kernel<H, kAct, int32_t>;
-}
-
 template <int kAct>
-const void* mlp_kernel_act(int H, bool i64) {
+const void* mlp_kernel_act(int H) {
   switch (H) {
-    case 16: return mlp_kernel_h<16, kAct>(i64);
-    case 32: return mlp_kernel_h<32, kAct>(i64);
-    case 64: return mlp_kernel_h<64, kAct>(i64);
-    case 128: return mlp_kernel_h<128, kAct>(i64);
+    case 16: return (const void*)mlp_cat_grad_kernel<16, kAct>;
+    case 32: return (const void*)mlp_cat_grad_kernel<32, kAct>;
+    case 64: return (const void*)mlp_cat_grad_kernel<64, kAct>;
+    case 128: return (const void*)mlp_cat_grad_kernel<128, kAct>;
     default: return nullptr;
   }
 }
@@ -414,8 +508,8 @@ extern "C" int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
   if (B < 0 || n < 0) return PPO_ERR_INVALID_ARG;
   if (obs_dim <= 0 || obs_dim > kMlpMaxIn || A <= 0 || A > kMlpMaxA) return PPO_ERR_UNSUPPORTED;
   if (activation != PPO_ACT_RELU && activation != PPO_ACT_TANH) return PPO_ERR_INVALID_ARG;
-  const void* kern = activation == PPO_ACT_TANH ? mlp_kernel_act<PPO_ACT_TANH>(hidden, actions_are_int64)
-                                                : mlp_kernel_act<PPO_ACT_RELU>(hidden, actions_are_int64);
+  const void* kern = activation == PPO_ACT_TANH ? mlp_kernel_act<PPO_ACT_TANH>(hidden)
+                                                : mlp_kernel_act<PPO_ACT_RELU>(hidden);
   if (!kern) return PPO_ERR_UNSUPPORTED;
   if (!mlp_net_ok(actor) || !mlp_net_ok(critic) || !params || !scalars_out)
     return PPO_ERR_INVALID_ARG;
@@ -470,7 +564,7 @@ extern "C" int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
   int st = hip_status(hipLaunchKernel(kern, dim3((unsigned)l.nblocks), dim3(kMlpBlock), args, 0,
                                       stream));
   if (st) return st;
-  const long rblocks = (l.P + kMlpBlock - 1) / kMlpBlock;
+  const long rblocks = (l.P + kRedCols - 1) / kRedCols;
   return hip_status(hipLaunchKernel((const void*)mlp_grad_reduce_kernel, dim3((unsigned)rblocks),
                                     dim3(kMlpBlock), args, 0, stream));
 }

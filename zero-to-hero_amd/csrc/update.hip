@@ -49,6 +49,16 @@ __global__ void __launch_bounds__(kBlock) gather_rows_kernel(GatherTable t,
   }
 }
 
+// dst[i] = src[i] for i < nwords (src may be pinned host memory mapped into
+// the device's address space).
+__global__ void __launch_bounds__(kBlock) copy_words_kernel(const unsigned* __restrict__ src,
+                                                            unsigned* __restrict__ dst,
+                                                            long nwords) {
+  const long stride = (long)gridDim.x * blockDim.x;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nwords; i += stride)
+    dst[i] = src[i];
+}
+
 // ---------------------------------------------------------------------------
 // clip_grad_norm_ + Adam
 // ---------------------------------------------------------------------------
@@ -117,16 +127,27 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
                                                              AdamScalars s, float* norm_out,
                                                              const int64_t* step_counter) {
   __shared__ float s_coef;
+  __shared__ float s_norm[PPO_ADAM_MAX_TENSORS];
   if (step_counter) adam_step_scalars(s, step_counter);
-  // Global norm: per-tensor norms rounded to fp32, then the norm of those (the
-  // two-level form of torch's _get_total_norm); every block derives the same
-  // value in the same order.
+  // Global norm: per-tensor norms rounded to fp32 (lane k of wave 0 sums
+  // tensor k's block partials in block order), then the norm of those in
+  // tensor order (the two-level form of torch's _get_total_norm); every block
+  // derives the same value in the same order.
+  if (threadIdx.x < PPO_ADAM_MAX_TENSORS) {
+    const int k = threadIdx.x;
+    float nk = 0.0f;
+    if (k < t.nt) {
+      double sk = 0.0;
+      for (long b = t.block_start[k]; b < t.block_start[k + 1]; ++b) sk += partial[b];
+      nk = (float)sqrt(sk);
+    }
+    s_norm[k] = nk;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
     float total_sq = 0.0f;
     for (int k = 0; k < t.nt; ++k) {
-      double sk = 0.0;
-      for (long b = t.block_start[k]; b < t.block_start[k + 1]; ++b) sk += partial[b];
-      const float nk = (float)sqrt(sk);
+      const float nk = s_norm[k];
       total_sq = __fadd_rn(total_sq, __fmul_rn(nk, nk));
     }
     const float total = __fsqrt_rn(total_sq);
@@ -199,6 +220,28 @@ extern "C" int ppo_gather_rows(const int64_t* index, int64_t B, int64_t n_src, i
   long blocks = std::min((total + kBlock - 1) / kBlock, 8192L);
   hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
                      reinterpret_cast<hipStream_t>(stream_ptr), t, index, (long)B, (long)n_src);
+  return last_launch_status();
+}
+
+extern "C" int ppo_copy_from_pinned(void* dst, const void* src_host, int64_t nbytes,
+                                    void* stream_ptr) {
+  using namespace ppo;
+  if (nbytes < 0 || nbytes % 4 || nbytes >= (1L << 31)) return PPO_ERR_INVALID_ARG;
+  if (nbytes == 0) return PPO_OK;
+  if (!dst || !src_host) return PPO_ERR_INVALID_ARG;
+  // the device's view of the pinned allocation; fails (and nothing is
+  // launched) for memory the runtime did not pin and map
+  void* src_dev = nullptr;
+  hipError_t e = hipHostGetDevicePointer(&src_dev, const_cast<void*>(src_host), 0);
+  if (e != hipSuccess || !src_dev) {
+    (void)hipGetLastError();
+    return PPO_ERR_INVALID_ARG;
+  }
+  const long nwords = nbytes / 4;
+  const long blocks = std::min((nwords + kBlock - 1) / kBlock, 1024L);
+  hipLaunchKernelGGL(copy_words_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
+                     reinterpret_cast<hipStream_t>(stream_ptr),
+                     static_cast<const unsigned*>(src_dev), static_cast<unsigned*>(dst), nwords);
   return last_launch_status();
 }
 

@@ -145,6 +145,20 @@ def _gae_inputs(rewards, values, dones, last_value):
     return device, T, N
 
 
+def _outputs(out, count, like: torch.Tensor) -> list:
+    """Caller-provided output tensors (fp32, contiguous, the shape of `like`,
+    on its device), or new ones."""
+    if out is None:
+        return [torch.empty_like(like) for _ in range(count)]
+    if len(out) != count:
+        raise ValueError(f"out must hold {count} tensors, got {len(out)}")
+    for k, t in enumerate(out):
+        _require(t, f"out[{k}]", (torch.float32,), like.device)
+        if t.shape != like.shape:
+            raise ValueError(f"out[{k}] must have shape {tuple(like.shape)}, got {tuple(t.shape)}")
+    return list(out)
+
+
 def gae(
     rewards: torch.Tensor,
     values: torch.Tensor,
@@ -152,6 +166,7 @@ def gae(
     last_value: Optional[torch.Tensor] = None,
     gamma: float = 0.99,
     lam: float = 0.95,
+    out: Optional[tuple] = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Advantages and returns of a [T,N] (or [T]) rollout on the GPU.
 
@@ -159,11 +174,11 @@ def gae(
     with the reference's operation order; `dones` is terminated-or-truncated
     (uint8 or bool); `last_value` [N] bootstraps past step T-1 (None = zeros,
     the reference's rule).  Returns (advantages, returns) fp32, same shape as
-    rewards, with returns = advantages + values (ppo.py:124).
+    rewards, with returns = advantages + values (ppo.py:124); written into
+    `out` = (advantages, returns) when given.
     """
     device, T, N = _gae_inputs(rewards, values, dones, last_value)
-    adv = torch.empty_like(rewards)
-    ret = torch.empty_like(rewards)
+    adv, ret = _outputs(out, 2, rewards)
     if T * N == 0:
         return adv, ret
     stream = _stream(device)
@@ -187,15 +202,15 @@ def gae_normalize(
     lam: float = 0.95,
     eps: float = 1e-8,
     return_stats: bool = False,
+    out: Optional[tuple] = None,
 ):
     """gae() plus the normalised advantages of ppo.py:126-127, fused: the
     advantage mean/std are accumulated inside the GAE pass.  Returns
     (advantages, returns, normalized_advantages[, stats]) where stats is a
-    [2] fp32 device tensor {mean, std}."""
+    [2] fp32 device tensor {mean, std}; the first three are written into
+    `out` when given."""
     device, T, N = _gae_inputs(rewards, values, dones, last_value)
-    adv = torch.empty_like(rewards)
-    ret = torch.empty_like(rewards)
-    adv_n = torch.empty_like(rewards)
+    adv, ret, adv_n = _outputs(out, 3, rewards)
     stats = torch.empty(2, dtype=torch.float32, device=device)
     if T * N > 0:
         stream = _stream(device)
@@ -323,6 +338,26 @@ def gather_rows(index: torch.Tensor, *arrays: torch.Tensor) -> list[torch.Tensor
     stream = _stream(device)
     _call("ppo_gather_rows", device, stream, index.data_ptr(), B, n, na, src, rbs, dst, stream)
     return outs
+
+
+def copy_pinned_to_device(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """dst <- src for a pinned host tensor `src`, as one kernel launch on the
+    current stream that reads the pinned memory over the bus
+    (ppo_copy_from_pinned).  Asynchronous: the host must not overwrite `src`
+    until the stream has passed this launch (record an event).  A small
+    host-to-device copy through the runtime can instead wait for the stream's
+    earlier work and stall the host."""
+    if not isinstance(src, torch.Tensor) or src.device.type != "cpu" or not src.is_pinned():
+        raise ValueError("src must be a pinned host tensor")
+    if not src.is_contiguous() or not dst.is_contiguous():
+        raise ValueError("src and dst must be contiguous")
+    if dst.device.type != "cuda" or dst.dtype != src.dtype or dst.numel() != src.numel():
+        raise ValueError("dst must be a CUDA tensor of src's dtype and size")
+    nbytes = src.numel() * src.element_size()
+    device = dst.device
+    stream = _stream(device)
+    _call("ppo_copy_from_pinned", device, stream, dst.data_ptr(), src.data_ptr(), nbytes, stream)
+    return dst
 
 
 # ---------------------------------------------------------------------------

@@ -83,9 +83,10 @@ class ClippedAdam:
     def step(self) -> torch.Tensor:
         # as torch: parameters without a gradient are skipped (and keep their step)
         live = [k for k, p in enumerate(self.params) if p.grad is not None]
-        norm = torch.zeros((), dtype=torch.float32, device=self.device)
         if not live:
-            return norm
+            return torch.zeros((), dtype=torch.float32, device=self.device)
+        # written by the kernel (no fill launch)
+        norm = torch.empty((), dtype=torch.float32, device=self.device)
         if self.capturable and len(live) != len(self.params):
             raise RuntimeError("ClippedAdam(capturable=True) steps all parameters together; "
                                "every parameter needs a gradient")

@@ -53,6 +53,7 @@ class RolloutBuffer:
         self.dones = torch.zeros((T, N), dtype=torch.uint8, device=dev)
         self.last_value = torch.zeros(N, **f32)
         self.step = 0
+        self._gae_out: Optional[list] = None  # advantages, returns, normalised ([T,N] each)
 
     def add(self, observations, actions, rewards, dones, values, log_probs) -> None:
         """Store step `self.step` for all N envs (ppo.py:93-106, batched)."""
@@ -99,6 +100,18 @@ class RolloutBuffer:
         adv, ret = ops.gae(r, v, d, self.last_value, gamma, lam)
         return adv, ret, None
 
+    def _advantages_in_place(self, gamma: float, lam: float, eps: float = 1e-8):
+        """compute_advantages(normalize=True) into storage the buffer keeps:
+        the same addresses on every call (graph replays read them), contents
+        overwritten by the next call."""
+        T = self.step
+        if self._gae_out is None:
+            self._gae_out = [torch.empty((self.T, self.N), dtype=torch.float32, device=self.device)
+                             for _ in range(3)]
+        out = tuple(o[:T] for o in self._gae_out)
+        r, v, d = self.rewards[:T], self.values[:T], self.dones[:T]
+        return ops.gae_normalize(r, v, d, self.last_value, gamma, lam, eps, out=out)
+
 
 class VecPPO:
     """PPOAgent._update (ppo.py:113-171) for a [T,N] rollout.
@@ -117,13 +130,16 @@ class VecPPO:
     of ops.ppo_mlp_cat_grads, which write the parameters' gradients directly.
 
     With `graphs=True` (requires `fused_update`) the minibatch loop is replayed
-    from CUDA/HIP graphs: the whole update runs on a private stream, the
-    flattened rollout and each epoch's permutation are copied into static
-    device buffers, the first epoch after a change of shape runs eagerly (the
-    warm-up that initialises library handles and autograd state), and the
-    minibatch sequence is then captured as graphs of `graph_chunk`
-    minibatches each and replayed for every later epoch.  The results equal
-    the eager fused path's: the same kernels run on the same data.
+    from CUDA/HIP graphs: the whole update runs on a private stream; the
+    graphs read the rollout buffer's own storage (its arrays and the advantage
+    outputs it keeps) and one [epochs, n] device tensor of permutations, which
+    is the only copy per update.  The first update of a buffer runs its first
+    epoch eagerly (the warm-up that initialises library handles and autograd
+    state), then captures every epoch's minibatch sequence as graphs of
+    `graph_chunk` minibatches and replays them; later updates of the same
+    buffer only replay.  Graphs are kept for the two most recent buffers.
+    The results equal the eager fused path's: the same kernels run on the
+    same data.
     """
 
     def __init__(
@@ -154,7 +170,8 @@ class VecPPO:
         if graph_chunk < 1:
             raise ValueError(f"graph_chunk must be >= 1, got {graph_chunk}")
         self.graphs, self.graph_chunk = graphs, graph_chunk
-        self._plan: Optional[_GraphPlan] = None
+        self._plans: dict = {}  # (shape, storage) key -> _GraphPlan, two at most
+        self._plan: Optional[_GraphPlan] = None  # the most recently used
         self._side_stream: Optional[torch.cuda.Stream] = None
         can_fuse = fused_update and log_std is None and ops.mlp_fusable(policy, value)
         if fused_mlp and not can_fuse:
@@ -212,7 +229,7 @@ class VecPPO:
         """Run `epochs` passes of shuffled minibatches; returns the last
         minibatch's loss scalars (device tensors)."""
         cfg = self.ppo_config
-        adv, ret, adv_n = buffer.compute_advantages(self.gamma, cfg.gae_lambda, True)
+        adv, ret, adv_n = buffer._advantages_in_place(self.gamma, cfg.gae_lambda)
         T = buffer.step
         n = T * buffer.N
         if n <= 1:
@@ -258,43 +275,51 @@ class VecPPO:
     def _update_graphed(self, device: torch.device, arrays: tuple) -> dict:
         cfg = self.ppo_config
         n, B = arrays[0].shape[0], self.batch_size
-        key = (n, B, cfg.epochs) + tuple((a.dtype, tuple(a.shape[1:])) for a in arrays)
+        key = (n, B, cfg.epochs) + tuple(
+            (a.dtype, tuple(a.shape[1:]), a.data_ptr()) for a in arrays)
         if self._side_stream is None:
             self._side_stream = torch.cuda.Stream(device=device)
         s = self._side_stream
         caller = torch.cuda.current_stream(device)
         s.wait_stream(caller)
         with torch.cuda.stream(s):
-            plan = self._plan
-            if plan is None or plan.key != key:
-                plan = self._plan = _GraphPlan(key, arrays, n, B, cfg.epochs, device)
-            for st, a in zip(plan.static, arrays):
-                st.copy_(a)
-            perms = torch.stack([torch.randperm(n, generator=self.generator)
-                                 for _ in range(cfg.epochs)])
-            plan.perms.copy_(perms.pin_memory(), non_blocking=True)
-            stats: dict = {}
+            plan = self._plans.pop(key, None)
+            if plan is None:
+                plan = _GraphPlan(key, arrays, n, B, cfg.epochs, device)
+            self._plans[key] = plan  # most recent last
+            while len(self._plans) > 2:
+                self._plans.pop(next(iter(self._plans)))
+            self._plan = plan
+            # this update's permutations: written on the host into one of two
+            # pinned buffers (the other may still be read by the previous
+            # update's upload), then uploaded by a kernel launch
+            k = plan.flip
+            plan.flip ^= 1
+            if plan.host_events[k] is not None:
+                plan.host_events[k].synchronize()
+            host = plan.perms_host[k]
             for e in range(cfg.epochs):
-                plan.perm.copy_(plan.perms[e])
-                if plan.graphs:
-                    for g in plan.graphs:
-                        g.replay()
-                    stats = plan.stats
-                elif not plan.warm:
-                    for j in range(plan.nmb):
-                        stats = self._graph_minibatch(plan, j)
-                    plan.warm = True
-                else:
-                    self._capture(plan, s)
-                    for g in plan.graphs:
-                        g.replay()
-                    stats = plan.stats
+                torch.randperm(n, generator=self.generator, out=host[e])
+            ops.copy_pinned_to_device(plan.perms, host)
+            ev = torch.cuda.Event()
+            ev.record(s)
+            plan.host_events[k] = ev
+            first = 0
+            if not plan.graphs:
+                for j in range(plan.nmb):
+                    self._graph_minibatch(plan, 0, j)
+                self._capture(plan, s)
+                first = 1
+            for e in range(first, cfg.epochs):
+                for g in plan.graphs[e]:
+                    g.replay()
+            stats = plan.stats
         caller.wait_stream(s)
         return stats
 
-    def _graph_minibatch(self, plan: "_GraphPlan", j: int) -> dict:
-        idx = plan.perm[j * plan.B : (j + 1) * plan.B]
-        return self._minibatch(idx, tuple(plan.static))
+    def _graph_minibatch(self, plan: "_GraphPlan", e: int, j: int) -> dict:
+        idx = plan.perms[e, j * plan.B : (j + 1) * plan.B]
+        return self._minibatch(idx, plan.arrays)
 
     def _capture(self, plan: "_GraphPlan", stream: torch.cuda.Stream) -> None:
         pool = torch.cuda.graph_pool_handle()
@@ -302,12 +327,15 @@ class VecPPO:
         ops._WORKSPACES.capture_refs = refs
         try:
             stats: dict = {}
-            for c in range(0, plan.nmb, self.graph_chunk):
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g, pool=pool, stream=stream):
-                    for j in range(c, min(c + self.graph_chunk, plan.nmb)):
-                        stats = self._graph_minibatch(plan, j)
-                plan.graphs.append(g)
+            for e in range(plan.epochs):
+                seq = []
+                for c in range(0, plan.nmb, self.graph_chunk):
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, pool=pool, stream=stream):
+                        for j in range(c, min(c + self.graph_chunk, plan.nmb)):
+                            stats = self._graph_minibatch(plan, e, j)
+                    seq.append(g)
+                plan.graphs.append(seq)
         except BaseException:
             plan.graphs.clear()
             raise
@@ -344,18 +372,21 @@ class VecPPO:
 
 
 class _GraphPlan:
-    """Static buffers and captured graphs of VecPPO's minibatch loop for one
-    rollout shape: `static` holds the flattened arrays the graphs gather from,
-    `perm` the current epoch's permutation (its slices are the minibatch
-    indices), `perms` every epoch's permutation for one update."""
+    """Captured graphs of VecPPO's minibatch loop for one rollout: `arrays`
+    are the flattened rollout arrays the graphs read (held, so their storage
+    stays allocated while the graphs exist), `perms` the update's [epochs, n]
+    permutations (row e's slices are epoch e's minibatch indices), `graphs`
+    one list of graphs per epoch."""
 
     def __init__(self, key, arrays, n: int, B: int, epochs: int, device) -> None:
-        self.key, self.n, self.B = key, n, B
+        self.key, self.n, self.B, self.epochs = key, n, B, epochs
         self.nmb = (n + B - 1) // B
-        self.static = [torch.empty_like(a) for a in arrays]
-        self.perm = torch.empty(n, dtype=torch.int64, device=device)
+        self.arrays = tuple(arrays)
         self.perms = torch.empty((epochs, n), dtype=torch.int64, device=device)
-        self.warm = False
+        self.perms_host = [torch.empty((epochs, n), dtype=torch.int64, pin_memory=True)
+                           for _ in range(2)]
+        self.host_events: list = [None, None]
+        self.flip = 0
         self.graphs: list = []
         self.stats: dict = {}
         self.refs: list = []
