@@ -322,6 +322,33 @@ int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
                          const ppo_loss_params* params, float* scalars_out, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Vectorised CartPole-v1 (the reference's environment, rl/deep/cli.py:    */
+/* 179-180, stepped by rl/deep/runner.py:56-74).                            */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Reset N environments: state[n] = -0.05 + 0.1 * uniforms[n] (fp64 [N,4]
+ * from the caller's U[0,1) fp32 [N,4]), steps[n] = 0, obs_out = (float)state.
+ */
+int ppo_cartpole_reset(double* state, int32_t* steps, const float* uniforms, float* obs_out,
+                       int64_t N, void* stream);
+
+/*
+ * One env.step(action) for N environments (gymnasium CartPoleEnv dynamics,
+ * fp64, explicit Euler, tau 0.02; see csrc/cartpole.hip): actions int32 (1
+ * pushes right); rewards_out = 1; dones_out = terminated (|x| > 2.4 or
+ * |theta| > 12 deg) or truncated (steps reach max_steps, 500 for v1);
+ * terminated_out (may be NULL) = terminated alone.  A done environment is
+ * reset in the same launch from reset_uniforms [N,4] and obs_out holds its
+ * reset observation.  No counterpart in the reference's own code (its
+ * environment comes from gymnasium); no workspace.
+ */
+int ppo_cartpole_step(double* state, int32_t* steps, const int32_t* actions,
+                      const float* reset_uniforms, int32_t max_steps, float* obs_out,
+                      float* rewards_out, uint8_t* dones_out, uint8_t* terminated_out,
+                      int64_t N, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -504,6 +504,61 @@ def _update_batch_grads(policy, value, observations, actions, old_log_probs, adv
 
 
 # ---------------------------------------------------------------------------
+# CartPole-v1 dynamics (the reference's environment, rl/deep/cli.py:179-180)
+# ---------------------------------------------------------------------------
+# The equations are not in the reference's sources: they live in gymnasium
+# (>= 1.3 per rl/uv.lock), which is not installed here.  This restates the
+# published cart-pole model (Barto, Sutton & Anderson 1983) with gymnasium's
+# CartPoleEnv constants and conventions (explicit Euler, tau 0.02, fp64
+# state, fp32 observations, |x| > 2.4 or |theta| > 12 degrees terminates,
+# reward 1 per step, TimeLimit 500).  Parity with gymnasium itself is
+# unpinned; tests/test_oracle.py pins this restatement by an exact rational
+# known answer and by mirror symmetry.
+CARTPOLE = dict(gravity=9.8, masscart=1.0, masspole=0.1, length=0.5, force_mag=10.0, tau=0.02,
+                x_threshold=2.4)
+
+
+def cartpole_step_reference(state, actions, steps, reset_uniforms, max_steps=500):
+    """One step of N environments in Python floats (fp64), each operation
+    rounded on its own: returns (next_state [N,4] f64 after same-step resets,
+    obs [N,4] f32, rewards [N] f32, dones [N] u8, terminated [N] u8, steps
+    [N] int32)."""
+    c = CARTPOLE
+    total_mass = c["masspole"] + c["masscart"]
+    polemass_length = c["masspole"] * c["length"]
+    theta_threshold = 12 * 2 * math.pi / 360
+    state = np.asarray(state, np.float64)
+    N = state.shape[0]
+    nxt = np.empty_like(state)
+    dones = np.zeros(N, np.uint8)
+    term_out = np.zeros(N, np.uint8)
+    steps_out = np.zeros(N, np.int32)
+    for n in range(N):
+        x, x_dot, theta, theta_dot = (float(v) for v in state[n])
+        force = c["force_mag"] if int(actions[n]) == 1 else -c["force_mag"]
+        costheta, sintheta = math.cos(theta), math.sin(theta)
+        temp = (force + polemass_length * (theta_dot * theta_dot) * sintheta) / total_mass
+        thetaacc = (c["gravity"] * sintheta - costheta * temp) / (
+            c["length"] * (4.0 / 3.0 - c["masspole"] * (costheta * costheta) / total_mass))
+        xacc = temp - polemass_length * thetaacc * costheta / total_mass
+        x = x + c["tau"] * x_dot
+        x_dot = x_dot + c["tau"] * xacc
+        theta = theta + c["tau"] * theta_dot
+        theta_dot = theta_dot + c["tau"] * thetaacc
+        term = (x < -c["x_threshold"] or x > c["x_threshold"]
+                or theta < -theta_threshold or theta > theta_threshold)
+        t = int(steps[n]) + 1
+        done = term or t >= max_steps
+        if done:
+            u = np.asarray(reset_uniforms[n], np.float64)
+            nxt[n] = -0.05 + (0.05 - -0.05) * u
+        else:
+            nxt[n] = (x, x_dot, theta, theta_dot)
+        dones[n], term_out[n], steps_out[n] = done, term, 0 if done else t
+    return (nxt, nxt.astype(np.float32), np.ones(N, np.float32), dones, term_out, steps_out)
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline step (bench.py's cpu_baseline leg)
 # ---------------------------------------------------------------------------
 def cpu_update_step(

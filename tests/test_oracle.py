@@ -432,3 +432,59 @@ def test_sample_reference_log_prob_matches_torch_categorical():
     a, lp, _ = ref.sample_categorical_reference(z.numpy(), u.numpy())
     want = torch.distributions.Categorical(logits=z).log_prob(torch.from_numpy(a))
     assert np.allclose(lp, want.numpy(), rtol=0, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# CartPole-v1 restatement (gymnasium's equations; parity with gymnasium itself
+# is unpinned: it is not installed)
+# ---------------------------------------------------------------------------
+def _cp(state, actions, steps=None, u=None, max_steps=500):
+    state = np.asarray(state, np.float64)
+    N = state.shape[0]
+    steps = np.zeros(N, np.int32) if steps is None else np.asarray(steps, np.int32)
+    u = np.full((N, 4), 0.5, np.float32) if u is None else np.asarray(u, np.float32)
+    return ref.cartpole_step_reference(state, np.asarray(actions), steps, u, max_steps)
+
+
+def test_cartpole_known_answer_from_rest():
+    """From the upright rest state, pushing right: with m_c = 1, m_p = 0.1,
+    l = 0.5, F = 10 the accelerations are exact rationals, xacc = 400/41 and
+    thetaacc = -600/41, so after tau = 0.02 the velocities are 8/41 and
+    -12/41 and the positions are still 0."""
+    nxt = _cp([[0.0, 0.0, 0.0, 0.0]], [1])[0][0]
+    assert nxt[0] == 0.0 and nxt[2] == 0.0
+    assert nxt[1] == pytest.approx(8 / 41, rel=1e-14)
+    assert nxt[3] == pytest.approx(-12 / 41, rel=1e-14)
+    # pushing left mirrors it
+    nxl = _cp([[0.0, 0.0, 0.0, 0.0]], [0])[0][0]
+    assert nxl[1] == -nxt[1] and nxl[3] == -nxt[3]
+
+
+def test_cartpole_mirror_symmetry_bitwise():
+    """step(-s, 1-a) == -step(s, a) exactly: every operation is odd or even
+    in the state's sign."""
+    g = np.random.default_rng(3)
+    s = g.uniform(-0.2, 0.2, (64, 4))
+    a = g.integers(0, 2, 64)
+    n1 = _cp(s, a)[0]
+    n2 = _cp(-s, 1 - a)[0]
+    done = _cp(s, a)[3].astype(bool)
+    np.testing.assert_array_equal(n1[~done], -n2[~done])
+
+
+def test_cartpole_termination_thresholds_and_truncation():
+    # x crosses 2.4 (x' = x + tau x_dot = 2.39 + 0.02 * 1 = 2.41): terminated
+    out = _cp([[2.39, 1.0, 0.0, 0.0]], [1])
+    assert out[3][0] == 1 and out[4][0] == 1
+    # theta crosses 12 degrees
+    th = 12 * 2 * math.pi / 360
+    out = _cp([[0.0, 0.0, th - 0.001, 1.0]], [1])
+    assert out[3][0] == 1 and out[4][0] == 1
+    # inside the bounds: not done, step count advances
+    out = _cp([[0.0, 0.0, 0.0, 0.0]], [1], steps=[7])
+    assert out[3][0] == 0 and out[5][0] == 8
+    # the 500th step truncates without termination, and resets
+    out = _cp([[0.0, 0.0, 0.0, 0.0]], [1], steps=[499], u=[[0.0, 1.0, 0.5, 0.25]])
+    assert out[3][0] == 1 and out[4][0] == 0 and out[5][0] == 0
+    np.testing.assert_allclose(out[0][0], [-0.05, 0.05, 0.0, -0.025], atol=1e-17)
+    assert out[1].dtype == np.float32 and out[2].tolist() == [1.0]

@@ -40,6 +40,7 @@ from .ops import (
     sample_categorical,
     sample_gaussian,
 )
+from .env import CartPoleVec
 from .optim import ClippedAdam
 from .rollout import RolloutBuffer, VecPPO
 
@@ -52,6 +53,7 @@ def load_library():
 
 
 __all__ = [
+    "CartPoleVec",
     "ClippedAdam",
     "LIB_PATH",
     "LossStats",

@@ -102,6 +102,8 @@ SIGNATURES = {
          ctypes.POINTER(_vp), ctypes.POINTER(_i32), ctypes.POINTER(_vp), _vp],
     ),
     "ppo_copy_from_pinned": (_int, [_vp, _vp, _i64, _vp]),
+    "ppo_cartpole_reset": (_int, [_vp, _vp, _vp, _vp, _i64, _vp]),
+    "ppo_cartpole_step": (_int, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i64, _vp]),
     "ppo_sample_cat_f32": (_int, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ppo_sample_gauss_f32": (_int, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ppo_mlp_cat_grad_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32]),

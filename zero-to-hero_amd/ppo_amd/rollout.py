@@ -225,6 +225,29 @@ class VecPPO:
                                              values=values, **outs)
         return acts, logp, outs["values_out"]
 
+    @torch.no_grad()
+    def collect(self, env, buffer: RolloutBuffer, observations: torch.Tensor,
+                generator: Optional[torch.Generator] = None, bootstrap: bool = True):
+        """Fill `buffer` with buffer.T steps of the vectorised environment
+        `env` (an object with step(actions int32 [N]) -> (observations,
+        rewards, dones, ...), e.g. CartPoleVec), starting from
+        `observations` [N, *obs_shape]: the rollout loop of
+        rl/deep/runner.py:56-74 for N environments, with select_action
+        (ppo.py:65-79) batched by act().  With `bootstrap` the value of the
+        state after the last step seeds the advantages of environments still
+        running (masked for those whose episode just ended); without it the
+        reference's zero is used.  Returns the observations after the last
+        step (a copy)."""
+        buffer.reset()
+        obs = observations
+        for _ in range(buffer.T):
+            acts, _, _ = self.act(obs, buffer=buffer, generator=generator)
+            obs, rewards, dones = env.step(acts)[:3]
+            buffer.add_outcome(rewards, dones)
+        obs = obs.clone()
+        buffer.finish(self.value(obs).reshape(-1) if bootstrap else None)
+        return obs
+
     def update(self, buffer: RolloutBuffer) -> dict:
         """Run `epochs` passes of shuffled minibatches; returns the last
         minibatch's loss scalars (device tensors)."""
