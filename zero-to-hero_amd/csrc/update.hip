@@ -49,13 +49,14 @@ __global__ void __launch_bounds__(kBlock) gather_rows_kernel(GatherTable t,
   }
 }
 
-// dst[i] = src[i] for i < nwords (src may be pinned host memory mapped into
-// the device's address space).
-__global__ void __launch_bounds__(kBlock) copy_words_kernel(const unsigned* __restrict__ src,
-                                                            unsigned* __restrict__ dst,
-                                                            long nwords) {
+// dst[i] = src[i] for i < n elements of T (src may be pinned host memory
+// mapped into the device's address space; 16-byte elements when both ends
+// are aligned, so each bus read carries four words).
+template <typename T>
+__global__ void __launch_bounds__(kBlock) copy_words_kernel(const T* __restrict__ src,
+                                                            T* __restrict__ dst, long n) {
   const long stride = (long)gridDim.x * blockDim.x;
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nwords; i += stride)
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
     dst[i] = src[i];
 }
 
@@ -237,11 +238,19 @@ extern "C" int ppo_copy_from_pinned(void* dst, const void* src_host, int64_t nby
     (void)hipGetLastError();
     return PPO_ERR_INVALID_ARG;
   }
-  const long nwords = nbytes / 4;
-  const long blocks = std::min((nwords + kBlock - 1) / kBlock, 1024L);
-  hipLaunchKernelGGL(copy_words_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
-                     reinterpret_cast<hipStream_t>(stream_ptr),
-                     static_cast<const unsigned*>(src_dev), static_cast<unsigned*>(dst), nwords);
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  if (nbytes % 16 == 0 && aligned(src_dev, 16) && aligned(dst, 16)) {
+    const long n = nbytes / 16;
+    const long blocks = std::min((n + kBlock - 1) / kBlock, 1024L);
+    hipLaunchKernelGGL(copy_words_kernel<uint4>, dim3((unsigned)blocks), dim3(kBlock), 0, stream,
+                       static_cast<const uint4*>(src_dev), static_cast<uint4*>(dst), n);
+  } else {
+    const long n = nbytes / 4;
+    const long blocks = std::min((n + kBlock - 1) / kBlock, 1024L);
+    hipLaunchKernelGGL(copy_words_kernel<unsigned>, dim3((unsigned)blocks), dim3(kBlock), 0,
+                       stream, static_cast<const unsigned*>(src_dev), static_cast<unsigned*>(dst),
+                       n);
+  }
   return last_launch_status();
 }
 
