@@ -322,6 +322,21 @@ int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
                          const ppo_loss_params* params, float* scalars_out, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/*
+ * PPOAgent.select_action (rl/deep/agents/ppo.py:65-79) for N observations
+ * through the actor and critic MLPs of ppo_mlp_cat_grad_f32 (only the weights
+ * and biases of the structs are read): logits = actor(obs), values =
+ * critic(obs), then ppo_sample_cat_f32's inverse-CDF draw at uniforms[n].
+ * Writes actions_out (int32), log_probs_out and values_out, and copies the
+ * observations to observations_out when it is not NULL (a rollout buffer
+ * row).  One launch; same size limits as ppo_mlp_cat_grad_f32.
+ */
+int ppo_mlp_act_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
+                        int32_t obs_dim, int32_t hidden, int32_t A, int32_t activation,
+                        const float* observations, int64_t N, const float* uniforms,
+                        float* observations_out, int32_t* actions_out, float* log_probs_out,
+                        float* values_out, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Vectorised CartPole-v1 (the reference's environment, rl/deep/cli.py:    */
 /* 179-180, stepped by rl/deep/runner.py:56-74).                            */
@@ -341,12 +356,16 @@ int ppo_cartpole_reset(double* state, int32_t* steps, const float* uniforms, flo
  * |theta| > 12 deg) or truncated (steps reach max_steps, 500 for v1);
  * terminated_out (may be NULL) = terminated alone.  A done environment is
  * reset in the same launch from reset_uniforms [N,4] and obs_out holds its
- * reset observation.  No counterpart in the reference's own code (its
- * environment comes from gymnasium); no workspace.
+ * reset observation.  Episode tally (all three NULL, or all set):
+ * episode_return[n] accumulates the rewards of the running episode; when it
+ * ends, its return is added to completed_sum[n] (fp64), completed_count[n]
+ * is incremented and episode_return[n] restarts at 0.  No counterpart in the
+ * reference's own code (its environment comes from gymnasium); no workspace.
  */
 int ppo_cartpole_step(double* state, int32_t* steps, const int32_t* actions,
                       const float* reset_uniforms, int32_t max_steps, float* obs_out,
                       float* rewards_out, uint8_t* dones_out, uint8_t* terminated_out,
+                      float* episode_return, double* completed_sum, int32_t* completed_count,
                       int64_t N, void* stream);
 
 #ifdef __cplusplus

@@ -34,7 +34,8 @@ def _kernel_step(dev, state, actions, steps, u, max_steps=500):
     term = torch.empty(N, dtype=torch.uint8, device=dev)
     rc = _lib.load().ppo_cartpole_step(st.data_ptr(), sp.data_ptr(), ac.data_ptr(), uu.data_ptr(),
                                        max_steps, obs.data_ptr(), rew.data_ptr(), done.data_ptr(),
-                                       term.data_ptr(), N, torch.cuda.current_stream().cuda_stream)
+                                       term.data_ptr(), None, None, None, N,
+                                       torch.cuda.current_stream().cuda_stream)
     assert rc == 0
     return (st.cpu().numpy(), obs.cpu().numpy(), rew.cpu().numpy(), done.cpu().numpy(),
             term.cpu().numpy(), sp.cpu().numpy())

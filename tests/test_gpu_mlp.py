@@ -172,3 +172,31 @@ def test_vecppo_fused_mlp_matches_unfused(dev, graphs):
         torch.testing.assert_close(a.detach(), b.detach(), rtol=0, atol=1e-5)
     for k in ("loss", "policy", "value", "entropy"):
         torch.testing.assert_close(s_f[k], s_u[k], rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("H,A,act", [(64, 2, "tanh"), (128, 5, "relu"), (32, 18, "tanh")])
+def test_mlp_act_matches_torch_forward_and_sampler(dev, H, A, act):
+    """ppo_mlp_act_cat_f32 (both forwards + the inverse-CDF draw in one
+    launch) against torch's MLP forwards + ppo_sample_cat_f32 at the same
+    uniforms: values and log-probs within 1e-5, actions equal except rows
+    whose uniform lies within 1e-5 of a CDF boundary (the two forwards round
+    differently), observations copied exactly."""
+    torch.manual_seed(H + A)
+    N, D = 1000, 6
+    pol, val = MLP(D, H, A, act).to(dev), MLP(D, H, 1, act).to(dev)
+    obs = torch.randn(N, D, device=dev)
+    u = torch.rand(N, device=dev)
+    obs_out = torch.empty(N, D, device=dev)
+    a1, lp1, v1 = ppo_amd.mlp_act_categorical(pol, val, obs, u, observations_out=obs_out)
+    with torch.no_grad():
+        logits = pol(obs)
+        v2 = val(obs).squeeze(1)
+    a2, lp2 = ppo_amd.sample_categorical(logits.contiguous(), u)
+    _, _, margin = ref.sample_categorical_reference(logits.cpu().double().numpy(),
+                                                    u.cpu().double().numpy())
+    clear = torch.from_numpy(margin > 1e-5)
+    assert clear.float().mean() > 0.95
+    assert torch.equal(a1.cpu()[clear], a2.cpu()[clear])
+    torch.testing.assert_close(lp1.cpu()[clear], lp2.cpu()[clear], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(v1, v2, rtol=1e-5, atol=1e-5)
+    assert torch.equal(obs_out, obs)

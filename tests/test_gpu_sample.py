@@ -84,13 +84,18 @@ def test_sample_gaussian_matches_torch_normal(dev, N, D):
     np.testing.assert_allclose(logp.cpu().numpy(), want_lp.numpy(), rtol=0, atol=2e-5)
 
 
-def test_vecppo_act_fills_buffer_rows(dev):
+@pytest.mark.parametrize("fused_mlp", [False, True])
+def test_vecppo_act_fills_buffer_rows(dev, fused_mlp):
+    """VecPPO.act writes row t of the buffer: torch's MLPs + the sampling
+    kernel (exact against torch's forward), or the fused forward + sampling
+    kernel (MFMA forward: values and log-probs within 1e-5)."""
     from ppo_amd.agent import MLP
 
     torch.manual_seed(2)
     T, N = 4, 16
     policy, value = MLP(4, 32, 3, "tanh").to(dev), MLP(4, 32, 1, "tanh").to(dev)
-    vec = ppo_amd.VecPPO(policy, value)
+    vec = ppo_amd.VecPPO(policy, value, fused_mlp=fused_mlp)
+    tol = 1e-5 if fused_mlp else 0.0
     buf = ppo_amd.RolloutBuffer(T, N, (4,), device=dev)
     g = torch.Generator(device=dev).manual_seed(11)
     for t in range(T):
@@ -101,9 +106,9 @@ def test_vecppo_act_fills_buffer_rows(dev):
             z = policy(obs)
             want_v = value(obs).squeeze(1)
         assert torch.equal(buf.observations[t], obs)
-        torch.testing.assert_close(buf.values[t], want_v, rtol=0, atol=0)
+        torch.testing.assert_close(buf.values[t], want_v, rtol=0, atol=tol)
         want_lp = torch.log_softmax(z, 1).gather(1, buf.actions[t].long()[:, None]).squeeze(1)
-        torch.testing.assert_close(buf.log_probs[t], want_lp, rtol=0, atol=2e-6)
+        torch.testing.assert_close(buf.log_probs[t], want_lp, rtol=0, atol=2e-6 + tol)
         buf.add_outcome(torch.ones(N, device=dev), torch.zeros(N, dtype=torch.uint8, device=dev))
     assert buf.step == T
     with pytest.raises(IndexError):

@@ -46,7 +46,8 @@ __global__ void __launch_bounds__(kBlock) cartpole_step_kernel(
     double* __restrict__ state, int32_t* __restrict__ steps, const int32_t* __restrict__ actions,
     const float* __restrict__ uniforms, int max_steps, float* __restrict__ obs,
     float* __restrict__ rewards, uint8_t* __restrict__ dones, uint8_t* __restrict__ terminated,
-    long N) {
+    float* __restrict__ ep_return, double* __restrict__ done_sum,
+    int32_t* __restrict__ done_count, long N) {
   const long n = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= N) return;
   // operation order as gymnasium evaluates it in Python floats
@@ -84,6 +85,14 @@ __global__ void __launch_bounds__(kBlock) cartpole_step_kernel(
   rewards[n] = 1.0f;
   dones[n] = done ? 1 : 0;
   if (terminated) terminated[n] = term ? 1 : 0;
+  if (ep_return) {
+    const float ret = ep_return[n] + 1.0f;
+    if (done) {
+      done_sum[n] += (double)ret;
+      done_count[n] += 1;
+    }
+    ep_return[n] = done ? 0.0f : ret;
+  }
 }
 
 __global__ void __launch_bounds__(kBlock) cartpole_reset_kernel(double* __restrict__ state,
@@ -121,9 +130,14 @@ extern "C" int ppo_cartpole_reset(double* state, int32_t* steps, const float* un
 extern "C" int ppo_cartpole_step(double* state, int32_t* steps, const int32_t* actions,
                                  const float* reset_uniforms, int32_t max_steps, float* obs_out,
                                  float* rewards_out, uint8_t* dones_out,
-                                 uint8_t* terminated_out, int64_t N, void* stream) {
+                                 uint8_t* terminated_out, float* episode_return,
+                                 double* completed_sum, int32_t* completed_count, int64_t N,
+                                 void* stream) {
   using namespace ppo;
   if (N < 0 || max_steps < 1) return PPO_ERR_INVALID_ARG;
+  if ((episode_return == nullptr) != (completed_sum == nullptr) ||
+      (episode_return == nullptr) != (completed_count == nullptr))
+    return PPO_ERR_INVALID_ARG;
   if (N == 0) return PPO_OK;
   if (!state || !steps || !actions || !reset_uniforms || !obs_out || !rewards_out || !dones_out)
     return PPO_ERR_INVALID_ARG;
@@ -131,6 +145,6 @@ extern "C" int ppo_cartpole_step(double* state, int32_t* steps, const int32_t* a
   hipLaunchKernelGGL(cartpole_step_kernel, dim3((unsigned)((N + kBlock - 1) / kBlock)),
                      dim3(kBlock), 0, reinterpret_cast<hipStream_t>(stream), state, steps,
                      actions, reset_uniforms, (int)max_steps, obs_out, rewards_out, dones_out,
-                     terminated_out, (long)N);
+                     terminated_out, episode_return, completed_sum, completed_count, (long)N);
   return last_launch_status();
 }

@@ -28,6 +28,7 @@
 
 #include "common.hpp"
 #include "row_math.hpp"
+#include "sample_row.hpp"
 
 namespace ppo {
 namespace {
@@ -263,6 +264,37 @@ __device__ __forceinline__ void net_backward(const MlpNet& net, const NetOffsets
   bgrad(g1, ld, H, gp + o.b[0]);
 }
 
+// Forward of both networks for the workgroup's 16 rows x (observations in
+// s_x): hidden activations into a1/a2 (actor) and c1/c2 (critic), logits into
+// z [16][kZld], values into v [16].  Tiles (network, column tile) over the
+// waves; LDS-only barriers between the layers and after the last.
+template <int H, int kAct>
+__device__ __forceinline__ void mlp_forward(const MlpNet& actor, const MlpNet& critic,
+                                            const float* x, int D, int A, float* a1, float* a2,
+                                            float* c1, float* c2, float* z, float* v) {
+  constexpr int ld = act_ld<H>();
+  constexpr int NT = H / 16;
+  constexpr int kWaves = kMlpBlock / kWave;
+  const int w = threadIdx.x / kWave;
+  for (int t = w; t < 2 * NT; t += kWaves) {
+    const MlpNet& net = t < NT ? actor : critic;
+    fwd_tile<0, kAct>(x, kXld, D, net.w[0], net.b[0], H, t < NT ? a1 : c1, ld, t % NT);
+  }
+  lds_barrier();
+  for (int t = w; t < 2 * NT; t += kWaves) {
+    const MlpNet& net = t < NT ? actor : critic;
+    fwd_tile<H, kAct>(t < NT ? a1 : c1, ld, H, net.w[1], net.b[1], H, t < NT ? a2 : c2, ld,
+                      t % NT);
+  }
+  lds_barrier();
+  const int AT = (A + 15) / 16;
+  for (int t = w; t < AT + 1; t += kWaves) {
+    if (t < AT) fwd_tile<H, -1>(a2, ld, H, actor.w[2], actor.b[2], A, z, kZld, t);
+    else fwd_tile<H, -1>(c2, ld, H, critic.w[2], critic.b[2], 1, v, 1, 0);
+  }
+  lds_barrier();
+}
+
 template <int H, int kAct>
 __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   constexpr int R = kMlpRows;
@@ -305,24 +337,7 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   }
   lds_barrier();
 
-  // forward, both networks: tiles (network, column tile) over the waves
-  for (int t = w; t < 2 * NT; t += kWaves) {
-    const MlpNet& net = t < NT ? a.actor : a.critic;
-    fwd_tile<0, kAct>(s_x, kXld, D, net.w[0], net.b[0], H, t < NT ? s_a1 : s_c1, ld, t % NT);
-  }
-  lds_barrier();
-  for (int t = w; t < 2 * NT; t += kWaves) {
-    const MlpNet& net = t < NT ? a.actor : a.critic;
-    fwd_tile<H, kAct>(t < NT ? s_a1 : s_c1, ld, H, net.w[1], net.b[1], H, t < NT ? s_a2 : s_c2,
-                      ld, t % NT);
-  }
-  lds_barrier();
-  const int AT = (A + 15) / 16;
-  for (int t = w; t < AT + 1; t += kWaves) {
-    if (t < AT) fwd_tile<H, -1>(s_a2, ld, H, a.actor.w[2], a.actor.b[2], A, s_z, kZld, t);
-    else fwd_tile<H, -1>(s_c2, ld, H, a.critic.w[2], a.critic.b[2], 1, s_v, 1, 0);
-  }
-  lds_barrier();
+  mlp_forward<H, kAct>(a.actor, a.critic, s_x, D, A, s_a1, s_a2, s_c1, s_c2, s_z, s_v);
 
   // loss rows: logits -> dlogits in place, value -> dvalue in place
   double acc[kMlpSums] = {0.0, 0.0, 0.0, 0.0, 0.0};
@@ -356,6 +371,57 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   net_backward<H, kAct>(a.actor, a.oa, gp, s_z, kZld, A, s_x, D, s_a1, s_a2, s_g1, s_g2);
   lds_barrier();
   net_backward<H, kAct>(a.critic, a.oc, gp, s_v, 1, 1, s_x, D, s_c1, s_c2, s_g1, s_g2);
+}
+
+// Action selection through both networks (ppo.py:65-79 for N observations):
+// the forward of mlp_cat_grad_kernel, then per row the inverse-CDF draw of
+// sample_row.hpp at the caller's uniform.  Writes actions (int32), their
+// log-probabilities and the critic's values, and copies the observations to
+// obs_out when given (a rollout buffer row).
+struct ActArgs {
+  MlpNet actor, critic;
+  int D, A;
+  const float* obs;
+  long N;
+  const float* u;
+  float* obs_out;
+  int32_t* act;
+  float* logp;
+  float* val;
+};
+
+template <int H, int kAct>
+__global__ void __launch_bounds__(kMlpBlock) mlp_act_cat_kernel(ActArgs a) {
+  constexpr int R = kMlpRows;
+  constexpr int ld = act_ld<H>();
+  __shared__ float s_x[R * kXld];
+  __shared__ float s_a1[R * ld], s_a2[R * ld], s_c1[R * ld], s_c2[R * ld];
+  __shared__ float s_z[R * kZld];
+  __shared__ float s_v[R];
+  const int tid = threadIdx.x;
+  const long row0 = (long)blockIdx.x * R;
+  const int D = a.D;
+  for (int e = tid; e < R * D; e += kMlpBlock) {
+    const int r = e / D, c = e - (e / D) * D;
+    const long row = row0 + r;
+    float x = 0.0f;
+    if (row < a.N) {
+      x = a.obs[row * D + c];
+      if (a.obs_out) a.obs_out[row * D + c] = x;
+    }
+    s_x[r * kXld + c] = x;
+  }
+  const float u = tid < R && row0 + tid < a.N ? a.u[row0 + tid] : 0.0f;
+  lds_barrier();
+  mlp_forward<H, kAct>(a.actor, a.critic, s_x, D, a.A, s_a1, s_a2, s_c1, s_c2, s_z, s_v);
+  if (tid < R && row0 + tid < a.N) {
+    int act;
+    float lp;
+    sample_cat_row(s_z + tid * kZld, a.A, u, act, lp);
+    a.act[row0 + tid] = act;
+    a.logp[row0 + tid] = lp;
+    a.val[row0 + tid] = s_v[tid];
+  }
 }
 
 // Sum the per-workgroup gradient partials into the parameters' gradient
@@ -467,6 +533,24 @@ const void* mlp_kernel_act(int H) {
   }
 }
 
+template <int kAct>
+const void* act_kernel_act(int H) {
+  switch (H) {
+    case 16: return (const void*)mlp_act_cat_kernel<16, kAct>;
+    case 32: return (const void*)mlp_act_cat_kernel<32, kAct>;
+    case 64: return (const void*)mlp_act_cat_kernel<64, kAct>;
+    case 128: return (const void*)mlp_act_cat_kernel<128, kAct>;
+    default: return nullptr;
+  }
+}
+
+bool mlp_net_weights_ok(const ppo_mlp3_f32* n) {
+  if (!n) return false;
+  for (int l = 0; l < 3; ++l)
+    if (!n->weight[l] || !n->bias[l] || !aligned(n->weight[l], 16)) return false;
+  return true;
+}
+
 bool mlp_net_ok(const ppo_mlp3_f32* n) {
   if (!n) return false;
   for (int l = 0; l < 3; ++l)
@@ -567,4 +651,40 @@ extern "C" int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
   const long rblocks = (l.P + kRedCols - 1) / kRedCols;
   return hip_status(hipLaunchKernel((const void*)mlp_grad_reduce_kernel, dim3((unsigned)rblocks),
                                     dim3(kMlpBlock), args, 0, stream));
+}
+
+extern "C" int ppo_mlp_act_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
+                                   int32_t obs_dim, int32_t hidden, int32_t A,
+                                   int32_t activation, const float* observations, int64_t N,
+                                   const float* uniforms, float* observations_out,
+                                   int32_t* actions_out, float* log_probs_out,
+                                   float* values_out, void* stream_ptr) {
+  using namespace ppo;
+  if (N < 0) return PPO_ERR_INVALID_ARG;
+  if (obs_dim <= 0 || obs_dim > kMlpMaxIn || A <= 0 || A > kMlpMaxA) return PPO_ERR_UNSUPPORTED;
+  if (activation != PPO_ACT_RELU && activation != PPO_ACT_TANH) return PPO_ERR_INVALID_ARG;
+  const void* kern = activation == PPO_ACT_TANH ? act_kernel_act<PPO_ACT_TANH>(hidden)
+                                                : act_kernel_act<PPO_ACT_RELU>(hidden);
+  if (!kern) return PPO_ERR_UNSUPPORTED;
+  if (!mlp_net_weights_ok(actor) || !mlp_net_weights_ok(critic)) return PPO_ERR_INVALID_ARG;
+  if (N == 0) return PPO_OK;
+  if (!observations || !uniforms || !actions_out || !log_probs_out || !values_out)
+    return PPO_ERR_INVALID_ARG;
+  if (N > (1L << 31)) return PPO_ERR_TOO_LARGE;
+  ActArgs a = {};
+  a.actor = to_net(actor);
+  a.critic = to_net(critic);
+  a.D = obs_dim;
+  a.A = A;
+  a.obs = observations;
+  a.N = N;
+  a.u = uniforms;
+  a.obs_out = observations_out;
+  a.act = actions_out;
+  a.logp = log_probs_out;
+  a.val = values_out;
+  void* args[] = {&a};
+  const long blocks = (N + kMlpRows - 1) / kMlpRows;
+  return hip_status(hipLaunchKernel(kern, dim3((unsigned)blocks), dim3(kMlpBlock), args, 0,
+                                    reinterpret_cast<hipStream_t>(stream_ptr)));
 }

@@ -14,6 +14,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "sample_row.hpp"
 
 namespace ppo {
 namespace {
@@ -28,23 +29,11 @@ __global__ void __launch_bounds__(kBlock) sample_cat_row_kernel(const float* __r
                                                                 const float* val, float* val_out) {
   const long n = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (n >= N) return;
-  const float* zr = z + n * A;
-  float m = -INFINITY;
-  for (int j = 0; j < A; ++j) m = fmaxf(m, zr[j]);
-  float s = 0.0f;
-  for (int j = 0; j < A; ++j) s += expf(zr[j] - m);
-  const float target = u[n] * s;
-  float c = 0.0f;
-  int a = -1, last_pos = 0;
-  for (int j = 0; j < A; ++j) {
-    const float e = expf(zr[j] - m);
-    c += e;
-    if (e > 0.0f) last_pos = j;
-    if (a < 0 && target < c) a = j;
-  }
-  if (a < 0) a = last_pos;  // u*s at or above the rounded total: the last reachable action
+  int a;
+  float lp;
+  sample_cat_row(z + n * A, A, u[n], a, lp);
   act[n] = a;
-  logp[n] = (zr[a] - m) - logf(s);
+  logp[n] = lp;
   if (val && val_out) val_out[n] = val[n];
 }
 

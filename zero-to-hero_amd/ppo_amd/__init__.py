@@ -30,6 +30,7 @@ from .ops import (
     gae,
     gather_rows,
     gae_normalize,
+    mlp_act_categorical,
     mlp_fusable,
     normalize_advantages,
     ppo_loss_discrete,
@@ -72,6 +73,7 @@ __all__ = [
     "gae_normalize",
     "gather_rows",
     "load_library",
+    "mlp_act_categorical",
     "mlp_fusable",
     "normalize_advantages",
     "ppo_loss_discrete",

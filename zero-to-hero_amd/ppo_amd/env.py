@@ -68,9 +68,10 @@ class CartPoleVec:
         self.terminated = torch.zeros(N, dtype=torch.uint8, device=dev)
         self.generator = torch.Generator(device=dev).manual_seed(seed)
         self._u = torch.empty(N, 4, dtype=torch.float32, device=dev)
+        # per-environment episode tally, kept by the step kernel
         self._ret = torch.zeros(N, dtype=torch.float32, device=dev)
-        self._done_sum = torch.zeros((), dtype=torch.float64, device=dev)
-        self._done_count = torch.zeros((), dtype=torch.float64, device=dev)
+        self._done_sum = torch.zeros(N, dtype=torch.float64, device=dev)
+        self._done_count = torch.zeros(N, dtype=torch.int32, device=dev)
 
     def reset(self) -> torch.Tensor:
         torch.rand(self.num_envs, 4, generator=self.generator, out=self._u)
@@ -82,27 +83,34 @@ class CartPoleVec:
         return self.obs
 
     def step(self, actions: torch.Tensor):
+        self.step_into(actions, self.rewards, self.dones)
+        return self.obs, self.rewards, self.dones, self.terminated
+
+    def step_into(self, actions: torch.Tensor, rewards_out: torch.Tensor,
+                  dones_out: torch.Tensor) -> torch.Tensor:
+        """step() writing the rewards and dones into the given [N] tensors
+        (e.g. row t of a RolloutBuffer) instead of the environment's own;
+        returns the observations."""
         _require(actions, "actions", (torch.int32,), self.device)
         if actions.shape != (self.num_envs,):
             raise ValueError(f"actions must be [N]=[{self.num_envs}], got {tuple(actions.shape)}")
+        _require(rewards_out, "rewards_out", (torch.float32,), self.device)
+        _require(dones_out, "dones_out", (torch.uint8,), self.device)
+        if rewards_out.numel() != self.num_envs or dones_out.numel() != self.num_envs:
+            raise ValueError("rewards_out and dones_out must hold N values")
         torch.rand(self.num_envs, 4, generator=self.generator, out=self._u)
         stream = _stream(self.device)
         _call("ppo_cartpole_step", self.device, stream, self.state.data_ptr(),
               self.steps.data_ptr(), actions.data_ptr(), self._u.data_ptr(), self.max_steps,
-              self.obs.data_ptr(), self.rewards.data_ptr(), self.dones.data_ptr(),
-              self.terminated.data_ptr(), self.num_envs, stream)
-        # episode bookkeeping without host synchronisation
-        self._ret += self.rewards
-        done = self.dones.to(torch.float32)
-        self._done_sum += (self._ret * done).sum(dtype=torch.float64)
-        self._done_count += done.sum(dtype=torch.float64)
-        self._ret *= 1.0 - done
-        return self.obs, self.rewards, self.dones, self.terminated
+              self.obs.data_ptr(), rewards_out.data_ptr(), dones_out.data_ptr(),
+              self.terminated.data_ptr(), self._ret.data_ptr(), self._done_sum.data_ptr(),
+              self._done_count.data_ptr(), self.num_envs, stream)
+        return self.obs
 
     def episode_stats(self) -> tuple[int, float]:
         """(completed episodes, their mean return) since the last call."""
-        count = int(self._done_count.item())
-        total = float(self._done_sum.item())
+        count = int(self._done_count.sum().item())
+        total = float(self._done_sum.sum().item())
         self._done_sum.zero_()
         self._done_count.zero_()
         return count, (total / count if count else float("nan"))

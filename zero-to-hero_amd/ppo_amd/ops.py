@@ -38,6 +38,7 @@ __all__ = [
     "ppo_loss_gaussian",
     "ppo_loss_gaussian_fused",
     "ppo_mlp_cat_grads",
+    "mlp_act_categorical",
     "mlp_fusable",
     "LossStats",
 ]
@@ -839,3 +840,56 @@ def ppo_mlp_cat_grads(
           _ptr(old_values) if vf_clip is not None else None, ctypes.byref(params),
           scalars.data_ptr(), ws.data_ptr(), ws.numel(), stream)
     return _stats_dict(scalars)
+
+
+def mlp_act_categorical(
+    policy: torch.nn.Module,
+    value: torch.nn.Module,
+    observations: torch.Tensor,
+    uniforms: Optional[torch.Tensor] = None,
+    generator: Optional[torch.Generator] = None,
+    observations_out: Optional[torch.Tensor] = None,
+    actions_out: Optional[torch.Tensor] = None,
+    log_probs_out: Optional[torch.Tensor] = None,
+    values_out: Optional[torch.Tensor] = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """PPOAgent.select_action (ppo.py:65-79) for N observations [N,D] in one
+    launch: both MLPs' forward (networks as in ppo_mlp_cat_grads) and
+    sample_categorical's inverse-CDF draw at `uniforms` [N] (torch.rand on
+    the device from `generator` when not given).  Returns (actions int32 [N],
+    log_probs [N], values [N]); the *_out tensors are written in place when
+    given, and observations_out (e.g. a rollout buffer row) receives a copy
+    of the observations."""
+    if not mlp_fusable(policy, value):
+        raise ValueError("policy/value are not MLPs the fused kernel supports (see mlp_fusable)")
+    lp, act = mlp_structure(policy)
+    lv, _ = mlp_structure(value)
+    D, H, A = lp[0].in_features, lp[0].out_features, lp[2].out_features
+    device = lp[0].weight.device
+    _require(observations, "observations", (torch.float32,), device)
+    if observations.dim() != 2 or observations.shape[1] != D:
+        raise ValueError(f"observations must be [N,{D}], got {tuple(observations.shape)}")
+    N = observations.shape[0]
+    if uniforms is None:
+        uniforms = torch.rand(N, device=device, generator=generator)
+    _require(uniforms, "uniforms", (torch.float32,), device)
+    if uniforms.shape != (N,):
+        raise ValueError(f"uniforms must be [N]=[{N}], got {tuple(uniforms.shape)}")
+    if observations_out is not None:
+        _require(observations_out, "observations_out", (torch.float32,), device)
+        if observations_out.numel() != N * D:
+            raise ValueError("observations_out must hold N x D values")
+    actions_out = _out(actions_out, "actions_out", (N,), torch.int32, device)
+    log_probs_out = _out(log_probs_out, "log_probs_out", (N,), torch.float32, device)
+    values_out = _out(values_out, "values_out", (N,), torch.float32, device)
+    s_actor, s_critic = _lib.Mlp3(), _lib.Mlp3()
+    for st, layers in ((s_actor, lp), (s_critic, lv)):
+        for i, m in enumerate(layers):
+            st.weight[i] = m.weight.data_ptr()
+            st.bias[i] = m.bias.data_ptr()
+    stream = _stream(device)
+    _call("ppo_mlp_act_cat_f32", device, stream, ctypes.byref(s_actor), ctypes.byref(s_critic),
+          D, H, A, _lib.PPO_ACT_TANH if act == "tanh" else _lib.PPO_ACT_RELU,
+          observations.data_ptr(), N, uniforms.data_ptr(), _ptr(observations_out),
+          actions_out.data_ptr(), log_probs_out.data_ptr(), values_out.data_ptr(), stream)
+    return actions_out, log_probs_out, values_out

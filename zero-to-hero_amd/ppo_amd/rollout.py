@@ -205,6 +205,17 @@ class VecPPO:
         buffer.add_outcome(rewards, dones)).  Returns (actions, log_probs,
         values), views of that row when a buffer is given.
         """
+        if self.fused_mlp and observations.dim() == 2:
+            outs: dict = {}
+            if buffer is not None:
+                if buffer.step >= buffer.T:
+                    raise IndexError(f"rollout buffer is full (T={buffer.T})")
+                t = buffer.step
+                outs = dict(observations_out=buffer.observations[t],
+                            actions_out=buffer.actions[t], log_probs_out=buffer.log_probs[t],
+                            values_out=buffer.values[t])
+            return ops.mlp_act_categorical(self.policy, self.value, observations.contiguous(),
+                                           generator=generator, **outs)
         values = self.value(observations).reshape(-1).contiguous()
         if buffer is not None:
             if buffer.step >= buffer.T:
@@ -240,10 +251,16 @@ class VecPPO:
         step (a copy)."""
         buffer.reset()
         obs = observations
+        into = hasattr(env, "step_into")
         for _ in range(buffer.T):
+            t = buffer.step
             acts, _, _ = self.act(obs, buffer=buffer, generator=generator)
-            obs, rewards, dones = env.step(acts)[:3]
-            buffer.add_outcome(rewards, dones)
+            if into:  # the environment writes the buffer row itself
+                obs = env.step_into(acts, buffer.rewards[t], buffer.dones[t])
+                buffer.step += 1
+            else:
+                obs, rewards, dones = env.step(acts)[:3]
+                buffer.add_outcome(rewards, dones)
         obs = obs.clone()
         buffer.finish(self.value(obs).reshape(-1) if bootstrap else None)
         return obs
