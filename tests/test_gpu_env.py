@@ -102,3 +102,43 @@ def test_ppo_trains_cartpole_on_device(dev):
     best = max(r["mean_return"] for r in recs if r["episodes"] > 0)
     print(f"cartpole: first {first:.1f}, best {best:.1f}", flush=True)
     assert first < 40 and best > 300
+
+
+def test_graphed_collection_matches_eager_steps(dev):
+    """VecPPO.collect replayed from one HIP graph fills the buffer exactly as
+    the same kernels run step by step on the same uniforms (max_steps 20, so
+    truncation resets read the reset uniforms), across the eager warm-up,
+    the capture and two replays."""
+    from ppo_amd.agent import MLP
+
+    torch.manual_seed(3)
+    T, N = 24, 96
+    policy, value = MLP(4, 64, 2, "tanh").to(dev), MLP(4, 64, 1, "tanh").to(dev)
+    vec = ppo_amd.VecPPO(policy, value, graphs=True)
+    env_a = ppo_amd.CartPoleVec(N, device=dev, seed=9, max_steps=20)
+    env_b = ppo_amd.CartPoleVec(N, device=dev, seed=9, max_steps=20)
+    buf_a = ppo_amd.RolloutBuffer(T, N, (4,), device=dev)
+    buf_b = ppo_amd.RolloutBuffer(T, N, (4,), device=dev)
+    obs_a, obs_b = env_a.reset().clone(), env_b.reset().clone()
+    gen = torch.Generator(device=dev).manual_seed(1)
+    for it in range(4):
+        obs_a = vec.collect(env_a, buf_a, obs_a, generator=gen)
+        plan = next(iter(vec._collect_plans.values()))
+        assert (plan.graph is not None) == (it >= 1)
+        ua, ur = plan.uact.clone(), plan.ureset.clone()
+        buf_b.reset()
+        o = obs_b
+        for t in range(T):
+            acts, _, _ = vec.act(o, buffer=buf_b, uniforms=ua[t].contiguous())
+            o = env_b.step_into(acts, buf_b.rewards[t], buf_b.dones[t],
+                                reset_uniforms=ur[t].contiguous())
+            buf_b.step += 1
+        obs_b = o.clone()
+        buf_b.finish(vec.value(obs_b).reshape(-1))
+        assert torch.equal(obs_a, obs_b), it
+        for name in ("observations", "actions", "log_probs", "values", "rewards", "dones",
+                     "last_value"):
+            assert torch.equal(getattr(buf_a, name), getattr(buf_b, name)), (it, name)
+        assert buf_a.step == buf_b.step == T
+        assert int(buf_a.dones.sum()) > 0
+    assert env_a.episode_stats() == env_b.episode_stats()

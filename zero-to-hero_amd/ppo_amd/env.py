@@ -87,10 +87,12 @@ class CartPoleVec:
         return self.obs, self.rewards, self.dones, self.terminated
 
     def step_into(self, actions: torch.Tensor, rewards_out: torch.Tensor,
-                  dones_out: torch.Tensor) -> torch.Tensor:
+                  dones_out: torch.Tensor,
+                  reset_uniforms: Optional[torch.Tensor] = None) -> torch.Tensor:
         """step() writing the rewards and dones into the given [N] tensors
         (e.g. row t of a RolloutBuffer) instead of the environment's own;
-        returns the observations."""
+        returns the observations.  `reset_uniforms` [N,4] U[0,1) replaces the
+        environment's own draw (no random launch: for graph capture)."""
         _require(actions, "actions", (torch.int32,), self.device)
         if actions.shape != (self.num_envs,):
             raise ValueError(f"actions must be [N]=[{self.num_envs}], got {tuple(actions.shape)}")
@@ -98,10 +100,17 @@ class CartPoleVec:
         _require(dones_out, "dones_out", (torch.uint8,), self.device)
         if rewards_out.numel() != self.num_envs or dones_out.numel() != self.num_envs:
             raise ValueError("rewards_out and dones_out must hold N values")
-        torch.rand(self.num_envs, 4, generator=self.generator, out=self._u)
+        if reset_uniforms is None:
+            torch.rand(self.num_envs, 4, generator=self.generator, out=self._u)
+            reset_uniforms = self._u
+        else:
+            _require(reset_uniforms, "reset_uniforms", (torch.float32,), self.device)
+            if reset_uniforms.numel() != self.num_envs * 4:
+                raise ValueError("reset_uniforms must hold N x 4 values")
         stream = _stream(self.device)
         _call("ppo_cartpole_step", self.device, stream, self.state.data_ptr(),
-              self.steps.data_ptr(), actions.data_ptr(), self._u.data_ptr(), self.max_steps,
+              self.steps.data_ptr(), actions.data_ptr(), reset_uniforms.data_ptr(),
+              self.max_steps,
               self.obs.data_ptr(), rewards_out.data_ptr(), dones_out.data_ptr(),
               self.terminated.data_ptr(), self._ret.data_ptr(), self._done_sum.data_ptr(),
               self._done_count.data_ptr(), self.num_envs, stream)

@@ -171,6 +171,7 @@ class VecPPO:
             raise ValueError(f"graph_chunk must be >= 1, got {graph_chunk}")
         self.graphs, self.graph_chunk = graphs, graph_chunk
         self._plans: dict = {}  # (shape, storage) key -> _GraphPlan, two at most
+        self._collect_plans: dict = {}  # (env, buffer) -> _CollectPlan
         self._plan: Optional[_GraphPlan] = None  # the most recently used
         self._side_stream: Optional[torch.cuda.Stream] = None
         can_fuse = fused_update and log_std is None and ops.mlp_fusable(policy, value)
@@ -194,7 +195,8 @@ class VecPPO:
 
     @torch.no_grad()
     def act(self, observations: torch.Tensor, buffer: Optional[RolloutBuffer] = None,
-            generator: Optional[torch.Generator] = None):
+            generator: Optional[torch.Generator] = None,
+            uniforms: Optional[torch.Tensor] = None):
         """PPOAgent.select_action (ppo.py:65-79) for all N envs at once.
 
         Runs the policy and value networks on observations [N, *obs_shape],
@@ -215,7 +217,7 @@ class VecPPO:
                             actions_out=buffer.actions[t], log_probs_out=buffer.log_probs[t],
                             values_out=buffer.values[t])
             return ops.mlp_act_categorical(self.policy, self.value, observations.contiguous(),
-                                           generator=generator, **outs)
+                                           uniforms=uniforms, generator=generator, **outs)
         values = self.value(observations).reshape(-1).contiguous()
         if buffer is not None:
             if buffer.step >= buffer.T:
@@ -238,7 +240,8 @@ class VecPPO:
 
     @torch.no_grad()
     def collect(self, env, buffer: RolloutBuffer, observations: torch.Tensor,
-                generator: Optional[torch.Generator] = None, bootstrap: bool = True):
+                generator: Optional[torch.Generator] = None, bootstrap: bool = True,
+                graphs: Optional[bool] = None):
         """Fill `buffer` with buffer.T steps of the vectorised environment
         `env` (an object with step(actions int32 [N]) -> (observations,
         rewards, dones, ...), e.g. CartPoleVec), starting from
@@ -248,7 +251,18 @@ class VecPPO:
         state after the last step seeds the advantages of environments still
         running (masked for those whose episode just ended); without it the
         reference's zero is used.  Returns the observations after the last
-        step (a copy)."""
+        step (a copy).
+
+        With `graphs` (default: the VecPPO's `graphs` setting) and an
+        environment with step_into(..., reset_uniforms) and the fused MLP
+        path, the T steps are replayed from one HIP graph: the rollout's
+        random numbers (action uniforms [T,N], reset uniforms [T,N,4]) are
+        drawn in one launch first and read by the graph; the first call for
+        a (environment, buffer) pair runs eagerly and captures."""
+        use_graph = self.graphs if graphs is None else graphs
+        if (use_graph and self.fused_mlp and hasattr(env, "step_into")
+                and observations.dim() == 2):
+            return self._collect_graphed(env, buffer, observations, generator, bootstrap)
         buffer.reset()
         obs = observations
         into = hasattr(env, "step_into")
@@ -264,6 +278,43 @@ class VecPPO:
         obs = obs.clone()
         buffer.finish(self.value(obs).reshape(-1) if bootstrap else None)
         return obs
+
+    def _collect_graphed(self, env, buffer, observations, generator, bootstrap):
+        key = (id(env), id(buffer), buffer.T, buffer.N, tuple(observations.shape))
+        plan = self._collect_plans.get(key)
+        dev = buffer.device
+        if plan is None:
+            plan = self._collect_plans[key] = _CollectPlan(buffer.T, buffer.N, observations, dev)
+        torch.rand(plan.u.shape, generator=generator, device=dev, out=plan.u)
+        plan.obs0.copy_(observations)
+        if plan.graph is None and plan.warm:
+            if self._side_stream is None:
+                self._side_stream = torch.cuda.Stream(device=dev)
+            s = self._side_stream
+            s.wait_stream(torch.cuda.current_stream(dev))
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                self._collect_steps(env, buffer, plan)
+            torch.cuda.current_stream(dev).wait_stream(s)
+            plan.graph = g
+        if plan.graph is not None:
+            plan.graph.replay()
+        else:
+            self._collect_steps(env, buffer, plan)  # warm-up, eager
+            plan.warm = True
+        buffer.step = buffer.T
+        obs = env.obs.clone()
+        buffer.finish(self.value(obs).reshape(-1) if bootstrap else None)
+        return obs
+
+    def _collect_steps(self, env, buffer, plan) -> None:
+        buffer.reset()
+        obs = plan.obs0
+        for t in range(buffer.T):
+            acts, _, _ = self.act(obs, buffer=buffer, uniforms=plan.uact[t])
+            obs = env.step_into(acts, buffer.rewards[t], buffer.dones[t],
+                                reset_uniforms=plan.ureset[t])
+            buffer.step += 1
 
     def update(self, buffer: RolloutBuffer) -> dict:
         """Run `epochs` passes of shuffled minibatches; returns the last
@@ -430,3 +481,17 @@ class _GraphPlan:
         self.graphs: list = []
         self.stats: dict = {}
         self.refs: list = []
+
+
+class _CollectPlan:
+    """Static inputs of a captured collection loop: the starting observations
+    and the rollout's uniforms, one [T, 5N] draw: per step N action uniforms,
+    then N x 4 reset uniforms (each step's slices contiguous)."""
+
+    def __init__(self, T: int, N: int, observations: torch.Tensor, device) -> None:
+        self.obs0 = torch.empty_like(observations)
+        self.u = torch.empty((T, 5 * N), dtype=torch.float32, device=device)
+        self.uact = self.u[:, :N]
+        self.ureset = self.u[:, N:].view(T, N, 4)
+        self.graph = None
+        self.warm = False
