@@ -1,9 +1,10 @@
 // Advantage normalisation (rl/deep/agents/ppo.py:126-127):
 //     if len(advantages) > 1:
 //         advantages = (advantages - advantages.mean()) / (advantages.std() + 1e-8)
-// Three kernels: a moments pass (fp64 sums of x and x^2 per thread, then per
-// block), a one-block finaliser combining the block partials in a fixed order,
-// and an fp32 elementwise pass.
+// A moments pass (fp64 sums of x and x^2 per thread, then per block), then
+// the block partials combined in a fixed order and an fp32 elementwise pass:
+// one kernel when the partials are few (every block combines them), else a
+// one-block finaliser and the elementwise pass.
 #include <algorithm>
 
 #include "common.hpp"
@@ -100,6 +101,74 @@ __global__ void __launch_bounds__(kBlock) normalize_kernel(const float* adv, flo
   for (long i = tail_start + gid; i < n; i += stride) out[i] = (adv[i] - mean) / denom;
 }
 
+// The finaliser fused into the elementwise pass, for few partials: every
+// block derives the normaliser parameters itself with norm_params (same
+// block size as the one-block finaliser, so the same fixed order and
+// bit-identical values), after issuing its first kNormU float4 loads so that
+// the partials' reduction overlaps them.  Block 0 also stores the parameters
+// in the header and {mean, std} in stats_out.
+#ifndef PPO_NORM_U
+#define PPO_NORM_U 4
+#endif
+constexpr int kNormU = PPO_NORM_U;
+constexpr long kFusedNormMaxPartials = 512;
+
+__global__ void __launch_bounds__(kFinalBlock) normalize_stats_kernel(
+    const float* adv, float* out, long n, const double* partials, long count, double eps,
+    WsHeader* hdr, float* stats_out) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  __shared__ float s_par[2];
+  const long n4 = n / 4;
+  const f4* a4 = reinterpret_cast<const f4*>(adv);
+  f4* o4 = reinterpret_cast<f4*>(out);
+  const long stride = (long)gridDim.x * kFinalBlock;
+  const long gid = (long)blockIdx.x * kFinalBlock + threadIdx.x;
+  f4 x[kNormU];
+#pragma unroll
+  for (int u = 0; u < kNormU; ++u) {
+    const long i = gid + u * stride;
+    x[u] = a4[i < n4 ? i : 0];  // unconditional (n >= 4): element 0 stands in past the end
+  }
+  const NormParams np = norm_params(partials, count, eps);
+  if (threadIdx.x == 0) {
+    s_par[0] = np.mean_used;
+    s_par[1] = np.denom;
+    if (blockIdx.x == 0) {
+      hdr->stats[0] = np.mean_used;
+      hdr->stats[1] = np.std;
+      hdr->stats[2] = np.denom;
+      if (stats_out) {
+        stats_out[0] = np.mean;
+        stats_out[1] = np.std;
+      }
+    }
+  }
+  __syncthreads();
+  const float mean = s_par[0], denom = s_par[1];
+#pragma unroll
+  for (int u = 0; u < kNormU; ++u) {
+    const long i = gid + u * stride;
+    if (i < n4) {
+      f4 y;
+      y[0] = (x[u][0] - mean) / denom;
+      y[1] = (x[u][1] - mean) / denom;
+      y[2] = (x[u][2] - mean) / denom;
+      y[3] = (x[u][3] - mean) / denom;
+      __builtin_nontemporal_store(y, o4 + i);
+    }
+  }
+  for (long i = gid + kNormU * stride; i < n4; i += stride) {
+    const f4 v = a4[i];
+    f4 y;
+    y[0] = (v[0] - mean) / denom;
+    y[1] = (v[1] - mean) / denom;
+    y[2] = (v[2] - mean) / denom;
+    y[3] = (v[3] - mean) / denom;
+    __builtin_nontemporal_store(y, o4 + i);
+  }
+  for (long i = n4 * 4 + gid; i < n; i += stride) out[i] = (adv[i] - mean) / denom;
+}
+
 }  // namespace
 
 int launch_finalize_stats(const double* partials, long count, double eps, WsHeader* hdr,
@@ -112,6 +181,14 @@ int launch_finalize_stats(const double* partials, long count, double eps, WsHead
 int launch_normalize(const double* partials, long count, double eps, const float* adv, float* out,
                      long n, WsHeader* hdr, float* stats_out, hipStream_t stream) {
   if (n <= 0) return PPO_OK;
+  if (count <= kFusedNormMaxPartials && n >= 4 && aligned(adv, 16) && aligned(out, 16)) {
+    const long per_block = (long)kFinalBlock * kNormU;
+    long blocks = ((n + 3) / 4 + per_block - 1) / per_block;
+    blocks = std::max(1L, std::min(blocks, 4096L));
+    hipLaunchKernelGGL(normalize_stats_kernel, dim3((unsigned)blocks), dim3(kFinalBlock), 0,
+                       stream, adv, out, n, partials, count, eps, hdr, stats_out);
+    return last_launch_status();
+  }
   int st = launch_finalize_stats(partials, count, eps, hdr, stats_out, stream);
   if (st) return st;
   const bool vec = aligned(adv, 16) && aligned(out, 16);

@@ -48,10 +48,13 @@ __device__ inline NormParams norm_params(const double* partials, long count, dou
 int launch_finalize_stats(const double* partials, long count, double eps, WsHeader* hdr,
                           float* stats_out, hipStream_t stream);
 
-// Enqueue the normaliser: a one-block kernel derives mean/denom from the
-// `count` (n, sum, sum of squares) partials left in the workspace by the
-// previous kernel on the same stream (and stores {mean, std} in stats_out if
-// not null), then out[i] = (adv[i] - mean) / denom in fp32 over n elements.
+// Enqueue the normaliser: mean/denom from the `count` (n, sum, sum of
+// squares) partials left in the workspace by the previous kernel on the same
+// stream (also stored in hdr->stats, and {mean, std} in stats_out if not
+// null), then out[i] = (adv[i] - mean) / denom in fp32 over n elements.  With
+// few partials and 16-byte aligned buffers this is one kernel whose blocks
+// each combine the partials; otherwise a one-block kernel precedes the
+// elementwise pass.
 // Defined in adv_norm.hip.
 int launch_normalize(const double* partials, long count, double eps, const float* adv, float* out,
                      long n, WsHeader* hdr, float* stats_out, hipStream_t stream);
