@@ -16,14 +16,17 @@
 //
 // At the reference's sizes (4-64-64 or 4-128-128 networks, minibatches of
 // 64-4096 rows) the torch sequence is ~35 small launches per minibatch;
-// here it is two.  Layout: a 256-thread workgroup owns kMlpRows = 16 rows.
-// Observations, activations and row gradients live in LDS; weights are read
-// from global memory (a few KiB to 64 KiB per layer, L2-resident).  Hidden
-// layers map thread t to output unit t % H and rows t / H + (256/H) i, so a
-// wave's LDS reads of the layer input are broadcasts and its weight-row reads
-// are per-lane rows; the backward maps threads to input units, so the
-// weight-column reads are coalesced.  All arithmetic is fp32, as torch's;
-// sums over the minibatch differ from torch's GEMM order only by rounding.
+// here it is two.  Layout: each block of kMlpRows = 16 minibatch rows is
+// handled by two 256-thread workgroups, one per network (the actor's and
+// the critic's forward, loss terms and backward share only the gathered
+// observations).  Observations, activations and row gradients live in LDS;
+// weights are read from global memory (a few KiB to 64 KiB per layer,
+// L2-resident).  Every layer is a set of 16x16 output tiles on the matrix
+// cores (v_mfma_f32_16x16x4f32, one tile per wave at a time): forward tiles
+// over output units, input-gradient tiles over input units, weight-gradient
+// tiles over (output, input) pairs summed over the 16 rows.  All arithmetic
+// is fp32, as torch's; sums over the minibatch differ from torch's GEMM
+// order only by rounding.
 #include <float.h>
 
 #include "common.hpp"
@@ -295,22 +298,49 @@ __device__ __forceinline__ void mlp_forward(const MlpNet& actor, const MlpNet& c
   lds_barrier();
 }
 
+// Forward of one network for the workgroup's 16 rows (observations in x):
+// hidden activations into h1/h2, the O outputs into out [16][ldout].  Column
+// tiles over the waves; LDS-only barriers between the layers and after the
+// last.
+template <int H, int kAct>
+__device__ __forceinline__ void net_forward(const MlpNet& net, const float* x, int D, int O,
+                                            float* h1, float* h2, float* out, int ldout) {
+  constexpr int ld = act_ld<H>();
+  constexpr int NT = H / 16;
+  constexpr int kWaves = kMlpBlock / kWave;
+  const int w = threadIdx.x / kWave;
+  for (int t = w; t < NT; t += kWaves) fwd_tile<0, kAct>(x, kXld, D, net.w[0], net.b[0], H, h1, ld, t);
+  lds_barrier();
+  for (int t = w; t < NT; t += kWaves) fwd_tile<H, kAct>(h1, ld, H, net.w[1], net.b[1], H, h2, ld, t);
+  lds_barrier();
+  for (int t = w; t < (O + 15) / 16; t += kWaves)
+    fwd_tile<H, -1>(h2, ld, H, net.w[2], net.b[2], O, out, ldout, t);
+  lds_barrier();
+}
+
+// One minibatch block of 16 rows is handled by two workgroups, 2b (actor)
+// and 2b + 1 (critic): the networks share nothing but the gathered
+// observations, so each workgroup runs one network's forward, its part of
+// the per-row loss and its backward.  They write disjoint parts of the
+// block's partials (the actor's and the critic's parameter columns of
+// gpart row b; the policy / entropy / kl / clip-fraction sums and the value
+// sum of spart column b), so the reduction sees exactly the values one
+// workgroup doing both networks would leave.
 template <int H, int kAct>
 __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   constexpr int R = kMlpRows;
   constexpr int ld = act_ld<H>();
-  constexpr int NT = H / 16;
-  constexpr int kWaves = kMlpBlock / kWave;
   __shared__ float s_x[R * kXld];
-  __shared__ float s_a1[R * ld], s_a2[R * ld], s_c1[R * ld], s_c2[R * ld];
+  __shared__ float s_h1[R * ld], s_h2[R * ld];
   __shared__ float s_g1[R * ld], s_g2[R * ld];
   __shared__ float s_z[R * kZld];
   __shared__ float s_v[R];
   __shared__ long s_row[R];
 
   const int tid = threadIdx.x;
-  const int w = tid / kWave;
-  const long row0 = (long)blockIdx.x * R;
+  const bool critic = (blockIdx.x & 1u) != 0u;
+  const long blk = (long)(blockIdx.x >> 1);
+  const long row0 = blk * R;
   const int D = a.D, A = a.A;
   // the loss inputs of row `tid` (tid < R) are loaded now, ahead of the
   // forward pass that precedes their use
@@ -321,12 +351,15 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
     const long src = i < a.B ? (a.idx ? (long)a.idx[i] : i) : -1;
     s_row[tid] = src;
     const long sc = src >= 0 ? src : 0;
-    rin.old_lp = a.old_lp[sc];
-    rin.adv = a.adv[sc];
-    rin.ret = a.ret[sc];
-    rin.vo = a.use_vclip ? a.old_val[sc] : 0.0f;
-    raw_act = a.act64 ? (long)reinterpret_cast<const int64_t*>(a.actions)[sc]
-                      : (long)reinterpret_cast<const int32_t*>(a.actions)[sc];
+    if (critic) {
+      rin.ret = a.ret[sc];
+      rin.vo = a.use_vclip ? a.old_val[sc] : 0.0f;
+    } else {
+      rin.old_lp = a.old_lp[sc];
+      rin.adv = a.adv[sc];
+      raw_act = a.act64 ? (long)reinterpret_cast<const int64_t*>(a.actions)[sc]
+                        : (long)reinterpret_cast<const int32_t*>(a.actions)[sc];
+    }
   }
   lds_barrier();
   // gather the observation rows (padding rows past B are zeros)
@@ -337,40 +370,52 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   }
   lds_barrier();
 
-  mlp_forward<H, kAct>(a.actor, a.critic, s_x, D, A, s_a1, s_a2, s_c1, s_c2, s_z, s_v);
+  if (critic) net_forward<H, kAct>(a.critic, s_x, D, 1, s_h1, s_h2, s_v, 1);
+  else net_forward<H, kAct>(a.actor, s_x, D, A, s_h1, s_h2, s_z, kZld);
 
-  // loss rows: logits -> dlogits in place, value -> dvalue in place
+  // loss rows: logits -> dlogits in place (actor), value -> dvalue in place
+  // (critic; the value terms do not depend on the log-prob, which is given
+  // its old value here)
   double acc[kMlpSums] = {0.0, 0.0, 0.0, 0.0, 0.0};
   if (tid < R) {
     const long src = s_row[tid];
     float* zr = s_z + tid * kZld;
     if (src >= 0) {
-      RowIn in = rin;
-      in.v = s_v[tid];
-      const int ai = (raw_act >= 0 && raw_act < A) ? (int)raw_act : -1;
-      float H_ent;
-      const RowOut o = cat_row_grad<kMlpMaxA>(a, zr, A, ai, a.ec * a.inv_b, in, H_ent);
-      s_v[tid] = o.dval;
-      acc[0] = (double)o.pol;
-      acc[1] = (double)o.vl;
-      acc[2] = (double)H_ent;
-      acc[3] = (double)o.kl;
-      acc[4] = (double)o.clipped;
+      if (critic) {
+        RowIn in = rin;
+        in.v = s_v[tid];
+        const RowOut o = ppo_row_math(a, in, in.old_lp);
+        s_v[tid] = o.dval;
+        acc[1] = (double)o.vl;
+      } else {
+        const int ai = (raw_act >= 0 && raw_act < A) ? (int)raw_act : -1;
+        float H_ent;
+        const RowOut o = cat_row_grad<kMlpMaxA>(a, zr, A, ai, a.ec * a.inv_b, rin, H_ent);
+        acc[0] = (double)o.pol;
+        acc[2] = (double)H_ent;
+        acc[3] = (double)o.kl;
+        acc[4] = (double)o.clipped;
+      }
+    } else if (critic) {
+      s_v[tid] = 0.0f;
     } else {
       for (int j = 0; j < A; ++j) zr[j] = 0.0f;
-      s_v[tid] = 0.0f;
     }
   }
   block_sum<kMlpSums>(acc);  // its barriers also publish s_z / s_v
   if (tid == 0) {
+    if (critic) {
+      a.spart[1 * a.nblocks + blk] = acc[1];
+    } else {
+      a.spart[0 * a.nblocks + blk] = acc[0];
 #pragma unroll
-    for (int k = 0; k < kMlpSums; ++k) a.spart[(long)k * a.nblocks + blockIdx.x] = acc[k];
+      for (int k = 2; k < kMlpSums; ++k) a.spart[(long)k * a.nblocks + blk] = acc[k];
+    }
   }
 
-  float* gp = a.gpart + (long)blockIdx.x * a.P;
-  net_backward<H, kAct>(a.actor, a.oa, gp, s_z, kZld, A, s_x, D, s_a1, s_a2, s_g1, s_g2);
-  lds_barrier();
-  net_backward<H, kAct>(a.critic, a.oc, gp, s_v, 1, 1, s_x, D, s_c1, s_c2, s_g1, s_g2);
+  float* gp = a.gpart + blk * a.P;
+  if (critic) net_backward<H, kAct>(a.critic, a.oc, gp, s_v, 1, 1, s_x, D, s_h1, s_h2, s_g1, s_g2);
+  else net_backward<H, kAct>(a.actor, a.oa, gp, s_z, kZld, A, s_x, D, s_h1, s_h2, s_g1, s_g2);
 }
 
 // Action selection through both networks (ppo.py:65-79 for N observations):
@@ -645,7 +690,7 @@ extern "C" int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
   a.scalars = scalars_out;
 
   void* args[] = {&a};
-  int st = hip_status(hipLaunchKernel(kern, dim3((unsigned)l.nblocks), dim3(kMlpBlock), args, 0,
+  int st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(kMlpBlock), args, 0,
                                       stream));
   if (st) return st;
   const long rblocks = (l.P + kRedCols - 1) / kRedCols;

@@ -64,7 +64,7 @@ __global__ void __launch_bounds__(kBlock) copy_words_kernel(const T* __restrict_
 // clip_grad_norm_ + Adam
 // ---------------------------------------------------------------------------
 constexpr int kAdamPerThread = 4;
-constexpr long kAdamChunk = (long)kBlock * kAdamPerThread * 4;  // elements per block
+constexpr long kAdamChunk = (long)kBlock * kAdamPerThread;  // elements per block
 
 struct AdamTable {
   float* p[PPO_ADAM_MAX_TENSORS];
@@ -129,26 +129,56 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
                                                              const int64_t* step_counter) {
   __shared__ float s_coef;
   __shared__ float s_norm[PPO_ADAM_MAX_TENSORS];
+  // The block's elements, moments and parameters are loaded first (they do
+  // not depend on the norm), so their latency overlaps the norm's.
+  const long b = blockIdx.x;
+  const int k = tensor_of_block(t, b);
+  const long lo = (b - t.block_start[k]) * kAdamChunk;
+  const long hi = lo + kAdamChunk < t.n[k] ? lo + kAdamChunk : t.n[k];
+  float* __restrict__ p = t.p[k];
+  float* __restrict__ g = t.g[k];
+  float* __restrict__ m = t.m[k];
+  float* __restrict__ v = t.v[k];
+  float gr[kAdamPerThread], mr[kAdamPerThread], vr[kAdamPerThread], pr[kAdamPerThread];
+#pragma unroll
+  for (int j = 0; j < kAdamPerThread; ++j) {
+    const long i = lo + threadIdx.x + (long)j * kBlock;
+    const long ic = i < hi ? i : lo;  // in range: lo < hi for every block
+    gr[j] = g[ic];
+    mr[j] = m[ic];
+    vr[j] = v[ic];
+    pr[j] = p[ic];
+  }
   if (step_counter) adam_step_scalars(s, step_counter);
   // Global norm: per-tensor norms rounded to fp32 (lane k of wave 0 sums
   // tensor k's block partials in block order), then the norm of those in
   // tensor order (the two-level form of torch's _get_total_norm); every block
   // derives the same value in the same order.
   if (threadIdx.x < PPO_ADAM_MAX_TENSORS) {
-    const int k = threadIdx.x;
+    const int kk = threadIdx.x;
     float nk = 0.0f;
-    if (k < t.nt) {
+    if (kk < t.nt) {
+      // sequential sum in block order, loads batched 8 at a time
       double sk = 0.0;
-      for (long b = t.block_start[k]; b < t.block_start[k + 1]; ++b) sk += partial[b];
+      long c = t.block_start[kk];
+      const long ce = t.block_start[kk + 1];
+      for (; c + 8 <= ce; c += 8) {
+        double x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = partial[c + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sk += x[j];
+      }
+      for (; c < ce; ++c) sk += partial[c];
       nk = (float)sqrt(sk);
     }
-    s_norm[k] = nk;
+    s_norm[kk] = nk;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     float total_sq = 0.0f;
-    for (int k = 0; k < t.nt; ++k) {
-      const float nk = s_norm[k];
+    for (int kk = 0; kk < t.nt; ++kk) {
+      const float nk = s_norm[kk];
       total_sq = __fadd_rn(total_sq, __fmul_rn(nk, nk));
     }
     const float total = __fsqrt_rn(total_sq);
@@ -162,24 +192,19 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
   }
   __syncthreads();
   const float coef = s_coef;
-  const long b = blockIdx.x;
-  const int k = tensor_of_block(t, b);
-  const long lo = (b - t.block_start[k]) * kAdamChunk;
-  const long hi = lo + kAdamChunk < t.n[k] ? lo + kAdamChunk : t.n[k];
-  float* __restrict__ p = t.p[k];
-  float* __restrict__ g = t.g[k];
-  float* __restrict__ m = t.m[k];
-  float* __restrict__ v = t.v[k];
-  for (long i = lo + threadIdx.x; i < hi; i += blockDim.x) {
-    const float gi = s.clip ? __fmul_rn(g[i], coef) : g[i];
+#pragma unroll
+  for (int j = 0; j < kAdamPerThread; ++j) {
+    const long i = lo + threadIdx.x + (long)j * kBlock;
+    if (i >= hi) break;
+    const float gi = s.clip ? __fmul_rn(gr[j], coef) : gr[j];
     if (s.clip) g[i] = gi;
     // exp_avg.lerp_(grad, 1 - beta1), weight < 0.5: m + w * (g - m)
-    const float mi = __fadd_rn(m[i], __fmul_rn(s.beta1_w, __fsub_rn(gi, m[i])));
+    const float mi = __fadd_rn(mr[j], __fmul_rn(s.beta1_w, __fsub_rn(gi, mr[j])));
     // exp_avg_sq.mul_(beta2).addcmul_(grad, grad, value=1 - beta2)
-    const float vi = __fadd_rn(__fmul_rn(v[i], s.beta2), __fmul_rn(__fmul_rn(s.one_m_beta2, gi), gi));
+    const float vi = __fadd_rn(__fmul_rn(vr[j], s.beta2), __fmul_rn(__fmul_rn(s.one_m_beta2, gi), gi));
     // denom = sqrt(v) / sqrt(1 - beta2^t) + eps;  p += (-lr / (1 - beta1^t)) * (m / denom)
     const float denom = __fadd_rn(__fdiv_rn(__fsqrt_rn(vi), s.bc2_sqrt), s.eps);
-    p[i] = __fadd_rn(p[i], __fmul_rn(s.neg_step, __fdiv_rn(mi, denom)));
+    p[i] = __fadd_rn(pr[j], __fmul_rn(s.neg_step, __fdiv_rn(mi, denom)));
     m[i] = mi;
     v[i] = vi;
   }

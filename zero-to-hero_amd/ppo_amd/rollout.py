@@ -171,7 +171,7 @@ class VecPPO:
             raise ValueError(f"graph_chunk must be >= 1, got {graph_chunk}")
         self.graphs, self.graph_chunk = graphs, graph_chunk
         self._plans: dict = {}  # (shape, storage) key -> _GraphPlan, two at most
-        self._collect_plans: dict = {}  # (env, buffer) -> _CollectPlan
+        self._collect_plans: dict = {}  # (env, buffer, shapes) -> _CollectPlan, two at most
         self._plan: Optional[_GraphPlan] = None  # the most recently used
         self._side_stream: Optional[torch.cuda.Stream] = None
         can_fuse = fused_update and log_std is None and ops.mlp_fusable(policy, value)
@@ -280,11 +280,17 @@ class VecPPO:
         return obs
 
     def _collect_graphed(self, env, buffer, observations, generator, bootstrap):
+        # The plan keeps the environment and the buffer alive, so their ids
+        # (and the storage its graph reads and writes) cannot be reused while
+        # the plan exists; at most two plans are kept, most recent last.
         key = (id(env), id(buffer), buffer.T, buffer.N, tuple(observations.shape))
-        plan = self._collect_plans.get(key)
+        plan = self._collect_plans.pop(key, None)
         dev = buffer.device
-        if plan is None:
-            plan = self._collect_plans[key] = _CollectPlan(buffer.T, buffer.N, observations, dev)
+        if plan is None or plan.env is not env or plan.buffer is not buffer:
+            plan = _CollectPlan(env, buffer, observations, dev)
+        self._collect_plans[key] = plan
+        while len(self._collect_plans) > 2:
+            self._collect_plans.pop(next(iter(self._collect_plans)))
         torch.rand(plan.u.shape, generator=generator, device=dev, out=plan.u)
         plan.obs0.copy_(observations)
         if plan.graph is None and plan.warm:
@@ -488,7 +494,9 @@ class _CollectPlan:
     and the rollout's uniforms, one [T, 5N] draw: per step N action uniforms,
     then N x 4 reset uniforms (each step's slices contiguous)."""
 
-    def __init__(self, T: int, N: int, observations: torch.Tensor, device) -> None:
+    def __init__(self, env, buffer, observations: torch.Tensor, device) -> None:
+        T, N = buffer.T, buffer.N
+        self.env, self.buffer = env, buffer
         self.obs0 = torch.empty_like(observations)
         self.u = torch.empty((T, 5 * N), dtype=torch.float32, device=device)
         self.uact = self.u[:, :N]
