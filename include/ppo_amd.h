@@ -368,6 +368,32 @@ int ppo_cartpole_step(double* state, int32_t* steps, const int32_t* actions,
                       float* episode_return, double* completed_sum, int32_t* completed_count,
                       int64_t N, void* stream);
 
+/*
+ * A whole rollout of T steps for N CartPole environments in one launch: per
+ * step, ppo_mlp_act_cat_f32 (actor 4-H-H-2, critic 4-H-H-1; only weights and
+ * biases are read) at action_uniforms[t * action_uniforms_stride + n], then
+ * ppo_cartpole_step with reset_uniforms[t * reset_uniforms_stride + 4n ..],
+ * writing rollout buffer rows t: obs_buf [T,N,4] (the observation acted on),
+ * actions_buf int32 [T,N], log_probs_buf, values_buf, rewards_buf [T,N] and
+ * dones_buf uint8 [T,N].  observations [N,4] are the current observations;
+ * observations_out (may equal observations) receives those after the last
+ * step; state, steps and the episode tally (as ppo_cartpole_step, all three
+ * NULL or all set) are updated in place.  The results equal T pairs of
+ * ppo_mlp_act_cat_f32 + ppo_cartpole_step launches on the same uniforms.
+ * Replaces the per-step loop of rl/deep/runner.py:56-74 (select_action,
+ * env.step, the agent's rollout append) for N environments; no workspace.
+ */
+int ppo_cartpole_rollout_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
+                             int32_t hidden, int32_t activation, int64_t N, int32_t T,
+                             int32_t max_steps, double* state, int32_t* steps,
+                             const float* observations, float* observations_out,
+                             const float* action_uniforms, int64_t action_uniforms_stride,
+                             const float* reset_uniforms, int64_t reset_uniforms_stride,
+                             float* obs_buf, int32_t* actions_buf, float* log_probs_buf,
+                             float* values_buf, float* rewards_buf, uint8_t* dones_buf,
+                             float* episode_return, double* completed_sum,
+                             int32_t* completed_count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -122,7 +122,7 @@ def test_graphed_collection_matches_eager_steps(dev):
     obs_a, obs_b = env_a.reset().clone(), env_b.reset().clone()
     gen = torch.Generator(device=dev).manual_seed(1)
     for it in range(4):
-        obs_a = vec.collect(env_a, buf_a, obs_a, generator=gen)
+        obs_a = vec.collect(env_a, buf_a, obs_a, generator=gen, fused=False)
         plan = next(iter(vec._collect_plans.values()))
         assert (plan.graph is not None) == (it >= 1)
         ua, ur = plan.uact.clone(), plan.ureset.clone()
@@ -142,3 +142,44 @@ def test_graphed_collection_matches_eager_steps(dev):
         assert buf_a.step == buf_b.step == T
         assert int(buf_a.dones.sum()) > 0
     assert env_a.episode_stats() == env_b.episode_stats()
+
+
+@pytest.mark.parametrize("N,H,act", [(96, 64, "tanh"), (37, 32, "relu"), (5, 128, "tanh")])
+def test_fused_rollout_matches_step_by_step(dev, N, H, act):
+    """ppo_cartpole_rollout_f32 (the whole rollout in one launch) fills the
+    buffer, advances the environments and keeps the episode tally exactly as
+    the per-step act + step launches do on the same uniforms (max_steps 20:
+    truncation resets included; ragged N)."""
+    from ppo_amd.agent import MLP
+
+    torch.manual_seed(4)
+    T = 24
+    policy, value = MLP(4, H, 2, act).to(dev), MLP(4, H, 1, act).to(dev)
+    vec = ppo_amd.VecPPO(policy, value, graphs=True)
+    envs = [ppo_amd.CartPoleVec(N, device=dev, seed=9, max_steps=20) for _ in range(2)]
+    # "cuda" without an index, as train_cartpole passes it
+    bufs = [ppo_amd.RolloutBuffer(T, N, (4,), device="cuda") for _ in range(2)]
+    obs = [e.reset().clone() for e in envs]
+    gens = [torch.Generator(device=dev).manual_seed(1) for _ in range(2)]
+    for it in range(3):
+        obs[0] = vec.collect(envs[0], bufs[0], obs[0], generator=gens[0], fused=True)
+        obs[1] = vec.collect(envs[1], bufs[1], obs[1], generator=gens[1], fused=False)
+        assert torch.equal(obs[0], obs[1]), it
+        for name in ("observations", "actions", "log_probs", "values", "rewards", "dones",
+                     "last_value"):
+            assert torch.equal(getattr(bufs[0], name), getattr(bufs[1], name)), (it, name)
+        for name in ("state", "steps", "obs", "_ret", "_done_sum", "_done_count"):
+            assert torch.equal(getattr(envs[0], name), getattr(envs[1], name)), (it, name)
+        assert bufs[0].step == T and int(bufs[0].dones.sum()) > 0
+    assert envs[0].episode_stats() == envs[1].episode_stats()
+
+
+def test_fused_rollout_rejects_other_shapes(dev):
+    from ppo_amd.agent import MLP
+
+    policy, value = MLP(6, 32, 3, "tanh").to(dev), MLP(6, 32, 1, "tanh").to(dev)
+    vec = ppo_amd.VecPPO(policy, value)
+    env = ppo_amd.CartPoleVec(8, device=dev)
+    buf = ppo_amd.RolloutBuffer(4, 8, (4,), device=dev)
+    with pytest.raises(ValueError):
+        vec.collect(env, buf, env.reset().clone(), fused=True)

@@ -30,6 +30,7 @@
 #include <float.h>
 
 #include "common.hpp"
+#include "cartpole_row.hpp"
 #include "row_math.hpp"
 #include "sample_row.hpp"
 
@@ -469,6 +470,120 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_act_cat_kernel(ActArgs a) {
   }
 }
 
+// A whole CartPole rollout in one launch (ppo_cartpole_rollout_f32): the T
+// steps of act (both forwards + the inverse-CDF draw, as mlp_act_cat_kernel)
+// and environment step (cartpole_advance, as the stand-alone step kernel)
+// for the workgroup's 16 environments.  The environments of a workgroup
+// depend on nothing outside it, so the steps need no launch boundary; the
+// observations stay in LDS from one step to the next and the state in the
+// registers of threads 0-15.  The results equal those of the two kernels
+// launched per step on the same uniforms (the same functions run in the
+// same order).
+struct RolloutArgs {
+  MlpNet actor, critic;
+  long N;
+  int T, max_steps;
+  const float* u_act;    // row t: N action uniforms, at u_act + t * su_act
+  const float* u_reset;  // row t: N x 4 reset uniforms, at u_reset + t * su_reset
+  long su_act, su_reset;
+  double* state;
+  int32_t* steps;
+  const float* obs_in;
+  float* obs_out;
+  float* obs_buf;  // [T][N][4]
+  int32_t* act_buf;
+  float *logp_buf, *val_buf, *rew_buf;
+  uint8_t* done_buf;
+  float* ep_return;
+  double* done_sum;
+  int32_t* done_count;
+};
+
+constexpr int kCartpoleObs = 4;
+constexpr int kCartpoleActions = 2;
+
+template <int H, int kAct>
+__global__ void __launch_bounds__(kMlpBlock) mlp_cartpole_rollout_kernel(RolloutArgs a) {
+  constexpr int R = kMlpRows;
+  constexpr int D = kCartpoleObs;
+  constexpr int ld = act_ld<H>();
+  __shared__ float s_x[R * kXld];
+  __shared__ float s_a1[R * ld], s_a2[R * ld], s_c1[R * ld], s_c2[R * ld];
+  __shared__ float s_z[R * kZld];
+  __shared__ float s_v[R];
+  const int tid = threadIdx.x;
+  const long row0 = (long)blockIdx.x * R;
+  const long n = row0 + tid;
+  const bool mine = tid < R && n < a.N;  // thread tid steps environment n
+  double st[4] = {0.0, 0.0, 0.0, 0.0};
+  int steps = 0;
+  float ep_ret = 0.0f;
+  double dsum = 0.0;  // the tally as the stand-alone step keeps it
+  int dcount = 0;
+  if (mine) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) st[k] = a.state[n * 4 + k];
+    steps = a.steps[n];
+    if (a.ep_return) {
+      ep_ret = a.ep_return[n];
+      dsum = a.done_sum[n];
+      dcount = a.done_count[n];
+    }
+  }
+  if (tid < R) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) s_x[tid * kXld + k] = mine ? a.obs_in[n * D + k] : 0.0f;
+  }
+  lds_barrier();
+  for (int t = 0; t < a.T; ++t) {
+    float u = 0.0f;
+    float ur[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (mine) {
+      u = a.u_act[(long)t * a.su_act + n];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ur[k] = a.u_reset[(long)t * a.su_reset + n * 4 + k];
+#pragma unroll
+      for (int k = 0; k < D; ++k) a.obs_buf[((long)t * a.N + n) * D + k] = s_x[tid * kXld + k];
+    }
+    mlp_forward<H, kAct>(a.actor, a.critic, s_x, D, kCartpoleActions, s_a1, s_a2, s_c1, s_c2,
+                         s_z, s_v);
+    if (mine) {
+      int act;
+      float lp;
+      sample_cat_row(s_z + tid * kZld, kCartpoleActions, u, act, lp);
+      const long o = (long)t * a.N + n;
+      a.act_buf[o] = act;
+      a.logp_buf[o] = lp;
+      a.val_buf[o] = s_v[tid];
+      const CartpoleStep r = cartpole_advance(st, act, steps, a.max_steps, ur);
+      a.rew_buf[o] = 1.0f;
+      a.done_buf[o] = r.done ? 1 : 0;
+      const float ret = ep_ret + 1.0f;
+      if (r.done) {
+        dsum += (double)ret;
+        dcount += 1;
+      }
+      ep_ret = r.done ? 0.0f : ret;
+#pragma unroll
+      for (int k = 0; k < D; ++k) s_x[tid * kXld + k] = (float)st[k];
+    }
+    lds_barrier();
+  }
+  if (mine) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      a.state[n * 4 + k] = st[k];
+      a.obs_out[n * D + k] = (float)st[k];
+    }
+    a.steps[n] = steps;
+    if (a.ep_return) {
+      a.ep_return[n] = ep_ret;
+      a.done_sum[n] = dsum;
+      a.done_count[n] = dcount;
+    }
+  }
+}
+
 // Sum the per-workgroup gradient partials into the parameters' gradient
 // tensors: a workgroup owns 64 consecutive parameters; wave w sums partials
 // w, w + 4, w + 8, ... (fp64, 8 loads in flight per step) and the four wave
@@ -585,6 +700,17 @@ const void* act_kernel_act(int H) {
     case 32: return (const void*)mlp_act_cat_kernel<32, kAct>;
     case 64: return (const void*)mlp_act_cat_kernel<64, kAct>;
     case 128: return (const void*)mlp_act_cat_kernel<128, kAct>;
+    default: return nullptr;
+  }
+}
+
+template <int kAct>
+const void* rollout_kernel_act(int H) {
+  switch (H) {
+    case 16: return (const void*)mlp_cartpole_rollout_kernel<16, kAct>;
+    case 32: return (const void*)mlp_cartpole_rollout_kernel<32, kAct>;
+    case 64: return (const void*)mlp_cartpole_rollout_kernel<64, kAct>;
+    case 128: return (const void*)mlp_cartpole_rollout_kernel<128, kAct>;
     default: return nullptr;
   }
 }
@@ -728,6 +854,60 @@ extern "C" int ppo_mlp_act_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32
   a.act = actions_out;
   a.logp = log_probs_out;
   a.val = values_out;
+  void* args[] = {&a};
+  const long blocks = (N + kMlpRows - 1) / kMlpRows;
+  return hip_status(hipLaunchKernel(kern, dim3((unsigned)blocks), dim3(kMlpBlock), args, 0,
+                                    reinterpret_cast<hipStream_t>(stream_ptr)));
+}
+
+extern "C" int ppo_cartpole_rollout_f32(
+    const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic, int32_t hidden, int32_t activation,
+    int64_t N, int32_t T, int32_t max_steps, double* state, int32_t* steps,
+    const float* observations, float* observations_out, const float* action_uniforms,
+    int64_t action_uniforms_stride, const float* reset_uniforms, int64_t reset_uniforms_stride,
+    float* obs_buf, int32_t* actions_buf, float* log_probs_buf, float* values_buf,
+    float* rewards_buf, uint8_t* dones_buf, float* episode_return, double* completed_sum,
+    int32_t* completed_count, void* stream_ptr) {
+  using namespace ppo;
+  if (N < 0 || T < 0 || max_steps < 1) return PPO_ERR_INVALID_ARG;
+  if (activation != PPO_ACT_RELU && activation != PPO_ACT_TANH) return PPO_ERR_INVALID_ARG;
+  const void* kern = activation == PPO_ACT_TANH ? rollout_kernel_act<PPO_ACT_TANH>(hidden)
+                                                : rollout_kernel_act<PPO_ACT_RELU>(hidden);
+  if (!kern) return PPO_ERR_UNSUPPORTED;
+  if (!mlp_net_weights_ok(actor) || !mlp_net_weights_ok(critic)) return PPO_ERR_INVALID_ARG;
+  if ((episode_return == nullptr) != (completed_sum == nullptr) ||
+      (episode_return == nullptr) != (completed_count == nullptr))
+    return PPO_ERR_INVALID_ARG;
+  if (N == 0 || T == 0) return PPO_OK;
+  if (!state || !steps || !observations || !observations_out || !action_uniforms ||
+      !reset_uniforms || !obs_buf || !actions_buf || !log_probs_buf || !values_buf ||
+      !rewards_buf || !dones_buf)
+    return PPO_ERR_INVALID_ARG;
+  if (action_uniforms_stride < N || reset_uniforms_stride < 4 * N) return PPO_ERR_INVALID_ARG;
+  if (N > (1L << 31) || (long)T * N > (1L << 40)) return PPO_ERR_TOO_LARGE;
+  RolloutArgs a = {};
+  a.actor = to_net(actor);
+  a.critic = to_net(critic);
+  a.N = N;
+  a.T = T;
+  a.max_steps = max_steps;
+  a.u_act = action_uniforms;
+  a.u_reset = reset_uniforms;
+  a.su_act = action_uniforms_stride;
+  a.su_reset = reset_uniforms_stride;
+  a.state = state;
+  a.steps = steps;
+  a.obs_in = observations;
+  a.obs_out = observations_out;
+  a.obs_buf = obs_buf;
+  a.act_buf = actions_buf;
+  a.logp_buf = log_probs_buf;
+  a.val_buf = values_buf;
+  a.rew_buf = rewards_buf;
+  a.done_buf = dones_buf;
+  a.ep_return = episode_return;
+  a.done_sum = completed_sum;
+  a.done_count = completed_count;
   void* args[] = {&a};
   const long blocks = (N + kMlpRows - 1) / kMlpRows;
   return hip_status(hipLaunchKernel(kern, dim3((unsigned)blocks), dim3(kMlpBlock), args, 0,

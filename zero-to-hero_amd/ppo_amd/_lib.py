@@ -105,6 +105,11 @@ SIGNATURES = {
     "ppo_cartpole_reset": (_int, [_vp, _vp, _vp, _vp, _i64, _vp]),
     "ppo_cartpole_step": (
         _int, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "ppo_cartpole_rollout_f32": (
+        _int,
+        [ctypes.POINTER(Mlp3), ctypes.POINTER(Mlp3), _i32, _i32, _i64, _i32, _i32, _vp, _vp, _vp,
+         _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+    ),
     "ppo_mlp_act_cat_f32": (
         _int,
         [ctypes.POINTER(Mlp3), ctypes.POINTER(Mlp3), _i32, _i32, _i32, _i32, _vp, _i64, _vp, _vp,

@@ -893,3 +893,62 @@ def mlp_act_categorical(
           observations.data_ptr(), N, uniforms.data_ptr(), _ptr(observations_out),
           actions_out.data_ptr(), log_probs_out.data_ptr(), values_out.data_ptr(), stream)
     return actions_out, log_probs_out, values_out
+
+
+def mlp_cartpole_rollout(
+    policy: torch.nn.Module,
+    value: torch.nn.Module,
+    env,
+    buffer,
+    observations: torch.Tensor,
+    action_uniforms: torch.Tensor,
+    reset_uniforms: torch.Tensor,
+) -> torch.Tensor:
+    """A whole rollout of `buffer.T` steps of `env` (a CartPoleVec) in one
+    launch (ppo_cartpole_rollout_f32): per step mlp_act_categorical at
+    action_uniforms[t] ([T,N] rows, any row stride) and env.step_into with
+    reset_uniforms[t] ([T,N,4] rows), filling buffer rows 0..T-1 (the caller
+    sets buffer.step).  Starts from `observations` [N,4]; returns env.obs,
+    which holds the observations after the last step.  The results equal the
+    step-by-step path's on the same uniforms."""
+    if not mlp_fusable(policy, value):
+        raise ValueError("policy/value are not MLPs the fused kernel supports (see mlp_fusable)")
+    lp, act = mlp_structure(policy)
+    lv, _ = mlp_structure(value)
+    D, H, A = lp[0].in_features, lp[0].out_features, lp[2].out_features
+    if D != 4 or A != 2:
+        raise ValueError(f"the CartPole rollout needs 4-H-H-2 / 4-H-H-1 networks, got D={D}, A={A}")
+    device = env.device
+    T, N = buffer.T, buffer.N
+    if N != env.num_envs:
+        raise ValueError(f"buffer has N={N}, the environment {env.num_envs}")
+    if buffer.actions.dtype != torch.int32 or buffer.actions.dim() != 2:
+        raise ValueError("the rollout buffer must hold categorical int32 actions")
+    if tuple(buffer.observations.shape) != (T, N, 4) or buffer.observations.device != device:
+        raise ValueError("the rollout buffer must hold [T,N,4] observations on the env's device")
+    _require(observations, "observations", (torch.float32,), device)
+    if tuple(observations.shape) != (N, 4):
+        raise ValueError(f"observations must be [N,4]=[{N},4], got {tuple(observations.shape)}")
+    if (action_uniforms.dtype != torch.float32 or action_uniforms.device != device
+            or tuple(action_uniforms.shape) != (T, N) or action_uniforms.stride(1) != 1):
+        raise ValueError("action_uniforms must be fp32 [T,N] rows of unit stride on the device")
+    if (reset_uniforms.dtype != torch.float32 or reset_uniforms.device != device
+            or tuple(reset_uniforms.shape) != (T, N, 4) or reset_uniforms.stride(2) != 1
+            or reset_uniforms.stride(1) != 4):
+        raise ValueError("reset_uniforms must be fp32 [T,N,4] with contiguous rows on the device")
+    s_actor, s_critic = _lib.Mlp3(), _lib.Mlp3()
+    for st, layers in ((s_actor, lp), (s_critic, lv)):
+        for i, m in enumerate(layers):
+            st.weight[i] = m.weight.data_ptr()
+            st.bias[i] = m.bias.data_ptr()
+    stream = _stream(device)
+    _call("ppo_cartpole_rollout_f32", device, stream, ctypes.byref(s_actor),
+          ctypes.byref(s_critic), H, _lib.PPO_ACT_TANH if act == "tanh" else _lib.PPO_ACT_RELU,
+          N, T, env.max_steps, env.state.data_ptr(), env.steps.data_ptr(),
+          observations.data_ptr(), env.obs.data_ptr(), action_uniforms.data_ptr(),
+          action_uniforms.stride(0), reset_uniforms.data_ptr(), reset_uniforms.stride(0),
+          buffer.observations.data_ptr(), buffer.actions.data_ptr(),
+          buffer.log_probs.data_ptr(), buffer.values.data_ptr(), buffer.rewards.data_ptr(),
+          buffer.dones.data_ptr(), env._ret.data_ptr(), env._done_sum.data_ptr(),
+          env._done_count.data_ptr(), stream)
+    return env.obs

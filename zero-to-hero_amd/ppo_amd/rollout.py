@@ -172,6 +172,7 @@ class VecPPO:
         self.graphs, self.graph_chunk = graphs, graph_chunk
         self._plans: dict = {}  # (shape, storage) key -> _GraphPlan, two at most
         self._collect_plans: dict = {}  # (env, buffer, shapes) -> _CollectPlan, two at most
+        self._rollout_u: Optional[torch.Tensor] = None  # uniforms of the fused rollout
         self._plan: Optional[_GraphPlan] = None  # the most recently used
         self._side_stream: Optional[torch.cuda.Stream] = None
         can_fuse = fused_update and log_std is None and ops.mlp_fusable(policy, value)
@@ -241,7 +242,7 @@ class VecPPO:
     @torch.no_grad()
     def collect(self, env, buffer: RolloutBuffer, observations: torch.Tensor,
                 generator: Optional[torch.Generator] = None, bootstrap: bool = True,
-                graphs: Optional[bool] = None):
+                graphs: Optional[bool] = None, fused: Optional[bool] = None):
         """Fill `buffer` with buffer.T steps of the vectorised environment
         `env` (an object with step(actions int32 [N]) -> (observations,
         rewards, dones, ...), e.g. CartPoleVec), starting from
@@ -258,7 +259,17 @@ class VecPPO:
         path, the T steps are replayed from one HIP graph: the rollout's
         random numbers (action uniforms [T,N], reset uniforms [T,N,4]) are
         drawn in one launch first and read by the graph; the first call for
-        a (environment, buffer) pair runs eagerly and captures."""
+        a (environment, buffer) pair runs eagerly and captures.
+
+        With `fused` (default: whenever possible) a CartPoleVec environment
+        and 4-H-H-2 / 4-H-H-1 MLPs on the fused path, the whole rollout is
+        one launch (ops.mlp_cartpole_rollout) on uniforms drawn the same way,
+        so it fills the buffer exactly as the per-step path does."""
+        if fused is not False and self._cartpole_fusable(env, observations):
+            return self._collect_fused(env, buffer, observations, generator, bootstrap)
+        if fused:
+            raise ValueError("fused collection needs a CartPoleVec, the fused MLP path and "
+                             "4-H-H-2 / 4-H-H-1 networks")
         use_graph = self.graphs if graphs is None else graphs
         if (use_graph and self.fused_mlp and hasattr(env, "step_into")
                 and observations.dim() == 2):
@@ -276,6 +287,29 @@ class VecPPO:
                 obs, rewards, dones = env.step(acts)[:3]
                 buffer.add_outcome(rewards, dones)
         obs = obs.clone()
+        buffer.finish(self.value(obs).reshape(-1) if bootstrap else None)
+        return obs
+
+    def _cartpole_fusable(self, env, observations) -> bool:
+        from .env import CartPoleVec
+        if not (self.fused_mlp and isinstance(env, CartPoleVec) and observations.dim() == 2):
+            return False
+        lp, _ = ops.mlp_structure(self.policy)
+        return lp[0].in_features == 4 and lp[2].out_features == 2
+
+    def _collect_fused(self, env, buffer, observations, generator, bootstrap):
+        T, N, dev = buffer.T, buffer.N, buffer.device
+        u = self._rollout_u
+        if u is None or tuple(u.shape) != (T, 5 * N) or u.device != dev:
+            u = self._rollout_u = torch.empty((T, 5 * N), dtype=torch.float32, device=dev)
+        # the layout of the graphed path's draw (_CollectPlan), so both paths
+        # consume the same numbers
+        torch.rand(u.shape, generator=generator, device=dev, out=u)
+        buffer.reset()
+        ops.mlp_cartpole_rollout(self.policy, self.value, env, buffer, observations.contiguous(),
+                                 u[:, :N], u[:, N:].view(T, N, 4))
+        buffer.step = T
+        obs = env.obs.clone()
         buffer.finish(self.value(obs).reshape(-1) if bootstrap else None)
         return obs
 
