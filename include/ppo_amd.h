@@ -323,6 +323,31 @@ int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
                          size_t workspace_bytes, void* stream);
 
 /*
+ * A whole minibatch step of PPOAgent._update_batch (rl/deep/agents/
+ * ppo.py:141-171): ppo_mlp_cat_grad_f32's gradients, then
+ * clip_grad_norm_(max_grad_norm) + Adam as ppo_adam_clip_f32 over the 12
+ * tensors in the order actor weight[0], bias[0], weight[1], bias[1],
+ * weight[2], bias[2], then the critic's (the order of
+ * list(policy.parameters()) + list(value.parameters())).  exp_avg and
+ * exp_avg_sq are host arrays of 12 device pointers in that order; the
+ * weights and biases of both structs are updated in place (so they must be
+ * writable), their gradients hold the clipped gradients afterwards.  Three
+ * launches instead of four: the gradient reduction also leaves each
+ * tensor's sum of squares in pieces, and increments adam->step_counter when
+ * it is set.  grad_norm_out (may be NULL) receives the total norm.  Same
+ * limits and workspace as ppo_mlp_cat_grad_f32.
+ */
+int ppo_mlp_cat_step_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
+                         int32_t obs_dim, int32_t hidden, int32_t A, int32_t activation,
+                         const float* observations, int64_t n, const int64_t* index, int64_t B,
+                         const void* actions, int actions_are_int64, const float* old_log_probs,
+                         const float* advantages, const float* returns, const float* old_values,
+                         const ppo_loss_params* params, float* const* exp_avg,
+                         float* const* exp_avg_sq, const ppo_adam_params* adam,
+                         float* scalars_out, float* grad_norm_out, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/*
  * PPOAgent.select_action (rl/deep/agents/ppo.py:65-79) for N observations
  * through the actor and critic MLPs of ppo_mlp_cat_grad_f32 (only the weights
  * and biases of the structs are read): logits = actor(obs), values =

@@ -114,6 +114,46 @@ def test_mlp_grads_match_unfused_gpu_path(dev):
         assert_grad_close(a.grad, b.grad)
 
 
+@pytest.mark.parametrize("capturable", [False, True])
+@pytest.mark.parametrize("max_norm", [0.5, 1e6])
+def test_mlp_step_matches_grads_then_clipped_adam(dev, capturable, max_norm):
+    """ppo_mlp_cat_step_f32 (gradients + clip + Adam in three launches) against
+    ppo_mlp_cat_grads followed by ClippedAdam.step(), over four steps: the
+    gradients are the same; the clip norm is summed from 64-element pieces
+    instead of 1024-element ones (fp64), so parameters, moments and norms
+    agree within 2e-6 relative."""
+    pol, val, cpu, gpu = _case(dev, 512, 4, 64, 2, "tanh", seed=21)
+    nets = [(copy.deepcopy(pol).to(dev), copy.deepcopy(val).to(dev)) for _ in range(2)]
+    opts = [ppo_amd.ClippedAdam(list(p.parameters()) + list(v.parameters()), lr=1e-3,
+                                max_grad_norm=max_norm, capturable=capturable)
+            for p, v in nets]
+    args = (gpu["obs"], gpu["actions"], gpu["old_lp"], gpu["adv"], gpu["ret"])
+    g = torch.Generator().manual_seed(22)
+    for step in range(4):
+        idx = torch.randperm(512, generator=g)[:256].to(dev)
+        s1, n1 = ppo_amd.ppo_mlp_cat_step(nets[0][0], nets[0][1], opts[0], *args, index=idx)
+        s2 = ppo_amd.ppo_mlp_cat_grads(nets[1][0], nets[1][1], *args, index=idx)
+        n2 = opts[1].step()
+        assert n1.item() == pytest.approx(n2.item(), rel=2e-6)
+        for k in s2:
+            assert torch.equal(s1[k], s2[k]), k
+        for a, b in zip(opts[0].params, opts[1].params):
+            torch.testing.assert_close(a.grad, b.grad, rtol=2e-6, atol=1e-9)
+            torch.testing.assert_close(a.detach(), b.detach(), rtol=2e-6, atol=1e-7)
+    for a, b in zip(opts[0].exp_avg + opts[0].exp_avg_sq, opts[1].exp_avg + opts[1].exp_avg_sq):
+        torch.testing.assert_close(a, b, rtol=2e-6, atol=1e-10)
+    assert opts[0].step_count() == opts[1].step_count() == 4
+
+
+def test_mlp_step_rejects_foreign_optimizer(dev):
+    pol, val, cpu, gpu = _case(dev, 64, 4, 32, 2, "tanh", seed=23)
+    p, v = pol.to(dev), val.to(dev)
+    opt = ppo_amd.ClippedAdam(list(v.parameters()) + list(p.parameters()))  # wrong order
+    with pytest.raises(ValueError):
+        ppo_amd.ppo_mlp_cat_step(p, v, opt, gpu["obs"], gpu["actions"], gpu["old_lp"],
+                                 gpu["adv"], gpu["ret"])
+
+
 def test_mlp_grads_deterministic(dev):
     pol, val, cpu, gpu = _case(dev, 2048, 4, 128, 2, "relu", seed=11)
     idx = torch.randperm(2048, generator=torch.Generator().manual_seed(12))[:1000].to(dev)

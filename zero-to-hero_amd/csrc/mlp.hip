@@ -30,6 +30,7 @@
 #include <float.h>
 
 #include "common.hpp"
+#include "adam.hpp"
 #include "cartpole_row.hpp"
 #include "row_math.hpp"
 #include "sample_row.hpp"
@@ -42,6 +43,7 @@ constexpr int kMlpRows = 16;
 constexpr int kMlpMaxIn = 64;
 constexpr int kMlpMaxA = 32;
 constexpr int kMlpSums = 5;  // policy, value, entropy, approx-kl, clipfrac
+constexpr int kMlpTensors = 12;  // weights and biases of the two 3-layer networks
 
 struct MlpNet {
   const float* w[3];
@@ -78,6 +80,15 @@ struct MlpArgs {
   long P;
   long nblocks;
   float* scalars;
+  // Reduction blocks are aligned to the 12 parameter tensors (tensor j =
+  // 6 * net + 2 * layer + is_bias, actor first): tensor j owns reduction
+  // blocks [tblk[j], tblk[j + 1]) and global parameters [toff[j],
+  // toff[j] + tnum[j]).
+  long tblk[kMlpTensors + 1];
+  long toff[kMlpTensors];
+  long tnum[kMlpTensors];
+  double* sqpart;          // per reduction block: sum of squares of its gradients (or null)
+  int64_t* step_counter;   // incremented once by reduction block 0 (or null)
 };
 
 template <int kAct>
@@ -585,25 +596,18 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cartpole_rollout_kernel(Rollout
 }
 
 // Sum the per-workgroup gradient partials into the parameters' gradient
-// tensors: a workgroup owns 64 consecutive parameters; wave w sums partials
-// w, w + 4, w + 8, ... (fp64, 8 loads in flight per step) and the four wave
-// sums are added in wave order, so the order is fixed (deterministic).
-// Workgroup 0 also forms the loss scalars.
+// tensors: a workgroup owns up to 64 consecutive parameters of one tensor;
+// wave w sums partials w, w + 4, w + 8, ... (fp64, 8 loads in flight per
+// step) and the four wave sums are added in wave order, so the order is
+// fixed (deterministic).  With sqpart the workgroup also leaves the fp64 sum
+// of the squares of the fp32 gradients it wrote (clip_grad_norm_'s
+// per-tensor sums, in pieces).  Workgroup 0 also forms the loss scalars.
 constexpr int kRedCols = 64;
 
-__device__ __forceinline__ float* grad_slot(const MlpArgs& a, long p) {
-  const MlpNet* nets[2] = {&a.actor, &a.critic};
-  const NetOffsets* offs[2] = {&a.oa, &a.oc};
-  float* dst = nullptr;
-#pragma unroll
-  for (int n = 0; n < 2; ++n)
-#pragma unroll
-    for (int l = 0; l < 3; ++l) {
-      if (p >= offs[n]->w[l] && p < offs[n]->b[l]) dst = nets[n]->gw[l] + (p - offs[n]->w[l]);
-      const long bend = (l < 2) ? offs[n]->w[l + 1] : (n == 0 ? a.oc.w[0] : a.P);
-      if (p >= offs[n]->b[l] && p < bend) dst = nets[n]->gb[l] + (p - offs[n]->b[l]);
-    }
-  return dst;
+__device__ __forceinline__ float* tensor_grad(const MlpArgs& a, int j) {
+  const MlpNet& net = j < 6 ? a.actor : a.critic;
+  const int l = (j % 6) / 2;
+  return (j & 1) ? net.gb[l] : net.gw[l];
 }
 
 __global__ void __launch_bounds__(kMlpBlock) mlp_grad_reduce_kernel(MlpArgs a) {
@@ -611,29 +615,39 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_grad_reduce_kernel(MlpArgs a) {
   __shared__ double s_sum[kWaves][kRedCols];
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
-  const long p = (long)blockIdx.x * kRedCols + lane;
-  const long pc = p < a.P ? p : a.P - 1;
+  const long blk = blockIdx.x;
+  int j = 0;
+  while (j + 1 < kMlpTensors && blk >= a.tblk[j + 1]) ++j;
+  const long local = (blk - a.tblk[j]) * kRedCols + lane;
+  const bool valid = local < a.tnum[j];
+  const long pc = a.toff[j] + (valid ? local : 0);
   double s = 0.0;
   for (long b0 = w; b0 < a.nblocks; b0 += 8 * kWaves) {
     float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const long b = b0 + (long)j * kWaves;
-      v[j] = a.gpart[(b < a.nblocks ? b : 0) * a.P + pc];
+    for (int q = 0; q < 8; ++q) {
+      const long b = b0 + (long)q * kWaves;
+      v[q] = a.gpart[(b < a.nblocks ? b : 0) * a.P + pc];
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (b0 + (long)j * kWaves < a.nblocks) s += (double)v[j];
+    for (int q = 0; q < 8; ++q)
+      if (b0 + (long)q * kWaves < a.nblocks) s += (double)v[q];
   }
   s_sum[w][lane] = s;
   __syncthreads();
-  if (w == 0 && p < a.P) {
+  if (w == 0) {
     double t = s_sum[0][lane];
 #pragma unroll
     for (int k = 1; k < kWaves; ++k) t += s_sum[k][lane];
-    *grad_slot(a, p) = (float)t;
+    const float g = (float)t;
+    if (valid) tensor_grad(a, j)[local] = g;
+    if (a.sqpart) {
+      const double sq = wave_sum(valid ? (double)g * (double)g : 0.0);
+      if (lane == 0) a.sqpart[blk] = sq;
+    }
   }
-  if (blockIdx.x == 0) {
+  if (blk == 0) {
+    if (threadIdx.x == 0 && a.step_counter) *a.step_counter += 1;
     double tot[kMlpSums];
     for (int k = 0; k < kMlpSums; ++k) tot[k] = 0.0;
     for (long b = threadIdx.x; b < a.nblocks; b += kMlpBlock)
@@ -668,17 +682,30 @@ NetOffsets net_offsets(long base, int D, int H, int O) {
 }
 
 struct MlpLayout {
-  long P, nblocks;
-  size_t gpart, spart, total;
+  long P, nblocks, rblocks;
+  long tblk[kMlpTensors + 1], toff[kMlpTensors], tnum[kMlpTensors];
+  size_t gpart, spart, sqpart, total;
 };
 
 MlpLayout mlp_layout(long B, int D, int H, int A) {
   MlpLayout l;
   l.P = mlp_params(D, H, A) + mlp_params(D, H, 1);
   l.nblocks = (B + kMlpRows - 1) / kMlpRows;
+  const NetOffsets o[2] = {net_offsets(0, D, H, A), net_offsets(mlp_params(D, H, A), D, H, 1)};
+  const int outs[2] = {A, 1};
+  l.tblk[0] = 0;
+  for (int j = 0; j < kMlpTensors; ++j) {
+    const int net = j / 6, layer = (j % 6) / 2;
+    const long in = layer == 0 ? D : H, out = layer == 2 ? outs[net] : H;
+    l.toff[j] = (j & 1) ? o[net].b[layer] : o[net].w[layer];
+    l.tnum[j] = (j & 1) ? out : out * in;
+    l.tblk[j + 1] = l.tblk[j] + (l.tnum[j] + kRedCols - 1) / kRedCols;
+  }
+  l.rblocks = l.tblk[kMlpTensors];
   l.gpart = kHeaderBytes;
   l.spart = l.gpart + align_up((size_t)l.nblocks * l.P * sizeof(float), 256);
-  l.total = l.spart + align_up((size_t)kMlpSums * l.nblocks * sizeof(double), 256);
+  l.sqpart = l.spart + align_up((size_t)kMlpSums * l.nblocks * sizeof(double), 256);
+  l.total = l.sqpart + align_up((size_t)l.rblocks * sizeof(double), 256);
   return l;
 }
 
@@ -750,22 +777,26 @@ extern "C" size_t ppo_mlp_cat_grad_workspace_bytes(int64_t B, int32_t obs_dim, i
   return mlp_layout(B, obs_dim, hidden, A).total;
 }
 
-extern "C" int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
-                                    int32_t obs_dim, int32_t hidden, int32_t A,
-                                    int32_t activation, const float* observations, int64_t n,
-                                    const int64_t* index, int64_t B, const void* actions,
-                                    int actions_are_int64, const float* old_log_probs,
-                                    const float* advantages, const float* returns,
-                                    const float* old_values, const ppo_loss_params* params,
-                                    float* scalars_out, void* workspace, size_t workspace_bytes,
-                                    void* stream_ptr) {
-  using namespace ppo;
+namespace ppo {
+namespace {
+
+// Validation and argument setup shared by ppo_mlp_cat_grad_f32 and
+// ppo_mlp_cat_step_f32; on PPO_OK, `kern`, `a` and `l` are ready to launch
+// (B == 0 returns PPO_OK with kern null: nothing to do).
+int mlp_setup(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic, int32_t obs_dim,
+              int32_t hidden, int32_t A, int32_t activation, const float* observations,
+              int64_t n, const int64_t* index, int64_t B, const void* actions,
+              int actions_are_int64, const float* old_log_probs, const float* advantages,
+              const float* returns, const float* old_values, const ppo_loss_params* params,
+              float* scalars_out, void* workspace, size_t workspace_bytes, const void*& kern,
+              MlpArgs& a, MlpLayout& l) {
+  kern = nullptr;
   if (B < 0 || n < 0) return PPO_ERR_INVALID_ARG;
   if (obs_dim <= 0 || obs_dim > kMlpMaxIn || A <= 0 || A > kMlpMaxA) return PPO_ERR_UNSUPPORTED;
   if (activation != PPO_ACT_RELU && activation != PPO_ACT_TANH) return PPO_ERR_INVALID_ARG;
-  const void* kern = activation == PPO_ACT_TANH ? mlp_kernel_act<PPO_ACT_TANH>(hidden)
-                                                : mlp_kernel_act<PPO_ACT_RELU>(hidden);
-  if (!kern) return PPO_ERR_UNSUPPORTED;
+  const void* k = activation == PPO_ACT_TANH ? mlp_kernel_act<PPO_ACT_TANH>(hidden)
+                                             : mlp_kernel_act<PPO_ACT_RELU>(hidden);
+  if (!k) return PPO_ERR_UNSUPPORTED;
   if (!mlp_net_ok(actor) || !mlp_net_ok(critic) || !params || !scalars_out)
     return PPO_ERR_INVALID_ARG;
   if (B == 0) return PPO_OK;
@@ -774,14 +805,12 @@ extern "C" int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
   if (B > (1L << 31) || n > (1L << 40)) return PPO_ERR_TOO_LARGE;
   if (!workspace || workspace_bytes < ppo_mlp_cat_grad_workspace_bytes(B, obs_dim, hidden, A))
     return PPO_ERR_WORKSPACE;
-  for (int l = 0; l < 3; ++l)
-    if (!aligned(actor->weight[l], 16) || !aligned(critic->weight[l], 16))
+  for (int li = 0; li < 3; ++li)
+    if (!aligned(actor->weight[li], 16) || !aligned(critic->weight[li], 16))
       return PPO_ERR_INVALID_ARG;
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
-  const MlpLayout l = mlp_layout(B, obs_dim, hidden, A);
+  l = mlp_layout(B, obs_dim, hidden, A);
   char* ws = static_cast<char*>(workspace);
-
-  MlpArgs a = {};
+  a = MlpArgs{};
   a.actor = to_net(actor);
   a.critic = to_net(critic);
   a.oa = net_offsets(0, obs_dim, hidden, A);
@@ -814,14 +843,91 @@ extern "C" int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
   a.P = l.P;
   a.nblocks = l.nblocks;
   a.scalars = scalars_out;
+  for (int j = 0; j <= kMlpTensors; ++j) a.tblk[j] = l.tblk[j];
+  for (int j = 0; j < kMlpTensors; ++j) {
+    a.toff[j] = l.toff[j];
+    a.tnum[j] = l.tnum[j];
+  }
+  a.sqpart = nullptr;
+  a.step_counter = nullptr;
+  kern = k;
+  return PPO_OK;
+}
 
+// The gradient kernel (two workgroups per 16-row block) and the reduction.
+int mlp_launch(const void* kern, MlpArgs& a, const MlpLayout& l, hipStream_t stream) {
   void* args[] = {&a};
-  int st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(kMlpBlock), args, 0,
-                                      stream));
+  int st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(kMlpBlock),
+                                      args, 0, stream));
   if (st) return st;
-  const long rblocks = (l.P + kRedCols - 1) / kRedCols;
-  return hip_status(hipLaunchKernel((const void*)mlp_grad_reduce_kernel, dim3((unsigned)rblocks),
+  return hip_status(hipLaunchKernel((const void*)mlp_grad_reduce_kernel, dim3((unsigned)l.rblocks),
                                     dim3(kMlpBlock), args, 0, stream));
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
+                                    int32_t obs_dim, int32_t hidden, int32_t A,
+                                    int32_t activation, const float* observations, int64_t n,
+                                    const int64_t* index, int64_t B, const void* actions,
+                                    int actions_are_int64, const float* old_log_probs,
+                                    const float* advantages, const float* returns,
+                                    const float* old_values, const ppo_loss_params* params,
+                                    float* scalars_out, void* workspace, size_t workspace_bytes,
+                                    void* stream_ptr) {
+  using namespace ppo;
+  const void* kern;
+  MlpArgs a;
+  MlpLayout l;
+  const int st = mlp_setup(actor, critic, obs_dim, hidden, A, activation, observations, n, index,
+                           B, actions, actions_are_int64, old_log_probs, advantages, returns,
+                           old_values, params, scalars_out, workspace, workspace_bytes, kern, a,
+                           l);
+  if (st || !kern) return st;
+  return mlp_launch(kern, a, l, reinterpret_cast<hipStream_t>(stream_ptr));
+}
+
+extern "C" int ppo_mlp_cat_step_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
+                                    int32_t obs_dim, int32_t hidden, int32_t A,
+                                    int32_t activation, const float* observations, int64_t n,
+                                    const int64_t* index, int64_t B, const void* actions,
+                                    int actions_are_int64, const float* old_log_probs,
+                                    const float* advantages, const float* returns,
+                                    const float* old_values, const ppo_loss_params* params,
+                                    float* const* exp_avg, float* const* exp_avg_sq,
+                                    const ppo_adam_params* adam, float* scalars_out,
+                                    float* grad_norm_out, void* workspace, size_t workspace_bytes,
+                                    void* stream_ptr) {
+  using namespace ppo;
+  if (!exp_avg || !exp_avg_sq || !adam) return PPO_ERR_INVALID_ARG;
+  for (int j = 0; j < kMlpTensors; ++j)
+    if (!exp_avg[j] || !exp_avg_sq[j]) return PPO_ERR_INVALID_ARG;
+  if ((!adam->step_counter && adam->step < 1) || !(adam->lr >= 0.0) || !(adam->eps >= 0.0))
+    return PPO_ERR_INVALID_ARG;
+  const void* kern;
+  MlpArgs a;
+  MlpLayout l;
+  int st = mlp_setup(actor, critic, obs_dim, hidden, A, activation, observations, n, index, B,
+                     actions, actions_are_int64, old_log_probs, advantages, returns, old_values,
+                     params, scalars_out, workspace, workspace_bytes, kern, a, l);
+  if (st || !kern) return st;
+  a.sqpart = reinterpret_cast<double*>(static_cast<char*>(workspace) + l.sqpart);
+  a.step_counter = adam->step_counter;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  if ((st = mlp_launch(kern, a, l, stream))) return st;
+  float* pp[kMlpTensors];
+  float* gp[kMlpTensors];
+  int64_t numel[kMlpTensors];
+  for (int j = 0; j < kMlpTensors; ++j) {
+    const ppo_mlp3_f32* net = j < 6 ? actor : critic;
+    const int li = (j % 6) / 2;
+    pp[j] = const_cast<float*>((j & 1) ? net->bias[li] : net->weight[li]);  // updated in place
+    gp[j] = (j & 1) ? net->bias_grad[li] : net->weight_grad[li];
+    numel[j] = l.tnum[j];
+  }
+  return launch_adam_presummed(kMlpTensors, pp, gp, exp_avg, exp_avg_sq, numel, adam, a.sqpart,
+                               l.tblk, grad_norm_out, stream);
 }
 
 extern "C" int ppo_mlp_act_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,

@@ -14,6 +14,7 @@
 //    operation rounded separately.
 #include <algorithm>
 
+#include "adam.hpp"
 #include "common.hpp"
 
 namespace ppo {
@@ -72,7 +73,8 @@ struct AdamTable {
   float* m[PPO_ADAM_MAX_TENSORS];
   float* v[PPO_ADAM_MAX_TENSORS];
   long n[PPO_ADAM_MAX_TENSORS];
-  long block_start[PPO_ADAM_MAX_TENSORS + 1];
+  long block_start[PPO_ADAM_MAX_TENSORS + 1];  // update blocks of each tensor
+  long part_start[PPO_ADAM_MAX_TENSORS + 1];   // its sum-of-squares partials
   int nt;
 };
 
@@ -151,7 +153,7 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
   }
   if (step_counter) adam_step_scalars(s, step_counter);
   // Global norm: per-tensor norms rounded to fp32 (lane k of wave 0 sums
-  // tensor k's block partials in block order), then the norm of those in
+  // tensor k's partials in order), then the norm of those in
   // tensor order (the two-level form of torch's _get_total_norm); every block
   // derives the same value in the same order.
   if (threadIdx.x < PPO_ADAM_MAX_TENSORS) {
@@ -160,8 +162,8 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
     if (kk < t.nt) {
       // sequential sum in block order, loads batched 8 at a time
       double sk = 0.0;
-      long c = t.block_start[kk];
-      const long ce = t.block_start[kk + 1];
+      long c = t.part_start[kk];
+      const long ce = t.part_start[kk + 1];
       for (; c + 8 <= ce; c += 8) {
         double x[8];
 #pragma unroll
@@ -210,6 +212,27 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
   }
 }
 
+// Host-side scalars exactly as torch forms them: Python doubles, rounded to
+// fp32 where the tensor op consumes them.
+AdamScalars make_adam_scalars(const ppo_adam_params* hp) {
+  const double step = hp->step_counter ? 1.0 : (double)hp->step;  // device path recomputes
+  const double bc1 = 1.0 - pow(hp->beta1, step);
+  const double bc2 = 1.0 - pow(hp->beta2, step);
+  AdamScalars s;
+  s.max_norm = (float)hp->max_grad_norm;
+  s.clip = hp->max_grad_norm > 0.0 ? 1 : 0;
+  s.beta1_w = (float)(1.0 - hp->beta1);
+  s.beta2 = (float)hp->beta2;
+  s.one_m_beta2 = (float)(1.0 - hp->beta2);
+  s.bc2_sqrt = (float)sqrt(bc2);
+  s.eps = (float)hp->eps;
+  s.neg_step = (float)((hp->lr / bc1) * -1.0);
+  s.lr_d = hp->lr;
+  s.beta1_d = hp->beta1;
+  s.beta2_d = hp->beta2;
+  return s;
+}
+
 long adam_blocks(int nt, const int64_t* numel, long* starts) {
   long b = 0;
   for (int k = 0; k < nt; ++k) {
@@ -221,6 +244,32 @@ long adam_blocks(int nt, const int64_t* numel, long* starts) {
 }
 
 }  // namespace
+
+int launch_adam_presummed(int nt, float* const* params, float* const* grads,
+                          float* const* exp_avg, float* const* exp_avg_sq, const int64_t* numel,
+                          const ppo_adam_params* hp, const double* partials,
+                          const long* part_start, float* grad_norm_out, hipStream_t stream) {
+  if (nt < 1 || nt > PPO_ADAM_MAX_TENSORS || !hp) return PPO_ERR_INVALID_ARG;
+  if ((!hp->step_counter && hp->step < 1) || !(hp->lr >= 0.0) || !(hp->eps >= 0.0))
+    return PPO_ERR_INVALID_ARG;
+  AdamTable t = {};
+  t.nt = nt;
+  for (int k = 0; k < nt; ++k) {
+    t.p[k] = params[k];
+    t.g[k] = grads[k];
+    t.m[k] = exp_avg[k];
+    t.v[k] = exp_avg_sq[k];
+    t.n[k] = numel[k];
+  }
+  for (int k = 0; k <= nt; ++k) t.part_start[k] = part_start[k];
+  const long blocks = adam_blocks(nt, numel, t.block_start);
+  if (blocks == 0) return PPO_OK;
+  if (blocks > 0x7fffffffL) return PPO_ERR_TOO_LARGE;
+  hipLaunchKernelGGL(adam_update_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, stream, t,
+                     partials, make_adam_scalars(hp), grad_norm_out, hp->step_counter);
+  return last_launch_status();
+}
+
 }  // namespace ppo
 
 extern "C" int ppo_gather_rows(const int64_t* index, int64_t B, int64_t n_src, int32_t narrays,
@@ -314,23 +363,8 @@ extern "C" int ppo_adam_clip_f32(int32_t ntensors, float* const* params, float* 
   const long blocks = adam_blocks(ntensors, numel, t.block_start);
   if (blocks == 0) return PPO_OK;
   if (blocks > 0x7fffffffL) return PPO_ERR_TOO_LARGE;
-  // Host-side scalars exactly as torch forms them: Python doubles, rounded to
-  // fp32 where the tensor op consumes them.
-  const double step = hp->step_counter ? 1.0 : (double)hp->step;  // device path recomputes
-  const double bc1 = 1.0 - pow(hp->beta1, step);
-  const double bc2 = 1.0 - pow(hp->beta2, step);
-  AdamScalars s;
-  s.max_norm = (float)hp->max_grad_norm;
-  s.clip = hp->max_grad_norm > 0.0 ? 1 : 0;
-  s.beta1_w = (float)(1.0 - hp->beta1);
-  s.beta2 = (float)hp->beta2;
-  s.one_m_beta2 = (float)(1.0 - hp->beta2);
-  s.bc2_sqrt = (float)sqrt(bc2);
-  s.eps = (float)hp->eps;
-  s.neg_step = (float)((hp->lr / bc1) * -1.0);
-  s.lr_d = hp->lr;
-  s.beta1_d = hp->beta1;
-  s.beta2_d = hp->beta2;
+  for (int k = 0; k <= ntensors; ++k) t.part_start[k] = t.block_start[k];
+  const AdamScalars s = make_adam_scalars(hp);
   double* partial = reinterpret_cast<double*>(static_cast<char*>(workspace) + kHeaderBytes);
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
   hipLaunchKernelGGL(adam_sumsq_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, stream, t,

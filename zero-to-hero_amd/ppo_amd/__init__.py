@@ -38,6 +38,7 @@ from .ops import (
     ppo_loss_gaussian,
     ppo_loss_gaussian_fused,
     ppo_mlp_cat_grads,
+    ppo_mlp_cat_step,
     sample_categorical,
     sample_gaussian,
 )
@@ -81,6 +82,7 @@ __all__ = [
     "ppo_loss_gaussian",
     "ppo_loss_gaussian_fused",
     "ppo_mlp_cat_grads",
+    "ppo_mlp_cat_step",
     "sample_categorical",
     "sample_gaussian",
 ]

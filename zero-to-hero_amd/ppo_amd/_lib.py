@@ -123,6 +123,12 @@ SIGNATURES = {
         [ctypes.POINTER(Mlp3), ctypes.POINTER(Mlp3), _i32, _i32, _i32, _i32, _vp, _i64, _vp,
          _i64, _vp, _int, _vp, _vp, _vp, _vp, ctypes.POINTER(LossParams), _vp, _vp, _sz, _vp],
     ),
+    "ppo_mlp_cat_step_f32": (
+        _int,
+        [ctypes.POINTER(Mlp3), ctypes.POINTER(Mlp3), _i32, _i32, _i32, _i32, _vp, _i64, _vp,
+         _i64, _vp, _int, _vp, _vp, _vp, _vp, ctypes.POINTER(LossParams), ctypes.POINTER(_vp),
+         ctypes.POINTER(_vp), ctypes.POINTER(AdamParams), _vp, _vp, _vp, _sz, _vp],
+    ),
     "ppo_adam_clip_workspace_bytes": (_sz, [_i32, ctypes.POINTER(_i64)]),
     "ppo_adam_clip_f32": (
         _int,

@@ -768,30 +768,11 @@ def _mlp_struct(layers: list) -> _lib.Mlp3:
     return s
 
 
-def ppo_mlp_cat_grads(
-    policy: torch.nn.Module,
-    value: torch.nn.Module,
-    observations: torch.Tensor,
-    actions: torch.Tensor,
-    old_log_probs: torch.Tensor,
-    advantages: torch.Tensor,
-    returns: torch.Tensor,
-    old_values: Optional[torch.Tensor] = None,
-    index: Optional[torch.Tensor] = None,
-    clip_ratio: float = 0.2,
-    vf_clip: Optional[float] = None,
-    value_coef: float = 0.5,
-    entropy_coef: float = 0.01,
-    scalars_out: Optional[torch.Tensor] = None,
-) -> LossStats:
-    """Forward and backward of PPOAgent._update_batch (ppo.py:141-169) for one
-    minibatch in two launches: the rows `index` (int64 [B]; None: all n rows)
-    of the rollout arrays (observations [n,D], actions [n] int32/int64,
-    old_log_probs / advantages / returns / old_values [n]) go through both
-    MLPs, the categorical PPO loss and its backward, and every parameter's
-    `.grad` is overwritten with d loss / d parameter (allocated if None).
-    Returns the loss scalars (0-d device tensors).  Both networks must satisfy
-    mlp_fusable(); follow with ClippedAdam.step()."""
+def _mlp_minibatch_args(policy, value, observations, actions, old_log_probs, advantages,
+                        returns, old_values, index, clip_ratio, vf_clip, value_coef,
+                        entropy_coef, scalars_out):
+    """Validated arguments of the fused minibatch entry points (the part of
+    their C signatures they share), the device, stream and workspace."""
     if not mlp_fusable(policy, value):
         raise ValueError("policy/value are not MLPs the fused kernel supports (see mlp_fusable)")
     lp, act = mlp_structure(policy)
@@ -829,17 +810,92 @@ def ppo_mlp_cat_grads(
     scalars = _out(scalars_out, "scalars_out", (_lib.PPO_NUM_SCALARS,), torch.float32, device)
     actor, critic = _mlp_struct(lp), _mlp_struct(lv)
     stream = _stream(device)
-    lib = _lib.load()
-    nbytes = lib.ppo_mlp_cat_grad_workspace_bytes(B, D, H, A)
+    nbytes = _lib.load().ppo_mlp_cat_grad_workspace_bytes(B, D, H, A)
     ws = _WORKSPACES.get(device, stream, nbytes)
-    _call("ppo_mlp_cat_grad_f32", device, stream, ctypes.byref(actor), ctypes.byref(critic),
-          D, H, A, _lib.PPO_ACT_TANH if act == "tanh" else _lib.PPO_ACT_RELU,
-          observations.data_ptr(), n, _ptr(index), B, actions.data_ptr(),
-          1 if actions.dtype == torch.int64 else 0, old_log_probs.data_ptr(),
-          advantages.data_ptr(), returns.data_ptr(),
-          _ptr(old_values) if vf_clip is not None else None, ctypes.byref(params),
-          scalars.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    head = (ctypes.byref(actor), ctypes.byref(critic), D, H, A,
+            _lib.PPO_ACT_TANH if act == "tanh" else _lib.PPO_ACT_RELU,
+            observations.data_ptr(), n, _ptr(index), B, actions.data_ptr(),
+            1 if actions.dtype == torch.int64 else 0, old_log_probs.data_ptr(),
+            advantages.data_ptr(), returns.data_ptr(),
+            _ptr(old_values) if vf_clip is not None else None, ctypes.byref(params))
+    # the ctypes structs must outlive the call
+    return device, stream, ws, scalars, head, (actor, critic, params)
+
+
+def ppo_mlp_cat_grads(
+    policy: torch.nn.Module,
+    value: torch.nn.Module,
+    observations: torch.Tensor,
+    actions: torch.Tensor,
+    old_log_probs: torch.Tensor,
+    advantages: torch.Tensor,
+    returns: torch.Tensor,
+    old_values: Optional[torch.Tensor] = None,
+    index: Optional[torch.Tensor] = None,
+    clip_ratio: float = 0.2,
+    vf_clip: Optional[float] = None,
+    value_coef: float = 0.5,
+    entropy_coef: float = 0.01,
+    scalars_out: Optional[torch.Tensor] = None,
+) -> LossStats:
+    """Forward and backward of PPOAgent._update_batch (ppo.py:141-169) for one
+    minibatch in two launches: the rows `index` (int64 [B]; None: all n rows)
+    of the rollout arrays (observations [n,D], actions [n] int32/int64,
+    old_log_probs / advantages / returns / old_values [n]) go through both
+    MLPs, the categorical PPO loss and its backward, and every parameter's
+    `.grad` is overwritten with d loss / d parameter (allocated if None).
+    Returns the loss scalars (0-d device tensors).  Both networks must satisfy
+    mlp_fusable(); follow with ClippedAdam.step()."""
+    device, stream, ws, scalars, head, keep = _mlp_minibatch_args(
+        policy, value, observations, actions, old_log_probs, advantages, returns, old_values,
+        index, clip_ratio, vf_clip, value_coef, entropy_coef, scalars_out)
+    _call("ppo_mlp_cat_grad_f32", device, stream, *head, scalars.data_ptr(), ws.data_ptr(),
+          ws.numel(), stream)
     return _stats_dict(scalars)
+
+
+def ppo_mlp_cat_step(
+    policy: torch.nn.Module,
+    value: torch.nn.Module,
+    optimizer,
+    observations: torch.Tensor,
+    actions: torch.Tensor,
+    old_log_probs: torch.Tensor,
+    advantages: torch.Tensor,
+    returns: torch.Tensor,
+    old_values: Optional[torch.Tensor] = None,
+    index: Optional[torch.Tensor] = None,
+    clip_ratio: float = 0.2,
+    vf_clip: Optional[float] = None,
+    value_coef: float = 0.5,
+    entropy_coef: float = 0.01,
+    scalars_out: Optional[torch.Tensor] = None,
+) -> tuple[LossStats, torch.Tensor]:
+    """ppo_mlp_cat_grads followed by optimizer.step() (a ClippedAdam over
+    list(policy.parameters()) + list(value.parameters()), in that order) as
+    three launches (ppo_mlp_cat_step_f32): the gradient reduction also
+    leaves the per-tensor sums of squares that clip_grad_norm_ needs.
+    Returns the loss scalars and the pre-clip gradient norm (0-d device
+    tensors)."""
+    from .optim import ClippedAdam
+
+    expect = list(policy.parameters()) + list(value.parameters())
+    if (not isinstance(optimizer, ClippedAdam) or len(optimizer.params) != len(expect)
+            or any(a is not b for a, b in zip(optimizer.params, expect))):
+        raise ValueError("optimizer must be a ClippedAdam over the policy's then the value "
+                         "network's parameters")
+    device, stream, ws, scalars, head, keep = _mlp_minibatch_args(
+        policy, value, observations, actions, old_log_probs, advantages, returns, old_values,
+        index, clip_ratio, vf_clip, value_coef, entropy_coef, scalars_out)
+    hp, step = optimizer._fused_params()
+    P = ctypes.c_void_p * len(expect)
+    m = P(*[t.data_ptr() for t in optimizer.exp_avg])
+    v = P(*[t.data_ptr() for t in optimizer.exp_avg_sq])
+    norm = torch.empty((), dtype=torch.float32, device=device)
+    _call("ppo_mlp_cat_step_f32", device, stream, *head, m, v, ctypes.byref(hp),
+          scalars.data_ptr(), norm.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    optimizer._advance(step)
+    return _stats_dict(scalars), norm
 
 
 def mlp_act_categorical(

@@ -79,6 +79,22 @@ class ClippedAdam:
                 else:
                     p.grad.zero_()
 
+    def _fused_params(self) -> tuple:
+        """Adam parameters for a fused step of all tensors together (the
+        gradients written by the same launch sequence) and the step number
+        it makes."""
+        if not self.capturable and len(set(self.steps)) != 1:
+            raise RuntimeError("a fused step needs every parameter at the same step count")
+        step = self.steps[0] + 1
+        hp = _lib.AdamParams(float(self.lr), float(self.betas[0]), float(self.betas[1]),
+                             float(self.eps), float(self.max_grad_norm), int(step),
+                             self.step_t.data_ptr() if self.capturable else None)
+        return hp, step
+
+    def _advance(self, step: int) -> None:
+        if not self.capturable:
+            self.steps = [step] * len(self.params)
+
     @torch.no_grad()
     def step(self) -> torch.Tensor:
         # as torch: parameters without a gradient are skipped (and keep their step)

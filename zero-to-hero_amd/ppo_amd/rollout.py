@@ -127,7 +127,9 @@ class VecPPO:
     With `fused_mlp` (default: whenever `fused_update` is on, the policy is
     categorical and both networks are MLPs that ops.mlp_fusable accepts) each
     minibatch's gather, MLP forwards, loss and backward are the two launches
-    of ops.ppo_mlp_cat_grads, which write the parameters' gradients directly.
+    of ops.ppo_mlp_cat_grads, which write the parameters' gradients directly,
+    and the clip + Adam step joins them (ops.ppo_mlp_cat_step: three
+    launches per minibatch).
 
     With `graphs=True` (requires `fused_update`) the minibatch loop is replayed
     from CUDA/HIP graphs: the whole update runs on a private stream; the
@@ -387,11 +389,11 @@ class VecPPO:
         if self.fused_mlp and arrays[0].dim() == 2:
             cfg = self.ppo_config
             obs, acts, old_lp, adv, ret, old_v = arrays
-            stats = ops.ppo_mlp_cat_grads(
-                self.policy, self.value, obs, acts, old_lp, adv, ret,
+            # gradients, clip to cfg.gradient_clip and Adam: three launches
+            stats, _ = ops.ppo_mlp_cat_step(
+                self.policy, self.value, self.optimizer, obs, acts, old_lp, adv, ret,
                 old_v if cfg.vf_clip is not None else None, idx, cfg.clip_ratio, cfg.vf_clip,
                 cfg.value_coef, cfg.entropy_coef, scalars_out=self._scalars)
-            self.optimizer.step()  # clips to cfg.gradient_clip, then Adam
             return stats
         if self.fused:
             batch = ops.gather_rows(idx, *arrays)
