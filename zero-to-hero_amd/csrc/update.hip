@@ -66,6 +66,7 @@ __global__ void __launch_bounds__(kBlock) copy_words_kernel(const T* __restrict_
 // ---------------------------------------------------------------------------
 constexpr int kAdamPerThread = 4;
 constexpr long kAdamChunk = (long)kBlock * kAdamPerThread;  // elements per block
+constexpr long kAdamLdsParts = 2048;  // sum-of-squares partials staged in LDS per round
 
 struct AdamTable {
   float* p[PPO_ADAM_MAX_TENSORS];
@@ -131,6 +132,7 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
                                                              const int64_t* step_counter) {
   __shared__ float s_coef;
   __shared__ float s_norm[PPO_ADAM_MAX_TENSORS];
+  __shared__ double s_part[kAdamLdsParts];
   // The block's elements, moments and parameters are loaded first (they do
   // not depend on the norm), so their latency overlaps the norm's.
   const long b = blockIdx.x;
@@ -152,45 +154,41 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
     pr[j] = p[ic];
   }
   if (step_counter) adam_step_scalars(s, step_counter);
-  // Global norm: per-tensor norms rounded to fp32 (lane k of wave 0 sums
-  // tensor k's partials in order), then the norm of those in
+  // Global norm: per-tensor norms rounded to fp32, then the norm of those in
   // tensor order (the two-level form of torch's _get_total_norm); every block
-  // derives the same value in the same order.
-  if (threadIdx.x < PPO_ADAM_MAX_TENSORS) {
-    const int kk = threadIdx.x;
-    float nk = 0.0f;
+  // derives the same value in the same order.  The sum-of-squares partials
+  // are staged in LDS by the whole block (one round of loads in flight),
+  // then lane kk of wave 0 sums tensor kk's in order.
+  const int kk = threadIdx.x;
+  double sk = 0.0;
+  const long total = t.part_start[t.nt];
+  for (long base = 0; base < total; base += kAdamLdsParts) {
+    const long cnt = total - base < kAdamLdsParts ? total - base : kAdamLdsParts;
+    for (long i = threadIdx.x; i < cnt; i += kBlock) s_part[i] = partial[base + i];
+    __syncthreads();
     if (kk < t.nt) {
-      // sequential sum in block order, loads batched 8 at a time
-      double sk = 0.0;
-      long c = t.part_start[kk];
-      const long ce = t.part_start[kk + 1];
-      for (; c + 8 <= ce; c += 8) {
-        double x[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = partial[c + j];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) sk += x[j];
-      }
-      for (; c < ce; ++c) sk += partial[c];
-      nk = (float)sqrt(sk);
+      const long c0 = t.part_start[kk] > base ? t.part_start[kk] : base;
+      const long c1 = t.part_start[kk + 1] < base + cnt ? t.part_start[kk + 1] : base + cnt;
+      for (long c = c0; c < c1; ++c) sk += s_part[c - base];
     }
-    s_norm[kk] = nk;
+    __syncthreads();
   }
+  if (kk < PPO_ADAM_MAX_TENSORS) s_norm[kk] = kk < t.nt ? (float)sqrt(sk) : 0.0f;
   __syncthreads();
   if (threadIdx.x == 0) {
     float total_sq = 0.0f;
-    for (int kk = 0; kk < t.nt; ++kk) {
-      const float nk = s_norm[kk];
+    for (int q = 0; q < t.nt; ++q) {
+      const float nk = s_norm[q];
       total_sq = __fadd_rn(total_sq, __fmul_rn(nk, nk));
     }
-    const float total = __fsqrt_rn(total_sq);
+    const float norm = __fsqrt_rn(total_sq);
     float coef = 1.0f;
     if (s.clip) {
-      const float c = __fdiv_rn(s.max_norm, __fadd_rn(total, 1e-6f));
+      const float c = __fdiv_rn(s.max_norm, __fadd_rn(norm, 1e-6f));
       coef = c < 1.0f ? c : 1.0f;
     }
     s_coef = coef;
-    if (blockIdx.x == 0 && norm_out) *norm_out = total;
+    if (blockIdx.x == 0 && norm_out) *norm_out = norm;
   }
   __syncthreads();
   const float coef = s_coef;
