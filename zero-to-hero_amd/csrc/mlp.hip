@@ -50,6 +50,7 @@ struct MlpNet {
   const float* b[3];
   float* gw[3];
   float* gb[3];
+  int ldw[3];  // row stride of w[l] in floats (its input count in global memory)
 };
 
 // Offsets of one network's tensors inside a flat gradient partial.
@@ -130,13 +131,13 @@ constexpr int kZld = kMlpMaxA + 2;    // logits / dlogits [16][kZld]
 // values are then loaded in one batch.
 template <int KC, int kAct>
 __device__ __forceinline__ void fwd_tile(const float* in, int ldin, int K,
-                                         const float* __restrict__ W,
+                                         const float* __restrict__ W, int ldw,
                                          const float* __restrict__ b, int N, float* out,
                                          int ldout, int tj) {
   const int l = threadIdx.x % kWave, i = l % 16, kk = l / 16;
   const int n = 16 * tj + i;
   const bool nok = n < N;
-  const float* wrow = W + (long)(nok ? n : 0) * K;
+  const float* wrow = W + (long)(nok ? n : 0) * ldw;
   v4f c = {0.0f, 0.0f, 0.0f, 0.0f};
   if constexpr (KC > 0) {
     // contraction order permuted so that each lane's weights are contiguous:
@@ -180,7 +181,7 @@ __device__ __forceinline__ void fwd_tile(const float* in, int ldin, int K,
 // time (0: runtime M).  W rows are read along k: coalesced.
 template <int H, int MC, int kAct>
 __device__ __forceinline__ void back_tile(const float* d, int ldd, int M,
-                                          const float* __restrict__ W, const float* h,
+                                          const float* __restrict__ W, int ldw, const float* h,
                                           float* gin, int tj) {
   constexpr int ld = act_ld<H>();
   const int l = threadIdx.x % kWave, i = l % 16, kk = l / 16;
@@ -189,14 +190,14 @@ __device__ __forceinline__ void back_tile(const float* d, int ldd, int M,
   if constexpr (MC > 0) {
     float bw[MC / 4];
 #pragma unroll
-    for (int q = 0; q < MC / 4; ++q) bw[q] = W[(long)(4 * q + kk) * H + col];
+    for (int q = 0; q < MC / 4; ++q) bw[q] = W[(long)(4 * q + kk) * ldw + col];
 #pragma unroll
     for (int q = 0; q < MC / 4; ++q) c = mfma4(d[i * ldd + 4 * q + kk], bw[q], c);
   } else {
     for (int m0 = 0; m0 < M; m0 += 4) {
       const int m = m0 + kk;
       const float av = m < M ? d[i * ldd + m] : 0.0f;
-      const float bv = m < M ? W[(long)m * H + col] : 0.0f;
+      const float bv = m < M ? W[(long)m * ldw + col] : 0.0f;
       c = mfma4(av, bv, c);
     }
   }
@@ -261,14 +262,14 @@ __device__ __forceinline__ void net_backward(const MlpNet& net, const NetOffsets
   // phase 1
   for (int t = w; t < MT3 * NT + NT; t += kWaves) {
     if (t < MT3 * NT) wgrad_tile(d3, ld3, M3, h2, ld, H, gp + o.w[2], t / NT, t % NT);
-    else back_tile<H, 0, kAct>(d3, ld3, M3, net.w[2], h2, g2, t - MT3 * NT);
+    else back_tile<H, 0, kAct>(d3, ld3, M3, net.w[2], net.ldw[2], h2, g2, t - MT3 * NT);
   }
   bgrad(d3, ld3, M3, gp + o.b[2]);
   lds_barrier();
   // phase 2
   for (int t = w; t < NT * NT + NT; t += kWaves) {
     if (t < NT * NT) wgrad_tile(g2, ld, H, h1, ld, H, gp + o.w[1], t / NT, t % NT);
-    else back_tile<H, H, kAct>(g2, ld, H, net.w[1], h1, g1, t - NT * NT);
+    else back_tile<H, H, kAct>(g2, ld, H, net.w[1], net.ldw[1], h1, g1, t - NT * NT);
   }
   bgrad(g2, ld, H, gp + o.b[1]);
   lds_barrier();
@@ -293,21 +294,86 @@ __device__ __forceinline__ void mlp_forward(const MlpNet& actor, const MlpNet& c
   const int w = threadIdx.x / kWave;
   for (int t = w; t < 2 * NT; t += kWaves) {
     const MlpNet& net = t < NT ? actor : critic;
-    fwd_tile<0, kAct>(x, kXld, D, net.w[0], net.b[0], H, t < NT ? a1 : c1, ld, t % NT);
+    fwd_tile<0, kAct>(x, kXld, D, net.w[0], net.ldw[0], net.b[0], H, t < NT ? a1 : c1, ld,
+                      t % NT);
   }
   lds_barrier();
   for (int t = w; t < 2 * NT; t += kWaves) {
     const MlpNet& net = t < NT ? actor : critic;
-    fwd_tile<H, kAct>(t < NT ? a1 : c1, ld, H, net.w[1], net.b[1], H, t < NT ? a2 : c2, ld,
+    fwd_tile<H, kAct>(t < NT ? a1 : c1, ld, H, net.w[1], net.ldw[1], net.b[1], H,
+                      t < NT ? a2 : c2, ld,
                       t % NT);
   }
   lds_barrier();
   const int AT = (A + 15) / 16;
   for (int t = w; t < AT + 1; t += kWaves) {
-    if (t < AT) fwd_tile<H, -1>(a2, ld, H, actor.w[2], actor.b[2], A, z, kZld, t);
-    else fwd_tile<H, -1>(c2, ld, H, critic.w[2], critic.b[2], 1, v, 1, 0);
+    if (t < AT) fwd_tile<H, -1>(a2, ld, H, actor.w[2], actor.ldw[2], actor.b[2], A, z, kZld, t);
+    else fwd_tile<H, -1>(c2, ld, H, critic.w[2], critic.ldw[2], critic.b[2], 1, v, 1, 0);
   }
   lds_barrier();
+}
+
+// LDS copy of one network's weights and biases, read by every tile of
+// every layer instead of global memory (H <= 64: it then fits beside the
+// activations).  Rows are padded: layer 0 to D + 1 floats (the scalar
+// first-layer reads of a tile's 16 rows fall in distinct banks), layers 1-2
+// to H + 4 (float4 rows stay 16-byte aligned and a tile's rows start in
+// different banks).  The copy is complete after the caller's next barrier.
+template <int H>
+constexpr int net_lds_floats() {
+  return H * (kMlpMaxIn + 1) + H + H * (H + 4) + H + kMlpMaxA * (H + 4) + kMlpMaxA;
+}
+constexpr int kMlpLdsMaxH = 64;  // largest hidden size whose weights are staged
+
+template <int H>
+__device__ __forceinline__ MlpNet stage_net(const MlpNet& g, int D, int O, float* lds) {
+  constexpr int ld1 = H + 4;
+  const int ld0 = D + 1;
+  float* w0 = lds;
+  float* b0 = w0 + H * (kMlpMaxIn + 1);
+  float* w1 = b0 + H;
+  float* b1 = w1 + H * ld1;
+  float* w2 = b1 + H;
+  float* b2 = w2 + kMlpMaxA * ld1;
+  constexpr int kW1Iters = (H * H / 4 + kMlpBlock - 1) / kMlpBlock;
+  float4 t1[kW1Iters];
+#pragma unroll
+  for (int q = 0; q < kW1Iters; ++q) {
+    const int e4 = threadIdx.x + q * kMlpBlock;
+    t1[q] = e4 < H * H / 4 ? reinterpret_cast<const float4*>(g.w[1])[e4]
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  for (int e = threadIdx.x; e < H * D; e += kMlpBlock) {
+    const int r = e / D, c = e - r * D;
+    w0[r * ld0 + c] = g.w[0][e];
+  }
+  for (int e4 = threadIdx.x; e4 < O * H / 4; e4 += kMlpBlock) {
+    const int r = (4 * e4) / H, c = 4 * e4 - r * H;
+    *reinterpret_cast<float4*>(w2 + r * ld1 + c) = reinterpret_cast<const float4*>(g.w[2])[e4];
+  }
+  if (threadIdx.x < H) {
+    b0[threadIdx.x] = g.b[0][threadIdx.x];
+    b1[threadIdx.x] = g.b[1][threadIdx.x];
+  }
+  if (threadIdx.x < O) b2[threadIdx.x] = g.b[2][threadIdx.x];
+#pragma unroll
+  for (int q = 0; q < kW1Iters; ++q) {
+    const int e4 = threadIdx.x + q * kMlpBlock;
+    if (e4 < H * H / 4) {
+      const int r = (4 * e4) / H, c = 4 * e4 - r * H;
+      *reinterpret_cast<float4*>(w1 + r * ld1 + c) = t1[q];
+    }
+  }
+  MlpNet n = g;
+  n.w[0] = w0;
+  n.w[1] = w1;
+  n.w[2] = w2;
+  n.b[0] = b0;
+  n.b[1] = b1;
+  n.b[2] = b2;
+  n.ldw[0] = ld0;
+  n.ldw[1] = n.ldw[2] = ld1;
+  return n;
 }
 
 // Forward of one network for the workgroup's 16 rows (observations in x):
@@ -321,12 +387,14 @@ __device__ __forceinline__ void net_forward(const MlpNet& net, const float* x, i
   constexpr int NT = H / 16;
   constexpr int kWaves = kMlpBlock / kWave;
   const int w = threadIdx.x / kWave;
-  for (int t = w; t < NT; t += kWaves) fwd_tile<0, kAct>(x, kXld, D, net.w[0], net.b[0], H, h1, ld, t);
+  for (int t = w; t < NT; t += kWaves)
+    fwd_tile<0, kAct>(x, kXld, D, net.w[0], net.ldw[0], net.b[0], H, h1, ld, t);
   lds_barrier();
-  for (int t = w; t < NT; t += kWaves) fwd_tile<H, kAct>(h1, ld, H, net.w[1], net.b[1], H, h2, ld, t);
+  for (int t = w; t < NT; t += kWaves)
+    fwd_tile<H, kAct>(h1, ld, H, net.w[1], net.ldw[1], net.b[1], H, h2, ld, t);
   lds_barrier();
   for (int t = w; t < (O + 15) / 16; t += kWaves)
-    fwd_tile<H, -1>(h2, ld, H, net.w[2], net.b[2], O, out, ldout, t);
+    fwd_tile<H, -1>(h2, ld, H, net.w[2], net.ldw[2], net.b[2], O, out, ldout, t);
   lds_barrier();
 }
 
@@ -354,6 +422,11 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   const long blk = (long)(blockIdx.x >> 1);
   const long row0 = blk * R;
   const int D = a.D, A = a.A;
+  // this workgroup's network, its weights staged in LDS when they fit
+  constexpr bool kStage = H <= kMlpLdsMaxH;
+  __shared__ __attribute__((aligned(16))) float s_w[kStage ? net_lds_floats<H>() : 1];
+  MlpNet net = critic ? a.critic : a.actor;
+  if constexpr (kStage) net = stage_net<H>(net, D, critic ? 1 : A, s_w);
   // the loss inputs of row `tid` (tid < R) are loaded now, ahead of the
   // forward pass that precedes their use
   RowIn rin = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
@@ -382,8 +455,8 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   }
   lds_barrier();
 
-  if (critic) net_forward<H, kAct>(a.critic, s_x, D, 1, s_h1, s_h2, s_v, 1);
-  else net_forward<H, kAct>(a.actor, s_x, D, A, s_h1, s_h2, s_z, kZld);
+  if (critic) net_forward<H, kAct>(net, s_x, D, 1, s_h1, s_h2, s_v, 1);
+  else net_forward<H, kAct>(net, s_x, D, A, s_h1, s_h2, s_z, kZld);
 
   // loss rows: logits -> dlogits in place (actor), value -> dvalue in place
   // (critic; the value terms do not depend on the log-prob, which is given
@@ -426,8 +499,8 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   }
 
   float* gp = a.gpart + blk * a.P;
-  if (critic) net_backward<H, kAct>(a.critic, a.oc, gp, s_v, 1, 1, s_x, D, s_h1, s_h2, s_g1, s_g2);
-  else net_backward<H, kAct>(a.actor, a.oa, gp, s_z, kZld, A, s_x, D, s_h1, s_h2, s_g1, s_g2);
+  if (critic) net_backward<H, kAct>(net, a.oc, gp, s_v, 1, 1, s_x, D, s_h1, s_h2, s_g1, s_g2);
+  else net_backward<H, kAct>(net, a.oa, gp, s_z, kZld, A, s_x, D, s_h1, s_h2, s_g1, s_g2);
 }
 
 // Action selection through both networks (ppo.py:65-79 for N observations):
@@ -522,6 +595,15 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cartpole_rollout_kernel(Rollout
   __shared__ float s_a1[R * ld], s_a2[R * ld], s_c1[R * ld], s_c2[R * ld];
   __shared__ float s_z[R * kZld];
   __shared__ float s_v[R];
+  // both networks' weights staged in LDS once for all T steps, when they fit
+  constexpr bool kStage = H <= kMlpLdsMaxH;
+  __shared__ __attribute__((aligned(16))) float s_wa[kStage ? net_lds_floats<H>() : 1];
+  __shared__ __attribute__((aligned(16))) float s_wc[kStage ? net_lds_floats<H>() : 1];
+  MlpNet actor = a.actor, critic = a.critic;
+  if constexpr (kStage) {
+    actor = stage_net<H>(a.actor, D, kCartpoleActions, s_wa);
+    critic = stage_net<H>(a.critic, D, 1, s_wc);
+  }
   const int tid = threadIdx.x;
   const long row0 = (long)blockIdx.x * R;
   const long n = row0 + tid;
@@ -556,8 +638,8 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cartpole_rollout_kernel(Rollout
 #pragma unroll
       for (int k = 0; k < D; ++k) a.obs_buf[((long)t * a.N + n) * D + k] = s_x[tid * kXld + k];
     }
-    mlp_forward<H, kAct>(a.actor, a.critic, s_x, D, kCartpoleActions, s_a1, s_a2, s_c1, s_c2,
-                         s_z, s_v);
+    mlp_forward<H, kAct>(actor, critic, s_x, D, kCartpoleActions, s_a1, s_a2, s_c1, s_c2, s_z,
+                         s_v);
     if (mine) {
       int act;
       float lp;
@@ -756,7 +838,7 @@ bool mlp_net_ok(const ppo_mlp3_f32* n) {
   return true;
 }
 
-MlpNet to_net(const ppo_mlp3_f32* n) {
+MlpNet to_net(const ppo_mlp3_f32* n, int D, int H) {
   MlpNet m;
   for (int l = 0; l < 3; ++l) {
     m.w[l] = n->weight[l];
@@ -764,6 +846,8 @@ MlpNet to_net(const ppo_mlp3_f32* n) {
     m.gw[l] = n->weight_grad[l];
     m.gb[l] = n->bias_grad[l];
   }
+  m.ldw[0] = D;
+  m.ldw[1] = m.ldw[2] = H;
   return m;
 }
 
@@ -811,8 +895,8 @@ int mlp_setup(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic, int32_t obs
   l = mlp_layout(B, obs_dim, hidden, A);
   char* ws = static_cast<char*>(workspace);
   a = MlpArgs{};
-  a.actor = to_net(actor);
-  a.critic = to_net(critic);
+  a.actor = to_net(actor, obs_dim, hidden);
+  a.critic = to_net(critic, obs_dim, hidden);
   a.oa = net_offsets(0, obs_dim, hidden, A);
   a.oc = net_offsets(mlp_params(obs_dim, hidden, A), obs_dim, hidden, 1);
   a.D = obs_dim;
@@ -949,8 +1033,8 @@ extern "C" int ppo_mlp_act_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32
     return PPO_ERR_INVALID_ARG;
   if (N > (1L << 31)) return PPO_ERR_TOO_LARGE;
   ActArgs a = {};
-  a.actor = to_net(actor);
-  a.critic = to_net(critic);
+  a.actor = to_net(actor, obs_dim, hidden);
+  a.critic = to_net(critic, obs_dim, hidden);
   a.D = obs_dim;
   a.A = A;
   a.obs = observations;
@@ -992,8 +1076,8 @@ extern "C" int ppo_cartpole_rollout_f32(
   if (action_uniforms_stride < N || reset_uniforms_stride < 4 * N) return PPO_ERR_INVALID_ARG;
   if (N > (1L << 31) || (long)T * N > (1L << 40)) return PPO_ERR_TOO_LARGE;
   RolloutArgs a = {};
-  a.actor = to_net(actor);
-  a.critic = to_net(critic);
+  a.actor = to_net(actor, kCartpoleObs, hidden);
+  a.critic = to_net(critic, kCartpoleObs, hidden);
   a.N = N;
   a.T = T;
   a.max_steps = max_steps;
