@@ -153,27 +153,57 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
     vr[j] = v[ic];
     pr[j] = p[ic];
   }
-  if (step_counter) adam_step_scalars(s, step_counter);
   // Global norm: per-tensor norms rounded to fp32, then the norm of those in
   // tensor order (the two-level form of torch's _get_total_norm); every block
   // derives the same value in the same order.  The sum-of-squares partials
-  // are staged in LDS by the whole block (one round of loads in flight),
-  // then lane kk of wave 0 sums tensor kk's in order.
-  const int kk = threadIdx.x;
-  double sk = 0.0;
+  // are staged in LDS by the whole block (their first round loaded with the
+  // elements above), then wave w sums tensors w, w + 4, ...: lane l takes
+  // partials l, l + 64, ... of the tensor and the wave's lanes are combined by
+  // a fixed shuffle tree.
+  constexpr int kPre = kAdamLdsParts / kBlock;
   const long total = t.part_start[t.nt];
+  double pre[kPre];
+#pragma unroll
+  for (int q = 0; q < kPre; ++q) {
+    const long i = threadIdx.x + (long)q * kBlock;
+    pre[q] = i < total && i < kAdamLdsParts ? partial[i] : 0.0;
+  }
+  if (step_counter) adam_step_scalars(s, step_counter);
+  const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
+  constexpr int kWavesA = kBlock / kWave;
+  constexpr int kPerWave = (PPO_ADAM_MAX_TENSORS + kWavesA - 1) / kWavesA;
+  double acc[kPerWave];
+#pragma unroll
+  for (int u = 0; u < kPerWave; ++u) acc[u] = 0.0;
   for (long base = 0; base < total; base += kAdamLdsParts) {
     const long cnt = total - base < kAdamLdsParts ? total - base : kAdamLdsParts;
-    for (long i = threadIdx.x; i < cnt; i += kBlock) s_part[i] = partial[base + i];
+    if (base == 0) {
+#pragma unroll
+      for (int q = 0; q < kPre; ++q) {
+        const long i = threadIdx.x + (long)q * kBlock;
+        if (i < cnt) s_part[i] = pre[q];
+      }
+    } else {
+      for (long i = threadIdx.x; i < cnt; i += kBlock) s_part[i] = partial[base + i];
+    }
     __syncthreads();
-    if (kk < t.nt) {
-      const long c0 = t.part_start[kk] > base ? t.part_start[kk] : base;
-      const long c1 = t.part_start[kk + 1] < base + cnt ? t.part_start[kk + 1] : base + cnt;
-      for (long c = c0; c < c1; ++c) sk += s_part[c - base];
+#pragma unroll
+    for (int u = 0; u < kPerWave; ++u) {
+      const int kk = wv + u * kWavesA;
+      if (kk < t.nt) {
+        const long c0 = t.part_start[kk] > base ? t.part_start[kk] : base;
+        const long c1 = t.part_start[kk + 1] < base + cnt ? t.part_start[kk + 1] : base + cnt;
+        for (long c = c0 + lane; c < c1; c += kWave) acc[u] += s_part[c - base];
+      }
     }
     __syncthreads();
   }
-  if (kk < PPO_ADAM_MAX_TENSORS) s_norm[kk] = kk < t.nt ? (float)sqrt(sk) : 0.0f;
+#pragma unroll
+  for (int u = 0; u < kPerWave; ++u) {
+    const int kk = wv + u * kWavesA;
+    const double sk = wave_sum(acc[u]);
+    if (lane == 0 && kk < PPO_ADAM_MAX_TENSORS) s_norm[kk] = kk < t.nt ? (float)sqrt(sk) : 0.0f;
+  }
   __syncthreads();
   if (threadIdx.x == 0) {
     float total_sq = 0.0f;
