@@ -152,6 +152,44 @@ def test_gae_config3_full_size(dev):
     assert exact > 0.99
 
 
+def test_gae_normalize_over_2_30_elements(dev):
+    """T = N = 32768 (2^30 elements, ~25 GB on the device): the strip walk
+    declines (its offsets are 32-bit) and the tile passes run with 64-bit
+    offsets.  Inputs are drawn on the device; 16 env columns (env columns are
+    independent) are checked against the C oracle to the usual ulp bar, the
+    returns bit-exactly, the normaliser's mean/std against an fp64 reduction
+    of the advantages (relative 1e-6) and adv_n bit-exactly against the fp32
+    formula at the returned statistics."""
+    T = N = 32768
+    print(f"gae_normalize T={T} N={N}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(77)
+    r = torch.randn(T, N, device=dev, generator=g)
+    v = torch.randn(T, N, device=dev, generator=g)
+    d = (torch.rand(T, N, device=dev, generator=g) < 0.01).to(torch.uint8)
+    lv = torch.randn(N, device=dev, generator=g)
+    adv, ret, adv_n, stats = ppo_amd.gae_normalize(r, v, d, lv, 0.99, 0.95, return_stats=True)
+    cols = torch.tensor([0, 1, 5, 1023, 4096, 9999, 16383, 16384, 20000, 24575, 30001, 32000,
+                         32764, 32765, 32766, 32767], device=dev)
+    rc, vc, dc = (x.index_select(1, cols).cpu().numpy() for x in (r, v, d))
+    a_ref, _ = ref.gae_c(rc, vc, dc, lv.index_select(0, cols).cpu().numpy(), 0.99, 0.95)
+    a_got = adv.index_select(1, cols)
+    exact = assert_gae_close(a_got.cpu().numpy(), a_ref)
+    assert exact > 0.99
+    assert torch.equal(ret.index_select(1, cols), a_got + v.index_select(1, cols))
+    s1 = s2 = 0.0
+    for k in range(0, T, 4096):  # fp64 moments in slices (an fp64 copy would be 8 GB)
+        x = adv[k:k + 4096].double()
+        s1 += float(x.sum())
+        s2 += float((x * x).sum())
+    n = float(T * N)
+    mean = s1 / n
+    std = ((s2 - s1 * mean) / (n - 1)) ** 0.5
+    assert stats[0].item() == pytest.approx(mean, rel=1e-6, abs=1e-7)
+    assert stats[1].item() == pytest.approx(std, rel=1e-6)
+    want_n = (a_got - stats[0]) / (stats[1] + torch.tensor(1e-8, device=dev))
+    assert torch.equal(adv_n.index_select(1, cols), want_n)
+
+
 def test_gae_multi_round_chunk_fold(dev):
     """T=262144, N=64: 4096 tiles in 32 carry chunks, more than one block's
     rows, so the later-chunk fold takes two rounds."""
