@@ -154,7 +154,7 @@ def test_gae_config3_full_size(dev):
 
 def test_gae_normalize_over_2_30_elements(dev):
     """T = N = 32768 (2^30 elements, ~25 GB on the device): the strip walk
-    declines (its offsets are 32-bit) and the tile passes run with 64-bit
+    declines (its offsets are 32-bit) and the span passes run with 64-bit
     offsets.  Inputs are drawn on the device; 16 env columns (env columns are
     independent) are checked against the C oracle to the usual ulp bar, the
     returns bit-exactly, the normaliser's mean/std against an fp64 reduction
@@ -323,3 +323,80 @@ def test_gae_normalize_strip_walk_matches_separate_ops(dev):
     torch.testing.assert_close(adv_n, ppo_amd.normalize_advantages(adv2), rtol=1e-6, atol=1e-7)
     n_ref = ref.normalize_reference(adv2.cpu().reshape(-1)).reshape(T, N)
     torch.testing.assert_close(adv_n.cpu(), n_ref, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Span passes (aligned rollouts narrower than the strip walk): strips of
+# E = 4..64 envs, 4096-element tiles, spans of tiles composed right to left.
+# ---------------------------------------------------------------------------
+def _gae_abi(dev, r, v, d, lv, gamma, lam, norm=False, fill=0xAB):
+    """ppo_gae_f32 / ppo_gae_norm_f32 through the C ABI with a fresh workspace
+    filled with `fill` (its contents on entry must not matter)."""
+    from ppo_amd import _lib
+
+    lib = _lib.load()
+    T, N = r.shape
+    ws = torch.full((lib.ppo_gae_workspace_bytes(T, N),), fill, dtype=torch.uint8, device=dev)
+    adv, ret, adv_n = (torch.empty(T, N, device=dev) for _ in range(3))
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    lvp = None if lv is None else lv.data_ptr()
+    if norm:
+        rc = lib.ppo_gae_norm_f32(r.data_ptr(), v.data_ptr(), d.data_ptr(), lvp, T, N, gamma, lam,
+                                  1e-8, adv.data_ptr(), ret.data_ptr(), adv_n.data_ptr(), None,
+                                  ws.data_ptr(), ws.numel(), stream)
+    else:
+        rc = lib.ppo_gae_f32(r.data_ptr(), v.data_ptr(), d.data_ptr(), lvp, T, N, gamma, lam,
+                             adv.data_ptr(), ret.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+    assert rc == 0
+    torch.cuda.synchronize(dev)
+    return adv, ret, adv_n
+
+
+@pytest.mark.parametrize(
+    "T,N,p",
+    [
+        (4096, 4, 0.01),     # E=4: 1024-step tiles, one strip
+        (1500, 8, 0.02),     # E=8, partial last tile
+        (10_000, 16, 0.005), # E=16 (config 3's geometry), 40 tiles
+        (3000, 32, 0.01),    # E=32
+        (777, 96, 0.05),     # E=32, three strips
+        (4000, 64, 0.001),   # E=64
+        (129, 1984, 0.02),   # E=64, 31 strips, partial tiles
+        (50, 1020, 0.1),     # E=4, 255 strips, one short tile each
+        (1, 16, 0.0),        # one step
+        (3_000_000, 4, 0.0005),  # spans of many tiles
+        (1 << 20, 16, 0.001),    # config 3's shape without the normaliser
+    ],
+)
+def test_gae_span_matches_oracle(dev, T, N, p):
+    """With the normaliser every aligned rollout narrower than the strip walk
+    takes the span passes; without it the narrow (N < 64), large ones do."""
+    r, v, d, lv = _inputs(T, N, p, seed=T + 31 * N)
+    a_ref, _ = ref.gae_c(r.numpy(), v.numpy(), d.numpy(), lv.numpy(), 0.99, 0.95)
+    for norm in (True, False):
+        print(f"gae span T={T} N={N} p={p} norm={norm}", flush=True)
+        adv, ret, adv_n = _gae_abi(dev, r.to(dev), v.to(dev), d.to(dev), lv.to(dev), 0.99, 0.95,
+                                   norm=norm)
+        assert_gae_close(adv.cpu().numpy(), a_ref)
+        np.testing.assert_array_equal(ret.cpu().numpy(), adv.cpu().numpy() + v.numpy())
+        if norm:
+            torch.testing.assert_close(adv_n, ppo_amd.normalize_advantages(adv), rtol=1e-6,
+                                       atol=1e-7)
+
+
+def test_gae_span_normalize_matches_separate_ops(dev):
+    T, N = 20_000, 24
+    r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.01, seed=12))
+    print(f"gae span norm T={T} N={N}", flush=True)
+    adv, ret, adv_n = _gae_abi(dev, r, v, d, lv, 0.995, 0.9, norm=True)
+    a_ref, _ = ref.gae_c(r.cpu().numpy(), v.cpu().numpy(), d.cpu().numpy(), lv.cpu().numpy(),
+                         0.995, 0.9)
+    assert_gae_close(adv.cpu().numpy(), a_ref)
+    torch.testing.assert_close(adv_n, ppo_amd.normalize_advantages(adv), rtol=1e-6, atol=1e-7)
+
+
+def test_gae_span_workspace_contents_do_not_matter(dev):
+    T, N = 65_536, 16
+    r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.001, seed=13))
+    outs = [_gae_abi(dev, r, v, d, lv, 0.999, 0.95, fill=f)[0] for f in (0x00, 0xFF, 0x7F)]
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])

@@ -74,6 +74,7 @@ struct GaeArgs {
   double eps;
   long Q, Tq, Tt, span;
   int Qw, Sw;
+  long nstrips, spans, span_tiles;  // span passes: env strips, spans per strip, tiles per span
 };
 
 // What a gae_tile_kernel launch computes.
@@ -225,6 +226,35 @@ StripPlan strip_plan(const GaePlan& p) {
   return sp;
 }
 
+#ifndef PPO_GAE_SPAN
+#define PPO_GAE_SPAN 1  // build-time switch: 0 keeps narrow rollouts on the tile passes
+#endif
+// Span geometry (gae_span_*_kernel): strips of E envs (the largest power of
+// two <= 64 dividing N), time tiles of 16 * 256/E steps (4096 elements), and
+// about `blocks` workgroups in all, each owning a span of `tps` consecutive
+// tiles of one strip.
+constexpr long kSpanMaxBlocks = 2048;
+
+struct SpanPlan {
+  int E;        // envs per strip (0: not applicable)
+  long nstrips, tt, tps, spans;  // strips, time tiles, tiles per span, spans per strip
+};
+
+SpanPlan span_plan(long T, long N, long blocks) {
+  SpanPlan c = {0, 0, 0, 0, 0};
+  if (T <= 0 || N <= 0 || N % 4 != 0) return c;
+  int E = 64;
+  while (N % E != 0) E >>= 1;
+  const long S = 16L * (256 / E);
+  c.nstrips = N / E;
+  c.tt = (T + S - 1) / S;
+  const long per_strip = std::max(1L, std::min(c.tt, blocks / c.nstrips));
+  c.tps = (c.tt + per_strip - 1) / per_strip;
+  c.spans = (c.tt + c.tps - 1) / c.tps;
+  if (c.nstrips * c.spans <= 0x7fffffffL) c.E = E;
+  return c;
+}
+
 struct GaeLayout {
   size_t summary, carry, chunk_sum, tstat, partial, total;
 };
@@ -232,19 +262,25 @@ struct GaeLayout {
 GaeLayout make_layout(const GaePlan& p, long N) {
   GaeLayout l;
   size_t off = kHeaderBytes;
-  l.summary = off;
-  off += align_up((size_t)p.Tt * N * sizeof(double2), 256);
+  l.summary = off;  // tile composites [Tt][N], or the span composites [spans][N]
+  {
+    const SpanPlan sp = span_plan(p.T, N, kSpanMaxBlocks);
+    off += align_up(std::max<size_t>((size_t)p.Tt * N, (size_t)sp.spans * N) * sizeof(double2), 256);
+  }
+  const long ncarry = std::max(p.Tt, span_plan(p.T, N, kSpanMaxBlocks).spans);
   l.carry = off;
-  off += align_up((size_t)p.Tt * N * sizeof(double), 256);
+  off += align_up((size_t)ncarry * N * sizeof(double), 256);
   l.chunk_sum = off;
-  off += align_up((size_t)make_carry_plan(p.Tt, N).nchunks * N * sizeof(double2), 256);
+  off += align_up((size_t)std::max(make_carry_plan(p.Tt, N).nchunks,
+                                   make_carry_plan(ncarry, N).nchunks) * N * sizeof(double2), 256);
   l.tstat = off;
   off += align_up((size_t)5 * p.Tt * N * sizeof(float), 256);
   l.partial = off;
   {
     const CarryPlan cp = make_carry_plan(p.Tt, N);
+    const SpanPlan sp = span_plan(p.T, N, kSpanMaxBlocks);
     const long parts = std::max<long>(std::max<long>(p.blocks(), cp.groups * cp.nchunks),
-                                      strip_plan(p).strips);
+                                      std::max<long>(strip_plan(p).strips, sp.nstrips * sp.spans));
     off += align_up((size_t)parts * 4 * sizeof(double), 256);
   }
   l.total = off;
@@ -1140,6 +1176,357 @@ __global__ void __launch_bounds__(kStripBlock) gae_strip_kernel(GaeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Narrow rollouts: span passes.
+// ---------------------------------------------------------------------------
+// Aligned rollouts too narrow for the strip walk (N % 4 == 0).  The env
+// columns are cut into strips of E envs (SpanPlan) and time into tiles of
+// S = 16 * 256/E steps, so a tile is 4096 elements, handled by a 256-thread
+// workgroup as 16 consecutive steps of one env per thread (thread = segment
+// s, env e).  A tile's rows are contiguous runs of E floats: they are loaded
+// with coalesced float4 / 32-bit loads into LDS (one empty row after every
+// 16, so the segments of a wave read different banks) and the outputs leave
+// the same way.  Each workgroup owns a span of consecutive tiles of one strip
+// (about three spans per CU):
+//   1. gae_span_sum_kernel walks its span and leaves the span's composite
+//      (a, P) per env: the advantage at the span's first step is a + P * x
+//      for the advantage x entering it from the right;
+//   2. the tile passes' carry scan (gae_carry_kernel) turns the span
+//      composites, laid out [spans][N], into the advantage entering each span;
+//   3. gae_span_final_kernel walks its span right to left from that carry: per tile the segment composites, a
+//      reverse scan (lane shuffles, then the waves' composites), the carry
+//      of every segment, and the exact serial recurrence in fp64 with the
+//      reference's operation order.  The tile's composite applied to its
+//      carry is the carry of the tile to its left.
+// Both passes read the rollout; the second read mostly hits the 256 MB
+// Infinity Cache, which the first pass's ordinary (temporal) loads filled.
+// (Single passes chaining tiles by a decoupled look-back -- fp64 values
+// published by agent-scope atomic stores, polled by atomic loads -- measured
+// 1.5-2.7x slower than these passes on MI355X: with HBM saturated by the
+// streams, each hop of the carry front costs microseconds, and the tiles'
+// waits, 11-20 us each in a trace of 4096-element tiles, held their CUs.
+// Persistent workgroups prefetching their next tile did not hide it.)
+constexpr int kSpanThreads = 256;
+constexpr int kSpanL = 16;
+constexpr int kSpanWaves = kSpanThreads / kWave;
+
+template <int E>
+struct SpanShared {
+  static constexpr int SEG = kSpanThreads / E;  // segments per tile
+  static constexpr int S = SEG * kSpanL;        // steps per tile
+  static constexpr int R = S + S / 16 + 1;      // padded rows + the next-value row
+  float r[R * E];                               // rewards, then advantages
+  float v[R * E];                               // values, then returns
+  uint8_t d[R * E];                             // done bytes
+  double2 wc[kSpanWaves][E];                    // wave composites per env
+  double x[E];                                  // carry entering the tile
+};
+
+// LDS row of tile row t: one empty row after every 16.
+__device__ __forceinline__ int span_row(int t) { return t + (t >> 4); }
+
+// One tile's rows in registers (F float4 of rewards and values, F words of
+// done bytes per thread) plus the value after the tile.
+template <int E>
+struct SpanRegs {
+  static constexpr int F = SpanShared<E>::S * (E / 4) / kSpanThreads;
+  f4 r[F], v[F];
+  unsigned d[F];
+  float nvt;
+};
+
+// Loads of time tile `tile` of the strip at col0 (unconditional: rows past
+// the horizon re-read the tile's first row).
+template <int E, bool kHasV>
+__device__ __forceinline__ void span_load(const GaeArgs& a, long tile, long col0,
+                                          SpanRegs<E>& x) {
+  constexpr int S = SpanShared<E>::S, G4 = E / 4;
+  const long t0 = tile * S;
+  const int nrows = (int)std::min<long>(S, a.T - t0);
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < SpanRegs<E>::F; ++k) {
+    const int f = tid + k * kSpanThreads;
+    const int row = f / G4, q = f % G4;
+    const long off = (row < nrows ? t0 + row : t0) * a.N + col0 + q * 4;
+    x.r[k] = ld(reinterpret_cast<const f4*>(a.r + off));
+    if constexpr (kHasV) x.v[k] = ld(reinterpret_cast<const f4*>(a.v + off));
+    x.d[k] = ld(reinterpret_cast<const unsigned*>(a.d + off));
+  }
+  x.nvt = 0.0f;
+  if constexpr (kHasV) {
+    const long tn = t0 + S;
+    x.nvt = ld(a.v + (tn < a.T ? tn * a.N : 0) + col0 + (tid % E));
+  }
+}
+
+template <int E, bool kHasV>
+__device__ __forceinline__ void span_stage(SpanShared<E>& sh, const SpanRegs<E>& x) {
+  constexpr int G4 = E / 4;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < SpanRegs<E>::F; ++k) {
+    const int f = tid + k * kSpanThreads;
+    const int p = span_row(f / G4) * E + (f % G4) * 4;
+    *reinterpret_cast<f4*>(&sh.r[p]) = x.r[k];
+    if constexpr (kHasV) *reinterpret_cast<f4*>(&sh.v[p]) = x.v[k];
+    *reinterpret_cast<unsigned*>(&sh.d[p]) = x.d[k];
+  }
+  if (tid < E) sh.v[(SpanShared<E>::R - 1) * E + tid] = x.nvt;
+}
+
+// Segment composite (zero carry) of this thread's 16 steps from the staged
+// tile, its deltas and done bits, and the reverse scan inside the wave:
+// (na, np) is the composite of the wave's segments to the right of this one;
+// lane j == 0 of each env leaves the wave's composite in sh.wc.
+template <int E, bool kHasV>
+__device__ __forceinline__ void span_segments(const GaeArgs& a, SpanShared<E>& sh, long t0,
+                                              int nrows, float lastv, double (&dl)[kSpanL],
+                                              unsigned& dm, int& nvalid, double& na,
+                                              double& np) {
+  constexpr int SW = kWave / E;  // segments per wave
+  const int tid = threadIdx.x;
+  const int e = tid % E, s = tid / E, w = tid / kWave, j = (tid % kWave) / E;
+  const int sr0 = s * kSpanL;
+  nvalid = std::max(0, std::min(kSpanL, nrows - sr0));
+  const double gl0 = mul(a.gl, 0.0);
+  dm = 0u;
+  double ia = 0.0, ip = 1.0;
+  {
+    const int nrow = sr0 + kSpanL;
+    double nvd = t0 + nrow >= a.T ? (double)lastv
+                                  : (kHasV ? (double)sh.v[span_row(nrow) * E + e] : 0.0);
+#pragma unroll
+    for (int i = kSpanL - 1; i >= 0; --i) {
+      if (i < nvalid) {
+        const int p = span_row(sr0 + i) * E + e;
+        const double vd = kHasV ? (double)sh.v[p] : 0.0;
+        const bool dn = sh.d[p] != 0;
+        dl[i] = sub(add((double)sh.r[p], mul(mul(a.gamma, nvd), dn ? 0.0 : 1.0)), vd);
+        const double c = dn ? gl0 : a.gl;
+        ia = add(dl[i], mul(c, ia));
+        ip = mul(ip, c);
+        nvd = vd;
+        dm |= (unsigned)dn << i;
+      } else {
+        dl[i] = 0.0;
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < SW; off <<= 1) {
+    const double pa = __shfl_down(ia, E * off);
+    const double pp = __shfl_down(ip, E * off);
+    if (j + off < SW) {
+      ia = ia + ip * pa;
+      ip = ip * pp;
+    }
+  }
+  na = __shfl_down(ia, E);
+  np = __shfl_down(ip, E);
+  if (j + 1 >= SW) {
+    na = 0.0;
+    np = 1.0;
+  }
+  if (j == 0) sh.wc[w][e] = make_double2(ia, ip);
+}
+
+// Composite of the whole tile for env e (after the wave composites are staged).
+template <int E>
+__device__ __forceinline__ double2 span_tile_composite(const SpanShared<E>& sh, int e) {
+  double ta = 0.0, tp = 1.0;
+#pragma unroll
+  for (int ww = kSpanWaves - 1; ww >= 0; --ww) {
+    const double2 c = sh.wc[ww][e];
+    ta = c.x + c.y * ta;
+    tp = c.y * tp;
+  }
+  return make_double2(ta, tp);
+}
+
+// (strip, span) of this workgroup and its tiles [lo, hi).
+struct SpanPos {
+  long strip, span, lo, hi;
+};
+__device__ __forceinline__ SpanPos span_pos(const GaeArgs& a) {
+  SpanPos p;
+  p.strip = blockIdx.x % a.nstrips;
+  p.span = blockIdx.x / a.nstrips;
+  p.lo = p.span * a.span_tiles;
+  p.hi = std::min(p.lo + a.span_tiles, a.Tt);
+  return p;
+}
+
+template <int E, bool kHasV>
+__global__ void __launch_bounds__(kSpanThreads) gae_span_sum_kernel(GaeArgs a) {
+  using Sh = SpanShared<E>;
+  __shared__ Sh sh;
+  const SpanPos sp = span_pos(a);
+  const long col0 = sp.strip * E;
+  const int tid = threadIdx.x, e = tid % E;
+  const float lastv = a.lastv ? a.lastv[col0 + e] : 0.0f;
+  double A = 0.0, P = 1.0;  // composite of the tiles walked so far (threads tid < E)
+  SpanRegs<E> x;
+  span_load<E, kHasV>(a, sp.hi - 1, col0, x);
+  for (long tile = sp.hi - 1; tile >= sp.lo; --tile) {
+    span_stage<E, kHasV>(sh, x);
+    if (tile > sp.lo) span_load<E, kHasV>(a, tile - 1, col0, x);
+    __syncthreads();
+    const long t0 = tile * Sh::S;
+    double dl[kSpanL], na, np;
+    unsigned dm;
+    int nvalid;
+    span_segments<E, kHasV>(a, sh, t0, (int)std::min<long>(Sh::S, a.T - t0), lastv, dl, dm,
+                            nvalid, na, np);
+    __syncthreads();
+    if (tid < E) {
+      const double2 t = span_tile_composite<E>(sh, e);
+      A = t.x + t.y * A;
+      P = t.y * P;
+    }
+  }
+  if (tid < E) a.summary[sp.span * a.N + col0 + e] = make_double2(A, P);
+}
+
+template <int E, bool kStats, bool kHasV>
+__global__ void __launch_bounds__(kSpanThreads) gae_span_final_kernel(GaeArgs a) {
+  using Sh = SpanShared<E>;
+  constexpr int S = Sh::S, G4 = E / 4, F = SpanRegs<E>::F;
+  __shared__ Sh sh;
+  const SpanPos sp = span_pos(a);
+  const long col0 = sp.strip * E;
+  const int tid = threadIdx.x, e = tid % E, q = tid / E, w = tid / kWave;
+  const float lastv = a.lastv ? a.lastv[col0 + e] : 0.0f;
+  SpanRegs<E> x;
+  span_load<E, kHasV>(a, sp.hi - 1, col0, x);
+
+  // carry entering the span (from the carry scan over the span composites)
+  if (tid < E) sh.x[e] = a.carry[sp.span * a.N + col0 + e];
+
+  float s1 = 0.0f, s2 = 0.0f;
+  double cnt = 0.0;
+  for (long tile = sp.hi - 1; tile >= sp.lo; --tile) {
+    span_stage<E, kHasV>(sh, x);
+    if (tile > sp.lo) span_load<E, kHasV>(a, tile - 1, col0, x);
+    __syncthreads();
+    const long t0 = tile * S;
+    const int nrows = (int)std::min<long>(S, a.T - t0);
+    double dl[kSpanL], na, np;
+    unsigned dm;
+    int nvalid;
+    span_segments<E, kHasV>(a, sh, t0, nrows, lastv, dl, dm, nvalid, na, np);
+    __syncthreads();
+    // carry entering this thread's wave, then its segment
+    const double X = sh.x[e];
+    double C = X;
+    for (int ww = kSpanWaves - 1; ww > w; --ww) {
+      const double2 c = sh.wc[ww][e];
+      C = c.x + c.y * C;
+    }
+    const double gl0 = mul(a.gl, 0.0);
+    double xv = na + np * C;
+    const int sr0 = q * kSpanL;
+#pragma unroll
+    for (int i = kSpanL - 1; i >= 0; --i) {
+      if (i < nvalid) {
+        xv = add(dl[i], mul((dm >> i) & 1u ? gl0 : a.gl, xv));
+        const float av = (float)xv;
+        const int p = span_row(sr0 + i) * E + e;
+        const float rt = kHasV ? av + sh.v[p] : av;
+        sh.r[p] = av;
+        sh.v[p] = rt;
+        if constexpr (kStats) {
+          s1 += av;
+          s2 += av * av;
+        }
+      }
+    }
+    if constexpr (kStats) cnt += (double)nvalid;
+    __syncthreads();
+    if (tid < E) {
+      const double2 t = span_tile_composite<E>(sh, e);
+      sh.x[e] = t.x + t.y * X;  // carry of the tile to the left
+    }
+#pragma unroll
+    for (int k = 0; k < F; ++k) {
+      const int f = tid + k * kSpanThreads;
+      const int row = f / G4, c4 = f % G4;
+      if (row < nrows) {
+        const int p = span_row(row) * E + c4 * 4;
+        const long off = (t0 + row) * a.N + col0 + c4 * 4;
+        st(*reinterpret_cast<const f4*>(&sh.r[p]), reinterpret_cast<f4*>(a.adv + off));
+        if (a.ret) st(*reinterpret_cast<const f4*>(&sh.v[p]), reinterpret_cast<f4*>(a.ret + off));
+      }
+    }
+    __syncthreads();
+  }
+  if constexpr (kStats) {
+    double acc[3] = {cnt, (double)s1, (double)s2};
+    block_sum<3>(acc);
+    if (tid == 0) {
+      a.partial[blockIdx.x * 4 + 0] = acc[0];
+      a.partial[blockIdx.x * 4 + 1] = acc[1];
+      a.partial[blockIdx.x * 4 + 2] = acc[2];
+      a.partial[blockIdx.x * 4 + 3] = 0.0;
+    }
+  }
+}
+
+template <int E>
+void span_kernels_e(bool norm, bool has_v, const void*& k1, const void*& k2) {
+  k1 = has_v ? (const void*)gae_span_sum_kernel<E, true> : (const void*)gae_span_sum_kernel<E, false>;
+  if (norm)
+    k2 = has_v ? (const void*)gae_span_final_kernel<E, true, true>
+               : (const void*)gae_span_final_kernel<E, true, false>;
+  else
+    k2 = has_v ? (const void*)gae_span_final_kernel<E, false, true>
+               : (const void*)gae_span_final_kernel<E, false, false>;
+}
+
+void span_kernels(int E, bool norm, bool has_v, const void*& k1, const void*& k2) {
+  switch (E) {
+    case 64: span_kernels_e<64>(norm, has_v, k1, k2); break;
+    case 32: span_kernels_e<32>(norm, has_v, k1, k2); break;
+    case 16: span_kernels_e<16>(norm, has_v, k1, k2); break;
+    case 8: span_kernels_e<8>(norm, has_v, k1, k2); break;
+    default: span_kernels_e<4>(norm, has_v, k1, k2); break;
+  }
+}
+
+int launch_span(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
+  const void *k1, *k2;
+  SpanPlan sp = span_plan(T, N, kSpanMaxBlocks);
+  span_kernels(sp.E, norm, a.v != nullptr, k1, k2);
+  const long resident = resident_blocks(k2, kSpanThreads, 0, 3 * 256);
+  sp = span_plan(T, N, std::min(kSpanMaxBlocks, resident));
+  a.nstrips = sp.nstrips;
+  a.spans = sp.spans;
+  a.span_tiles = sp.tps;
+  a.Tt = sp.tt;
+  const dim3 grid((unsigned)(sp.nstrips * sp.spans));
+  void* args[] = {&a};
+  int st;
+  if ((st = hip_status(hipLaunchKernel(k1, grid, dim3(kSpanThreads), args, 0, stream)))) return st;
+  // carries of the spans: the tile passes' carry scan over [spans][N]
+  const CarryPlan cp = make_carry_plan(sp.spans, N);
+  const dim3 cgrid((unsigned)cp.groups, (unsigned)cp.nchunks);
+  double* carry = const_cast<double*>(a.carry);
+  if (cp.nchunks > 1) {
+    hipLaunchKernelGGL(gae_carry_kernel<true>, cgrid, dim3(cp.Ew * cp.Rw), 0, stream, a.summary,
+                       carry, a.chunk_sum, sp.spans, N, cp.Ew, cp.Rw, cp.nchunks, nullptr, nullptr,
+                       T, 0L);
+    if ((st = last_launch_status())) return st;
+  }
+  hipLaunchKernelGGL(gae_carry_kernel<false>, cgrid, dim3(cp.Ew * cp.Rw), 0, stream, a.summary,
+                     carry, a.chunk_sum, sp.spans, N, cp.Ew, cp.Rw, cp.nchunks, nullptr, nullptr,
+                     T, 0L);
+  if ((st = last_launch_status())) return st;
+  if ((st = hip_status(hipLaunchKernel(k2, grid, dim3(kSpanThreads), args, 0, stream)))) return st;
+  if (!norm) return PPO_OK;
+  return launch_normalize(a.partial, sp.nstrips * sp.spans, a.eps, a.adv, a.adv_n, a.T * a.N,
+                          a.hdr, a.stats_out, stream);
+}
+
 // Pass kernels by (VW, L, solo) geometry.
 template <int kMode>
 const void* tile_kernel(int vw, const PassGeom& g) {
@@ -1279,6 +1666,15 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
   a.adv_n = adv_norm_out;
   a.tstat = reinterpret_cast<float*>(ws + l.tstat);
 
+  // Aligned rollouts too narrow for the strip walk take the span passes when
+  // normalising or narrower than 64 envs (measured on MI355X, us, span vs
+  // tile passes: N=4 x T=4M 92 vs 250, N=16 x T=1M 87 vs 98; with the
+  // normaliser 122 vs 411, 118 vs 145, and 117-122 vs 122-125 for N = 64-1024;
+  // without it N = 64-1024 are within 2%, and below 2^20 elements the tile
+  // passes' launches are ~1.5 us shorter).
+  if (PPO_GAE_SPAN && vec && span_plan(T, N, kSpanMaxBlocks).E > 0 &&
+      strip_plan(make_plan(T, N, 4)).E == 0 && (norm || (N < 64 && T * N >= (1L << 20))))
+    return launch_span(T, N, a, norm, stream);
   return launch_gae(p, a, norm, stream);
 }
 
