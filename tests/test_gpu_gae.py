@@ -395,6 +395,21 @@ def test_gae_span_normalize_matches_separate_ops(dev):
     torch.testing.assert_close(adv_n, ppo_amd.normalize_advantages(adv), rtol=1e-6, atol=1e-7)
 
 
+@pytest.mark.parametrize("T,N", [(1 << 17, 16), (1 << 19, 4)])
+def test_discounted_returns_span_passes(dev, T, N):
+    """REINFORCE returns (values absent) on shapes that take the span passes
+    (aligned, N < 64, >= 2^20 elements): GAE with lambda = 1 and zero values."""
+    g = torch.Generator().manual_seed(T + N)
+    r = torch.randn(T, N, generator=g)
+    d = (torch.rand(T, N, generator=g) < 0.002).to(torch.uint8)
+    boot = torch.randn(N, generator=g)
+    print(f"discounted returns span T={T} N={N}", flush=True)
+    got = ppo_amd.discounted_returns(r.to(dev), d.to(dev), 0.997, boot.to(dev)).cpu().numpy()
+    expect, _ = ref.gae_c(r.numpy(), np.zeros((T, N), np.float32), d.numpy(), boot.numpy(),
+                          0.997, 1.0)
+    assert_gae_close(got, expect)
+
+
 def test_gae_span_workspace_contents_do_not_matter(dev):
     T, N = 65_536, 16
     r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.001, seed=13))
