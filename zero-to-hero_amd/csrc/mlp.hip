@@ -679,12 +679,18 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cartpole_rollout_kernel(Rollout
 
 // Sum the per-workgroup gradient partials into the parameters' gradient
 // tensors: a workgroup owns up to 64 consecutive parameters of one tensor;
-// wave w sums partials w, w + 4, w + 8, ... (fp64, 8 loads in flight per
-// step) and the four wave sums are added in wave order, so the order is
-// fixed (deterministic).  With sqpart the workgroup also leaves the fp64 sum
-// of the squares of the fp32 gradients it wrote (clip_grad_norm_'s
-// per-tensor sums, in pieces).  Workgroup 0 also forms the loss scalars.
+// wave w of its kWaves sums partials w, w + kWaves, ... (fp64, kLoads loads
+// in flight per step) and the wave sums are added in wave order, so the
+// order is fixed for a given geometry (deterministic).  The partial rows are
+// read from HBM at a stride of the whole parameter count, so the kernel is
+// latency-bound: for >= 128 partial rows, 16 waves x 16 loads put a
+// 4096-row minibatch's 256 rows in flight at once (update of T=2048 x N=64 in
+// minibatches of 4096: 4.69 -> 4.37 ms); fewer rows keep 4 waves x 8 loads.
+// With sqpart the workgroup also leaves the fp64 sum of the squares of the
+// fp32 gradients it wrote (clip_grad_norm_'s per-tensor sums, in pieces).
+// Workgroup 0 also forms the loss scalars.
 constexpr int kRedCols = 64;
+constexpr long kRedWideRows = 128;  // partial rows from which the wide geometry is used
 
 __device__ __forceinline__ float* tensor_grad(const MlpArgs& a, int j) {
   const MlpNet& net = j < 6 ? a.actor : a.critic;
@@ -692,8 +698,9 @@ __device__ __forceinline__ float* tensor_grad(const MlpArgs& a, int j) {
   return (j & 1) ? net.gb[l] : net.gw[l];
 }
 
-__global__ void __launch_bounds__(kMlpBlock) mlp_grad_reduce_kernel(MlpArgs a) {
-  constexpr int kWaves = kMlpBlock / kWave;
+template <int kWaves, int kRedLoads>
+__global__ void __launch_bounds__(kWaves * kWave) mlp_grad_reduce_kernel(MlpArgs a) {
+  constexpr int kRedBlock = kWaves * kWave;
   __shared__ double s_sum[kWaves][kRedCols];
   const int lane = threadIdx.x % kWave;
   const int w = threadIdx.x / kWave;
@@ -704,15 +711,15 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_grad_reduce_kernel(MlpArgs a) {
   const bool valid = local < a.tnum[j];
   const long pc = a.toff[j] + (valid ? local : 0);
   double s = 0.0;
-  for (long b0 = w; b0 < a.nblocks; b0 += 8 * kWaves) {
-    float v[8];
+  for (long b0 = w; b0 < a.nblocks; b0 += kRedLoads * kWaves) {
+    float v[kRedLoads];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < kRedLoads; ++q) {
       const long b = b0 + (long)q * kWaves;
       v[q] = a.gpart[(b < a.nblocks ? b : 0) * a.P + pc];
     }
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
+    for (int q = 0; q < kRedLoads; ++q)
       if (b0 + (long)q * kWaves < a.nblocks) s += (double)v[q];
   }
   s_sum[w][lane] = s;
@@ -732,7 +739,7 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_grad_reduce_kernel(MlpArgs a) {
     if (threadIdx.x == 0 && a.step_counter) *a.step_counter += 1;
     double tot[kMlpSums];
     for (int k = 0; k < kMlpSums; ++k) tot[k] = 0.0;
-    for (long b = threadIdx.x; b < a.nblocks; b += kMlpBlock)
+    for (long b = threadIdx.x; b < a.nblocks; b += kRedBlock)
       for (int k = 0; k < kMlpSums; ++k) tot[k] += a.spart[(long)k * a.nblocks + b];
     block_sum<kMlpSums>(tot);
     if (threadIdx.x == 0) {
@@ -944,8 +951,11 @@ int mlp_launch(const void* kern, MlpArgs& a, const MlpLayout& l, hipStream_t str
   int st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(kMlpBlock),
                                       args, 0, stream));
   if (st) return st;
-  return hip_status(hipLaunchKernel((const void*)mlp_grad_reduce_kernel, dim3((unsigned)l.rblocks),
-                                    dim3(kMlpBlock), args, 0, stream));
+  const bool wide = l.nblocks >= kRedWideRows;
+  return hip_status(hipLaunchKernel(wide ? (const void*)mlp_grad_reduce_kernel<16, 16>
+                                         : (const void*)mlp_grad_reduce_kernel<4, 8>,
+                                    dim3((unsigned)l.rblocks), dim3(wide ? 1024 : 256), args, 0,
+                                    stream));
 }
 
 }  // namespace
