@@ -288,10 +288,21 @@ GaeLayout make_layout(const GaePlan& p, long N) {
 }
 
 // fp64 multiply / add with no contraction into FMA: the reference evaluates
-// each Python float operation with its own rounding.
-__device__ __forceinline__ double mul(double a, double b) { return __dmul_rn(a, b); }
-__device__ __forceinline__ double add(double a, double b) { return __dadd_rn(a, b); }
-__device__ __forceinline__ double sub(double a, double b) { return __dsub_rn(a, b); }
+// each Python float operation with its own rounding.  (HIP's __dmul_rn /
+// __dadd_rn are plain operators that the backend may still fuse; the pragma
+// takes the contraction flag off these operations themselves.)
+__device__ __forceinline__ double mul(double a, double b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ double add(double a, double b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ double sub(double a, double b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
 
 // Rollout arrays are streamed: nontemporal loads and stores.
 typedef float f4 __attribute__((ext_vector_type(4)));

@@ -101,31 +101,6 @@ __global__ void __launch_bounds__(kBlock) adam_sumsq_kernel(AdamTable t, double*
   if (threadIdx.x == 0) partial[b] = acc[0];
 }
 
-struct AdamScalars {
-  // host-formed scalars (used when no device step counter is given)
-  float max_norm;      // clip threshold
-  float beta1_w;       // 1 - beta1, the lerp weight
-  float beta2;
-  float one_m_beta2;   // 1 - beta2
-  float bc2_sqrt;      // sqrt(1 - beta2^step)
-  float eps;
-  float neg_step;      // -(lr / (1 - beta1^step))
-  int clip;            // 0: no clipping (max_norm <= 0)
-  // for the device step counter: the Python doubles the bias corrections
-  // are formed from
-  double lr_d, beta1_d, beta2_d;
-};
-
-// Bias-correction scalars for `step`, formed as torch forms them in Python
-// doubles (1 - beta^t, lr / bc1 * -1, bc2 ** 0.5) and rounded to fp32.
-__device__ inline void adam_step_scalars(AdamScalars& s, const int64_t* step_counter) {
-  const double step = (double)*step_counter;
-  const double bc1 = 1.0 - pow(s.beta1_d, step);
-  const double bc2 = 1.0 - pow(s.beta2_d, step);
-  s.neg_step = (float)((s.lr_d / bc1) * -1.0);
-  s.bc2_sqrt = (float)sqrt(bc2);
-}
-
 __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
                                                              const double* __restrict__ partial,
                                                              AdamScalars s, float* norm_out,
@@ -168,7 +143,7 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
     const long i = threadIdx.x + (long)q * kBlock;
     pre[q] = i < total && i < kAdamLdsParts ? partial[i] : 0.0;
   }
-  if (step_counter) adam_step_scalars(s, step_counter);
+  if (step_counter) adam_step_scalars_at(s, (double)*step_counter);
   const int lane = threadIdx.x % kWave, wv = threadIdx.x / kWave;
   constexpr int kWavesA = kBlock / kWave;
   constexpr int kPerWave = (PPO_ADAM_MAX_TENSORS + kWavesA - 1) / kWavesA;
@@ -206,18 +181,8 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    float total_sq = 0.0f;
-    for (int q = 0; q < t.nt; ++q) {
-      const float nk = s_norm[q];
-      total_sq = __fadd_rn(total_sq, __fmul_rn(nk, nk));
-    }
-    const float norm = __fsqrt_rn(total_sq);
-    float coef = 1.0f;
-    if (s.clip) {
-      const float c = __fdiv_rn(s.max_norm, __fadd_rn(norm, 1e-6f));
-      coef = c < 1.0f ? c : 1.0f;
-    }
-    s_coef = coef;
+    float norm;
+    s_coef = adam_coef_from_norms(s, s_norm, t.nt, norm);
     if (blockIdx.x == 0 && norm_out) *norm_out = norm;
   }
   __syncthreads();
@@ -226,22 +191,28 @@ __global__ void __launch_bounds__(kBlock) adam_update_kernel(AdamTable t,
   for (int j = 0; j < kAdamPerThread; ++j) {
     const long i = lo + threadIdx.x + (long)j * kBlock;
     if (i >= hi) break;
-    const float gi = s.clip ? __fmul_rn(gr[j], coef) : gr[j];
+    float gi, mi, vi, pi;
+    adam_elem(s, coef, gr[j], mr[j], vr[j], pr[j], gi, mi, vi, pi);
     if (s.clip) g[i] = gi;
-    // exp_avg.lerp_(grad, 1 - beta1), weight < 0.5: m + w * (g - m)
-    const float mi = __fadd_rn(mr[j], __fmul_rn(s.beta1_w, __fsub_rn(gi, mr[j])));
-    // exp_avg_sq.mul_(beta2).addcmul_(grad, grad, value=1 - beta2)
-    const float vi = __fadd_rn(__fmul_rn(vr[j], s.beta2), __fmul_rn(__fmul_rn(s.one_m_beta2, gi), gi));
-    // denom = sqrt(v) / sqrt(1 - beta2^t) + eps;  p += (-lr / (1 - beta1^t)) * (m / denom)
-    const float denom = __fadd_rn(__fdiv_rn(__fsqrt_rn(vi), s.bc2_sqrt), s.eps);
-    p[i] = __fadd_rn(pr[j], __fmul_rn(s.neg_step, __fdiv_rn(mi, denom)));
+    p[i] = pi;
     m[i] = mi;
     v[i] = vi;
   }
 }
 
-// Host-side scalars exactly as torch forms them: Python doubles, rounded to
-// fp32 where the tensor op consumes them.
+
+long adam_blocks(int nt, const int64_t* numel, long* starts) {
+  long b = 0;
+  for (int k = 0; k < nt; ++k) {
+    starts[k] = b;
+    b += (numel[k] + kAdamChunk - 1) / kAdamChunk;
+  }
+  starts[nt] = b;
+  return b;
+}
+
+}  // namespace
+
 AdamScalars make_adam_scalars(const ppo_adam_params* hp) {
   const double step = hp->step_counter ? 1.0 : (double)hp->step;  // device path recomputes
   const double bc1 = 1.0 - pow(hp->beta1, step);
@@ -260,18 +231,6 @@ AdamScalars make_adam_scalars(const ppo_adam_params* hp) {
   s.beta2_d = hp->beta2;
   return s;
 }
-
-long adam_blocks(int nt, const int64_t* numel, long* starts) {
-  long b = 0;
-  for (int k = 0; k < nt; ++k) {
-    starts[k] = b;
-    b += (numel[k] + kAdamChunk - 1) / kAdamChunk;
-  }
-  starts[nt] = b;
-  return b;
-}
-
-}  // namespace
 
 int launch_adam_presummed(int nt, float* const* params, float* const* grads,
                           float* const* exp_avg, float* const* exp_avg_sq, const int64_t* numel,
