@@ -193,7 +193,8 @@ int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t B,
  * dst[k][b] = src[k][index[b]] for b < B, rows of row_bytes[k] bytes (a
  * multiple of 4), all in one launch.  An index outside [0, n_src) yields a
  * zero row (it is never dereferenced).  index is int64 (torch.randperm's
- * dtype).
+ * dtype).  PPO_ERR_TOO_LARGE when a combined row exceeds 2^30 words or
+ * B times it exceeds 2^50.
  */
 int ppo_gather_rows(const int64_t* index, int64_t B, int64_t n_src, int32_t narrays,
                     const void* const* src, const int32_t* row_bytes, void* const* dst,

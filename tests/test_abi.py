@@ -88,6 +88,18 @@ def test_host_side_errors_before_launch():
     assert lib.ppo_sample_cat_f32(p, 4, 3, p, None, p, None, None, None) == 1
     assert lib.ppo_sample_cat_f32(None, 0, 3, None, None, None, None, None, None) == 0
     assert lib.ppo_sample_gauss_f32(p, p, 4, 25, p, p, p, None, None, None) == 3
+    # gather: 8 arrays of 2^29 - 1 words per row (~2^32 words) exceed the kernel's
+    # 2^30-word row table; rows that are not whole words are refused
+    ptrs = (ctypes.c_void_p * 8)(*([256] * 8))
+    wide = (ctypes.c_int32 * 8)(*([2**31 - 4] * 8))
+    assert lib.ppo_gather_rows(p, 4, 4, 8, ptrs, wide, ptrs, None) == 3
+    odd = (ctypes.c_int32 * 8)(*([6] * 8))
+    assert lib.ppo_gather_rows(p, 4, 4, 8, ptrs, odd, ptrs, None) == 1
+    # Adam: a negative tensor size is an argument error, checked before the workspace
+    numel = (ctypes.c_int64 * 1)(-8)
+    hp = _lib.AdamParams(1e-3, 0.9, 0.999, 1e-8, 0.5, 1, None)
+    assert lib.ppo_adam_clip_f32(1, ptrs, ptrs, ptrs, ptrs, numel, ctypes.byref(hp), None,
+                                 None, 0, None) == 1
 
 
 def test_error_mapping():

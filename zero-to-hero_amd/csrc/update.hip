@@ -268,16 +268,18 @@ extern "C" int ppo_gather_rows(const int64_t* index, int64_t B, int64_t n_src, i
   if (!index || !src || !row_bytes || !dst) return PPO_ERR_INVALID_ARG;
   GatherTable t = {};
   t.narr = narrays;
-  int w = 0;
+  long w = 0;
   for (int k = 0; k < narrays; ++k) {
     if (!src[k] || !dst[k] || row_bytes[k] <= 0 || row_bytes[k] % 4) return PPO_ERR_INVALID_ARG;
     t.src[k] = static_cast<const unsigned*>(src[k]);
     t.dst[k] = static_cast<unsigned*>(dst[k]);
     t.words[k] = row_bytes[k] / 4;
-    t.word_start[k] = w;
+    t.word_start[k] = (int)w;
     w += t.words[k];
   }
-  t.word_start[narrays] = w;
+  t.word_start[narrays] = (int)w;
+  // word offsets are 32-bit in the kernel's table; B * w must not overflow
+  if (w > (1L << 30) || B > (1L << 50) / w) return PPO_ERR_TOO_LARGE;
   const long total = (long)B * w;
   long blocks = std::min((total + kBlock - 1) / kBlock, 8192L);
   hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)blocks), dim3(kBlock), 0,
@@ -333,6 +335,8 @@ extern "C" int ppo_adam_clip_f32(int32_t ntensors, float* const* params, float* 
   if (!params || !grads || !exp_avg || !exp_avg_sq || !numel || !hp) return PPO_ERR_INVALID_ARG;
   if ((!hp->step_counter && hp->step < 1) || !(hp->lr >= 0.0) || !(hp->eps >= 0.0))
     return PPO_ERR_INVALID_ARG;
+  for (int k = 0; k < ntensors; ++k)
+    if (numel[k] < 0) return PPO_ERR_INVALID_ARG;
   if (!workspace || workspace_bytes < ppo_adam_clip_workspace_bytes(ntensors, numel))
     return PPO_ERR_WORKSPACE;
   AdamTable t = {};
