@@ -415,3 +415,42 @@ def test_gae_span_workspace_contents_do_not_matter(dev):
     r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.001, seed=13))
     outs = [_gae_abi(dev, r, v, d, lv, 0.999, 0.95, fill=f)[0] for f in (0x00, 0xFF, 0x7F)]
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+# ---------------------------------------------------------------------------
+# Seeded sweep across the routing boundaries: shapes drawn so that the tile
+# passes, the span passes and the strip walk all occur (aligned and unaligned
+# N, short and long horizons), with and without the fused normaliser.
+# ---------------------------------------------------------------------------
+def _sweep_shapes(count=24, seed=2024, max_elems=1 << 21):
+    rng = np.random.default_rng(seed)
+    shapes = []
+    while len(shapes) < count:
+        N = int(2 ** rng.uniform(0, 13))
+        if rng.random() < 0.6:
+            N = max(4, N - N % 4)  # aligned: span passes / strip walk eligible
+        T = int(2 ** rng.uniform(0, 20))
+        T = max(1, min(T, max_elems // N))
+        shapes.append((T, N, float(rng.choice([0.0, 0.001, 0.01, 0.2])), bool(rng.random() < 0.5)))
+    # strip walk: 8-env strips, 32-env strips, and 16-env strips whose last
+    # strip is ragged (N % 16 == 4)
+    shapes += [(1024, 2048, 0.01, False), (512, 8192, 0.01, True), (2048, 4100, 0.01, True)]
+    return shapes
+
+
+@pytest.mark.parametrize("T,N,p,norm", _sweep_shapes())
+def test_gae_routing_sweep_matches_oracle(dev, T, N, p, norm):
+    seed = T * 31 + N * 7 + int(norm)
+    r, v, d, lv = _inputs(T, N, p, seed)
+    print(f"gae sweep T={T} N={N} p={p} norm={norm} seed={seed}", flush=True)
+    args = (r.to(dev), v.to(dev), d.to(dev), lv.to(dev), 0.99, 0.95)
+    if norm:
+        adv, ret, adv_n = ppo_amd.gae_normalize(*args)
+    else:
+        adv, ret = ppo_amd.gae(*args)
+    a_ref, _ = ref.gae_c(r.numpy(), v.numpy(), d.numpy(), lv.numpy(), 0.99, 0.95)
+    assert_gae_close(adv.cpu().numpy(), a_ref)
+    np.testing.assert_array_equal(ret.cpu().numpy(), adv.cpu().numpy() + v.numpy())
+    if norm:
+        n_ref = ref.normalize_reference(adv.cpu().reshape(-1)).reshape(T, N)
+        torch.testing.assert_close(adv_n.cpu(), n_ref, rtol=1e-5, atol=1e-6)
