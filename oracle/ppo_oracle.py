@@ -266,6 +266,7 @@ def loss_categorical_reference(
         "entropy": entropy_bonus.mean().detach(),
         "approx_kl": approx_kl,
         "clipfrac": clipfrac,
+        "ratio": ratio.detach(),
         "dlogits": logits.grad.detach(),
         "dvalues": values.grad.detach(),
     }
@@ -321,6 +322,7 @@ def loss_gaussian_reference(
         "entropy": entropy_bonus.mean().detach(),
         "approx_kl": approx_kl,
         "clipfrac": clipfrac,
+        "ratio": ratio.detach(),
         "dmu": mu.grad.detach(),
         "dlog_std": log_std.grad.detach(),
         "dvalues": values.grad.detach(),
@@ -500,6 +502,7 @@ def _update_batch_grads(policy, value, observations, actions, old_log_probs, adv
         "entropy": entropy_bonus.mean().detach(),
         "approx_kl": approx_kl,
         "clipfrac": clipfrac,
+        "ratio": ratio.detach(),
     }
 
 

@@ -28,13 +28,33 @@ def assert_grad_close(got, expect, rtol=1e-4, floor=1e-5):
     torch.testing.assert_close(got, expect, rtol=rtol, atol=atol)
 
 
+def clip_edge_rows(ratio, clip=0.2, band=1e-5):
+    """Rows whose oracle ratio lies within `band` (relative) of a clip bound
+    1 -/+ clip.  The clipped surrogate's gradient is discontinuous there: a
+    log-prob summed in another order (torch's vectorised reduction against
+    the kernel's dim loop) moves the ratio by an ulp or so and can put the row
+    on the other side, switching its whole policy gradient on or off.  Such
+    rows are left out of the element-wise gradient comparison (and widen the
+    clipfrac tolerance by their count); every other row is held to the bar."""
+    r = ratio.detach().cpu().double()
+    return ((r - (1.0 - clip)).abs() < band * r) | ((r - (1.0 + clip)).abs() < band * r)
+
+
+def assert_rows_close(got, expect, edge):
+    keep = ~edge
+    got = got.detach().cpu().double()
+    expect = expect.detach().cpu().double()
+    assert_grad_close(got[keep], expect[keep])
+    print(f"  {int(edge.sum())} of {edge.numel()} rows within 1e-5 of a clip bound", flush=True)
+
+
 def assert_fixture_scalars(scalars, z):
     o = {k: torch.tensor(float(z["scalars"][i])) for i, k in enumerate(NAMES)}
     o["dvalues"] = torch.from_numpy(z["dvalues"])
     assert_scalars_close(scalars, o)
 
 
-def assert_scalars_close(scalars, o, rtol=1e-5):
+def assert_scalars_close(scalars, o, rtol=1e-5, edge_rows=0):
     """The reference's scalars (loss, policy, value, entropy) to rel 1e-5.
     approx_kl = mean(old_lp - lp) is a build-only diagnostic and a
     cancellation: each fp32 log-prob (magnitude ~log A) carries ~1e-7 of
@@ -46,7 +66,8 @@ def assert_scalars_close(scalars, o, rtol=1e-5):
         if k == "approx_kl":
             assert s[i].item() == pytest.approx(e, abs=1e-6), k
         elif k == "clipfrac":
-            assert s[i].item() == pytest.approx(e, abs=2.0 / o["dvalues"].numel() + 1e-7), k
+            slack = (2.0 + edge_rows) / o["dvalues"].numel()
+            assert s[i].item() == pytest.approx(e, abs=slack + 1e-7), k
         else:
             assert s[i].item() == pytest.approx(e, rel=rtol, abs=1e-7), k
 
@@ -77,8 +98,9 @@ def run_cat(dev, B, A, seed, vf_clip=0.2, act_dtype=torch.int32, inputs=None):
     )
     o = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val, old_v,
                                        0.2, vf_clip, 0.5, 0.01)
-    assert_scalars_close(scalars, o)
-    assert_grad_close(dlogits, o["dlogits"])
+    edge = clip_edge_rows(o["ratio"])
+    assert_scalars_close(scalars, o, edge_rows=int(edge.sum()))
+    assert_rows_close(dlogits, o["dlogits"], edge)
     assert_grad_close(dvalues, o["dvalues"])
     return scalars, dlogits, dvalues
 
@@ -209,9 +231,18 @@ def run_gauss(dev, B, D, seed, vf_clip=0.2):
         *[x.to(dev) for x in inp], 0.2, vf_clip, 0.5, 0.01
     )
     o = ref.loss_gaussian_reference(*inp, 0.2, vf_clip, 0.5, 0.01)
-    assert_scalars_close(scalars, o)
-    assert_grad_close(dmu, o["dmu"])
-    assert_grad_close(dls, o["dlog_std"])
+    edge = clip_edge_rows(o["ratio"])
+    assert_scalars_close(scalars, o, edge_rows=int(edge.sum()))
+    assert_rows_close(dmu, o["dmu"], edge)
+    # dlog_std sums over rows: an edge row may add or drop its policy term
+    # |A| r ((x - mu)^2 / sigma^2 - 1) / B (x1.5 at a tie), so the
+    # tolerance widens by exactly that much for those rows
+    r = o["ratio"].double()
+    z2 = ((acts.double() - mu.double()) / log_std.double().exp()) ** 2
+    extra = ((adv.double().abs() * r * 1.5)[:, None] * (z2 - 1).abs())[edge].sum(0) / B
+    diff = (dls.detach().cpu().double() - o["dlog_std"].double()).abs()
+    lim = 1e-4 * o["dlog_std"].double().abs() + 1e-5 * float(o["dlog_std"].abs().max()) + extra
+    assert bool((diff <= lim).all()), (diff, lim)
     assert_grad_close(dv, o["dvalues"])
 
 
@@ -272,3 +303,30 @@ def test_gauss_autograd(dev):
     assert_grad_close(m.grad, o["dmu"])
     assert_grad_close(ls.grad, o["dlog_std"])
     assert_grad_close(vv.grad, o["dvalues"])
+
+
+# ---------------------------------------------------------------------------
+# Seeded sweep over row counts on both sides of the persistent grid's capacity
+# (262,144 rows per round at 4096 waves x 64 rows), ragged final tiles, and
+# the width specialisations, action dtypes and value-clip settings.
+# ---------------------------------------------------------------------------
+def _loss_sweep(count, widths, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(count):
+        # half the cases past one grid round (200k-700k rows), half 1..~16k rows
+        B = int(rng.uniform(2e5, 7e5)) if rng.random() < 0.5 else int(2 ** rng.uniform(0, 14))
+        cases.append((B, int(rng.choice(widths)), bool(rng.random() < 0.5),
+                      bool(rng.random() < 0.3)))
+    return cases
+
+
+@pytest.mark.parametrize("B,A,clip,i64", _loss_sweep(12, [1, 2, 6, 18, 33, 100], 7))
+def test_cat_row_count_sweep(dev, B, A, clip, i64):
+    run_cat(dev, B, A, seed=B + 1000 * A, vf_clip=0.2 if clip else None,
+            act_dtype=torch.int64 if i64 else torch.int32)
+
+
+@pytest.mark.parametrize("B,D,clip,_", _loss_sweep(8, [1, 6, 8, 9, 17], 11))
+def test_gauss_row_count_sweep(dev, B, D, clip, _):
+    run_gauss(dev, B, D, seed=B + 1000 * D, vf_clip=0.2 if clip else None)
