@@ -160,6 +160,26 @@ int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A,
                      float* dlogits, float* dvalues, float* scalars_out,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * ppo_loss_cat_f32 without a workspace argument and without any allocation:
+ * no counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The per-workgroup partial sums live in a library-owned
+ * device array of 262,400 bytes (one copy per GPU, held until the process
+ * ends), enough for every B and A ppo_loss_cat_f32 accepts; a size needing
+ * more returns PPO_ERR_TOO_LARGE.  All calls on one GPU share that array, so
+ * calls that overlap on one GPU (different streams, no ordering between
+ * them) race and give wrong scalars; calls ordered on one stream are safe.
+ * Results equal ppo_loss_cat_f32's bit for bit.
+ */
+int ppo_loss_cat_f32_noalloc(const float* logits, int64_t B, int32_t A,
+                             const void* actions, int actions_are_int64,
+                             const float* old_log_probs, const float* advantages,
+                             const float* returns, const float* values,
+                             const float* old_values, const ppo_loss_params* params,
+                             float* dlogits, float* dvalues, float* scalars_out,
+                             void* stream);
+
 size_t ppo_loss_gauss_workspace_bytes(int64_t B, int32_t D);
 
 /*

@@ -1110,18 +1110,25 @@ extern "C" size_t ppo_loss_cat_workspace_bytes(int64_t B, int32_t A) {
   return kHeaderBytes + align_up((size_t)cat_blocks(B, A) * kScalarSlots * sizeof(double), 256);
 }
 
-extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const void* actions,
-                                int actions_are_int64, const float* old_log_probs,
-                                const float* advantages, const float* returns,
-                                const float* values, const float* old_values,
-                                const ppo_loss_params* params, float* dlogits, float* dvalues,
-                                float* scalars_out, void* workspace, size_t workspace_bytes,
-                                void* stream_ptr) {
-  using namespace ppo;
+namespace ppo {
+namespace {
+
+// Argument checks of ppo_loss_cat_f32 that come before the workspace check.
+int loss_cat_check(const float* logits, int64_t B, int32_t A, const void* actions,
+                   const float* dlogits) {
   if (B <= 0 || A <= 0) return PPO_ERR_INVALID_ARG;
   if (!logits || !actions || !dlogits) return PPO_ERR_INVALID_ARG;
   if ((long)B * A > (1L << 50)) return PPO_ERR_TOO_LARGE;
-  if (!workspace || workspace_bytes < ppo_loss_cat_workspace_bytes(B, A)) return PPO_ERR_WORKSPACE;
+  return PPO_OK;
+}
+
+// ppo_loss_cat_f32 after its checks; `workspace` holds at least
+// ppo_loss_cat_workspace_bytes(B, A) bytes of device memory.
+int loss_cat_launch(const float* logits, int64_t B, int32_t A, const void* actions,
+                    int actions_are_int64, const float* old_log_probs, const float* advantages,
+                    const float* returns, const float* values, const float* old_values,
+                    const ppo_loss_params* params, float* dlogits, float* dvalues,
+                    float* scalars_out, void* workspace, void* stream_ptr) {
   LossArgs a = {};
   int st = fill_common(a, B, params, old_log_probs, advantages, returns, values, old_values,
                        dvalues, scalars_out);
@@ -1199,6 +1206,79 @@ extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const
   if ((st = last_launch_status())) return st;
   hipLaunchKernelGGL(loss_finalize_kernel<0>, dim3(1), dim3(kFinalBlock), 0, stream, a, blocks, 0);
   return last_launch_status();
+}
+
+}  // namespace
+
+// Scratch of the allocation-free entry point: the per-workgroup partial sums
+// of the largest grid either categorical kernel family launches, behind the
+// workspace header.  One copy per device, zero-initialised at load and held
+// until the process ends; every call on a device reuses it.
+constexpr size_t kLossScratchBytes =
+    kHeaderBytes + (size_t)(kWaveRowBlocks > kLossGridCap ? kWaveRowBlocks : kLossGridCap) *
+                       kScalarSlots * sizeof(double);
+__device__ __align__(256) unsigned char scratch[kLossScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+// Device address of `scratch` on the current device, looked up once per
+// device with that device current.  In host code the name `scratch` is only
+// a host-side handle: kernels must be given this address.
+int scratch_address(void** out) {
+  int dev = 0;
+  int st = hip_status(hipGetDevice(&dev));
+  if (st) return st;
+  if (dev < 0 || dev >= kMaxDevices) return PPO_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if ((st = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))))) return st;
+    if (!p) return PPO_ERR_HIP_BASE + (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PPO_OK;
+}
+
+}  // namespace
+}  // namespace ppo
+
+extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const void* actions,
+                                int actions_are_int64, const float* old_log_probs,
+                                const float* advantages, const float* returns,
+                                const float* values, const float* old_values,
+                                const ppo_loss_params* params, float* dlogits, float* dvalues,
+                                float* scalars_out, void* workspace, size_t workspace_bytes,
+                                void* stream_ptr) {
+  using namespace ppo;
+  int st = loss_cat_check(logits, B, A, actions, dlogits);
+  if (st) return st;
+  if (!workspace || workspace_bytes < ppo_loss_cat_workspace_bytes(B, A)) return PPO_ERR_WORKSPACE;
+  return loss_cat_launch(logits, B, A, actions, actions_are_int64, old_log_probs, advantages,
+                         returns, values, old_values, params, dlogits, dvalues, scalars_out,
+                         workspace, stream_ptr);
+}
+
+extern "C" int ppo_loss_cat_f32_noalloc(const float* logits, int64_t B, int32_t A,
+                                        const void* actions, int actions_are_int64,
+                                        const float* old_log_probs, const float* advantages,
+                                        const float* returns, const float* values,
+                                        const float* old_values, const ppo_loss_params* params,
+                                        float* dlogits, float* dvalues, float* scalars_out,
+                                        void* stream_ptr) {
+  using namespace ppo;
+  int st = loss_cat_check(logits, B, A, actions, dlogits);
+  if (st) return st;
+  if (ppo_loss_cat_workspace_bytes(B, A) > kLossScratchBytes) return PPO_ERR_TOO_LARGE;
+  void* ws = nullptr;
+  if ((st = scratch_address(&ws))) return st;
+  return loss_cat_launch(logits, B, A, actions, actions_are_int64, old_log_probs, advantages,
+                         returns, values, old_values, params, dlogits, dvalues, scalars_out, ws,
+                         stream_ptr);
 }
 
 extern "C" size_t ppo_loss_gauss_workspace_bytes(int64_t B, int32_t D) {

@@ -90,6 +90,11 @@ SIGNATURES = {
         [_vp, _i64, _i32, _vp, _int, _vp, _vp, _vp, _vp, _vp,
          ctypes.POINTER(LossParams), _vp, _vp, _vp, _vp, _sz, _vp],
     ),
+    "ppo_loss_cat_f32_noalloc": (
+        _int,
+        [_vp, _i64, _i32, _vp, _int, _vp, _vp, _vp, _vp, _vp,
+         ctypes.POINTER(LossParams), _vp, _vp, _vp, _vp],
+    ),
     "ppo_loss_gauss_workspace_bytes": (_sz, [_i64, _i32]),
     "ppo_loss_gauss_f32": (
         _int,
