@@ -11,7 +11,7 @@ CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
 def build(force: bool = True) -> str:
     """Compile every HIP source with hipcc (see csrc/Makefile); returns the
     path of the library.  `force` rebuilds even when the .so is up to date."""
-    cmd = ["make", "-s", "-C", CSRC]
+    cmd = ["make", "-s", "-j8", "-C", CSRC]
     if force:
         cmd.insert(2, "-B")
     subprocess.run(cmd, check=True)
