@@ -96,6 +96,21 @@ int ppo_gae_norm_f32(const float* rewards, const float* values,
                      float* stats_out, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/*
+ * Which kernels ppo_gae_f32 (normalize = 0) or ppo_gae_norm_f32 (1) run for
+ * a T x N rollout with 16-byte-aligned buffers on the current device, as one
+ * of the PPO_GAE_ROUTE_* values (diagnostics and tests; no counterpart in the
+ * reference).  has_values = 0 means values == NULL.  Misaligned buffers take
+ * the scalar tile passes whatever this returns.  The environment variable
+ * PPO_AMD_GAE_RESIDENT=0 turns the resident pass off.
+ */
+#define PPO_GAE_ROUTE_NONE 0      /* empty or oversized rollout                */
+#define PPO_GAE_ROUTE_RESIDENT 1  /* one launch, whole rollout in registers    */
+#define PPO_GAE_ROUTE_STRIP 2     /* strip walk (+ normalise pass)             */
+#define PPO_GAE_ROUTE_SPAN 3      /* span passes + carry scan (+ normalise)    */
+#define PPO_GAE_ROUTE_TILES 4     /* tile passes + carry scan                  */
+int ppo_gae_route(int64_t T, int64_t N, int normalize, int has_values);
+
 /* ------------------------------------------------------------------------ */
 /* Advantage normalisation on its own.                                      */
 /* ------------------------------------------------------------------------ */

@@ -29,6 +29,13 @@ def _c_oracle():
     ref.build_c()
 
 
+@pytest.fixture
+def no_resident(monkeypatch):
+    """Turns the resident pass off, so shapes it would take run on the strip
+    walk / span / tile passes they are chosen to exercise."""
+    monkeypatch.setenv("PPO_AMD_GAE_RESIDENT", "0")
+
+
 def _inputs(T, N, p_done, seed, last=True):
     g = torch.Generator().manual_seed(seed)
     r = torch.randn(T, N, generator=g)
@@ -283,21 +290,21 @@ def test_discounted_returns_vectorised_with_dones(dev):
         (129, 8192, 0.05), (640, 8196, 0.01),                  # E=32
     ],
 )
-def test_gae_strip_walk_matches_oracle(dev, T, N, p):
+def test_gae_strip_walk_matches_oracle(no_resident, dev, T, N, p):
     exact = _run(dev, T, N, p, seed=T * 31 + N)
     assert exact > 0.99
 
 
-def test_gae_strip_walk_without_bootstrap(dev):
+def test_gae_strip_walk_without_bootstrap(no_resident, dev):
     _run(dev, 700, 4096, 0.01, seed=41, last=False)
 
 
-def test_gae_strip_walk_all_or_no_dones(dev):
+def test_gae_strip_walk_all_or_no_dones(no_resident, dev):
     _run(dev, 300, 2048, 1.0, seed=42)
     _run(dev, 300, 2048, 0.0, seed=43)
 
 
-def test_discounted_returns_strip_walk(dev):
+def test_discounted_returns_strip_walk(no_resident, dev):
     """values = None (REINFORCE returns) on the strip walk."""
     T, N = 600, 4096
     g = torch.Generator().manual_seed(44)
@@ -310,7 +317,7 @@ def test_discounted_returns_strip_walk(dev):
     assert_gae_close(got, expect)
 
 
-def test_gae_normalize_strip_walk_matches_separate_ops(dev):
+def test_gae_normalize_strip_walk_matches_separate_ops(no_resident, dev):
     g = torch.Generator().manual_seed(45)
     T, N = 777, 2056
     r = torch.randn(T, N, generator=g).to(dev)
@@ -368,7 +375,7 @@ def _gae_abi(dev, r, v, d, lv, gamma, lam, norm=False, fill=0xAB):
         (1 << 20, 16, 0.001),    # config 3's shape without the normaliser
     ],
 )
-def test_gae_span_matches_oracle(dev, T, N, p):
+def test_gae_span_matches_oracle(no_resident, dev, T, N, p):
     """With the normaliser every aligned rollout narrower than the strip walk
     takes the span passes; without it the narrow (N < 64), large ones do."""
     r, v, d, lv = _inputs(T, N, p, seed=T + 31 * N)
@@ -384,7 +391,7 @@ def test_gae_span_matches_oracle(dev, T, N, p):
                                        atol=1e-7)
 
 
-def test_gae_span_normalize_matches_separate_ops(dev):
+def test_gae_span_normalize_matches_separate_ops(no_resident, dev):
     T, N = 20_000, 24
     r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.01, seed=12))
     print(f"gae span norm T={T} N={N}", flush=True)
@@ -396,7 +403,7 @@ def test_gae_span_normalize_matches_separate_ops(dev):
 
 
 @pytest.mark.parametrize("T,N", [(1 << 17, 16), (1 << 19, 4)])
-def test_discounted_returns_span_passes(dev, T, N):
+def test_discounted_returns_span_passes(no_resident, dev, T, N):
     """REINFORCE returns (values absent) on shapes that take the span passes
     (aligned, N < 64, >= 2^20 elements): GAE with lambda = 1 and zero values."""
     g = torch.Generator().manual_seed(T + N)
@@ -410,7 +417,7 @@ def test_discounted_returns_span_passes(dev, T, N):
     assert_gae_close(got, expect)
 
 
-def test_gae_span_workspace_contents_do_not_matter(dev):
+def test_gae_span_workspace_contents_do_not_matter(no_resident, dev):
     T, N = 65_536, 16
     r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.001, seed=13))
     outs = [_gae_abi(dev, r, v, d, lv, 0.999, 0.95, fill=f)[0] for f in (0x00, 0xFF, 0x7F)]
@@ -438,11 +445,14 @@ def _sweep_shapes(count=24, seed=2024, max_elems=1 << 21):
     return shapes
 
 
+@pytest.mark.parametrize("resident", [True, False])
 @pytest.mark.parametrize("T,N,p,norm", _sweep_shapes())
-def test_gae_routing_sweep_matches_oracle(dev, T, N, p, norm):
+def test_gae_routing_sweep_matches_oracle(dev, monkeypatch, T, N, p, norm, resident):
+    if not resident:
+        monkeypatch.setenv("PPO_AMD_GAE_RESIDENT", "0")
     seed = T * 31 + N * 7 + int(norm)
     r, v, d, lv = _inputs(T, N, p, seed)
-    print(f"gae sweep T={T} N={N} p={p} norm={norm} seed={seed}", flush=True)
+    print(f"gae sweep T={T} N={N} p={p} norm={norm} seed={seed} resident={resident}", flush=True)
     args = (r.to(dev), v.to(dev), d.to(dev), lv.to(dev), 0.99, 0.95)
     if norm:
         adv, ret, adv_n = ppo_amd.gae_normalize(*args)
@@ -454,3 +464,155 @@ def test_gae_routing_sweep_matches_oracle(dev, T, N, p, norm):
     if norm:
         n_ref = ref.normalize_reference(adv.cpu().reshape(-1)).reshape(T, N)
         torch.testing.assert_close(adv_n.cpu(), n_ref, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# Resident pass (aligned rollouts whose tiles fit on the device at once):
+# tiles of 64, 128 or 32 envs x 512-2048 steps held in registers, composites
+# exchanged between the tiles of an env column, statistics between all tiles.
+# Shapes cover one tile, several tiles per column (one look-back pass and
+# more than one: 16 composites are read per pass at E = 32), ragged last
+# tiles, each tile width, the halved segment length of short horizons, and
+# the largest grid (config 2).
+# ---------------------------------------------------------------------------
+RESIDENT_SHAPES = [
+    (2048, 4096, 0.01),   # config 2: 64-env tiles, 16 steps per thread, 64 columns x 4 tiles
+    (1024, 1024, 0.02),   # 4 steps per thread, 128 tiles
+    (3000, 1024, 0.01),   # 8 steps per thread, ragged last tile
+    (1025, 2048, 0.05),   # last tile holds one row
+    (16_384, 512, 0.002), # 32 tiles in a column: a look-back of 31 composites
+    (4000, 288, 0.01),    # 32-env tiles, 4 steps per thread
+    (15_500, 288, 0.001), # 32-env tiles, 16 steps per thread, ragged
+    (2048, 1024, 0.0),    # no dones: every carry crosses every tile
+    (1024, 2048, 1.0),    # every step done
+]
+
+
+def _route(T, N, norm, has_values=True):
+    from ppo_amd import _lib
+
+    return _lib.GAE_ROUTES[_lib.load().ppo_gae_route(T, N, int(norm), int(has_values))]
+
+
+def _resident_case(dev, T, N, p, norm, seed, last=True, fill=0xAB):
+    assert _route(T, N, norm) == "resident"
+    r, v, d, lv = (None if x is None else x.to(dev) for x in _inputs(T, N, p, seed, last))
+    print(f"gae resident T={T} N={N} p={p} norm={norm} seed={seed} last={last} fill={fill}",
+          flush=True)
+    adv, ret, adv_n = _gae_abi(dev, r, v, d, lv, 0.99, 0.95, norm=norm, fill=fill)
+    a_ref, _ = ref.gae_c(r.cpu().numpy(), v.cpu().numpy(), d.cpu().numpy(),
+                         None if lv is None else lv.cpu().numpy(), 0.99, 0.95)
+    exact = assert_gae_close(adv.cpu().numpy(), a_ref)
+    assert torch.equal(ret, adv + v)
+    if norm:
+        n_ref = ref.normalize_reference(torch.from_numpy(a_ref).reshape(-1)).reshape(T, N)
+        torch.testing.assert_close(adv_n.cpu(), n_ref, rtol=1e-5, atol=1e-6)
+    return exact, adv, adv_n
+
+
+@pytest.mark.parametrize("norm", [True, False])
+@pytest.mark.parametrize("T,N,p", RESIDENT_SHAPES)
+def test_gae_resident_matches_oracle(dev, T, N, p, norm):
+    exact, _, _ = _resident_case(dev, T, N, p, norm, seed=T * 13 + N)
+    assert exact > 0.99
+
+
+def test_gae_resident_without_bootstrap(dev):
+    _resident_case(dev, 1500, 1024, 0.01, True, seed=5, last=False)
+
+
+def test_gae_resident_workspace_contents_do_not_matter(dev):
+    """The slots are cleared by the call itself: a workspace full of any
+    pattern, or left by a previous call of another shape, gives the same
+    bits."""
+    outs = [_resident_case(dev, 2048, 512, 0.01, True, seed=6, fill=f)[1:]
+            for f in (0x00, 0xFF, 0x7F)]
+    for a, n in outs[1:]:
+        assert torch.equal(a, outs[0][0]) and torch.equal(n, outs[0][1])
+    # one workspace through calls of several shapes, then the first again
+    from ppo_amd import _lib
+
+    lib = _lib.load()
+    shapes = [(2048, 512), (100, 64), (20_000, 32), (2048, 512)]
+    nbytes = max(lib.ppo_gae_workspace_bytes(T, N) for T, N in shapes)
+    ws = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    got = []
+    for T, N in shapes:
+        r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.01, seed=6))
+        adv, ret, adv_n = (torch.empty(T, N, device=dev) for _ in range(3))
+        rc = lib.ppo_gae_norm_f32(r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N,
+                                  0.99, 0.95, 1e-8, adv.data_ptr(), ret.data_ptr(),
+                                  adv_n.data_ptr(), None, ws.data_ptr(), ws.numel(), stream)
+        assert rc == 0
+        got.append((adv, adv_n))
+    torch.cuda.synchronize(dev)
+    assert torch.equal(got[0][0], got[3][0]) and torch.equal(got[0][1], got[3][1])
+    assert torch.equal(got[0][0], outs[0][0]) and torch.equal(got[0][1], outs[0][1])
+
+
+def test_gae_resident_normalise_in_place(dev):
+    """adv_norm_out may alias adv_out."""
+    T, N = 2048, 1024
+    assert _route(T, N, True) == "resident"
+    r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.01, seed=8))
+    adv, ret, adv_n = ppo_amd.gae_normalize(r, v, d, lv)
+    from ppo_amd import _lib
+
+    lib = _lib.load()
+    ws = torch.empty(lib.ppo_gae_workspace_bytes(T, N), dtype=torch.uint8, device=dev)
+    out, ret2 = torch.empty(T, N, device=dev), torch.empty(T, N, device=dev)
+    rc = lib.ppo_gae_norm_f32(r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N, 0.99,
+                              0.95, 1e-8, out.data_ptr(), ret2.data_ptr(), out.data_ptr(), None,
+                              ws.data_ptr(), ws.numel(), torch.cuda.current_stream(dev).cuda_stream)
+    assert rc == 0
+    assert torch.equal(out, adv_n) and torch.equal(ret2, ret)
+
+
+def test_discounted_returns_resident(dev):
+    """values = None (REINFORCE returns) on the resident pass."""
+    T, N = 4096, 512
+    assert _route(T, N, False, has_values=False) == "resident"
+    g = torch.Generator().manual_seed(9)
+    r = torch.randn(T, N, generator=g)
+    d = (torch.rand(T, N, generator=g) < 0.01).to(torch.uint8)
+    got = ppo_amd.discounted_returns(r.to(dev), gamma=0.97, dones=d.to(dev)).cpu().numpy()
+    a_ref, _ = ref.gae_c(r.numpy(), np.zeros((T, N), np.float32), d.numpy(), None, 0.97, 1.0)
+    assert_gae_close(got, a_ref)
+
+
+def test_gae_resident_agrees_with_strip_walk_bitwise_mostly(dev, monkeypatch):
+    """Config 2 on both routes: the same oracle bar, and the same bits in all
+    but a few elements (they compose the carries in different orders)."""
+    r, v, d, lv = (x.to(dev) for x in _inputs(2048, 4096, 0.01, seed=24))
+    a1, _, n1 = ppo_amd.gae_normalize(r, v, d, lv)
+    monkeypatch.setenv("PPO_AMD_GAE_RESIDENT", "0")
+    a2, _, n2 = ppo_amd.gae_normalize(r, v, d, lv)
+    same = float((a1 == a2).float().mean())
+    print(f"  resident vs strip walk: {same:.6f} of advantages bit-identical", flush=True)
+    assert same > 0.99
+    torch.testing.assert_close(n1, n2, rtol=1e-5, atol=1e-6)
+
+
+def test_gae_resident_non_finite_carry(dev):
+    """An infinite value late in the horizon makes the carry entering the
+    tiles to its left non-finite: elements whose recurrence reaches it through
+    a done (0 * inf) are NaN, the others +-inf, exactly as the reference's
+    float recurrence gives (the resident pass finishes carry-free segments
+    before the look-back and must patch them)."""
+    T, N = 2048, 1024
+    assert _route(T, N, True) == "resident"
+    r, v, d, lv = _inputs(T, N, 0.01, seed=10)
+    v[1800, :8] = float("inf")
+    v[1500, 8:12] = float("nan")
+    print(f"gae resident non-finite T={T} N={N}", flush=True)
+    adv, ret, _ = _gae_abi(dev, r.to(dev), v.to(dev), d.to(dev), lv.to(dev), 0.99, 0.95,
+                           norm=True)
+    a_ref, _ = ref.gae_c(r.numpy(), v.numpy(), d.numpy(), lv.numpy(), 0.99, 0.95)
+    got = adv.cpu().numpy()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(a_ref))
+    np.testing.assert_array_equal(np.isposinf(got), np.isposinf(a_ref))
+    np.testing.assert_array_equal(np.isneginf(got), np.isneginf(a_ref))
+    fin = np.isfinite(a_ref)
+    assert np.isnan(a_ref).sum() > 1000  # the case is exercised
+    assert_gae_close(got[fin], a_ref[fin])

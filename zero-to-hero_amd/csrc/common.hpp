@@ -103,6 +103,32 @@ __device__ inline void block_sum(double (&x)[K]) {
   __syncthreads();
 }
 
+// block_sum with LDS-only barriers (lds_barrier): the same fixed order and
+// result, but a wave's outstanding global stores are not drained at the
+// barriers, as __syncthreads() would do.
+template <int K>
+__device__ inline void block_sum_lds(double (&x)[K]) {
+  __shared__ double s_part[16][K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) x[k] = wave_sum(x[k]);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) s_part[wid][k] = x[k];
+  }
+  lds_barrier();
+  if (wid == 0) {
+    const int nw = blockDim.x / kWave;
+    double v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) v[k] = lane < nw ? s_part[lane < 16 ? lane : 0][k] : 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) x[k] = wave_sum(v[k]);
+  }
+  lds_barrier();
+}
+
 // Sums of `count` partial (n, sum x, sum x^2, pad) quadruples, combined by
 // one block in a fixed order (thread t takes partials t, t + blockDim, ...,
 // then the block tree), so every call gets bit-identical totals.  Result

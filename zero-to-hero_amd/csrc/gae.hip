@@ -43,7 +43,10 @@
 // horizon and walks it backwards in chunks, carrying the advantage from chunk
 // to chunk, so the rollout is read once; the normaliser then needs one
 // elementwise pass over the advantages.
+#include <stdlib.h>
+
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "common.hpp"
@@ -75,6 +78,9 @@ struct GaeArgs {
   long Q, Tq, Tt, span;
   int Qw, Sw;
   long nstrips, spans, span_tiles;  // span passes: env strips, spans per strip, tiles per span
+  uint64_t* slots;     // resident pass: barrier counter, tile composites, per-workgroup partials
+  unsigned nonce;      // resident pass: tag of this call in the barrier counter
+  long res_nc, res_nt; // resident pass: env columns, time tiles
 };
 
 // What a gae_tile_kernel launch computes.
@@ -255,8 +261,94 @@ SpanPlan span_plan(long T, long N, long blocks) {
   return c;
 }
 
+// Resident-pass geometry (gae_resident_kernel): 1024-thread workgroups, each
+// owning a tile of E envs x TS = (1024/(E/4))*L steps (4 envs and L steps per
+// thread) whose rows stay in registers from load to store.  The grid is one
+// tile per workgroup and must be resident at once (checked at launch against
+// the occupancy of the chosen kernel), so tiles can wait on each other.
+// PPO_GAE_RES: build-time switch, 0 keeps every rollout on the other paths;
+// PPO_GAE_RES_E: build-time choice of the tile width (0: by the plan).
+#ifndef PPO_GAE_RES
+#define PPO_GAE_RES 1
+#endif
+#ifndef PPO_GAE_RES_E
+#define PPO_GAE_RES_E 0
+#endif
+#ifndef PPO_GAE_RES_BLOCK
+#define PPO_GAE_RES_BLOCK 512
+#endif
+// PPO_GAE_RES_EARLY: segments that do not depend on their tile's carry store
+// their rows before the look-back (measured slower on config 2: the polls of
+// the look-back then wait behind the whole chip's stores).
+#ifndef PPO_GAE_RES_EARLY
+#define PPO_GAE_RES_EARLY 0
+#endif
+// PPO_GAE_RES_XCD: tiles handed out so that each XCD owns a contiguous run
+// PPO_GAE_RES_CTLSTATS: the control wave alone polls the statistics partials
+// (1), or every wave does, behind its own stores (0)
+#ifndef PPO_GAE_RES_CTLSTATS
+#define PPO_GAE_RES_CTLSTATS 0
+#endif
+#ifndef PPO_GAE_RES_XCD
+#define PPO_GAE_RES_XCD 0
+#endif
+constexpr int kResBlock = PPO_GAE_RES_BLOCK;
+constexpr long kResMaxTiles = 256;  // one 1024-thread workgroup per CU on MI355X
+
+struct ResPlan {
+  int E, L;          // E = 0: not applicable
+  long nc, nt, TS;   // env columns, time tiles, steps per tile
+  long tiles() const { return nc * nt; }
+};
+
+// Among tiles of 64 or 32 envs and 16, 8 or 4 steps per thread, the shape
+// giving the most tiles that still fit on the device at once (<= 256), with
+// no more than a quarter of a column's threads idle past the horizon; ties
+// go to wider tiles (longer row segments).  Rollouts that give fewer than
+// 128 tiles (too little parallelism), or more than 16 tiles per env column
+// (a long look-back) without filling the device, take the other paths:
+// measured on MI355X, e.g. T x N = 1024 x 512 (16-64 tiles) 28 us against
+// 24 us on the tile passes, 16384 x 64 (128 tiles, 64 per column) 33 us
+// against 27 us on the span passes, while 2048 x 4096 runs 45 us against
+// 55 us, 4096 x 2048 45 us against 72 and 32768 x 256 (64 per column, 256
+// tiles) 57 us against 67.
+ResPlan res_plan(long T, long N) {
+  ResPlan best = {0, 0, 0, 0, 0};
+  if (!PPO_GAE_RES || T <= 0 || N <= 0 || T * N >= (1L << 30)) return best;
+  const int Es[2] = {64, 32};
+  const int Ls[3] = {16, 8, 4};
+  for (int E : Es) {
+    if (PPO_GAE_RES_E && E != PPO_GAE_RES_E) continue;
+    if (N % E != 0) continue;
+    for (int L : Ls) {
+      const long TS = (long)(kResBlock / (E / 4)) * L;
+      const long nt = (T + TS - 1) / TS;
+      const long nc = N / E;
+      if (nc * nt > kResMaxTiles || nt > 64) continue;
+      if (4 * (nt * TS - T) > nt * TS) continue;  // a quarter of the threads idle
+      if (nc * nt > best.tiles()) {
+        best.E = E;
+        best.L = L;
+        best.nc = nc;
+        best.nt = nt;
+        best.TS = TS;
+      }
+    }
+  }
+  if (best.tiles() < 128 || (best.nt > 16 && best.tiles() < kResMaxTiles)) best.E = 0;
+  return best;
+}
+
+// 64-bit slot words of the resident pass: per tile, E composites (a, P) of
+// two words each, then three words (n, sum, sum of squares) per workgroup.
+// The first 32 words hold the start barrier's counter.
+constexpr size_t kResSlotBase = 32;
+size_t res_slot_words(const ResPlan& rp) {
+  return rp.E ? kResSlotBase + (size_t)rp.tiles() * (2 * rp.E + 3) : 0;
+}
+
 struct GaeLayout {
-  size_t summary, carry, chunk_sum, tstat, partial, total;
+  size_t summary, carry, chunk_sum, tstat, partial, slots, total;
 };
 
 GaeLayout make_layout(const GaePlan& p, long N) {
@@ -283,6 +375,8 @@ GaeLayout make_layout(const GaePlan& p, long N) {
                                       std::max<long>(strip_plan(p).strips, sp.nstrips * sp.spans));
     off += align_up((size_t)parts * 4 * sizeof(double), 256);
   }
+  l.slots = off;
+  off += align_up(res_slot_words(res_plan(p.T, N)) * sizeof(uint64_t), 256);
   l.total = off;
   return l;
 }
@@ -1538,6 +1632,594 @@ int launch_span(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
                           a.hdr, a.stats_out, stream);
 }
 
+// ---------------------------------------------------------------------------
+// Resident pass: the whole rollout in registers, one launch.
+// ---------------------------------------------------------------------------
+// Each 1024-thread workgroup owns a tile of E adjacent envs x TS consecutive
+// steps (ResPlan); thread (segment s, env-group g) owns 4 envs x L steps.
+// All of a tile's loads are issued at once and its rows stay in registers
+// until the normalised advantages are stored, so the rollout is read once and
+// each output written once (21 bytes per element with the normaliser):
+//   1. per thread, the segment composite (a, P) with a zero carry (fp64,
+//      reference operation order); a reverse scan over the segments (lane
+//      shuffles, then the 16 waves' composites in LDS) gives every segment
+//      the composite of the segments to its right and the tile its own.
+//   2. a tile publishes its per-env composite; the advantage entering it is
+//      the fold of the composites of the tiles to its right in the same env
+//      column, read in parallel (one composite per thread) and folded in
+//      order from the horizon's end.
+//   3. with the normaliser, the workgroup publishes (n, sum, sum of squares)
+//      of its advantages at once: step 1 also summed each step's suffix
+//      composite (a_t, P_t) and their products, and the advantage at step t
+//      is a_t + P_t x for the carry x entering the segment, so the sums are
+//      closed-form in x (fp64 advantages, fp32 per-thread sums).  Then each
+//      thread applies its carry and runs the exact serial recurrence,
+//      storing each row of adv and ret as soon as it is done.
+//   4. every workgroup reads all partials in the same fixed order, so all
+//      derive bit-identical mean and std (the partials were published before
+//      step 3, so the wait overlaps it), and stores the normalised
+//      advantages from the registers.
+// Cross-workgroup values travel through 64-bit slots written by agent-scope
+// relaxed atomic stores and polled by agent-scope atomic loads, one value per
+// slot, encoded so that no value encodes to zero: a zero word is an empty
+// slot, so every slot is its own ready flag and no fence (on gfx950 a full L2
+// write-back) is needed.  Each workgroup empties the slots it will fill and
+// then arrives at a start barrier (res_arrive); slots are read only after it.
+// Waits are bounded (a slot still empty after the bound reads as NaN, which
+// then shows in the outputs); the host launches the pass only when the whole
+// grid fits on the device at once, so every producer runs while its
+// consumers wait.
+constexpr int kResWaves = kResBlock / kWave;
+constexpr uint64_t kSlotTag = 0x7FF4A5A55A5A0F0FULL;  // a signalling-NaN pattern
+constexpr long kSlotSpin = 1L << 22;                  // polls before giving up
+
+__device__ __forceinline__ void slot_put(uint64_t* p, double x) {
+  uint64_t b = __builtin_bit_cast(uint64_t, x);
+  if (x != x) b = 0x7FF8000000000000ULL;  // one NaN pattern, never the tag
+  __hip_atomic_store(p, b ^ kSlotTag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ double slot_value(uint64_t w) {
+  return __builtin_bit_cast(double, w ^ kSlotTag);
+}
+
+__device__ __forceinline__ double slot_get(uint64_t* p) {
+  for (long it = 0; it < kSlotSpin; ++it) {
+    const uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (w != 0) return __builtin_bit_cast(double, w ^ kSlotTag);
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return __builtin_nan("");
+}
+
+__device__ __forceinline__ void slot_clear(uint64_t* p) {
+  __hip_atomic_store(p, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Start barrier of the resident pass: one counter word (nonce:32, count:32).
+// A workgroup arrives by one compare-and-swap attempt that resets a counter
+// tagged with another nonce (an earlier call's, or whatever the workspace
+// held) or holding a complete count (a previous replay of the same captured
+// call) to (nonce, 0), then one atomic add; neither result is waited for,
+// and both go to the same address, so they apply in order.  (A retry loop of
+// compare-and-swaps from 256 workgroups serialises at memory latency.)  The
+// barrier is complete when the counter reads (nonce, >= nblocks).
+// `v` is the counter as read after this workgroup's slots were emptied.
+__device__ void res_arrive(uint64_t* ctr, uint64_t v, unsigned nonce, unsigned nblocks) {
+  const uint64_t tag = (uint64_t)nonce << 32;
+  if ((v >> 32) != nonce || (unsigned)v >= nblocks)
+    __hip_atomic_compare_exchange_strong(ctr, &v, tag, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_add(ctr, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ void res_wait(uint64_t* ctr, unsigned nonce, unsigned nblocks) {
+  for (long it = 0; it < kSlotSpin; ++it) {
+    const uint64_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((v >> 32) == nonce && (unsigned)v >= nblocks) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+#ifdef PPO_GAE_RES_TRACE
+// Phase timestamps of the resident pass (wall clock, 100 MHz), one row of 8
+// per workgroup: a measurement build only.
+__device__ uint64_t g_res_trace[4096 * 8];
+#define RES_MARK(k) \
+  if (threadIdx.x == 0) g_res_trace[blockIdx.x * 8 + (k)] = wall_clock64()
+#else
+#define RES_MARK(k)
+#endif
+
+template <int E>
+struct ResShared {
+  double2 wc[kResWaves][E];                 // wave composites (a, P) per env
+  float ssum[5][4][kResBlock];              // per thread and env: sums of a, P, aa, aP, PP
+  double carry[E];                          // advantage entering the tile
+  float norm[2];                            // mean and denominator
+};
+
+template <int E, int L, bool kStats, bool kHasV>
+__global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
+  constexpr int VW = 4;
+  constexpr int G = E / VW;            // threads per tile row
+  constexpr int SW = kWave / G;        // segments per wave
+  constexpr int S = kResBlock / G;     // segments per tile
+  constexpr long TS = (long)S * L;     // steps per tile
+  static_assert(kWave % G == 0 && L <= 32, "resident geometry");
+  __shared__ ResShared<E> sh;
+
+  const int tid = threadIdx.x;
+  const int g = tid % G, sg = tid / G, w = tid / kWave, j = (tid % kWave) / G;
+  const long nc = a.res_nc, nt = a.res_nt;
+  // the first workgroups take the tiles at the end of the horizon, whose
+  // composites the others wait for
+  long b = blockIdx.x;
+  if (PPO_GAE_RES_XCD && gridDim.x % kXcds == 0)
+    b = (b % kXcds) * (gridDim.x / kXcds) + b / kXcds;
+  const long tt = nt - 1 - b / nc;  // time tile (0 = the first steps)
+  const long col = b % nc;
+  const long tile = tt * nc + col;
+  const long env0 = col * E + (long)g * VW;
+  const long t0 = tt * TS + (long)sg * L;
+  const int nvalid = t0 >= a.T ? 0 : (a.T - t0 < L ? (int)(a.T - t0) : L);
+  const unsigned n32 = (unsigned)a.N;
+  uint64_t* ctr = a.slots;
+  uint64_t* comp = a.slots + kResSlotBase;                // [tiles][E][2]
+  uint64_t* part = comp + (size_t)nc * nt * 2 * E;        // [grid][3]
+  RES_MARK(0);
+  // Wave 0 empties the slots this workgroup will fill (its composites and its
+  // partial), waits until those stores are done, and arrives at the start
+  // barrier; no workgroup reads a slot before the barrier is complete, so no
+  // reader can see what the slot held before this call.  The other waves
+  // start their loads meanwhile.
+  if (w == 0) {
+    for (int q = tid; q < 2 * E; q += kWave)
+      if (tt > 0) slot_clear(comp + (size_t)tile * 2 * E + q);
+    if (tid < 3) slot_clear(part + (size_t)blockIdx.x * 3 + tid);
+    uint64_t v = 0;
+    if (tid == 0) v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // the emptying stores (and that read) are done
+    if (tid == 0) res_arrive(ctr, v, a.nonce, gridDim.x);
+  }
+
+  // ---- loads: every row of the segment, unconditional (rows past the
+  // horizon re-read row 0), plus the value row after the segment
+  float r[L][VW], v[L][VW], nv[VW];
+  unsigned d[L];
+  // issued last row first: step 1 consumes the rows in that order, so its
+  // arithmetic starts as the first loads land
+#pragma unroll
+  for (int i = L - 1; i >= 0; --i) {
+    const unsigned off = (t0 + i < a.T ? (unsigned)(t0 + i) * n32 : 0u) + (unsigned)env0;
+    load_vec<VW>(at_byte(a.r, off * 4u), r[i]);
+    if constexpr (kHasV) {
+      load_vec<VW>(at_byte(a.v, off * 4u), v[i]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) v[i][k] = 0.0f;
+    }
+    d[i] = load_done_raw<VW>(at_byte(a.d, off));
+  }
+  {
+    const long tn = t0 + L;
+#pragma unroll
+    for (int k = 0; k < VW; ++k) nv[k] = 0.0f;
+    if (tn < a.T) {
+      if constexpr (kHasV) load_vec<VW>(a.v + (unsigned)tn * n32 + (unsigned)env0, nv);
+    } else if (a.lastv) {
+      load_vec<VW>(a.lastv + env0, nv);
+    }
+  }
+
+  // ---- 1. segment composites and the reverse scan inside the tile
+  const double gl0 = mul(a.gl, 0.0);
+  double na[VW], np[VW];
+  // With the normaliser, the sums over the segment's steps of the suffix
+  // composites (a_t, P_t) (steps t..segment end, zero carry) and of their
+  // products: the advantage at step t is a_t + P_t x for the carry x entering
+  // the segment, so once x is known the segment's sum of advantages and of
+  // their squares follow without the advantages themselves.
+  {
+    float sa[VW], sp[VW], saa[VW], sap[VW], spp[VW];
+    double ia[VW], ip[VW], nvd[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      ia[k] = 0.0;
+      ip[k] = 1.0;
+      nvd[k] = nv[k];
+      sa[k] = sp[k] = saa[k] = sap[k] = spp[k] = 0.0f;
+    }
+#pragma unroll
+    for (int i = L - 1; i >= 0; --i) {
+      if (i < nvalid) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          const bool done = ((d[i] >> (8 * k)) & 0xffu) != 0u;
+          const double vd = (double)v[i][k];
+          const double dl =
+              sub(add((double)r[i][k], mul(mul(a.gamma, nvd[k]), done ? 0.0 : 1.0)), vd);
+          const double cc = done ? gl0 : a.gl;
+          ia[k] = add(dl, mul(cc, ia[k]));
+          ip[k] = mul(ip[k], cc);
+          nvd[k] = vd;
+          if constexpr (kStats) {
+            const float fa = (float)ia[k], fp = (float)ip[k];
+            sa[k] += fa;
+            sp[k] += fp;
+            saa[k] += fa * fa;
+            sap[k] += fa * fp;
+            spp[k] += fp * fp;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      na[k] = ia[k];
+      np[k] = ip[k];
+      if constexpr (kStats) {
+        // parked in LDS until the carries are known (registers are short)
+        sh.ssum[0][k][tid] = sa[k];
+        sh.ssum[1][k][tid] = sp[k];
+        sh.ssum[2][k][tid] = saa[k];
+        sh.ssum[3][k][tid] = sap[k];
+        sh.ssum[4][k][tid] = spp[k];
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < VW; ++k) {
+    double ia = na[k], ip = np[k];
+#pragma unroll
+    for (int off = 1; off < SW; off <<= 1) {
+      const double pa = __shfl_down(ia, G * off);
+      const double pp = __shfl_down(ip, G * off);
+      if (j + off < SW) {
+        ia = ia + ip * pa;
+        ip = ip * pp;
+      }
+    }
+    na[k] = __shfl_down(ia, G);
+    np[k] = __shfl_down(ip, G);
+    if (j + 1 >= SW) {
+      na[k] = 0.0;
+      np[k] = 1.0;
+    }
+    if (j == 0) sh.wc[w][g * VW + k] = make_double2(ia, ip);
+  }
+  __syncthreads();
+  RES_MARK(1);
+
+  // ---- 2. publish the tile composite
+  if (tid < E && tt > 0) {
+    double ta = 0.0, tp = 1.0;
+#pragma unroll
+    for (int ww = kResWaves - 1; ww >= 0; --ww) {
+      const double2 c = sh.wc[ww][tid];
+      ta = c.x + c.y * ta;
+      tp = c.y * tp;
+    }
+    slot_put(comp + ((size_t)tile * E + tid) * 2 + 0, ta);
+    slot_put(comp + ((size_t)tile * E + tid) * 2 + 1, tp);
+  }
+
+  // ---- 3. exact recurrence from each segment's carry, adv and ret
+  // The deltas are formed again from the rows rather than kept from step 1
+  // (fp64, two registers each): the empty asm hides from the compiler that
+  // the rows are unchanged, so it cannot keep step 1's values alive instead.
+#pragma unroll
+  for (int i = 0; i < L; ++i) {
+#pragma unroll
+    for (int k = 0; k < VW; ++k) asm volatile("" : "+v"(r[i][k]), "+v"(v[i][k]));
+    asm volatile("" : "+v"(d[i]));
+  }
+  // Runs the recurrence of this thread's segment from its carries xs, rows
+  // from the last, storing each row of adv and ret as soon as its 4 envs are
+  // done; the advantages replace the rewards in r.
+  auto segment_out = [&](const double (&xs)[VW]) {
+    double xv[VW], nvd[VW];
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      xv[k] = xs[k];
+      nvd[k] = nv[k];
+    }
+#pragma unroll
+    for (int i = L - 1; i >= 0; --i) {
+      if (i < nvalid) {
+#pragma unroll
+        for (int k = 0; k < VW; ++k) {
+          const bool done = ((d[i] >> (8 * k)) & 0xffu) != 0u;
+          const double vd = (double)v[i][k];
+          const double dl =
+              sub(add((double)r[i][k], mul(mul(a.gamma, nvd[k]), done ? 0.0 : 1.0)), vd);
+          xv[k] = add(dl, mul(done ? gl0 : a.gl, xv[k]));
+          nvd[k] = vd;
+          r[i][k] = (float)xv[k];
+        }
+        const unsigned off = ((unsigned)(t0 + i) * n32 + (unsigned)env0) * 4u;
+        store_vec<VW>(at_byte(a.adv, off), r[i]);
+        if (a.ret) {
+          float rt[VW];
+#pragma unroll
+          for (int k = 0; k < VW; ++k) rt[k] = r[i][k] + v[i][k];
+          store_vec<VW>(at_byte(a.ret, off), rt);
+        }
+      }
+    }
+  };
+  // The last wave is the control wave: it alone polls slots (the start
+  // barrier, the look-back, the statistics), and it stores its own rows only
+  // at the end.  On gfx950 one counter covers a wave's loads and stores in
+  // issue order, so a poll issued behind a wave's stores waits for all of
+  // them to drain; the other waves store freely and meet the control wave at
+  // LDS-only barriers, which do not wait for stores either.
+  constexpr int kCtl = kResWaves - 1;
+  const bool ctl = w == kCtl;
+  // A segment whose composite to the tile's end has P == 0 (a done to its
+  // right inside the tile: gamma*lambda*0 multiplies the carry) does not
+  // depend on the tile's carry: its carry is the fold of the waves to its
+  // right from zero, and it is finished before the look-back.  (The fold from
+  // the true carry gives the same value unless that carry is not finite, where
+  // 0 * inf makes every advantage of the tile NaN, as in the reference's
+  // recurrence; that case is patched after the look-back.)
+  double x[VW];
+  bool early = true;
+#pragma unroll
+  for (int k = 0; k < VW; ++k) {
+    const int e = g * VW + k;
+    double C = 0.0, Pw = 1.0;
+    for (int ww = kResWaves - 1; ww > w; --ww) {
+      const double2 c = sh.wc[ww][e];
+      C = c.x + c.y * C;
+      Pw = c.y * Pw;
+    }
+    x[k] = na[k] + np[k] * C;
+    early = early && np[k] * Pw == 0.0;
+  }
+  early = early && PPO_GAE_RES_EARLY;
+  if (early && !ctl) segment_out(x);
+
+  // ---- look-back (control wave): fold the composites of the tiles to the
+  // right, env e in lane e % 64, all of a pass's loads issued together
+  if (ctl) {
+    const int lane = tid % kWave;
+    constexpr int EPL = E > kWave ? E / kWave : 1;  // envs per lane
+    constexpr int LB = EPL > 1 ? 2 : 4;             // tiles per pass
+    if (lane == 0) res_wait(ctr, a.nonce, gridDim.x);  // slots emptied by their owners
+    double xc[EPL];
+#pragma unroll
+    for (int q = 0; q < EPL; ++q) xc[q] = 0.0;
+    for (long hi = nt - 1; hi > tt; hi -= LB) {
+      const int cnt = (int)(hi - tt < LB ? hi - tt : LB);
+      uint64_t wa[LB][EPL], wp[LB][EPL];
+#pragma unroll
+      for (int q = 0; q < LB; ++q) {
+#pragma unroll
+        for (int m = 0; m < EPL; ++m) {
+          const int e = lane + m * kWave;
+          wa[q][m] = wp[q][m] = 0;
+          if (q < cnt && e < E) {
+            uint64_t* sl = comp + ((size_t)((hi - q) * nc + col) * E + e) * 2;
+            wa[q][m] = __hip_atomic_load(sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wp[q][m] = __hip_atomic_load(sl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < LB; ++q) {
+#pragma unroll
+        for (int m = 0; m < EPL; ++m) {
+          const int e = lane + m * kWave;
+          if (q < cnt && e < E) {
+            uint64_t* sl = comp + ((size_t)((hi - q) * nc + col) * E + e) * 2;
+            const double ca = wa[q][m] ? slot_value(wa[q][m]) : slot_get(sl);
+            const double cp = wp[q][m] ? slot_value(wp[q][m]) : slot_get(sl + 1);
+            xc[m] = ca + cp * xc[m];
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < EPL; ++m) {
+      const int e = lane + m * kWave;
+      if (e < E) sh.carry[e] = xc[m];
+    }
+  }
+  lds_barrier();
+  RES_MARK(2);
+
+  if (!early || ctl) {
+    // (the control wave stores nothing before the look-back, so it always
+    // takes its carries from the true tile carry)
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      const int e = g * VW + k;
+      double C = sh.carry[e];
+      for (int ww = kResWaves - 1; ww > w; --ww) {
+        const double2 c = sh.wc[ww][e];
+        C = c.x + c.y * C;
+      }
+      x[k] = na[k] + np[k] * C;
+    }
+  } else {
+    // an early segment of a tile whose carry is not finite
+    bool patch = false;
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      if (!__builtin_isfinite(sh.carry[g * VW + k])) {
+        x[k] = __builtin_nan("");
+        patch = true;
+      }
+    }
+    if (patch) {
+#pragma unroll
+      for (int i = 0; i < L; ++i) {
+        if (i < nvalid) {
+#pragma unroll
+          for (int k = 0; k < VW; ++k)
+            if (x[k] != x[k]) r[i][k] = __builtin_nanf("");
+          const unsigned off = ((unsigned)(t0 + i) * n32 + (unsigned)env0) * 4u;
+          store_vec<VW>(at_byte(a.adv, off), r[i]);
+          if (a.ret) {
+            float rt[VW];
+#pragma unroll
+            for (int k = 0; k < VW; ++k) rt[k] = r[i][k] + v[i][k];
+            store_vec<VW>(at_byte(a.ret, off), rt);
+          }
+        }
+      }
+    }
+  }
+  if constexpr (kStats) {
+    // ---- the statistics partial, published before this workgroup's stores
+    double acc[3] = {(double)(nvalid * VW), 0.0, 0.0};
+#pragma unroll
+    for (int k = 0; k < VW; ++k) {
+      const double sa = sh.ssum[0][k][tid], sp = sh.ssum[1][k][tid];
+      const double saa = sh.ssum[2][k][tid], sap = sh.ssum[3][k][tid], spp = sh.ssum[4][k][tid];
+      acc[1] += sa + sp * x[k];
+      acc[2] += saa + 2.0 * sap * x[k] + spp * x[k] * x[k];
+    }
+    block_sum_lds<3>(acc);
+    if (tid == 0) {
+      uint64_t* pp = part + (size_t)blockIdx.x * 3;
+      slot_put(pp + 0, acc[0]);
+      slot_put(pp + 1, acc[1]);
+      slot_put(pp + 2, acc[2]);
+    }
+  }
+  if (!early && (!ctl || !PPO_GAE_RES_CTLSTATS)) segment_out(x);
+  RES_MARK(3);
+
+  if constexpr (kStats) {
+    if (ctl || !PPO_GAE_RES_CTLSTATS) {
+      // lane l sums partials l, l + 64, ... in order, then the wave sum: the
+      // same order in every workgroup, so all derive the same statistics
+      const int lane = tid % kWave;
+      double tot[3] = {0.0, 0.0, 0.0};
+      for (long u0 = 0; u0 < (long)gridDim.x; u0 += 4 * kWave) {
+        uint64_t wv[4][3];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const long u = u0 + q * kWave + lane;
+#pragma unroll
+          for (int c = 0; c < 3; ++c)
+            wv[q][c] = u < (long)gridDim.x ? __hip_atomic_load(part + (size_t)u * 3 + c,
+                                                               __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT)
+                                           : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const long u = u0 + q * kWave + lane;
+          if (u < (long)gridDim.x) {
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+              tot[c] += wv[q][c] ? slot_value(wv[q][c]) : slot_get(part + (size_t)u * 3 + c);
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 3; ++c) tot[c] = wave_sum(tot[c]);
+      if (lane == 0) {
+        // norm_params' formulas on these totals
+        const double n = tot[0];
+        const double mean = tot[1] / n;
+        float mean_f = (float)mean, std_f, mean_used, denom;
+        if (n > 1.0) {
+          const double m2 = tot[2] - tot[1] * mean;
+          std_f = (float)sqrt((m2 > 0.0 ? m2 : 0.0) / (n - 1.0));
+          mean_used = mean_f;
+          denom = std_f + (float)a.eps;
+        } else {
+          std_f = __builtin_nanf("");
+          mean_used = 0.0f;
+          denom = 1.0f;
+        }
+        sh.norm[0] = mean_used;
+        sh.norm[1] = denom;
+        if (blockIdx.x == 0) {
+          a.hdr->stats[0] = mean_used;
+          a.hdr->stats[1] = std_f;
+          a.hdr->stats[2] = denom;
+          if (a.stats_out) {
+            a.stats_out[0] = mean_f;
+            a.stats_out[1] = std_f;
+          }
+        }
+      }
+    }
+    lds_barrier();
+  }
+  RES_MARK(4);
+  if (ctl && (early || PPO_GAE_RES_CTLSTATS)) segment_out(x);  // after its polls
+  if constexpr (kStats) {
+    const float mean = sh.norm[0], denom = sh.norm[1];
+#pragma unroll
+    for (int i = 0; i < L; ++i) {
+      if (i < nvalid) {
+        const unsigned off = ((unsigned)(t0 + i) * n32 + (unsigned)env0) * 4u;
+        float y[VW];
+#pragma unroll
+        for (int k = 0; k < VW; ++k) y[k] = (r[i][k] - mean) / denom;
+        store_vec<VW>(at_byte(a.adv_n, off), y);
+      }
+    }
+  }
+  RES_MARK(5);
+}
+
+template <int E, int L>
+const void* res_kernel_el(bool stats, bool has_v) {
+  if (stats)
+    return has_v ? (const void*)gae_resident_kernel<E, L, true, true>
+                 : (const void*)gae_resident_kernel<E, L, true, false>;
+  return has_v ? (const void*)gae_resident_kernel<E, L, false, true>
+               : (const void*)gae_resident_kernel<E, L, false, false>;
+}
+
+const void* res_kernel(const ResPlan& rp, bool stats, bool has_v) {
+  if (rp.E == 64)
+    return rp.L == 16 ? res_kernel_el<64, 16>(stats, has_v)
+                      : (rp.L == 8 ? res_kernel_el<64, 8>(stats, has_v)
+                                   : res_kernel_el<64, 4>(stats, has_v));
+  return rp.L == 16 ? res_kernel_el<32, 16>(stats, has_v)
+                    : (rp.L == 8 ? res_kernel_el<32, 8>(stats, has_v)
+                                 : res_kernel_el<32, 4>(stats, has_v));
+}
+
+// Launches the resident pass when the plan applies and the whole grid fits
+// on the device at once; returns -1 (nothing launched) otherwise.
+// The environment variable PPO_AMD_GAE_RESIDENT=0 turns the resident pass
+// off (every rollout then takes the strip walk, span or tile passes), so that
+// those paths can be tested on shapes the resident pass would take.
+bool resident_ok(long T, long N, bool norm, bool has_v) {
+  const char* env = getenv("PPO_AMD_GAE_RESIDENT");
+  if (env && env[0] == '0') return false;
+  const ResPlan rp = res_plan(T, N);
+  if (rp.E == 0) return false;
+  return resident_blocks(res_kernel(rp, norm, has_v), kResBlock, 0, 0) >= rp.tiles();
+}
+
+int launch_resident(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
+  if (!resident_ok(T, N, norm, a.v != nullptr)) return -1;
+  const ResPlan rp = res_plan(T, N);
+  const void* kern = res_kernel(rp, norm, a.v != nullptr);
+  a.res_nc = rp.nc;
+  a.res_nt = rp.nt;
+  // a different tag for every call (zero is skipped)
+  static std::atomic<unsigned> calls{0x5bd1e995u};
+  unsigned nonce;
+  do {
+    nonce = calls.fetch_add(0x9e3779b9u, std::memory_order_relaxed);
+  } while (nonce == 0u);
+  a.nonce = nonce;
+  void* args[] = {&a};
+  return hip_status(
+      hipLaunchKernel(kern, dim3((unsigned)rp.tiles()), dim3(kResBlock), args, 0, stream));
+}
+
 // Pass kernels by (VW, L, solo) geometry.
 template <int kMode>
 const void* tile_kernel(int vw, const PassGeom& g) {
@@ -1631,6 +2313,22 @@ int launch_gae(const GaePlan& p, GaeArgs a, bool norm, hipStream_t stream) {
                           a.stats_out, stream);
 }
 
+// Narrow rollouts without the normaliser (16 <= N < 1024) take the
+// one-env-per-thread tiles even when aligned: measured 10-13% faster for
+// N = 16-256 (config 3: 107.7 -> 97.4 us), while N = 4 is 40% slower.
+bool narrow_scalar(long T, long N, bool norm) { return !norm && N >= 16 && N / 4 < kBlock; }
+
+// Aligned rollouts too narrow for the strip walk take the span passes when
+// normalising or narrower than 64 envs (measured on MI355X, us, span vs tile
+// passes: N=4 x T=4M 92 vs 250, N=16 x T=1M 87 vs 98; with the normaliser
+// 122 vs 411, 118 vs 145, and 117-122 vs 122-125 for N = 64-1024; without it
+// N = 64-1024 are within 2%, and below 2^20 elements the tile passes'
+// launches are ~1.5 us shorter).
+bool span_route(long T, long N, bool norm) {
+  return PPO_GAE_SPAN && span_plan(T, N, kSpanMaxBlocks).E > 0 &&
+         strip_plan(make_plan(T, N, 4)).E == 0 && (norm || (N < 64 && T * N >= (1L << 20)));
+}
+
 int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
              const float* last_value, int64_t T, int64_t N, double gamma, double lam, double eps,
              float* adv_out, float* ret_out, float* adv_norm_out, float* stats_out, bool norm,
@@ -1646,11 +2344,7 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
   const bool vec = (N % 4 == 0) && aligned(rewards, 16) && (!values || aligned(values, 16)) &&
                    aligned(adv_out, 16) && (!ret_out || aligned(ret_out, 16)) &&
                    aligned(dones, 4) && (!last_value || aligned(last_value, 16));
-  // Narrow rollouts without the normaliser (16 <= N < 1024) take the
-  // one-env-per-thread tiles even when aligned: measured 10-13% faster for
-  // N = 16-256 (config 3: 107.7 -> 97.4 us), while N = 4 is 40% slower.
-  const bool narrow1 = !norm && N >= 16 && N / 4 < kBlock;
-  const GaePlan p = make_plan(T, N, vec && !narrow1 ? 4 : 1);
+  const GaePlan p = make_plan(T, N, vec && !narrow_scalar(T, N, norm) ? 4 : 1);
   if (p.blocks() > 0x7fffffffL || make_carry_plan(p.Tt, N).nchunks > 65535)
     return PPO_ERR_TOO_LARGE;
   const GaeLayout l = make_layout(p, N);
@@ -1676,21 +2370,33 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
   a.eps = eps;
   a.adv_n = adv_norm_out;
   a.tstat = reinterpret_cast<float*>(ws + l.tstat);
+  a.slots = reinterpret_cast<uint64_t*>(ws + l.slots);
 
-  // Aligned rollouts too narrow for the strip walk take the span passes when
-  // normalising or narrower than 64 envs (measured on MI355X, us, span vs
-  // tile passes: N=4 x T=4M 92 vs 250, N=16 x T=1M 87 vs 98; with the
-  // normaliser 122 vs 411, 118 vs 145, and 117-122 vs 122-125 for N = 64-1024;
-  // without it N = 64-1024 are within 2%, and below 2^20 elements the tile
-  // passes' launches are ~1.5 us shorter).
-  if (PPO_GAE_SPAN && vec && span_plan(T, N, kSpanMaxBlocks).E > 0 &&
-      strip_plan(make_plan(T, N, 4)).E == 0 && (norm || (N < 64 && T * N >= (1L << 20))))
-    return launch_span(T, N, a, norm, stream);
+  // Aligned rollouts whose tiles all fit on the device at once take the
+  // resident pass (one read of the rollout, one write of each output).
+  if (vec && (!norm || aligned(adv_norm_out, 16))) {
+    const int st = launch_resident(T, N, a, norm, stream);
+    if (st >= 0) return st;
+  }
+
+  if (vec && span_route(T, N, norm)) return launch_span(T, N, a, norm, stream);
   return launch_gae(p, a, norm, stream);
 }
 
 }  // namespace
 }  // namespace ppo
+
+extern "C" int ppo_gae_route(int64_t T, int64_t N, int normalize, int has_values) {
+  using namespace ppo;
+  if (T <= 0 || N <= 0) return PPO_GAE_ROUTE_NONE;
+  const bool norm = normalize != 0;
+  if (N > (1L << 31) || T > (1L << 40) || T * N > (1L << 50)) return PPO_GAE_ROUTE_NONE;
+  const bool vec = N % 4 == 0;
+  if (vec && resident_ok(T, N, norm, has_values != 0)) return PPO_GAE_ROUTE_RESIDENT;
+  if (vec && span_route(T, N, norm)) return PPO_GAE_ROUTE_SPAN;
+  const GaePlan p = make_plan(T, N, vec && !narrow_scalar(T, N, norm) ? 4 : 1);
+  return strip_plan(p).E > 0 ? PPO_GAE_ROUTE_STRIP : PPO_GAE_ROUTE_TILES;
+}
 
 extern "C" size_t ppo_gae_workspace_bytes(int64_t T, int64_t N) {
   using namespace ppo;
@@ -1717,3 +2423,11 @@ extern "C" int ppo_gae_norm_f32(const float* rewards, const float* values, const
                        ret_out, adv_norm_out, stats_out, true, workspace, workspace_bytes,
                        stream);
 }
+
+#ifdef PPO_GAE_RES_TRACE
+extern "C" void* ppo_debug_res_trace(void) {
+  void* p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(ppo::g_res_trace)) != hipSuccess) return nullptr;
+  return p;
+}
+#endif

@@ -55,6 +55,8 @@ class Mlp3(ctypes.Structure):
     ]
 
 
+GAE_ROUTES = {0: "none", 1: "resident", 2: "strip", 3: "span", 4: "tiles"}
+
 PPO_ACT_RELU = 0
 PPO_ACT_TANH = 1
 PPO_ERR_UNSUPPORTED = 4
@@ -74,6 +76,7 @@ SIGNATURES = {
     "ppo_amd_version": (_int, []),
     "ppo_amd_strerror": (ctypes.c_char_p, [_int]),
     "ppo_gae_workspace_bytes": (_sz, [_i64, _i64]),
+    "ppo_gae_route": (_int, [_i64, _i64, _int, _int]),
     "ppo_gae_f32": (
         _int,
         [_vp, _vp, _vp, _vp, _i64, _i64, _f64, _f64, _vp, _vp, _vp, _sz, _vp],
