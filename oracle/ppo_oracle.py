@@ -521,15 +521,35 @@ CARTPOLE = dict(gravity=9.8, masscart=1.0, masspole=0.1, length=0.5, force_mag=1
                 x_threshold=2.4)
 
 
+def _cartpole_dynamics(state4, action):
+    """One explicit-Euler step of gymnasium's CartPoleEnv (the reference's
+    environment, rl/deep/cli.py:179-180) in Python floats: (x, x_dot, theta,
+    theta_dot, terminated)."""
+    c = CARTPOLE
+    total_mass = c["masspole"] + c["masscart"]
+    polemass_length = c["masspole"] * c["length"]
+    theta_threshold = 12 * 2 * math.pi / 360
+    x, x_dot, theta, theta_dot = (float(v) for v in state4)
+    force = c["force_mag"] if action == 1 else -c["force_mag"]
+    costheta, sintheta = math.cos(theta), math.sin(theta)
+    temp = (force + polemass_length * (theta_dot * theta_dot) * sintheta) / total_mass
+    thetaacc = (c["gravity"] * sintheta - costheta * temp) / (
+        c["length"] * (4.0 / 3.0 - c["masspole"] * (costheta * costheta) / total_mass))
+    xacc = temp - polemass_length * thetaacc * costheta / total_mass
+    x = x + c["tau"] * x_dot
+    x_dot = x_dot + c["tau"] * xacc
+    theta = theta + c["tau"] * theta_dot
+    theta_dot = theta_dot + c["tau"] * thetaacc
+    term = (x < -c["x_threshold"] or x > c["x_threshold"]
+            or theta < -theta_threshold or theta > theta_threshold)
+    return x, x_dot, theta, theta_dot, term
+
+
 def cartpole_step_reference(state, actions, steps, reset_uniforms, max_steps=500):
     """One step of N environments in Python floats (fp64), each operation
     rounded on its own: returns (next_state [N,4] f64 after same-step resets,
     obs [N,4] f32, rewards [N] f32, dones [N] u8, terminated [N] u8, steps
     [N] int32)."""
-    c = CARTPOLE
-    total_mass = c["masspole"] + c["masscart"]
-    polemass_length = c["masspole"] * c["length"]
-    theta_threshold = 12 * 2 * math.pi / 360
     state = np.asarray(state, np.float64)
     N = state.shape[0]
     nxt = np.empty_like(state)
@@ -537,19 +557,7 @@ def cartpole_step_reference(state, actions, steps, reset_uniforms, max_steps=500
     term_out = np.zeros(N, np.uint8)
     steps_out = np.zeros(N, np.int32)
     for n in range(N):
-        x, x_dot, theta, theta_dot = (float(v) for v in state[n])
-        force = c["force_mag"] if int(actions[n]) == 1 else -c["force_mag"]
-        costheta, sintheta = math.cos(theta), math.sin(theta)
-        temp = (force + polemass_length * (theta_dot * theta_dot) * sintheta) / total_mass
-        thetaacc = (c["gravity"] * sintheta - costheta * temp) / (
-            c["length"] * (4.0 / 3.0 - c["masspole"] * (costheta * costheta) / total_mass))
-        xacc = temp - polemass_length * thetaacc * costheta / total_mass
-        x = x + c["tau"] * x_dot
-        x_dot = x_dot + c["tau"] * xacc
-        theta = theta + c["tau"] * theta_dot
-        theta_dot = theta_dot + c["tau"] * thetaacc
-        term = (x < -c["x_threshold"] or x > c["x_threshold"]
-                or theta < -theta_threshold or theta > theta_threshold)
+        x, x_dot, theta, theta_dot, term = _cartpole_dynamics(state[n], int(actions[n]))
         t = int(steps[n]) + 1
         done = term or t >= max_steps
         if done:
@@ -559,6 +567,128 @@ def cartpole_step_reference(state, actions, steps, reset_uniforms, max_steps=500
             nxt[n] = (x, x_dot, theta, theta_dot)
         dones[n], term_out[n], steps_out[n] = done, term, 0 if done else t
     return (nxt, nxt.astype(np.float32), np.ones(N, np.float32), dones, term_out, steps_out)
+
+
+class CartPoleHost:
+    """A single CartPole-v1 environment with gymnasium's API as the runner
+    uses it (rl/deep/runner.py:52-84): reset(seed) -> (obs, info), step(a) ->
+    (obs, 1.0, terminated, truncated, info), no automatic reset, truncation
+    at 500 steps; observation_space.shape == (4,), action_space.n == 2 and
+    action_space.seed().  The dynamics are _cartpole_dynamics; the reset state
+    is U(-0.05, 0.05)^4 from numpy's default_rng(seed) (gymnasium draws it from
+    its own PCG64 stream, which is not reproduced here)."""
+
+    class _Space:
+        def __init__(self, shape=None, n=None):
+            self.shape, self.n = shape, n
+
+        def seed(self, seed=None):
+            return [seed]
+
+    def __init__(self, max_steps: int = 500):
+        self.observation_space = self._Space(shape=(4,))
+        self.action_space = self._Space(n=2)
+        self.max_steps = max_steps
+        self.state = np.zeros(4)
+        self.steps = 0
+
+    def reset(self, seed=None):
+        self.state = np.random.default_rng(seed).uniform(-0.05, 0.05, size=4)
+        self.steps = 0
+        return self.state.astype(np.float32), {}
+
+    def step(self, action):
+        x, x_dot, theta, theta_dot, term = _cartpole_dynamics(self.state, int(action))
+        self.state = np.array([x, x_dot, theta, theta_dot])
+        self.steps += 1
+        trunc = not term and self.steps >= self.max_steps
+        return self.state.astype(np.float32), 1.0, bool(term), bool(trunc), {}
+
+
+def reference_mlp(input_size: int, hidden_size: int, output_size: int) -> nn.Module:
+    """MLP of rl/deep/agents/common.py:16-28: Linear-ReLU-Linear-ReLU-Linear,
+    constructed in the same order (so one seed gives the same weights)."""
+    return nn.Sequential(
+        nn.Linear(input_size, hidden_size), nn.ReLU(),
+        nn.Linear(hidden_size, hidden_size), nn.ReLU(),
+        nn.Linear(hidden_size, output_size),
+    )
+
+
+class ReferenceAgent:
+    """PPOAgent of rl/deep/agents/ppo.py:38-171 on the CPU for a CartPole-like
+    env: the same seeding (:47), weight construction order, Adam, action
+    sampling from a CPU Categorical on the global generator (:65-79), rollout
+    bookkeeping (:81-111) and reference_update at the end of an episode."""
+
+    name = "ppo"
+
+    def __init__(self, hidden_size: int = 128, batch_size: int = 128, seed: int = 24,
+                 config: OracleConfig | None = None):
+        torch.manual_seed(seed)                                          # :47
+        self.config = config or OracleConfig(batch_size=batch_size)
+        self.policy = reference_mlp(4, hidden_size, 2)                   # :52
+        self.value = reference_mlp(4, hidden_size, 1)                    # :53
+        self.optimizer = torch.optim.Adam(
+            list(self.policy.parameters()) + list(self.value.parameters()), lr=self.config.lr)
+        self.rollout, self.pending = [], None
+
+    def start_episode(self, episode: int) -> None:                      # :61-63
+        self.rollout, self.pending = [], None
+
+    @torch.no_grad()
+    def select_action(self, observation, training: bool = True) -> int:  # :65-79
+        obs = torch.as_tensor(observation, dtype=torch.float32)
+        logits = self.policy(obs)
+        if not training:
+            return int(torch.argmax(logits).item())
+        dist = Categorical(logits=logits)
+        action = dist.sample()
+        self.pending = (dist.log_prob(action), self.value(obs).squeeze())
+        return int(action.item())
+
+    def update(self, observation, action, reward, next_observation, terminated,
+               truncated) -> None:                                       # :81-107
+        if self.pending is None:
+            return
+        self.rollout.append((observation, action, reward, bool(terminated or truncated),
+                             self.pending[0], self.pending[1]))
+        self.pending = None
+
+    def end_episode(self) -> None:                                       # :109-111
+        if not self.rollout:
+            return
+        obs = torch.as_tensor(np.array([s[0] for s in self.rollout]), dtype=torch.float32)
+        actions = torch.as_tensor([s[1] for s in self.rollout], dtype=torch.int64)
+        lps = torch.stack([s[4] for s in self.rollout])
+        vals = torch.stack([s[5] for s in self.rollout])
+        reference_update(self.policy, self.value, self.optimizer, obs, actions, lps, vals,
+                         [s[2] for s in self.rollout], [s[3] for s in self.rollout],
+                         self.config)
+
+
+def run_episode(env, agent, episode: int, seed: int, training: bool):
+    """rl/deep/runner.py:42-84 (_run_episode): returns (return, length,
+    terminated, truncated)."""
+    observation, _ = env.reset(seed=seed + episode)
+    env.action_space.seed(seed + episode)
+    observation = np.asarray(observation, dtype=np.float32)
+    agent.start_episode(episode)
+    episode_return, length = 0.0, 0
+    while True:
+        action = agent.select_action(observation, training=training)
+        next_observation, reward, terminated, truncated, _ = env.step(action)
+        next_observation = np.asarray(next_observation, dtype=np.float32)
+        if training:
+            agent.update(observation, action, float(reward), next_observation, terminated,
+                         truncated)
+        episode_return += float(reward)
+        length += 1
+        observation = next_observation
+        if terminated or truncated:
+            break
+    agent.end_episode()
+    return episode_return, length, bool(terminated), bool(truncated)
 
 
 # ---------------------------------------------------------------------------

@@ -121,3 +121,195 @@ def test_vec_update_matches_reference(dev):
                          generator=torch.Generator().manual_seed(7))
     for a, b in zip(vec.parameters, list(cpu_policy.parameters()) + list(cpu_value.parameters())):
         torch.testing.assert_close(a.detach().cpu(), b.detach(), rtol=0, atol=2e-5)
+
+
+# ---------------------------------------------------------------------------
+# The drop-in agent driven the way the reference's runner drives it
+# ---------------------------------------------------------------------------
+def test_agent_drives_like_reference_runner(dev):
+    """rl/deep/tests/test_runner.py:9-25 for the GPU agent: 16 training
+    episodes and 4 evaluation episodes of single-env CartPole through
+    start_episode / select_action / update / end_episode (runner.py:42-84),
+    with the test's config (hidden 16, batch 4, seed 24) and its assertions.
+    The same episodes are then run by the CPU restatement of the reference
+    agent (oracle.ReferenceAgent) from the same seed: both consume the global
+    CPU generator identically (Categorical sampling, torch.randperm), so the
+    trajectories agree step for step and the parameters to fp32 noise."""
+    config = TrainingConfig(batch_size=4, warmup_steps=4, hidden_size=16, seed=24)
+    print("runner-style: GPU agent", flush=True)
+    env = ref.CartPoleHost()
+    agent = PPOAgent(env, config, device=dev)
+    train = [ref.run_episode(env, agent, ep, config.seed, training=True) for ep in range(16)]
+    evals = [ref.run_episode(ref.CartPoleHost(), agent, ep, config.seed, training=False)
+             for ep in range(4)]
+    assert train[0][2] or train[0][3]
+    assert np.mean([e[0] for e in evals]) >= 8
+    term = np.mean([e[2] for e in evals])
+    success = np.mean([e[3] for e in evals])
+    assert term + success == 1.0
+
+    print("runner-style: CPU reference agent", flush=True)
+    cpu_env = ref.CartPoleHost()
+    cpu = ref.ReferenceAgent(hidden_size=16, batch_size=4, seed=24)
+    cpu_train = [ref.run_episode(cpu_env, cpu, ep, 24, training=True) for ep in range(16)]
+    cpu_evals = [ref.run_episode(ref.CartPoleHost(), cpu, ep, 24, training=False)
+                 for ep in range(4)]
+    assert [t[:2] for t in train] == [t[:2] for t in cpu_train]
+    assert [t[:2] for t in evals] == [t[:2] for t in cpu_evals]
+    cpu_params = list(cpu.policy.parameters()) + list(cpu.value.parameters())
+    worst = max(float((a.detach().cpu() - b.detach()).abs().max())
+                for a, b in zip(agent.parameters, cpu_params))
+    print(f"  {sum(t[1] for t in train)} training steps; max |param diff| {worst:.2e}",
+          flush=True)
+    for a, b in zip(agent.parameters, cpu_params):
+        torch.testing.assert_close(a.detach().cpu(), b.detach(), rtol=0, atol=1e-6)
+
+
+def test_agent_minibatch_indices_follow_randperm(dev, monkeypatch):
+    """ppo.py:129-139: the rows _update hands to _update_batch are the slices
+    of torch.randperm drawn on the global CPU generator, epoch by epoch, bit
+    for bit.  Each step's observation carries its own index."""
+    T, B = 30, 7
+    config = TrainingConfig(hidden_size=16, batch_size=B)
+    agent = PPOAgent(cartpole_like(), config, device=dev)
+    agent.rollout = [
+        _rollout_step(1.0, t == T - 1, np.array([t, 0, 0, 0], np.float32), t % 2, -0.7, 0.1)
+        for t in range(T)
+    ]
+    seen = []
+    monkeypatch.setattr(agent, "_update_batch",
+                        lambda obs, *a, **k: seen.append(obs[:, 0].cpu().to(torch.int64)))
+    torch.manual_seed(99)
+    agent._update()
+    torch.manual_seed(99)
+    expected = []
+    for _ in range(agent.ppo_config.epochs):
+        idx = torch.randperm(T)
+        expected += [idx[s : s + B] for s in range(0, T, B)]
+    assert len(seen) == len(expected)
+    for a, b in zip(seen, expected):
+        assert torch.equal(a, b)
+
+
+def test_agent_rejects_out_of_range_actions_without_syncing(dev):
+    agent = PPOAgent(cartpole_like(), TrainingConfig(hidden_size=16), device=dev)
+    agent.rollout = [_rollout_step(1.0, False, action=0), _rollout_step(1.0, True, action=2)]
+    with pytest.raises(ValueError, match="support"):
+        agent._update()
+
+
+def test_agent_advantages_with_non_representable_rewards(dev):
+    """Rewards that fp32 cannot hold (0.1, 0.3, ...) enter the kernel rounded
+    to fp32: the advantages stay within max|r| * 2^-24 / (1 - gamma*lambda)
+    (plus one fp32 ulp of the result) of the reference's Python-float loop
+    (ppo.py:173-193), the bound PPOAgent._advantages states."""
+    config = TrainingConfig(hidden_size=16)
+    pcfg = PPOConfig()
+    agent = PPOAgent(cartpole_like(), config, pcfg, device=dev)
+    g = torch.Generator().manual_seed(3)
+    T = 500
+    rewards = [round(0.1 * int(k), 1) for k in torch.randint(-9, 10, (T,), generator=g)]
+    values = torch.randn(T, generator=g)
+    dones = [bool(x) for x in (torch.rand(T, generator=g) < 0.02)] + [True]
+    dones = dones[:T]
+    agent.rollout = [_rollout_step(r, dn, value=float(v)) for r, dn, v in zip(rewards, dones, values)]
+    got = agent._advantages(values).cpu().double()
+    want = torch.tensor(ref.advantages_python(rewards, dones, [float(v) for v in values],
+                                              config.gamma, pcfg.gae_lambda), dtype=torch.float64)
+    bound = max(abs(r) for r in rewards) * 2.0**-24 / (1 - config.gamma * pcfg.gae_lambda)
+    ulp = want.abs() * 2.0**-23
+    err = (got - want).abs()
+    print(f"  max |adv - reference| {float(err.max()):.2e} (bound {bound:.2e})", flush=True)
+    assert bool((err <= bound + ulp).all())
+
+
+def test_agent_vf_clip_uses_rollout_values(dev, monkeypatch):
+    """PPOConfig.vf_clip (a field the reference does not have) carries the
+    rollout's values into _update_batch: one minibatch's raw gradients match
+    update_batch_grads_reference with value clipping; without the old values
+    _update_batch refuses."""
+    T, H = 64, 32
+    config = TrainingConfig(hidden_size=H, batch_size=T)
+    pcfg = PPOConfig(vf_clip=0.2, gradient_clip=1e9)
+    agent = PPOAgent(cartpole_like(), config, pcfg, device=dev)
+    cpu_policy = copy.deepcopy(agent.policy).cpu()
+    cpu_value = copy.deepcopy(agent.value).cpu()
+    g = torch.Generator().manual_seed(4)
+    obs = torch.randn(T, 4, generator=g)
+    acts = torch.randint(0, 2, (T,), generator=g)
+    lps = -torch.rand(T, generator=g)
+    adv = torch.randn(T, generator=g)
+    ret = torch.randn(T, generator=g)
+    with torch.no_grad():
+        old_v = cpu_value(obs).squeeze(1) + 0.3 * torch.randn(T, generator=g)
+    monkeypatch.setattr(agent.optimizer, "step", lambda: None)
+    with pytest.raises(ValueError, match="old_values"):
+        agent._update_batch(obs.to(dev), acts.to(dev), lps.to(dev), adv.to(dev), ret.to(dev))
+    agent._update_batch(obs.to(dev), acts.to(dev), lps.to(dev), adv.to(dev), ret.to(dev),
+                        old_values=old_v.to(dev))
+    o = ref.update_batch_grads_reference(cpu_policy, cpu_value, obs, acts, lps, adv, ret,
+                                         old_values=old_v, vf_clip=0.2)
+    for p, gref in zip(agent.parameters, o["grads"]):
+        torch.testing.assert_close(p.grad.cpu(), gref, rtol=1e-4, atol=1e-5 * float(gref.abs().max()))
+    # and a whole _update runs with vf_clip set
+    agent.rollout = [_rollout_step(1.0, t == 19, value=0.1 * t) for t in range(20)]
+    agent._update()
+
+
+# ---------------------------------------------------------------------------
+# BASELINE config 1 at its own shape: T=128 x N=8, 4-64-64 tanh, minibatches
+# of 256, 4 epochs, through every VecPPO update path, against the CPU oracle
+# (two rollouts in a row, so the graph path replays captured graphs).
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("mode", ["unfused", "fused_mlp", "graphs"])
+def test_vec_update_config1_matches_reference(dev, mode):
+    T, N, H, MB = 128, 8, 64, 256
+    torch.manual_seed(24)
+    policy = MLP(4, H, 2, "tanh")
+    value = MLP(4, H, 1, "tanh")
+    cpu_policy, cpu_value = copy.deepcopy(policy), copy.deepcopy(value)
+    cpu_opt = torch.optim.Adam(list(cpu_policy.parameters()) + list(cpu_value.parameters()),
+                               lr=3e-4)
+    kw = {"unfused": dict(fused_update=False),
+          "fused_mlp": dict(fused_mlp=True),
+          "graphs": dict(fused_mlp=True, graphs=True)}[mode]
+    vec = ppo_amd.VecPPO(policy.to(dev), value.to(dev), PPOConfig(), gamma=0.99, lr=3e-4,
+                         batch_size=MB, generator=torch.Generator().manual_seed(7), **kw)
+    cpu_gen = torch.Generator().manual_seed(7)
+    buf = ppo_amd.RolloutBuffer(T, N, (4,), device=dev)
+    for rollout in range(2):
+        print(f"config1 mode={mode} rollout={rollout}", flush=True)
+        g = torch.Generator().manual_seed(50 + rollout)
+        obs = (torch.rand(T, N, 4, generator=g) - 0.5) * 0.1
+        with torch.no_grad():
+            logits = cpu_policy(obs)
+            acts = torch.multinomial(torch.softmax(logits.reshape(-1, 2), -1), 1,
+                                     generator=g).reshape(T, N)
+            lps = torch.log_softmax(logits, -1).gather(2, acts[..., None]).squeeze(2)
+            vals = cpu_value(obs).squeeze(2)
+        rewards = torch.ones(T, N)
+        dones = (torch.rand(T, N, generator=g) < 1 / 200).to(torch.uint8)
+        last_v = torch.randn(N, generator=g)
+        buf.reset()
+        for t in range(T):
+            buf.add(obs[t].to(dev), acts[t].to(torch.int32).to(dev), rewards[t].to(dev),
+                    dones[t].to(dev), vals[t].to(dev), lps[t].to(dev))
+        buf.finish(last_v.to(dev))
+        vec.update(buf)
+        torch.cuda.synchronize()
+
+        adv, ret = ref.gae_numpy(rewards.numpy(), vals.numpy(), dones.numpy(), last_v.numpy(),
+                                 0.99, 0.95)
+        adv_n = ref.normalize_reference(torch.from_numpy(adv).reshape(-1))
+        ref.reference_epochs(cpu_policy, cpu_value, cpu_opt, obs.reshape(-1, 4),
+                             acts.reshape(-1), lps.reshape(-1), adv_n,
+                             torch.from_numpy(ret).reshape(-1),
+                             ref.OracleConfig(batch_size=MB), generator=cpu_gen)
+        cpu_params = list(cpu_policy.parameters()) + list(cpu_value.parameters())
+        worst = max(float((a.detach().cpu() - b.detach()).abs().max())
+                    for a, b in zip(vec.parameters, cpu_params))
+        print(f"  max |param diff| {worst:.2e}", flush=True)
+        for a, b in zip(vec.parameters, cpu_params):
+            torch.testing.assert_close(a.detach().cpu(), b.detach(), rtol=0, atol=2e-5)
+    if mode == "graphs":
+        assert vec.update_graphed_ready()

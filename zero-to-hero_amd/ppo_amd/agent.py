@@ -221,20 +221,22 @@ class PPOAgent:
             np.array([step.transition.observation for step in self.rollout]),
             dtype=torch.float32,
         ).to(dev)
-        actions = torch.as_tensor(
+        actions_host = torch.as_tensor(
             [step.transition.action for step in self.rollout], dtype=torch.int64
-        ).to(dev)
-        old_log_probs = torch.stack([step.log_prob for step in self.rollout]).to(dev)
-        old_values = torch.stack([step.value for step in self.rollout]).to(
-            device=dev, dtype=torch.float32
         )
         action_count = self.policy.net[-1].out_features
-        if bool(((actions < 0) | (actions >= action_count)).any()):
-            # torch.distributions' support check raises this inside :151
+        # checked on the host copy (no device synchronisation); torch.
+        # distributions' support check raises this inside :151
+        if bool(((actions_host < 0) | (actions_host >= action_count)).any()):
             raise ValueError(
                 "The value argument must be within the support of the categorical "
                 f"distribution (actions in [0, {action_count}))"
             )
+        actions = actions_host.to(dev)
+        old_log_probs = torch.stack([step.log_prob for step in self.rollout]).to(dev)
+        old_values = torch.stack([step.value for step in self.rollout]).to(
+            device=dev, dtype=torch.float32
+        )
         advantages = self._advantages(old_values)
         returns = advantages + old_values
 
@@ -245,12 +247,17 @@ class PPOAgent:
             indices = torch.randperm(len(actions))
             for start in range(0, len(actions), self.config.batch_size):
                 batch_indices = indices[start : start + self.config.batch_size].to(dev)
+                extra = {}
+                if self.ppo_config.vf_clip is not None:
+                    # the clipped value loss needs the rollout's values
+                    extra["old_values"] = old_values[batch_indices]
                 self._update_batch(
                     observations[batch_indices],
                     actions[batch_indices],
                     old_log_probs[batch_indices],
                     advantages[batch_indices],
                     returns[batch_indices],
+                    **extra,
                 )
 
     def _update_batch(
@@ -260,10 +267,15 @@ class PPOAgent:
         old_log_probs: torch.Tensor,
         advantages: torch.Tensor,
         returns: torch.Tensor,
+        old_values: Optional[torch.Tensor] = None,
     ) -> None:
         """ppo.py:141-171: MLP forwards in torch, the fused loss kernel for
         the loss and its gradient, then backward through the MLPs,
-        clip_grad_norm_ and Adam."""
+        clip_grad_norm_ and Adam.  `old_values` (the rollout's values of the
+        minibatch rows) is needed only with PPOConfig.vf_clip, which the
+        reference does not have; ValueError if it is missing then."""
+        if self.ppo_config.vf_clip is not None and old_values is None:
+            raise ValueError("PPOConfig.vf_clip needs the minibatch's old_values")
         logits = self.policy(observations)
         values = self.value(observations).squeeze(1)
         loss, _ = ops.ppo_loss_discrete(
@@ -277,7 +289,7 @@ class PPOAgent:
             vf_clip=self.ppo_config.vf_clip,
             value_coef=self.ppo_config.value_coef,
             entropy_coef=self.ppo_config.entropy_coef,
-            old_values=None,
+            old_values=None if old_values is None else old_values.contiguous(),
         )
         self.optimizer.zero_grad()
         loss.backward()
@@ -286,7 +298,16 @@ class PPOAgent:
 
     def _advantages(self, values: torch.Tensor) -> torch.Tensor:
         """ppo.py:173-193 on the GPU: one env, no bootstrap, `terminated or
-        truncated` as the done flag.  Returns fp32 advantages on the device."""
+        truncated` as the done flag.  Returns fp32 advantages on the device.
+
+        The recurrence runs in fp64 in the reference's operation order, but
+        the rewards enter as fp32 (the kernel's rollout layout): a reward that
+        fp32 represents exactly (CartPole's 1.0, any integer, any multiple of
+        a power of two) gives the reference's advantages bit for bit; any
+        other reward r is off by at most |r| * 2^-24, so an advantage moves by
+        at most max|r| * 2^-24 / (1 - gamma * lambda), i.e. relative ~1e-6
+        for gamma = 0.99, lambda = 0.95 (tests/test_gpu_agent.py checks the
+        bound with rewards of 0.1)."""
         rewards = torch.tensor(
             [step.transition.reward for step in self.rollout], dtype=torch.float32
         )
