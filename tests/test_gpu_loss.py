@@ -7,6 +7,7 @@ with an absolute floor of 1e-5 * max|g_ref| for elements near zero (the
 gradient of a softmax row sums to zero, so some entries are cancellations).
 """
 
+import math
 import os
 
 import numpy as np
@@ -28,16 +29,23 @@ def assert_grad_close(got, expect, rtol=1e-4, floor=1e-5):
     torch.testing.assert_close(got, expect, rtol=rtol, atol=atol)
 
 
-def clip_edge_rows(ratio, clip=0.2, band=1e-5):
-    """Rows whose oracle ratio lies within `band` (relative) of a clip bound
-    1 -/+ clip.  The clipped surrogate's gradient is discontinuous there: a
-    log-prob summed in another order (torch's vectorised reduction against
-    the kernel's dim loop) moves the ratio by an ulp or so and can put the row
-    on the other side, switching its whole policy gradient on or off.  Such
-    rows are left out of the element-wise gradient comparison (and widen the
-    clipfrac tolerance by their count); every other row is held to the bar."""
+EDGE_ULPS = 8
+
+
+def clip_edge_rows(ratio, lp, old_lp, clip=0.2, ulps=EDGE_ULPS):
+    """Rows whose oracle ratio lies within `ulps` fp32 ulps of the log-probs
+    (relative) of a clip bound 1 -/+ clip.  The clipped surrogate's gradient
+    is discontinuous there: a log-prob summed in another order (torch's
+    vectorised reduction against the kernel's dim loop) moves lp by an ulp or
+    so, hence the ratio by that much relative, and can put the row on the
+    other side of the bound, switching its policy gradient between the
+    unclipped value, half of it (torch.minimum's tie) and zero.  Such rows
+    are checked against those one-sided gradients (assert_edge_rows) instead
+    of the oracle's own choice; every other row is held to the usual bar."""
     r = ratio.detach().cpu().double()
-    return ((r - (1.0 - clip)).abs() < band * r) | ((r - (1.0 + clip)).abs() < band * r)
+    m = torch.maximum(lp.detach().cpu().double().abs(), old_lp.detach().cpu().double().abs())
+    band = ulps * m.clamp_min(1.0) * 2.0**-23
+    return ((r - (1.0 - clip)).abs() <= band * r) | ((r - (1.0 + clip)).abs() <= band * r)
 
 
 def assert_rows_close(got, expect, edge):
@@ -45,7 +53,46 @@ def assert_rows_close(got, expect, edge):
     got = got.detach().cpu().double()
     expect = expect.detach().cpu().double()
     assert_grad_close(got[keep], expect[keep])
-    print(f"  {int(edge.sum())} of {edge.numel()} rows within 1e-5 of a clip bound", flush=True)
+    print(f"  {int(edge.sum())} of {edge.numel()} rows within {EDGE_ULPS} ulps of a clip bound",
+          flush=True)
+
+
+def assert_edge_rows(got, candidates, edge, floor):
+    """Each edge row equals one of its one-sided gradients: candidates is
+    [k, n_edge, width] (k = clipped, tie, unclipped), compared at the usual
+    per-element bar (rel 1e-4, absolute floor `floor`)."""
+    if not bool(edge.any()):
+        return
+    g = got.detach().cpu().double()[edge]
+    err = (g[None] - candidates).abs()
+    lim = 1e-4 * candidates.abs() + floor
+    ok = (err <= lim).all(dim=2).any(dim=0)
+    assert bool(ok.all()), f"{int((~ok).sum())} edge rows match no one-sided gradient"
+
+
+def cat_edge_candidates(logits, actions, adv, ratio, edge, ec=0.01):
+    """d loss / d logits of the edge rows with the policy term's lp-gradient
+    g in {0, -A r / 2, -A r} (clipped, tie, unclipped) and the entropy term,
+    in fp64: [g (onehot - p) + ec p (log p + H)] / B."""
+    B = logits.shape[0]
+    z = logits.detach().cpu().double()[edge]
+    logp = torch.log_softmax(z, -1)
+    p = logp.exp()
+    H = -(p * logp).sum(1, keepdim=True)
+    onehot = torch.nn.functional.one_hot(actions.long().cpu()[edge], z.shape[1]).double()
+    ent = ec * p * (logp + H)
+    full = (-adv.cpu().double()[edge] * ratio.detach().cpu().double()[edge])[:, None]
+    return torch.stack([(g * (onehot - p) + ent) / B for g in (0.0 * full, 0.5 * full, full)])
+
+
+def gauss_edge_candidates(mu, log_std, acts, adv, ratio, edge):
+    """d loss / d mu of the edge rows for g in {0, -A r / 2, -A r}:
+    g (a - mu) / sigma^2 / B (the entropy does not depend on mu)."""
+    B = mu.shape[0]
+    var = (2.0 * log_std.detach().cpu().double()).exp()
+    dlp = (acts.cpu().double()[edge] - mu.cpu().double()[edge]) / var
+    full = (-adv.cpu().double()[edge] * ratio.detach().cpu().double()[edge])[:, None]
+    return torch.stack([g * dlp / B for g in (0.0 * full, 0.5 * full, full)])
 
 
 def assert_fixture_scalars(scalars, z):
@@ -98,9 +145,12 @@ def run_cat(dev, B, A, seed, vf_clip=0.2, act_dtype=torch.int32, inputs=None):
     )
     o = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val, old_v,
                                        0.2, vf_clip, 0.5, 0.01)
-    edge = clip_edge_rows(o["ratio"])
+    lp = torch.log_softmax(logits, -1).gather(1, actions.long()[:, None]).squeeze(1)
+    edge = clip_edge_rows(o["ratio"], lp, old_lp)
     assert_scalars_close(scalars, o, edge_rows=int(edge.sum()))
     assert_rows_close(dlogits, o["dlogits"], edge)
+    assert_edge_rows(dlogits, cat_edge_candidates(logits, actions, adv, o["ratio"], edge), edge,
+                     1e-5 * float(o["dlogits"].abs().max()))
     assert_grad_close(dvalues, o["dvalues"])
     return scalars, dlogits, dvalues
 
@@ -152,6 +202,64 @@ def test_cat_ties_and_zero_advantage(dev):
     old_lp[: B // 2] = lp[: B // 2]
     adv[::7] = 0.0
     run_cat(dev, B, A, seed=0, inputs=(logits, actions, old_lp, adv, ret, val, old_v))
+
+
+def _exact_bound_old_lp(lp, c, want=8):
+    """fp32 old log-probs for which torch's fp32 ratio exp(lp - old_lp) is
+    exactly fp32(c), with exp of that fp32 difference within 0.25 ulp of c in
+    fp64 (so an exp with error below a quarter ulp lands on c too)."""
+    c32 = torch.tensor(c, dtype=torch.float32)
+    lp32 = torch.tensor(lp, dtype=torch.float32)
+    ulp_c = float(torch.nextafter(c32, torch.tensor(2.0)) - c32)
+    x0 = (lp32.double() - math.log(float(c32))).float()
+    found = []
+    for direction in (-100.0, 100.0):
+        x = x0
+        for _ in range(256):
+            d = lp32 - x
+            if torch.exp(d) == c32 and abs(math.exp(float(d)) - float(c32)) < 0.25 * ulp_c:
+                found.append(float(x))
+            x = torch.nextafter(x, torch.tensor(direction))
+    found = sorted(set(found))[:want]
+    assert found, f"no exact-bound old log-prob for {c}"
+    return found
+
+
+def test_cat_ratio_exactly_on_the_clip_bounds(dev):
+    """The fp32 ratio lands exactly on 1 - clip and 1 + clip (uniform logits,
+    so lp = -log 2 in the kernel and in torch alike; old_lp chosen so that
+    exp(lp - old_lp) rounds to the bound).  torch.clamp passes the gradient at
+    its inclusive bounds and torch.minimum splits a tie 1/2-1/2, so the
+    reference's policy gradient there is the full unclipped one: the kernel
+    must give exactly that, not zero (which exclusive bounds would give)."""
+    A = 2
+    lp = float(torch.log_softmax(torch.zeros(A), -1)[0])
+    rows = []
+    for c in (0.8, 1.2):
+        for olp in _exact_bound_old_lp(lp, c):
+            for a in (1.5, -0.75):
+                rows.append((olp, a))
+    B = len(rows)
+    logits = torch.zeros(B, A)
+    actions = torch.tensor([i % A for i in range(B)], dtype=torch.int32)
+    old_lp = torch.tensor([r[0] for r in rows], dtype=torch.float32)
+    adv = torch.tensor([r[1] for r in rows], dtype=torch.float32)
+    g = torch.Generator().manual_seed(13)
+    ret = torch.randn(B, generator=g)
+    val = torch.randn(B, generator=g)
+    print(f"loss_cat exact clip bounds B={B}", flush=True)
+    scalars, dlogits, dvalues = ppo_amd.ppo_loss_discrete_fused(
+        logits.to(dev), actions.to(dev), old_lp.to(dev), adv.to(dev), ret.to(dev), val.to(dev),
+        None, 0.2, None, 0.5, 0.01)
+    o = ref.loss_categorical_reference(logits, actions, old_lp, adv, ret, val, None,
+                                       0.2, None, 0.5, 0.01)
+    r = o["ratio"]
+    assert bool(((r == torch.tensor(0.8)) | (r == torch.tensor(1.2))).all())
+    # the reference's rows carry the full policy gradient -A r (onehot - p) / B
+    full = cat_edge_candidates(logits, actions, adv, r, torch.ones(B, dtype=torch.bool))[2]
+    torch.testing.assert_close(o["dlogits"].double(), full, rtol=1e-6, atol=1e-9)
+    assert_grad_close(dlogits, o["dlogits"])
+    assert_scalars_close(scalars, o)
 
 
 def test_cat_misaligned_logits(dev):
@@ -231,9 +339,12 @@ def run_gauss(dev, B, D, seed, vf_clip=0.2):
         *[x.to(dev) for x in inp], 0.2, vf_clip, 0.5, 0.01
     )
     o = ref.loss_gaussian_reference(*inp, 0.2, vf_clip, 0.5, 0.01)
-    edge = clip_edge_rows(o["ratio"])
+    lp = torch.distributions.Normal(mu, log_std.exp()).log_prob(acts).sum(-1)
+    edge = clip_edge_rows(o["ratio"], lp, old_lp)
     assert_scalars_close(scalars, o, edge_rows=int(edge.sum()))
     assert_rows_close(dmu, o["dmu"], edge)
+    assert_edge_rows(dmu, gauss_edge_candidates(mu, log_std, acts, adv, o["ratio"], edge), edge,
+                     1e-5 * float(o["dmu"].abs().max()))
     # dlog_std sums over rows: an edge row may add or drop its policy term
     # |A| r ((x - mu)^2 / sigma^2 - 1) / B (x1.5 at a tie), so the
     # tolerance widens by exactly that much for those rows
