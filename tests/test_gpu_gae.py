@@ -616,3 +616,33 @@ def test_gae_resident_non_finite_carry(dev):
     fin = np.isfinite(a_ref)
     assert np.isnan(a_ref).sum() > 1000  # the case is exercised
     assert_gae_close(got[fin], a_ref[fin])
+
+
+# Rounds (no normaliser, rollouts longer than one resident grid): rounds of
+# 256 tiles from the end of the horizon backwards, each handing the advantage
+# at its left edge to the next; one to many env columns, a partial last round.
+ROUND_SHAPES = [
+    (1 << 20, 16, 0.001),   # config 3's shape: 16-env tiles, 2 rounds
+    (600_000, 32, 0.002),   # 32-env tiles, 3 rounds, the last one partial
+    (200_000, 128, 0.01),   # 2 columns x 128 tiles per round, 4 rounds
+    (300_000, 64, 0.0),     # no dones: every carry crosses every tile and round
+]
+
+
+@pytest.mark.parametrize("T,N,p", ROUND_SHAPES)
+def test_gae_resident_rounds_match_oracle(dev, T, N, p):
+    assert _route(T, N, False) == "resident"
+    exact, _, _ = _resident_case(dev, T, N, p, False, seed=T % 1000 + N)
+    assert exact > 0.99
+
+
+def test_discounted_returns_resident_rounds(dev):
+    """values = None (REINFORCE returns) in rounds."""
+    T, N = 1 << 20, 16
+    assert _route(T, N, False, has_values=False) == "resident"
+    g = torch.Generator().manual_seed(19)
+    r = torch.randn(T, N, generator=g)
+    d = (torch.rand(T, N, generator=g) < 0.001).to(torch.uint8)
+    got = ppo_amd.discounted_returns(r.to(dev), gamma=0.999, dones=d.to(dev)).cpu().numpy()
+    a_ref, _ = ref.gae_c(r.numpy(), np.zeros((T, N), np.float32), d.numpy(), None, 0.999, 1.0)
+    assert_gae_close(got, a_ref)

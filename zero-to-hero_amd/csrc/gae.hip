@@ -81,6 +81,7 @@ struct GaeArgs {
   uint64_t* slots;     // resident pass: barrier counter, tile composites, per-workgroup partials
   unsigned nonce;      // resident pass: tag of this call in the barrier counter
   long res_nc, res_nt; // resident pass: env columns, time tiles
+  long res_ntr, res_rounds;  // resident pass: time tiles per round, rounds
 };
 
 // What a gae_tile_kernel launch computes.
@@ -277,45 +278,36 @@ SpanPlan span_plan(long T, long N, long blocks) {
 #ifndef PPO_GAE_RES_BLOCK
 #define PPO_GAE_RES_BLOCK 512
 #endif
-// PPO_GAE_RES_EARLY: segments that do not depend on their tile's carry store
-// their rows before the look-back (measured slower on config 2: the polls of
-// the look-back then wait behind the whole chip's stores).
-#ifndef PPO_GAE_RES_EARLY
-#define PPO_GAE_RES_EARLY 0
-#endif
-// PPO_GAE_RES_XCD: tiles handed out so that each XCD owns a contiguous run
-// PPO_GAE_RES_CTLSTATS: the control wave alone polls the statistics partials
-// (1), or every wave does, behind its own stores (0)
-#ifndef PPO_GAE_RES_CTLSTATS
-#define PPO_GAE_RES_CTLSTATS 0
-#endif
-#ifndef PPO_GAE_RES_XCD
-#define PPO_GAE_RES_XCD 0
-#endif
 constexpr int kResBlock = PPO_GAE_RES_BLOCK;
 constexpr long kResMaxTiles = 256;  // one 1024-thread workgroup per CU on MI355X
 
 struct ResPlan {
   int E, L;          // E = 0: not applicable
   long nc, nt, TS;   // env columns, time tiles, steps per tile
+  long ntr, rounds;  // time tiles per round (per column), rounds
+  long grid() const { return nc * ntr; }
   long tiles() const { return nc * nt; }
 };
 
-// Among tiles of 64 or 32 envs and 16, 8 or 4 steps per thread, the shape
-// giving the most tiles that still fit on the device at once (<= 256), with
-// no more than a quarter of a column's threads idle past the horizon; ties
-// go to wider tiles (longer row segments).  Rollouts that give fewer than
-// 128 tiles (too little parallelism), or more than 16 tiles per env column
-// (a long look-back) without filling the device, take the other paths:
-// measured on MI355X, e.g. T x N = 1024 x 512 (16-64 tiles) 28 us against
-// 24 us on the tile passes, 16384 x 64 (128 tiles, 64 per column) 33 us
-// against 27 us on the span passes, while 2048 x 4096 runs 45 us against
-// 55 us, 4096 x 2048 45 us against 72 and 32768 x 256 (64 per column, 256
-// tiles) 57 us against 67.
-ResPlan res_plan(long T, long N) {
-  ResPlan best = {0, 0, 0, 0, 0};
+// Single round: among tiles of 64, 32 or 16 envs and 16, 8 or 4 steps per
+// thread, the shape giving the most tiles that still fit on the device at
+// once (<= 256), with no more than a quarter of a column's threads idle past
+// the horizon; ties go to wider tiles (longer row segments).  Rollouts that
+// give fewer than 128 tiles (too little parallelism), or more than 16 tiles
+// per env column without filling the device, take the other paths: measured
+// on MI355X, e.g. T x N = 1024 x 512 (16-64 tiles) 28 us against 24 us on the
+// tile passes, while 2048 x 4096 runs 45 us against 55 us, 4096 x 2048 45 us
+// against 72 and 32768 x 256 (64 tiles per column, 256 tiles) 57 us against 67.
+// Without the normaliser, rollouts too long for one round (more than 256
+// tiles of 16 steps per thread) run in rounds of 256 tiles, from the end of
+// the horizon backwards (at most kResMaxRounds), each round handing the
+// advantage at its left edge to the next.
+constexpr long kResMaxRounds = 8;
+
+ResPlan res_plan(long T, long N, bool norm) {
+  ResPlan best = {0, 0, 0, 0, 0, 0, 0};
   if (!PPO_GAE_RES || T <= 0 || N <= 0 || T * N >= (1L << 30)) return best;
-  const int Es[2] = {64, 32};
+  const int Es[3] = {64, 32, 16};
   const int Ls[3] = {16, 8, 4};
   for (int E : Es) {
     if (PPO_GAE_RES_E && E != PPO_GAE_RES_E) continue;
@@ -324,7 +316,7 @@ ResPlan res_plan(long T, long N) {
       const long TS = (long)(kResBlock / (E / 4)) * L;
       const long nt = (T + TS - 1) / TS;
       const long nc = N / E;
-      if (nc * nt > kResMaxTiles || nt > 64) continue;
+      if (nc * nt > kResMaxTiles) continue;
       if (4 * (nt * TS - T) > nt * TS) continue;  // a quarter of the threads idle
       if (nc * nt > best.tiles()) {
         best.E = E;
@@ -332,19 +324,50 @@ ResPlan res_plan(long T, long N) {
         best.nc = nc;
         best.nt = nt;
         best.TS = TS;
+        best.ntr = nt;
+        best.rounds = 1;
       }
     }
   }
-  if (best.tiles() < 128 || (best.nt > 16 && best.tiles() < kResMaxTiles)) best.E = 0;
+  if (best.E && (best.tiles() < 128 || (best.nt > 16 && best.tiles() < kResMaxTiles)))
+    best.E = 0;
+  if (best.E || norm) return best;
+  // rounds: the widest tile dividing N, 16 steps per thread
+  for (int E : Es) {
+    if (PPO_GAE_RES_E && E != PPO_GAE_RES_E) continue;
+    if (N % E != 0) continue;
+    const long nc = N / E;
+    if (nc > kResMaxTiles) continue;
+    const long TS = (long)(kResBlock / (E / 4)) * 16;
+    const long nt = (T + TS - 1) / TS;
+    const long ntr = kResMaxTiles / nc;
+    const long rounds = (nt + ntr - 1) / ntr;
+    if (rounds < 2 || rounds > kResMaxRounds) continue;
+    if (4 * (nt * TS - T) > nt * TS) continue;
+    best.E = E;
+    best.L = 16;
+    best.nc = nc;
+    best.nt = nt;
+    best.TS = TS;
+    best.ntr = ntr;
+    best.rounds = rounds;
+    return best;
+  }
   return best;
 }
 
-// 64-bit slot words of the resident pass: per tile, E composites (a, P) of
-// two words each, then three words (n, sum, sum of squares) per workgroup.
-// The first 32 words hold the start barrier's counter.
+// 64-bit slot words of the resident pass: the start barrier's counter (a
+// block of 32 words), per tile E composites (a, P) of two words each, per
+// round one carry per env (the advantage at the round's left edge), then
+// three words (n, sum, sum of squares) per workgroup.
 constexpr size_t kResSlotBase = 32;
 size_t res_slot_words(const ResPlan& rp) {
-  return rp.E ? kResSlotBase + (size_t)rp.tiles() * (2 * rp.E + 3) : 0;
+  if (!rp.E) return 0;
+  return kResSlotBase + (size_t)rp.tiles() * 2 * rp.E + (size_t)rp.rounds * rp.nc * rp.E +
+         (size_t)rp.grid() * 3;
+}
+size_t res_slot_words_max(long T, long N) {
+  return std::max(res_slot_words(res_plan(T, N, true)), res_slot_words(res_plan(T, N, false)));
 }
 
 struct GaeLayout {
@@ -376,7 +399,7 @@ GaeLayout make_layout(const GaePlan& p, long N) {
     off += align_up((size_t)parts * 4 * sizeof(double), 256);
   }
   l.slots = off;
-  off += align_up(res_slot_words(res_plan(p.T, N)) * sizeof(uint64_t), 256);
+  off += align_up(res_slot_words_max(p.T, N) * sizeof(uint64_t), 256);
   l.total = off;
   return l;
 }
@@ -1724,58 +1747,72 @@ __device__ void res_wait(uint64_t* ctr, unsigned nonce, unsigned nblocks) {
 #ifdef PPO_GAE_RES_TRACE
 // Phase timestamps of the resident pass (wall clock, 100 MHz), one row of 8
 // per workgroup: a measurement build only.
-__device__ uint64_t g_res_trace[4096 * 8];
+__device__ uint64_t g_res_trace[4096 * 32];
 #define RES_MARK(k) \
-  if (threadIdx.x == 0) g_res_trace[blockIdx.x * 8 + (k)] = wall_clock64()
+  if (threadIdx.x == 0) g_res_trace[blockIdx.x * 32 + (k) + 6 * res_round] = wall_clock64()
 #else
 #define RES_MARK(k)
 #endif
 
 template <int E>
 struct ResShared {
+  static constexpr int Q = kResBlock / E;   // look-back chunks per env
   double2 wc[kResWaves][E];                 // wave composites (a, P) per env
+  double2 lb[Q][E];                         // look-back: composite of each chunk of tiles
   float ssum[5][4][kResBlock];              // per thread and env: sums of a, P, aa, aP, PP
   double carry[E];                          // advantage entering the tile
   float norm[2];                            // mean and denominator
 };
 
-template <int E, int L, bool kStats, bool kHasV>
+template <int E, int L, bool kStats, bool kHasV, bool kRounds>
 __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
   constexpr int VW = 4;
   constexpr int G = E / VW;            // threads per tile row
   constexpr int SW = kWave / G;        // segments per wave
   constexpr int S = kResBlock / G;     // segments per tile
   constexpr long TS = (long)S * L;     // steps per tile
+  constexpr int Q = ResShared<E>::Q;
+  constexpr int LB = 4;                // look-back tiles in flight per thread
   static_assert(kWave % G == 0 && L <= 32, "resident geometry");
+  static_assert(!(kStats && kRounds), "the normaliser needs every advantage resident at once");
   __shared__ ResShared<E> sh;
 
   const int tid = threadIdx.x;
   const int g = tid % G, sg = tid / G, w = tid / kWave, j = (tid % kWave) / G;
+  // (kRounds = false: one round, the whole horizon)
   const long nc = a.res_nc, nt = a.res_nt;
-  // the first workgroups take the tiles at the end of the horizon, whose
+  const long ntr = kRounds ? a.res_ntr : nt, rounds = kRounds ? a.res_rounds : 1;
+  // workgroup b owns, in each round, time tile `tl` of the round (0 = the
+  // round's last steps) of env column `col`; rounds run from the end of the
+  // horizon backwards, and the first workgroups take the tiles whose
   // composites the others wait for
-  long b = blockIdx.x;
-  if (PPO_GAE_RES_XCD && gridDim.x % kXcds == 0)
-    b = (b % kXcds) * (gridDim.x / kXcds) + b / kXcds;
-  const long tt = nt - 1 - b / nc;  // time tile (0 = the first steps)
-  const long col = b % nc;
-  const long tile = tt * nc + col;
+  const long col = (long)blockIdx.x % nc, tl = (long)blockIdx.x / nc;
   const long env0 = col * E + (long)g * VW;
-  const long t0 = tt * TS + (long)sg * L;
-  const int nvalid = t0 >= a.T ? 0 : (a.T - t0 < L ? (int)(a.T - t0) : L);
   const unsigned n32 = (unsigned)a.N;
   uint64_t* ctr = a.slots;
-  uint64_t* comp = a.slots + kResSlotBase;                // [tiles][E][2]
-  uint64_t* part = comp + (size_t)nc * nt * 2 * E;        // [grid][3]
+  uint64_t* comp = a.slots + kResSlotBase;           // [nt][nc][E][2]
+  uint64_t* bnd = comp + (size_t)nt * nc * 2 * E;    // [rounds][N]
+  uint64_t* part = bnd + (size_t)rounds * a.N;       // [grid][3]
+  auto tile_tt = [&](long rd) { return nt - 1 - (rd * ntr + tl); };  // < 0: no tile
+#ifdef PPO_GAE_RES_TRACE
+  long res_round = 0;
+#endif
   RES_MARK(0);
-  // Wave 0 empties the slots this workgroup will fill (its composites and its
-  // partial), waits until those stores are done, and arrives at the start
-  // barrier; no workgroup reads a slot before the barrier is complete, so no
-  // reader can see what the slot held before this call.  The other waves
-  // start their loads meanwhile.
+  // Wave 0 empties the slots this workgroup will fill (its tiles' composites,
+  // a round's left-edge carries, its partial), waits until those stores are
+  // done, and arrives at the start barrier; no workgroup reads a slot before
+  // the barrier is complete, so no reader can see what the slot held before
+  // this call.  The other waves start their loads meanwhile.
   if (w == 0) {
-    for (int q = tid; q < 2 * E; q += kWave)
-      if (tt > 0) slot_clear(comp + (size_t)tile * 2 * E + q);
+    for (long rd = 0; rd < rounds; ++rd) {
+      const long tt = tile_tt(rd);
+      if (tt > 0) {
+        for (int q = tid; q < 2 * E; q += kWave)
+          slot_clear(comp + (size_t)(tt * nc + col) * 2 * E + q);
+        if (tl == ntr - 1 && rd + 1 < rounds && tid < E)
+          slot_clear(bnd + (size_t)rd * a.N + col * E + tid);
+      }
+    }
     if (tid < 3) slot_clear(part + (size_t)blockIdx.x * 3 + tid);
     uint64_t v = 0;
     if (tid == 0) v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1783,15 +1820,13 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
     if (tid == 0) res_arrive(ctr, v, a.nonce, gridDim.x);
   }
 
-  // ---- loads: every row of the segment, unconditional (rows past the
-  // horizon re-read row 0), plus the value row after the segment
+  const double gl0 = mul(a.gl, 0.0);
   float r[L][VW], v[L][VW], nv[VW];
   unsigned d[L];
-  // issued last row first: step 1 consumes the rows in that order, so its
-  // arithmetic starts as the first loads land
-#pragma unroll
-  for (int i = L - 1; i >= 0; --i) {
-    const unsigned off = (t0 + i < a.T ? (unsigned)(t0 + i) * n32 : 0u) + (unsigned)env0;
+  // ---- loads: every row of a segment, unconditional (rows past the
+  // horizon re-read row 0), plus the value row after the segment
+  auto load_row = [&](long ts0, int i) {
+    const unsigned off = (ts0 + i < a.T ? (unsigned)(ts0 + i) * n32 : 0u) + (unsigned)env0;
     load_vec<VW>(at_byte(a.r, off * 4u), r[i]);
     if constexpr (kHasV) {
       load_vec<VW>(at_byte(a.v, off * 4u), v[i]);
@@ -1800,9 +1835,9 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       for (int k = 0; k < VW; ++k) v[i][k] = 0.0f;
     }
     d[i] = load_done_raw<VW>(at_byte(a.d, off));
-  }
-  {
-    const long tn = t0 + L;
+  };
+  auto load_next_value = [&](long ts0) {
+    const long tn = ts0 + L;
 #pragma unroll
     for (int k = 0; k < VW; ++k) nv[k] = 0.0f;
     if (tn < a.T) {
@@ -1810,228 +1845,176 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
     } else if (a.lastv) {
       load_vec<VW>(a.lastv + env0, nv);
     }
-  }
-
-  // ---- 1. segment composites and the reverse scan inside the tile
-  const double gl0 = mul(a.gl, 0.0);
-  double na[VW], np[VW];
-  // With the normaliser, the sums over the segment's steps of the suffix
-  // composites (a_t, P_t) (steps t..segment end, zero carry) and of their
-  // products: the advantage at step t is a_t + P_t x for the carry x entering
-  // the segment, so once x is known the segment's sum of advantages and of
-  // their squares follow without the advantages themselves.
-  {
-    float sa[VW], sp[VW], saa[VW], sap[VW], spp[VW];
-    double ia[VW], ip[VW], nvd[VW];
-#pragma unroll
-    for (int k = 0; k < VW; ++k) {
-      ia[k] = 0.0;
-      ip[k] = 1.0;
-      nvd[k] = nv[k];
-      sa[k] = sp[k] = saa[k] = sap[k] = spp[k] = 0.0f;
-    }
-#pragma unroll
-    for (int i = L - 1; i >= 0; --i) {
-      if (i < nvalid) {
-#pragma unroll
-        for (int k = 0; k < VW; ++k) {
-          const bool done = ((d[i] >> (8 * k)) & 0xffu) != 0u;
-          const double vd = (double)v[i][k];
-          const double dl =
-              sub(add((double)r[i][k], mul(mul(a.gamma, nvd[k]), done ? 0.0 : 1.0)), vd);
-          const double cc = done ? gl0 : a.gl;
-          ia[k] = add(dl, mul(cc, ia[k]));
-          ip[k] = mul(ip[k], cc);
-          nvd[k] = vd;
-          if constexpr (kStats) {
-            const float fa = (float)ia[k], fp = (float)ip[k];
-            sa[k] += fa;
-            sp[k] += fp;
-            saa[k] += fa * fa;
-            sap[k] += fa * fp;
-            spp[k] += fp * fp;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < VW; ++k) {
-      na[k] = ia[k];
-      np[k] = ip[k];
-      if constexpr (kStats) {
-        // parked in LDS until the carries are known (registers are short)
-        sh.ssum[0][k][tid] = sa[k];
-        sh.ssum[1][k][tid] = sp[k];
-        sh.ssum[2][k][tid] = saa[k];
-        sh.ssum[3][k][tid] = sap[k];
-        sh.ssum[4][k][tid] = spp[k];
-      }
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < VW; ++k) {
-    double ia = na[k], ip = np[k];
-#pragma unroll
-    for (int off = 1; off < SW; off <<= 1) {
-      const double pa = __shfl_down(ia, G * off);
-      const double pp = __shfl_down(ip, G * off);
-      if (j + off < SW) {
-        ia = ia + ip * pa;
-        ip = ip * pp;
-      }
-    }
-    na[k] = __shfl_down(ia, G);
-    np[k] = __shfl_down(ip, G);
-    if (j + 1 >= SW) {
-      na[k] = 0.0;
-      np[k] = 1.0;
-    }
-    if (j == 0) sh.wc[w][g * VW + k] = make_double2(ia, ip);
-  }
-  __syncthreads();
-  RES_MARK(1);
-
-  // ---- 2. publish the tile composite
-  if (tid < E && tt > 0) {
-    double ta = 0.0, tp = 1.0;
-#pragma unroll
-    for (int ww = kResWaves - 1; ww >= 0; --ww) {
-      const double2 c = sh.wc[ww][tid];
-      ta = c.x + c.y * ta;
-      tp = c.y * tp;
-    }
-    slot_put(comp + ((size_t)tile * E + tid) * 2 + 0, ta);
-    slot_put(comp + ((size_t)tile * E + tid) * 2 + 1, tp);
-  }
-
-  // ---- 3. exact recurrence from each segment's carry, adv and ret
-  // The deltas are formed again from the rows rather than kept from step 1
-  // (fp64, two registers each): the empty asm hides from the compiler that
-  // the rows are unchanged, so it cannot keep step 1's values alive instead.
-#pragma unroll
-  for (int i = 0; i < L; ++i) {
-#pragma unroll
-    for (int k = 0; k < VW; ++k) asm volatile("" : "+v"(r[i][k]), "+v"(v[i][k]));
-    asm volatile("" : "+v"(d[i]));
-  }
-  // Runs the recurrence of this thread's segment from its carries xs, rows
-  // from the last, storing each row of adv and ret as soon as its 4 envs are
-  // done; the advantages replace the rewards in r.
-  auto segment_out = [&](const double (&xs)[VW]) {
-    double xv[VW], nvd[VW];
-#pragma unroll
-    for (int k = 0; k < VW; ++k) {
-      xv[k] = xs[k];
-      nvd[k] = nv[k];
-    }
-#pragma unroll
-    for (int i = L - 1; i >= 0; --i) {
-      if (i < nvalid) {
-#pragma unroll
-        for (int k = 0; k < VW; ++k) {
-          const bool done = ((d[i] >> (8 * k)) & 0xffu) != 0u;
-          const double vd = (double)v[i][k];
-          const double dl =
-              sub(add((double)r[i][k], mul(mul(a.gamma, nvd[k]), done ? 0.0 : 1.0)), vd);
-          xv[k] = add(dl, mul(done ? gl0 : a.gl, xv[k]));
-          nvd[k] = vd;
-          r[i][k] = (float)xv[k];
-        }
-        const unsigned off = ((unsigned)(t0 + i) * n32 + (unsigned)env0) * 4u;
-        store_vec<VW>(at_byte(a.adv, off), r[i]);
-        if (a.ret) {
-          float rt[VW];
-#pragma unroll
-          for (int k = 0; k < VW; ++k) rt[k] = r[i][k] + v[i][k];
-          store_vec<VW>(at_byte(a.ret, off), rt);
-        }
-      }
-    }
   };
-  // The last wave is the control wave: it alone polls slots (the start
-  // barrier, the look-back, the statistics), and it stores its own rows only
-  // at the end.  On gfx950 one counter covers a wave's loads and stores in
-  // issue order, so a poll issued behind a wave's stores waits for all of
-  // them to drain; the other waves store freely and meet the control wave at
-  // LDS-only barriers, which do not wait for stores either.
-  constexpr int kCtl = kResWaves - 1;
-  const bool ctl = w == kCtl;
-  // A segment whose composite to the tile's end has P == 0 (a done to its
-  // right inside the tile: gamma*lambda*0 multiplies the carry) does not
-  // depend on the tile's carry: its carry is the fold of the waves to its
-  // right from zero, and it is finished before the look-back.  (The fold from
-  // the true carry gives the same value unless that carry is not finite, where
-  // 0 * inf makes every advantage of the tile NaN, as in the reference's
-  // recurrence; that case is patched after the look-back.)
-  double x[VW];
-  bool early = true;
+  int nvalid = 0;
+  long t0 = 0;
+  // the first round's rows, last row first, as step 1 consumes them; later
+  // rounds' rows are loaded row by row as the round before stores its own
+  // (software pipelining across rounds: the registers are the buffers)
+  if (tile_tt(0) >= 0) {
+    const long ts0 = tile_tt(0) * TS + (long)sg * L;
 #pragma unroll
-  for (int k = 0; k < VW; ++k) {
-    const int e = g * VW + k;
-    double C = 0.0, Pw = 1.0;
-    for (int ww = kResWaves - 1; ww > w; --ww) {
-      const double2 c = sh.wc[ww][e];
-      C = c.x + c.y * C;
-      Pw = c.y * Pw;
-    }
-    x[k] = na[k] + np[k] * C;
-    early = early && np[k] * Pw == 0.0;
+    for (int i = L - 1; i >= 0; --i) load_row(ts0, i);
+    load_next_value(ts0);
   }
-  early = early && PPO_GAE_RES_EARLY;
-  if (early && !ctl) segment_out(x);
+  for (long rd = 0; rd < rounds; ++rd) {
+    const long tt = tile_tt(rd);
+    if (tt < 0) break;  // (the last round may hold fewer tiles)
+    t0 = tt * TS + (long)sg * L;
+    nvalid = t0 >= a.T ? 0 : (a.T - t0 < L ? (int)(a.T - t0) : L);
+    const long tt_next = kRounds && rd + 1 < rounds ? tile_tt(rd + 1) : -1;
+#ifdef PPO_GAE_RES_TRACE
+    res_round = rd;
+#endif
+    const long t0_next = tt_next * TS + (long)sg * L;
 
-  // ---- look-back (control wave): fold the composites of the tiles to the
-  // right, env e in lane e % 64, all of a pass's loads issued together
-  if (ctl) {
-    const int lane = tid % kWave;
-    constexpr int EPL = E > kWave ? E / kWave : 1;  // envs per lane
-    constexpr int LB = EPL > 1 ? 2 : 4;             // tiles per pass
-    if (lane == 0) res_wait(ctr, a.nonce, gridDim.x);  // slots emptied by their owners
-    double xc[EPL];
+    // ---- 1. segment composites and the reverse scan inside the tile.  With
+    // the normaliser, also the sums over the segment's steps of the suffix
+    // composites (a_t, P_t) (steps t..segment end, zero carry) and of their
+    // products: the advantage at step t is a_t + P_t x for the carry x
+    // entering the segment, so once x is known the segment's sum of
+    // advantages and of their squares follow without the advantages.
+    double na[VW], np[VW];
+    {
+      float sa[VW], sp[VW], saa[VW], sap[VW], spp[VW];
+      double ia[VW], ip[VW], nvd[VW];
 #pragma unroll
-    for (int q = 0; q < EPL; ++q) xc[q] = 0.0;
-    for (long hi = nt - 1; hi > tt; hi -= LB) {
-      const int cnt = (int)(hi - tt < LB ? hi - tt : LB);
-      uint64_t wa[LB][EPL], wp[LB][EPL];
+      for (int k = 0; k < VW; ++k) {
+        ia[k] = 0.0;
+        ip[k] = 1.0;
+        nvd[k] = nv[k];
+        sa[k] = sp[k] = saa[k] = sap[k] = spp[k] = 0.0f;
+      }
 #pragma unroll
-      for (int q = 0; q < LB; ++q) {
+      for (int i = L - 1; i >= 0; --i) {
+        if (i < nvalid) {
 #pragma unroll
-        for (int m = 0; m < EPL; ++m) {
-          const int e = lane + m * kWave;
-          wa[q][m] = wp[q][m] = 0;
-          if (q < cnt && e < E) {
-            uint64_t* sl = comp + ((size_t)((hi - q) * nc + col) * E + e) * 2;
-            wa[q][m] = __hip_atomic_load(sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            wp[q][m] = __hip_atomic_load(sl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          for (int k = 0; k < VW; ++k) {
+            const bool done = ((d[i] >> (8 * k)) & 0xffu) != 0u;
+            const double vd = (double)v[i][k];
+            const double dl =
+                sub(add((double)r[i][k], mul(mul(a.gamma, nvd[k]), done ? 0.0 : 1.0)), vd);
+            const double cc = done ? gl0 : a.gl;
+            ia[k] = add(dl, mul(cc, ia[k]));
+            ip[k] = mul(ip[k], cc);
+            nvd[k] = vd;
+            if constexpr (kStats) {
+              const float fa = (float)ia[k], fp = (float)ip[k];
+              sa[k] += fa;
+              sp[k] += fp;
+              saa[k] += fa * fa;
+              sap[k] += fa * fp;
+              spp[k] += fp * fp;
+            }
           }
         }
       }
 #pragma unroll
-      for (int q = 0; q < LB; ++q) {
-#pragma unroll
-        for (int m = 0; m < EPL; ++m) {
-          const int e = lane + m * kWave;
-          if (q < cnt && e < E) {
-            uint64_t* sl = comp + ((size_t)((hi - q) * nc + col) * E + e) * 2;
-            const double ca = wa[q][m] ? slot_value(wa[q][m]) : slot_get(sl);
-            const double cp = wp[q][m] ? slot_value(wp[q][m]) : slot_get(sl + 1);
-            xc[m] = ca + cp * xc[m];
-          }
+      for (int k = 0; k < VW; ++k) {
+        na[k] = ia[k];
+        np[k] = ip[k];
+        if constexpr (kStats) {
+          // parked in LDS until the carries are known (registers are short)
+          sh.ssum[0][k][tid] = sa[k];
+          sh.ssum[1][k][tid] = sp[k];
+          sh.ssum[2][k][tid] = saa[k];
+          sh.ssum[3][k][tid] = sap[k];
+          sh.ssum[4][k][tid] = spp[k];
         }
       }
     }
 #pragma unroll
-    for (int m = 0; m < EPL; ++m) {
-      const int e = lane + m * kWave;
-      if (e < E) sh.carry[e] = xc[m];
+    for (int k = 0; k < VW; ++k) {
+      double ia = na[k], ip = np[k];
+#pragma unroll
+      for (int off = 1; off < SW; off <<= 1) {
+        const double pa = __shfl_down(ia, G * off);
+        const double pp = __shfl_down(ip, G * off);
+        if (j + off < SW) {
+          ia = ia + ip * pa;
+          ip = ip * pp;
+        }
+      }
+      na[k] = __shfl_down(ia, G);
+      np[k] = __shfl_down(ip, G);
+      if (j + 1 >= SW) {
+        na[k] = 0.0;
+        np[k] = 1.0;
+      }
+      if (j == 0) sh.wc[w][g * VW + k] = make_double2(ia, ip);
     }
-  }
-  lds_barrier();
-  RES_MARK(2);
+    __syncthreads();
+    RES_MARK(1);
 
-  if (!early || ctl) {
-    // (the control wave stores nothing before the look-back, so it always
-    // takes its carries from the true tile carry)
+    // ---- 2. publish the tile composite
+    if (tid < E && tt > 0) {
+      double ta = 0.0, tp = 1.0;
+#pragma unroll
+      for (int ww = kResWaves - 1; ww >= 0; --ww) {
+        const double2 c = sh.wc[ww][tid];
+        ta = c.x + c.y * ta;
+        tp = c.y * tp;
+      }
+      slot_put(comp + ((size_t)(tt * nc + col) * E + tid) * 2 + 0, ta);
+      slot_put(comp + ((size_t)(tt * nc + col) * E + tid) * 2 + 1, tp);
+    }
+    // the start barrier (once): every workgroup's slots are empty by now
+    if (rd == 0 && tid == 0) res_wait(ctr, a.nonce, gridDim.x);
+    __syncthreads();
+
+    // ---- look-back: the tiles to the right inside this round (hi down to
+    // tt + 1), in Q chunks per env, each folded by one thread with its loads
+    // in flight together; then the chunks in order, from the carry entering
+    // the round (the previous round's left-edge carry, zero for the first)
+    {
+      // (tile indices fit in 32 bits: at most 256 tiles per round and
+      // kResMaxRounds rounds)
+      const int e = tid % E, q = tid / E;
+      const int hi = (int)(nt - 1 - rd * ntr);
+      const int m = hi - (int)tt;             // tiles to fold
+      const int cs = (m + Q - 1) / Q;         // tiles per chunk
+      const int u_hi = hi - q * cs, u_lo = max((int)tt + 1, hi - (q + 1) * cs + 1);
+      // slot pair of tile u for env e: word offset ((u * nc + col) * E + e) * 2
+      const unsigned step = (unsigned)(nc * E * 2), base = (unsigned)((col * E + e) * 2);
+      double A = 0.0, P = 1.0;
+      for (int u0 = u_hi; u0 >= u_lo; u0 -= LB) {
+        uint64_t wa[LB], wp[LB];
+#pragma unroll
+        for (int k = 0; k < LB; ++k) {
+          wa[k] = wp[k] = 0;
+          if (u0 - k >= u_lo) {
+            uint64_t* sl = comp + (base + (unsigned)(u0 - k) * step);
+            wa[k] = __hip_atomic_load(sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wp[k] = __hip_atomic_load(sl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < LB; ++k) {
+          if (u0 - k >= u_lo) {
+            uint64_t* sl = comp + (base + (unsigned)(u0 - k) * step);
+            const double ca = wa[k] ? slot_value(wa[k]) : slot_get(sl);
+            const double cp = wp[k] ? slot_value(wp[k]) : slot_get(sl + 1);
+            A = ca + cp * A;
+            P = cp * P;
+          }
+        }
+      }
+      sh.lb[q][e] = make_double2(A, P);
+      __syncthreads();
+      if (tid < E) {
+        double xc = rd > 0 ? slot_get(bnd + (size_t)(rd - 1) * a.N + col * E + e) : 0.0;
+        for (int qq = 0; qq < Q; ++qq) {
+          const double2 c = sh.lb[qq][e];
+          xc = c.x + c.y * xc;
+        }
+        sh.carry[e] = xc;
+      }
+      __syncthreads();
+    }
+    RES_MARK(2);
+
+    // ---- 3. carry entering each of this thread's segments (one per env)
+    double x[VW];
 #pragma unroll
     for (int k = 0; k < VW; ++k) {
       const int e = g * VW + k;
@@ -2042,23 +2025,66 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       }
       x[k] = na[k] + np[k] * C;
     }
-  } else {
-    // an early segment of a tile whose carry is not finite
-    bool patch = false;
+    // a round's left-edge tile hands the advantage at its left edge to the
+    // next round
+    if (tl == ntr - 1 && rd + 1 < rounds && tt > 0 && tid < E) {
+      double C = sh.carry[tid];
 #pragma unroll
-    for (int k = 0; k < VW; ++k) {
-      if (!__builtin_isfinite(sh.carry[g * VW + k])) {
-        x[k] = __builtin_nan("");
-        patch = true;
+      for (int ww = kResWaves - 1; ww >= 0; --ww) {
+        const double2 c = sh.wc[ww][tid];
+        C = c.x + c.y * C;
+      }
+      slot_put(bnd + (size_t)rd * a.N + col * E + tid, C);
+    }
+    if constexpr (kStats) {
+      // the statistics partial (a single round), published before this
+      // workgroup's stores
+      double acc[3] = {(double)(nvalid * VW), 0.0, 0.0};
+#pragma unroll
+      for (int k = 0; k < VW; ++k) {
+        const double sa = sh.ssum[0][k][tid], sp = sh.ssum[1][k][tid];
+        const double saa = sh.ssum[2][k][tid], sap = sh.ssum[3][k][tid], spp = sh.ssum[4][k][tid];
+        acc[1] += sa + sp * x[k];
+        acc[2] += saa + 2.0 * sap * x[k] + spp * x[k] * x[k];
+      }
+      block_sum_lds<3>(acc);
+      if (tid == 0) {
+        uint64_t* pp = part + (size_t)blockIdx.x * 3;
+        slot_put(pp + 0, acc[0]);
+        slot_put(pp + 1, acc[1]);
+        slot_put(pp + 2, acc[2]);
       }
     }
-    if (patch) {
+
+    // ---- exact recurrence from each segment's carry, adv and ret.  The
+    // deltas are formed again from the rows rather than kept from step 1
+    // (fp64, two registers each): the empty asm hides from the compiler that
+    // the rows are unchanged, so it cannot keep step 1's values alive instead.
 #pragma unroll
-      for (int i = 0; i < L; ++i) {
+    for (int i = 0; i < L; ++i) {
+#pragma unroll
+      for (int k = 0; k < VW; ++k) asm volatile("" : "+v"(r[i][k]), "+v"(v[i][k]));
+    }
+#pragma unroll
+    for (int i = 0; i < L; ++i) asm volatile("" : "+v"(d[i]));
+    {
+      double nvd[VW];
+#pragma unroll
+      for (int k = 0; k < VW; ++k) nvd[k] = nv[k];
+      // rows from the last: each row is stored as soon as its 4 envs are done
+#pragma unroll
+      for (int i = L - 1; i >= 0; --i) {
         if (i < nvalid) {
 #pragma unroll
-          for (int k = 0; k < VW; ++k)
-            if (x[k] != x[k]) r[i][k] = __builtin_nanf("");
+          for (int k = 0; k < VW; ++k) {
+            const bool done = ((d[i] >> (8 * k)) & 0xffu) != 0u;
+            const double vd = (double)v[i][k];
+            const double dl =
+                sub(add((double)r[i][k], mul(mul(a.gamma, nvd[k]), done ? 0.0 : 1.0)), vd);
+            x[k] = add(dl, mul(done ? gl0 : a.gl, x[k]));
+            nvd[k] = vd;
+            r[i][k] = (float)x[k];  // the advantage replaces the reward
+          }
           const unsigned off = ((unsigned)(t0 + i) * n32 + (unsigned)env0) * 4u;
           store_vec<VW>(at_byte(a.adv, off), r[i]);
           if (a.ret) {
@@ -2068,146 +2094,121 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
             store_vec<VW>(at_byte(a.ret, off), rt);
           }
         }
+        if constexpr (kRounds) {
+          if (tt_next >= 0) load_row(t0_next, i);  // row i of the next round's tile
+        }
       }
     }
-  }
-  if constexpr (kStats) {
-    // ---- the statistics partial, published before this workgroup's stores
-    double acc[3] = {(double)(nvalid * VW), 0.0, 0.0};
-#pragma unroll
-    for (int k = 0; k < VW; ++k) {
-      const double sa = sh.ssum[0][k][tid], sp = sh.ssum[1][k][tid];
-      const double saa = sh.ssum[2][k][tid], sap = sh.ssum[3][k][tid], spp = sh.ssum[4][k][tid];
-      acc[1] += sa + sp * x[k];
-      acc[2] += saa + 2.0 * sap * x[k] + spp * x[k] * x[k];
+    if constexpr (kRounds) {
+      if (tt_next >= 0) load_next_value(t0_next);
     }
-    block_sum_lds<3>(acc);
-    if (tid == 0) {
-      uint64_t* pp = part + (size_t)blockIdx.x * 3;
-      slot_put(pp + 0, acc[0]);
-      slot_put(pp + 1, acc[1]);
-      slot_put(pp + 2, acc[2]);
-    }
-  }
-  if (!early && (!ctl || !PPO_GAE_RES_CTLSTATS)) segment_out(x);
-  RES_MARK(3);
-
-  if constexpr (kStats) {
-    if (ctl || !PPO_GAE_RES_CTLSTATS) {
-      // lane l sums partials l, l + 64, ... in order, then the wave sum: the
-      // same order in every workgroup, so all derive the same statistics
-      const int lane = tid % kWave;
-      double tot[3] = {0.0, 0.0, 0.0};
-      for (long u0 = 0; u0 < (long)gridDim.x; u0 += 4 * kWave) {
-        uint64_t wv[4][3];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const long u = u0 + q * kWave + lane;
-#pragma unroll
-          for (int c = 0; c < 3; ++c)
-            wv[q][c] = u < (long)gridDim.x ? __hip_atomic_load(part + (size_t)u * 3 + c,
-                                                               __ATOMIC_RELAXED,
-                                                               __HIP_MEMORY_SCOPE_AGENT)
-                                           : 0;
+    RES_MARK(3);
+    if constexpr (kStats) {
+      // ---- 4. statistics of all advantages (every workgroup reads all partials
+      // in the same fixed order, so all derive bit-identical mean and std), then
+      // the normalised advantages from the registers
+      {
+        double tot[3] = {0.0, 0.0, 0.0};
+        for (long u = tid; u < (long)gridDim.x; u += kResBlock) {
+          uint64_t* pp = part + (size_t)u * 3;
+          tot[0] += slot_get(pp + 0);
+          tot[1] += slot_get(pp + 1);
+          tot[2] += slot_get(pp + 2);
         }
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const long u = u0 + q * kWave + lane;
-          if (u < (long)gridDim.x) {
-#pragma unroll
-            for (int c = 0; c < 3; ++c)
-              tot[c] += wv[q][c] ? slot_value(wv[q][c]) : slot_get(part + (size_t)u * 3 + c);
+        block_sum_lds<3>(tot);
+        if (tid == 0) {
+          // norm_params' formulas on these totals
+          const double n = tot[0];
+          const double mean = tot[1] / n;
+          float mean_f = (float)mean, std_f, mean_used, denom;
+          if (n > 1.0) {
+            const double m2 = tot[2] - tot[1] * mean;
+            std_f = (float)sqrt((m2 > 0.0 ? m2 : 0.0) / (n - 1.0));
+            mean_used = mean_f;
+            denom = std_f + (float)a.eps;
+          } else {
+            std_f = __builtin_nanf("");
+            mean_used = 0.0f;
+            denom = 1.0f;
+          }
+          sh.norm[0] = mean_used;
+          sh.norm[1] = denom;
+          if (blockIdx.x == 0) {
+            a.hdr->stats[0] = mean_used;
+            a.hdr->stats[1] = std_f;
+            a.hdr->stats[2] = denom;
+            if (a.stats_out) {
+              a.stats_out[0] = mean_f;
+              a.stats_out[1] = std_f;
+            }
           }
         }
+        lds_barrier();
       }
+      RES_MARK(4);
+      const float mean = sh.norm[0], denom = sh.norm[1];
 #pragma unroll
-      for (int c = 0; c < 3; ++c) tot[c] = wave_sum(tot[c]);
-      if (lane == 0) {
-        // norm_params' formulas on these totals
-        const double n = tot[0];
-        const double mean = tot[1] / n;
-        float mean_f = (float)mean, std_f, mean_used, denom;
-        if (n > 1.0) {
-          const double m2 = tot[2] - tot[1] * mean;
-          std_f = (float)sqrt((m2 > 0.0 ? m2 : 0.0) / (n - 1.0));
-          mean_used = mean_f;
-          denom = std_f + (float)a.eps;
-        } else {
-          std_f = __builtin_nanf("");
-          mean_used = 0.0f;
-          denom = 1.0f;
-        }
-        sh.norm[0] = mean_used;
-        sh.norm[1] = denom;
-        if (blockIdx.x == 0) {
-          a.hdr->stats[0] = mean_used;
-          a.hdr->stats[1] = std_f;
-          a.hdr->stats[2] = denom;
-          if (a.stats_out) {
-            a.stats_out[0] = mean_f;
-            a.stats_out[1] = std_f;
-          }
+      for (int i = 0; i < L; ++i) {
+        if (i < nvalid) {
+          const unsigned off = ((unsigned)(t0 + i) * n32 + (unsigned)env0) * 4u;
+          float y[VW];
+#pragma unroll
+          for (int k = 0; k < VW; ++k) y[k] = (r[i][k] - mean) / denom;
+          store_vec<VW>(at_byte(a.adv_n, off), y);
         }
       }
+      RES_MARK(5);
     }
-    lds_barrier();
+    lds_barrier();  // this round's LDS (composites, carries) is read before the next overwrites it
   }
-  RES_MARK(4);
-  if (ctl && (early || PPO_GAE_RES_CTLSTATS)) segment_out(x);  // after its polls
-  if constexpr (kStats) {
-    const float mean = sh.norm[0], denom = sh.norm[1];
-#pragma unroll
-    for (int i = 0; i < L; ++i) {
-      if (i < nvalid) {
-        const unsigned off = ((unsigned)(t0 + i) * n32 + (unsigned)env0) * 4u;
-        float y[VW];
-#pragma unroll
-        for (int k = 0; k < VW; ++k) y[k] = (r[i][k] - mean) / denom;
-        store_vec<VW>(at_byte(a.adv_n, off), y);
-      }
-    }
-  }
-  RES_MARK(5);
 }
 
 template <int E, int L>
 const void* res_kernel_el(bool stats, bool has_v) {
   if (stats)
-    return has_v ? (const void*)gae_resident_kernel<E, L, true, true>
-                 : (const void*)gae_resident_kernel<E, L, true, false>;
-  return has_v ? (const void*)gae_resident_kernel<E, L, false, true>
-               : (const void*)gae_resident_kernel<E, L, false, false>;
+    return has_v ? (const void*)gae_resident_kernel<E, L, true, true, false>
+                 : (const void*)gae_resident_kernel<E, L, true, false, false>;
+  return has_v ? (const void*)gae_resident_kernel<E, L, false, true, false>
+               : (const void*)gae_resident_kernel<E, L, false, false, false>;
+}
+
+template <int E>
+const void* res_kernel_e(int L, bool stats, bool has_v, bool rounds) {
+  if (rounds)  // (rounds always use 16 steps per thread and no normaliser)
+    return has_v ? (const void*)gae_resident_kernel<E, 16, false, true, true>
+                 : (const void*)gae_resident_kernel<E, 16, false, false, true>;
+  return L == 16 ? res_kernel_el<E, 16>(stats, has_v)
+                 : (L == 8 ? res_kernel_el<E, 8>(stats, has_v) : res_kernel_el<E, 4>(stats, has_v));
 }
 
 const void* res_kernel(const ResPlan& rp, bool stats, bool has_v) {
-  if (rp.E == 64)
-    return rp.L == 16 ? res_kernel_el<64, 16>(stats, has_v)
-                      : (rp.L == 8 ? res_kernel_el<64, 8>(stats, has_v)
-                                   : res_kernel_el<64, 4>(stats, has_v));
-  return rp.L == 16 ? res_kernel_el<32, 16>(stats, has_v)
-                    : (rp.L == 8 ? res_kernel_el<32, 8>(stats, has_v)
-                                 : res_kernel_el<32, 4>(stats, has_v));
+  const bool rounds = rp.rounds > 1;
+  if (rp.E == 64) return res_kernel_e<64>(rp.L, stats, has_v, rounds);
+  if (rp.E == 32) return res_kernel_e<32>(rp.L, stats, has_v, rounds);
+  return res_kernel_e<16>(rp.L, stats, has_v, rounds);
 }
 
-// Launches the resident pass when the plan applies and the whole grid fits
-// on the device at once; returns -1 (nothing launched) otherwise.
 // The environment variable PPO_AMD_GAE_RESIDENT=0 turns the resident pass
 // off (every rollout then takes the strip walk, span or tile passes), so that
 // those paths can be tested on shapes the resident pass would take.
 bool resident_ok(long T, long N, bool norm, bool has_v) {
   const char* env = getenv("PPO_AMD_GAE_RESIDENT");
   if (env && env[0] == '0') return false;
-  const ResPlan rp = res_plan(T, N);
+  const ResPlan rp = res_plan(T, N, norm);
   if (rp.E == 0) return false;
-  return resident_blocks(res_kernel(rp, norm, has_v), kResBlock, 0, 0) >= rp.tiles();
+  return resident_blocks(res_kernel(rp, norm, has_v), kResBlock, 0, 0) >= rp.grid();
 }
 
+// Launches the resident pass when the plan applies and the whole grid fits
+// on the device at once; returns -1 (nothing launched) otherwise.
 int launch_resident(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
   if (!resident_ok(T, N, norm, a.v != nullptr)) return -1;
-  const ResPlan rp = res_plan(T, N);
+  const ResPlan rp = res_plan(T, N, norm);
   const void* kern = res_kernel(rp, norm, a.v != nullptr);
   a.res_nc = rp.nc;
   a.res_nt = rp.nt;
+  a.res_ntr = rp.ntr;
+  a.res_rounds = rp.rounds;
   // a different tag for every call (zero is skipped)
   static std::atomic<unsigned> calls{0x5bd1e995u};
   unsigned nonce;
@@ -2217,7 +2218,7 @@ int launch_resident(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
   a.nonce = nonce;
   void* args[] = {&a};
   return hip_status(
-      hipLaunchKernel(kern, dim3((unsigned)rp.tiles()), dim3(kResBlock), args, 0, stream));
+      hipLaunchKernel(kern, dim3((unsigned)rp.grid()), dim3(kResBlock), args, 0, stream));
 }
 
 // Pass kernels by (VW, L, solo) geometry.
