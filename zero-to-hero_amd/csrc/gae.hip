@@ -50,6 +50,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "grid_sync.hpp"
 #include "stats.hpp"
 
 namespace ppo {
@@ -360,7 +361,7 @@ ResPlan res_plan(long T, long N, bool norm) {
 // block of 32 words), per tile E composites (a, P) of two words each, per
 // round one carry per env (the advantage at the round's left edge), then
 // three words (n, sum, sum of squares) per workgroup.
-constexpr size_t kResSlotBase = 32;
+constexpr size_t kResSlotBase = kSyncWords;
 size_t res_slot_words(const ResPlan& rp) {
   if (!rp.E) return 0;
   return kResSlotBase + (size_t)rp.tiles() * 2 * rp.E + (size_t)rp.rounds * rp.nc * rp.E +
@@ -1682,71 +1683,14 @@ int launch_span(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
 //      derive bit-identical mean and std (the partials were published before
 //      step 3, so the wait overlaps it), and stores the normalised
 //      advantages from the registers.
-// Cross-workgroup values travel through 64-bit slots written by agent-scope
-// relaxed atomic stores and polled by agent-scope atomic loads, one value per
-// slot, encoded so that no value encodes to zero: a zero word is an empty
-// slot, so every slot is its own ready flag and no fence (on gfx950 a full L2
-// write-back) is needed.  Each workgroup empties the slots it will fill and
-// then arrives at a start barrier (res_arrive); slots are read only after it.
-// Waits are bounded (a slot still empty after the bound reads as NaN, which
-// then shows in the outputs); the host launches the pass only when the whole
-// grid fits on the device at once, so every producer runs while its
-// consumers wait.
+// Cross-workgroup values travel through the self-validating slots of
+// grid_sync.hpp (start barrier, bounded waits); the host launches the pass
+// only when the whole grid fits on the device at once, so every producer
+// runs while its consumers wait.
 constexpr int kResWaves = kResBlock / kWave;
-constexpr uint64_t kSlotTag = 0x7FF4A5A55A5A0F0FULL;  // a signalling-NaN pattern
-constexpr long kSlotSpin = 1L << 22;                  // polls before giving up
-
-__device__ __forceinline__ void slot_put(uint64_t* p, double x) {
-  uint64_t b = __builtin_bit_cast(uint64_t, x);
-  if (x != x) b = 0x7FF8000000000000ULL;  // one NaN pattern, never the tag
-  __hip_atomic_store(p, b ^ kSlotTag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ double slot_value(uint64_t w) {
-  return __builtin_bit_cast(double, w ^ kSlotTag);
-}
-
-__device__ __forceinline__ double slot_get(uint64_t* p) {
-  for (long it = 0; it < kSlotSpin; ++it) {
-    const uint64_t w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (w != 0) return __builtin_bit_cast(double, w ^ kSlotTag);
-    __builtin_amdgcn_s_sleep(1);
-  }
-  return __builtin_nan("");
-}
-
-__device__ __forceinline__ void slot_clear(uint64_t* p) {
-  __hip_atomic_store(p, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Start barrier of the resident pass: one counter word (nonce:32, count:32).
-// A workgroup arrives by one compare-and-swap attempt that resets a counter
-// tagged with another nonce (an earlier call's, or whatever the workspace
-// held) or holding a complete count (a previous replay of the same captured
-// call) to (nonce, 0), then one atomic add; neither result is waited for,
-// and both go to the same address, so they apply in order.  (A retry loop of
-// compare-and-swaps from 256 workgroups serialises at memory latency.)  The
-// barrier is complete when the counter reads (nonce, >= nblocks).
-// `v` is the counter as read after this workgroup's slots were emptied.
-__device__ void res_arrive(uint64_t* ctr, uint64_t v, unsigned nonce, unsigned nblocks) {
-  const uint64_t tag = (uint64_t)nonce << 32;
-  if ((v >> 32) != nonce || (unsigned)v >= nblocks)
-    __hip_atomic_compare_exchange_strong(ctr, &v, tag, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_fetch_add(ctr, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ void res_wait(uint64_t* ctr, unsigned nonce, unsigned nblocks) {
-  for (long it = 0; it < kSlotSpin; ++it) {
-    const uint64_t v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if ((v >> 32) == nonce && (unsigned)v >= nblocks) return;
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
-
 #ifdef PPO_GAE_RES_TRACE
-// Phase timestamps of the resident pass (wall clock, 100 MHz), one row of 8
-// per workgroup: a measurement build only.
+// Phase timestamps of the resident pass (wall clock, 100 MHz), one row of 32
+// per workgroup (6 marks per round): a measurement build only.
 __device__ uint64_t g_res_trace[4096 * 32];
 #define RES_MARK(k) \
   if (threadIdx.x == 0) g_res_trace[blockIdx.x * 32 + (k) + 6 * res_round] = wall_clock64()
@@ -1813,11 +1757,7 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
           slot_clear(bnd + (size_t)rd * a.N + col * E + tid);
       }
     }
-    if (tid < 3) slot_clear(part + (size_t)blockIdx.x * 3 + tid);
-    uint64_t v = 0;
-    if (tid == 0) v = __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);  // the emptying stores (and that read) are done
-    if (tid == 0) res_arrive(ctr, v, a.nonce, gridDim.x);
+    sync_start(ctr, part + (size_t)blockIdx.x * 3, 3, a.nonce);
   }
 
   const double gl0 = mul(a.gl, 0.0);
@@ -1984,16 +1924,16 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
           wa[k] = wp[k] = 0;
           if (u0 - k >= u_lo) {
             uint64_t* sl = comp + (base + (unsigned)(u0 - k) * step);
-            wa[k] = __hip_atomic_load(sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            wp[k] = __hip_atomic_load(sl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wa[k] = slot_peek(sl);
+            wp[k] = slot_peek(sl + 1);
           }
         }
 #pragma unroll
         for (int k = 0; k < LB; ++k) {
           if (u0 - k >= u_lo) {
             uint64_t* sl = comp + (base + (unsigned)(u0 - k) * step);
-            const double ca = wa[k] ? slot_value(wa[k]) : slot_get(sl);
-            const double cp = wp[k] ? slot_value(wp[k]) : slot_get(sl + 1);
+            const double ca = slot_or_get(wa[k], sl);
+            const double cp = slot_or_get(wp[k], sl + 1);
             A = ca + cp * A;
             P = cp * P;
           }
@@ -2209,13 +2149,7 @@ int launch_resident(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
   a.res_nt = rp.nt;
   a.res_ntr = rp.ntr;
   a.res_rounds = rp.rounds;
-  // a different tag for every call (zero is skipped)
-  static std::atomic<unsigned> calls{0x5bd1e995u};
-  unsigned nonce;
-  do {
-    nonce = calls.fetch_add(0x9e3779b9u, std::memory_order_relaxed);
-  } while (nonce == 0u);
-  a.nonce = nonce;
+  a.nonce = next_nonce();
   void* args[] = {&a};
   return hip_status(
       hipLaunchKernel(kern, dim3((unsigned)rp.grid()), dim3(kResBlock), args, 0, stream));
