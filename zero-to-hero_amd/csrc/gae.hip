@@ -280,7 +280,7 @@ SpanPlan span_plan(long T, long N, long blocks) {
 #define PPO_GAE_RES_BLOCK 512
 #endif
 constexpr int kResBlock = PPO_GAE_RES_BLOCK;
-constexpr long kResMaxTiles = 256;  // one 1024-thread workgroup per CU on MI355X
+constexpr long kResMaxTiles = 256;  // one workgroup per CU on MI355X
 
 struct ResPlan {
   int E, L;          // E = 0: not applicable
