@@ -1659,14 +1659,14 @@ int launch_span(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 // Resident pass: the whole rollout in registers, one launch.
 // ---------------------------------------------------------------------------
-// Each 1024-thread workgroup owns a tile of E adjacent envs x TS consecutive
+// Each workgroup (kResBlock threads) owns a tile of E adjacent envs x TS consecutive
 // steps (ResPlan); thread (segment s, env-group g) owns 4 envs x L steps.
 // All of a tile's loads are issued at once and its rows stay in registers
 // until the normalised advantages are stored, so the rollout is read once and
 // each output written once (21 bytes per element with the normaliser):
 //   1. per thread, the segment composite (a, P) with a zero carry (fp64,
 //      reference operation order); a reverse scan over the segments (lane
-//      shuffles, then the 16 waves' composites in LDS) gives every segment
+//      shuffles, then the waves' composites in LDS) gives every segment
 //      the composite of the segments to its right and the tile its own.
 //   2. a tile publishes its per-env composite; the advantage entering it is
 //      the fold of the composites of the tiles to its right in the same env
