@@ -16,13 +16,13 @@ constexpr int kWave = 64;
 constexpr int kBlock = 256;              // threads per workgroup for streaming kernels
 constexpr size_t kHeaderBytes = 256;     // WsHeader at the front of every workspace
 
-// Workspace header.  Cross-workgroup results are always combined by a
-// separate one-block kernel launched after the producer on the same stream:
-// on gfx950 an in-kernel "last block finalises" handshake needs an agent-scope
-// release fence per workgroup, which compiles to a full L2 write-back
-// (buffer_wbl2) and costs far more than one extra launch.
+// Workspace header.  No cross-workgroup combine here uses a release fence: on
+// gfx950 an agent-scope release compiles to a full L2 write-back (buffer_wbl2)
+// per workgroup.  Values that cross workgroups inside a launch travel through
+// agent-scope atomic stores and loads whose completion is awaited explicitly.
 struct WsHeader {
   float stats[4];         // {mean, std, denom, 0} written by the stats finaliser
+  uint64_t epoch;         // Gaussian loss: advanced by one per call (any start value)
 };
 static_assert(sizeof(WsHeader) <= kHeaderBytes, "header too big");
 
