@@ -476,7 +476,8 @@ def test_gae_routing_sweep_matches_oracle(dev, monkeypatch, T, N, p, norm, resid
 # the largest grid (config 2).
 # ---------------------------------------------------------------------------
 RESIDENT_SHAPES = [
-    (2048, 4096, 0.01),   # config 2: 64-env tiles, 16 steps per thread, 64 columns x 4 tiles
+    (2048, 4096, 0.01),   # config 2: 128-env tiles, 16 steps per thread, 32 columns x 8 tiles
+    (1000, 8192, 0.01),   # 128-env tiles, ragged last tile
     (1024, 1024, 0.02),   # 4 steps per thread, 128 tiles
     (3000, 1024, 0.01),   # 8 steps per thread, ragged last tile
     (1025, 2048, 0.05),   # last tile holds one row

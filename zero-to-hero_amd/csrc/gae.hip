@@ -276,6 +276,7 @@ SpanPlan span_plan(long T, long N, long blocks) {
 #ifndef PPO_GAE_RES_E
 #define PPO_GAE_RES_E 0
 #endif
+
 #ifndef PPO_GAE_RES_BLOCK
 #define PPO_GAE_RES_BLOCK 512
 #endif
@@ -290,10 +291,14 @@ struct ResPlan {
   long tiles() const { return nc * nt; }
 };
 
-// Single round: among tiles of 64, 32 or 16 envs and 16, 8 or 4 steps per
-// thread, the shape giving the most tiles that still fit on the device at
-// once (<= 256), with no more than a quarter of a column's threads idle past
-// the horizon; ties go to wider tiles (longer row segments).  Rollouts that
+// Single round: among tiles of 128 envs and 16 steps per thread, or 64, 32
+// or 16 envs and 16, 8 or 4 steps per thread, the shape giving the most tiles
+// that still fit on the device at once (<= 256), with no more than a quarter
+// of a column's threads idle past the horizon; ties go to wider tiles (longer
+// row segments: at T x N = 2048 x 4096 with the normaliser, 128-env tiles
+// measured 38.2-38.5 us per call in the north-star step against 39.1-39.3 us
+// for 64-env tiles; 256-env tiles were slower, their look-back folding 15
+// tiles per column, so 128-env tiles are taken only up to 8 tiles per column).  Rollouts that
 // give fewer than 128 tiles (too little parallelism), or more than 16 tiles
 // per env column without filling the device, take the other paths: measured
 // on MI355X, e.g. T x N = 1024 x 512 (16-64 tiles) 28 us against 24 us on the
@@ -308,16 +313,18 @@ constexpr long kResMaxRounds = 8;
 ResPlan res_plan(long T, long N, bool norm) {
   ResPlan best = {0, 0, 0, 0, 0, 0, 0};
   if (!PPO_GAE_RES || T <= 0 || N <= 0 || T * N >= (1L << 30)) return best;
-  const int Es[3] = {64, 32, 16};
+  const int Es[4] = {128, 64, 32, 16};
   const int Ls[3] = {16, 8, 4};
   for (int E : Es) {
     if (PPO_GAE_RES_E && E != PPO_GAE_RES_E) continue;
     if (N % E != 0) continue;
     for (int L : Ls) {
+      if (E == 128 && L != 16) continue;  // (128-env tiles: 16 steps per thread only)
       const long TS = (long)(kResBlock / (E / 4)) * L;
       const long nt = (T + TS - 1) / TS;
       const long nc = N / E;
       if (nc * nt > kResMaxTiles) continue;
+      if (E == 128 && nt > 8) continue;  // (a longer look-back than 64-env tiles')
       if (4 * (nt * TS - T) > nt * TS) continue;  // a quarter of the threads idle
       if (nc * nt > best.tiles()) {
         best.E = E;
@@ -333,8 +340,9 @@ ResPlan res_plan(long T, long N, bool norm) {
   if (best.E && (best.tiles() < 128 || (best.nt > 16 && best.tiles() < kResMaxTiles)))
     best.E = 0;
   if (best.E || norm) return best;
-  // rounds: the widest tile dividing N, 16 steps per thread
+  // rounds: the widest tile of at most 64 envs dividing N, 16 steps per thread
   for (int E : Es) {
+    if (E == 128) continue;
     if (PPO_GAE_RES_E && E != PPO_GAE_RES_E) continue;
     if (N % E != 0) continue;
     const long nc = N / E;
@@ -2123,6 +2131,8 @@ const void* res_kernel_e(int L, bool stats, bool has_v, bool rounds) {
 
 const void* res_kernel(const ResPlan& rp, bool stats, bool has_v) {
   const bool rounds = rp.rounds > 1;
+  if (rp.E == 128 && !rounds) return res_kernel_el<128, 16>(stats, has_v);
+  if (rp.E == 128) return nullptr;  // (not planned: rounds use at most 64-env tiles)
   if (rp.E == 64) return res_kernel_e<64>(rp.L, stats, has_v, rounds);
   if (rp.E == 32) return res_kernel_e<32>(rp.L, stats, has_v, rounds);
   return res_kernel_e<16>(rp.L, stats, has_v, rounds);
@@ -2136,7 +2146,8 @@ bool resident_ok(long T, long N, bool norm, bool has_v) {
   if (env && env[0] == '0') return false;
   const ResPlan rp = res_plan(T, N, norm);
   if (rp.E == 0) return false;
-  return resident_blocks(res_kernel(rp, norm, has_v), kResBlock, 0, 0) >= rp.grid();
+  const void* kern = res_kernel(rp, norm, has_v);
+  return kern && resident_blocks(kern, kResBlock, 0, 0) >= rp.grid();
 }
 
 // Launches the resident pass when the plan applies and the whole grid fits
