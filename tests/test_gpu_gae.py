@@ -647,3 +647,65 @@ def test_discounted_returns_resident_rounds(dev):
     got = ppo_amd.discounted_returns(r.to(dev), gamma=0.999, dones=d.to(dev)).cpu().numpy()
     a_ref, _ = ref.gae_c(r.numpy(), np.zeros((T, N), np.float32), d.numpy(), None, 0.999, 1.0)
     assert_gae_close(got, a_ref)
+
+
+@pytest.mark.parametrize(
+    "T,N,norm",
+    [
+        (2048, 4096, True),    # one round, 128-env tiles, with the normaliser
+        (1024, 1024, True),    # one round, 64-env tiles, 4 steps per thread
+        (200_000, 128, False), # rounds
+    ],
+)
+def test_gae_resident_graph_replays_match_eager(dev, T, N, norm):
+    """A captured resident-pass call replays with the nonce of its capture: the
+    start barrier must reset the counters that the previous replay (or an eager
+    call in between) completed.  Every replay, with new inputs copied in, and
+    an eager call on the same workspace after it must equal a call on a fresh
+    workspace bit for bit."""
+    from ppo_amd import _lib
+
+    lib = _lib.load()
+    assert _route(T, N, norm) == "resident"
+    print(f"gae resident graph replays T={T} N={N} norm={norm}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(T + N)
+
+    def rollout():
+        return (torch.randn(T, N, device=dev, generator=g), torch.randn(T, N, device=dev, generator=g),
+                (torch.rand(T, N, device=dev, generator=g) < 0.01).to(torch.uint8),
+                torch.randn(N, device=dev, generator=g))
+
+    r, v, d, lv = rollout()
+    ws = torch.full((lib.ppo_gae_workspace_bytes(T, N),), 0x5A, dtype=torch.uint8, device=dev)
+    adv, ret, adv_n = (torch.empty(T, N, device=dev) for _ in range(3))
+
+    def call():
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        if norm:
+            rc = lib.ppo_gae_norm_f32(r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N,
+                                      0.99, 0.95, 1e-8, adv.data_ptr(), ret.data_ptr(),
+                                      adv_n.data_ptr(), None, ws.data_ptr(), ws.numel(), stream)
+        else:
+            rc = lib.ppo_gae_f32(r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N,
+                                 0.99, 0.95, adv.data_ptr(), ret.data_ptr(), ws.data_ptr(),
+                                 ws.numel(), stream)
+        assert rc == 0
+
+    call()
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=torch.cuda.Stream(dev)):
+        call()
+    outs = (adv, ret, adv_n) if norm else (adv, ret)
+    for rep in range(4):
+        for dst, src in zip((r, v, d, lv), rollout()):
+            dst.copy_(src)
+        want = _gae_abi(dev, r, v, d, lv, 0.99, 0.95, norm=norm)
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        for got, w in zip(outs, want):
+            assert torch.equal(got, w), f"replay {rep}"
+        call()  # eager, same workspace, between replays
+        torch.cuda.synchronize(dev)
+        for got, w in zip(outs, want):
+            assert torch.equal(got, w), f"eager after replay {rep}"
