@@ -441,3 +441,45 @@ def test_cat_row_count_sweep(dev, B, A, clip, i64):
 @pytest.mark.parametrize("B,D,clip,_", _loss_sweep(8, [1, 6, 8, 9, 17], 11))
 def test_gauss_row_count_sweep(dev, B, D, clip, _):
     run_gauss(dev, B, D, seed=B + 1000 * D, vf_clip=0.2 if clip else None)
+
+
+# ---------------------------------------------------------------------------
+# Past 2^31 elements: B = 120,000,000 rows x A = 18 (2.16e9 logits, ~21 GB on
+# the device), checked against the same entry point on chunks below 2^31
+# elements (each of which the tests above tie to the oracle).  Rows are
+# independent except for the 1/B in every gradient and the means, so a row's
+# gradient times B must match between the whole call and its chunk's call,
+# and each scalar must equal the B-weighted mean of the chunks' scalars.
+# ---------------------------------------------------------------------------
+def test_cat_past_2_31_elements(dev):
+    B, A, chunks = 120_000_000, 18, 4
+    print(f"loss_cat B={B} A={A} (past 2^31 elements)", flush=True)
+    g = torch.Generator(device=dev).manual_seed(31)
+    logits = torch.randn(B, A, device=dev, generator=g)
+    actions = torch.randint(0, A, (B,), device=dev, generator=g, dtype=torch.int32)
+    old_lp = torch.log_softmax(logits, -1).gather(1, actions[:, None].long()).squeeze(1)
+    old_lp += 0.05 * torch.randn(B, device=dev, generator=g)
+    adv, ret, old_v = (torch.randn(B, device=dev, generator=g) for _ in range(3))
+    val = old_v + 0.1 * torch.randn(B, device=dev, generator=g)
+    scalars, dlogits, dv = ppo_amd.ppo_loss_discrete_fused(logits, actions, old_lp, adv, ret, val,
+                                                           old_v, 0.2, 0.2, 0.5, 0.01)
+    torch.cuda.synchronize(dev)
+    assert torch.isfinite(scalars).all()
+    weighted = torch.zeros(6, dtype=torch.float64)
+    step = B // chunks
+    for c in range(chunks):
+        sl = slice(c * step, B if c == chunks - 1 else (c + 1) * step)
+        bc = sl.stop - sl.start
+        sc, dlc, dvc = ppo_amd.ppo_loss_discrete_fused(
+            logits[sl], actions[sl], old_lp[sl], adv[sl], ret[sl], val[sl], old_v[sl],
+            0.2, 0.2, 0.5, 0.01)
+        weighted += sc.double().cpu() * bc / B
+        # gradients x rows: identical up to fp32 rounding of the 1/B factors
+        for big, small in ((dlogits[sl], dlc), (dv[sl], dvc)):
+            x = big.double() * B
+            y = small.double() * bc
+            tol = 1e-5 * y.abs() + 1e-6 * float(y.abs().max())
+            assert bool(((x - y).abs() <= tol).all()), c
+        del sc, dlc, dvc
+    # every scalar is linear in the chunks' (fp32-rounded) means
+    torch.testing.assert_close(scalars.double().cpu(), weighted, rtol=2e-5, atol=1e-6)
