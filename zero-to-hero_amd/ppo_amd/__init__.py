@@ -11,6 +11,9 @@ include/ppo_amd.h) behind the reference's own PPO surface:
             and common.py, same names and signatures
   rollout   RolloutBuffer ([T,N] env-contiguous, on device) and VecPPO
   optim     ClippedAdam (clip_grad_norm_ + Adam, two launches)
+  torch_ops the hot path as registered operators, torch.ops.ppo_amd.*
+            (gae, gae_normalize, normalize_advantages, ppo_loss_discrete,
+            ppo_loss_gaussian), visible to torch.compile and the dispatcher
 """
 
 from . import _lib
@@ -42,6 +45,7 @@ from .ops import (
     sample_categorical,
     sample_gaussian,
 )
+from . import torch_ops  # registers torch.ops.ppo_amd.*
 from .env import CartPoleVec
 from .optim import ClippedAdam
 from .rollout import RolloutBuffer, VecPPO
