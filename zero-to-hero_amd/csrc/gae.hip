@@ -1784,26 +1784,33 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
     }
     d[i] = load_done_raw<VW>(at_byte(a.d, off));
   };
+  // (branch-free: one load from a valid address, zeros selected after; a
+  // load under a branch leaves the compiler unable to count the wave's
+  // outstanding loads, and it then waits for all of them)
   auto load_next_value = [&](long ts0) {
     const long tn = ts0 + L;
+    const bool inner = tn < a.T;
+    const float* src = inner ? (kHasV ? a.v + (unsigned)tn * n32 + (unsigned)env0 : a.r + env0)
+                             : (a.lastv ? a.lastv + env0 : a.r + env0);
+    float x[VW];
+    load_vec<VW>(src, x);
+    const bool use = inner ? kHasV : a.lastv != nullptr;
 #pragma unroll
-    for (int k = 0; k < VW; ++k) nv[k] = 0.0f;
-    if (tn < a.T) {
-      if constexpr (kHasV) load_vec<VW>(a.v + (unsigned)tn * n32 + (unsigned)env0, nv);
-    } else if (a.lastv) {
-      load_vec<VW>(a.lastv + env0, nv);
-    }
+    for (int k = 0; k < VW; ++k) nv[k] = use ? x[k] : 0.0f;
   };
   int nvalid = 0;
   long t0 = 0;
   // the first round's rows, last row first, as step 1 consumes them; later
   // rounds' rows are loaded row by row as the round before stores its own
-  // (software pipelining across rounds: the registers are the buffers)
+  // (software pipelining across rounds: the registers are the buffers).  The
+  // value row after the segment goes first: step 1 needs it before any row,
+  // and a wave's loads complete in order, so a wait for the last-issued load
+  // would be a wait for all of them.
   if (tile_tt(0) >= 0) {
     const long ts0 = tile_tt(0) * TS + (long)sg * L;
+    load_next_value(ts0);
 #pragma unroll
     for (int i = L - 1; i >= 0; --i) load_row(ts0, i);
-    load_next_value(ts0);
   }
   for (long rd = 0; rd < rounds; ++rd) {
     const long tt = tile_tt(rd);
@@ -1838,13 +1845,16 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
         if (i < nvalid) {
 #pragma unroll
           for (int k = 0; k < VW; ++k) {
+            // (the composites only carry the advantage between segments: fp64
+            // with fused multiply-adds, 5 operations; the advantages
+            // themselves come from the exact recurrence below)
             const bool done = ((d[i] >> (8 * k)) & 0xffu) != 0u;
             const double vd = (double)v[i][k];
             const double dl =
-                sub(add((double)r[i][k], mul(mul(a.gamma, nvd[k]), done ? 0.0 : 1.0)), vd);
+                __builtin_fma(a.gamma * nvd[k], done ? 0.0 : 1.0, (double)r[i][k]) - vd;
             const double cc = done ? gl0 : a.gl;
-            ia[k] = add(dl, mul(cc, ia[k]));
-            ip[k] = mul(ip[k], cc);
+            ia[k] = __builtin_fma(cc, ia[k], dl);
+            ip[k] = ip[k] * cc;
             nvd[k] = vd;
             if constexpr (kStats) {
               const float fa = (float)ia[k], fp = (float)ip[k];
@@ -2019,6 +2029,11 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       double nvd[VW];
 #pragma unroll
       for (int k = 0; k < VW; ++k) nvd[k] = nv[k];
+      if constexpr (kRounds) {
+        // (first of the next round's loads; after the last round, rows past
+        // the horizon: every thread re-reads row 0, unconditionally)
+        load_next_value(tt_next >= 0 ? t0_next : a.T);
+      }
       // rows from the last: each row is stored as soon as its 4 envs are done
 #pragma unroll
       for (int i = L - 1; i >= 0; --i) {
@@ -2042,13 +2057,8 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
             store_vec<VW>(at_byte(a.ret, off), rt);
           }
         }
-        if constexpr (kRounds) {
-          if (tt_next >= 0) load_row(t0_next, i);  // row i of the next round's tile
-        }
+        if constexpr (kRounds) load_row(tt_next >= 0 ? t0_next : a.T, i);  // next round's row i
       }
-    }
-    if constexpr (kRounds) {
-      if (tt_next >= 0) load_next_value(t0_next);
     }
     RES_MARK(3);
     if constexpr (kStats) {
