@@ -34,6 +34,12 @@
 extern "C" {
 #endif
 
+/* The library is built with hidden symbol visibility; only what this header
+   declares is exported. */
+#if defined(__GNUC__)
+#pragma GCC visibility push(default)
+#endif
+
 #define PPO_OK 0
 #define PPO_ERR_INVALID_ARG 1     /* null pointer, negative size, bad coefficient */
 #define PPO_ERR_WORKSPACE 2       /* workspace missing or smaller than required */
@@ -454,6 +460,10 @@ int ppo_cartpole_rollout_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* crit
                              float* values_buf, float* rewards_buf, uint8_t* dones_buf,
                              float* episode_return, double* completed_sum,
                              int32_t* completed_count, void* stream);
+
+#if defined(__GNUC__)
+#pragma GCC visibility pop
+#endif
 
 #ifdef __cplusplus
 }

@@ -2381,7 +2381,7 @@ extern "C" int ppo_gae_norm_f32(const float* rewards, const float* values, const
 }
 
 #ifdef PPO_GAE_RES_TRACE
-extern "C" void* ppo_debug_res_trace(void) {
+extern "C" __attribute__((visibility("default"))) void* ppo_debug_res_trace(void) {
   void* p = nullptr;
   if (hipGetSymbolAddress(&p, HIP_SYMBOL(ppo::g_res_trace)) != hipSuccess) return nullptr;
   return p;
