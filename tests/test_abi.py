@@ -39,6 +39,9 @@ def test_nm_shows_c_linkage():
     syms = os.popen(f"nm -D --defined-only {_lib.LIB_PATH}").read()
     for name in declared_functions():
         assert re.search(rf"\bT {name}$", syms, flags=re.M), name
+    # and nothing else: the library is built with hidden visibility
+    exported = set(re.findall(r"\bT (\S+)$", syms, flags=re.M))
+    assert exported == set(declared_functions()), sorted(exported ^ set(declared_functions()))
 
 
 def test_version_and_strerror():
