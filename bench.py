@@ -1,12 +1,12 @@
 """PPO-update throughput on one MI355X.
 
 A "step" is one pass of the PPO update hot path over one synthetic rollout of
-T x N = 2048 x 4096 = 8,388,608 samples (BASELINE config 2's rollout):
+T x N = 2048 x 4096 = 8,388,608 samples (the benchmark's GAE + normalise rollout):
   1. ppo_gae_norm_f32  — GAE with bootstrap + returns + advantage
                          normalisation (rl/deep/agents/ppo.py:123-127)
   2. ppo_loss_cat_f32  — fused categorical PPO loss forward+backward over all
                          B = T*N samples, A = 18 actions, vf_clip = 0.2
-                         (ppo.py:150-169; BASELINE config-4 layout)
+                         (ppo.py:150-169; A = 18, value clipping 0.2)
 Inputs are resident in HBM before the timed region.  `value` is samples/s
 (B / step time).  `roofline` is for the dominant kernel (the fused loss:
 172 algorithmic bytes per sample), timed with HIP events on the stream it is
@@ -15,7 +15,7 @@ launched on.  `cpu_baseline` times the CPU restatement of the same path
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--suite]
 
---suite additionally prints one line per BASELINE config (2-5) kernel, for
+--suite additionally prints one line per benchmark configuration (2-5) kernel, for
 the roofline table; --update-suite times the whole minibatch update loop;
 the driver's contract line is always the last line.
 """
@@ -60,7 +60,7 @@ def parse_args():
 
 
 def synthetic_rollout(torch, dev, T, N, A, seed=24):
-    """BASELINE config-2 rollout + config-4 loss inputs, generated on the GPU
+    """The T x N rollout and the categorical loss inputs, generated on the GPU
     from a seeded generator."""
     g = torch.Generator(device=dev).manual_seed(seed)
     B = T * N
@@ -245,7 +245,7 @@ def time_events(torch, fn, reps, flush=None):
 
 
 def suite(torch, lib, dev):
-    """One line per BASELINE config kernel chain (2: GAE+normalise, 3: long-T
+    """One line per benchmark configuration's kernel chain (2: GAE+normalise, 3: long-T
     GAE scan, 4: discrete loss, 5: Gaussian loss), each timed through the C
     ABI with preallocated outputs (HIP events on the launch stream).  Each
     timed call follows a read of a 512 MiB buffer, so its inputs come from HBM
@@ -339,7 +339,7 @@ def suite(torch, lib, dev):
 def update_suite(torch, dev, reps=10):
     """The whole update loop (ppo.py:113-171 generalised to [T,N]): GAE +
     normalisation + `epochs` x shuffled minibatches of MLP forward, fused loss,
-    backward and optimizer step.  BASELINE config 1 (T=128, N=8, MLP 4-64-64
+    backward and optimizer step.  Configuration 1 (T=128, N=8, MLP 4-64-64
     tanh, A=2, 4 epochs x 4 minibatches of 256) and a larger T=2048, N=64 case
     (minibatches of 4096).  Times VecPPO with the fused MLP minibatch kernel +
     ClippedAdam replayed from graphs, the same eagerly, graph replay with

@@ -167,7 +167,7 @@ def gae_c(
     lam: float,
 ) -> tuple[np.ndarray, np.ndarray]:
     """gae_ref.c through ctypes: same contract and bits as gae_numpy(), fast
-    enough for the full BASELINE shapes (8M-17M elements in well under 1 s)."""
+    enough for the full benchmark shapes (8M-17M elements in well under 1 s)."""
     T, N = rewards.shape
     r = np.ascontiguousarray(rewards, dtype=np.float32)
     v = np.ascontiguousarray(values, dtype=np.float32)

@@ -257,7 +257,7 @@ def test_agent_vf_clip_uses_rollout_values(dev, monkeypatch):
 
 
 # ---------------------------------------------------------------------------
-# BASELINE config 1 at its own shape: T=128 x N=8, 4-64-64 tanh, minibatches
+# Configuration 1 at its own shape: T=128 x N=8, 4-64-64 tanh, minibatches
 # of 256, 4 epochs, through every VecPPO update path, against the CPU oracle
 # (two rollouts in a row, so the graph path replays captured graphs).
 # ---------------------------------------------------------------------------

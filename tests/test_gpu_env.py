@@ -91,7 +91,7 @@ def test_cartpole_vec_reset_and_episode_tally(dev):
 
 
 def test_ppo_trains_cartpole_on_device(dev):
-    """PPO (BASELINE config 1 networks: 4-64-64 tanh) on 64 vectorised
+    """PPO (configuration 1's networks: 4-64-64 tanh) on 64 vectorised
     CartPole-v1 environments, every step on the GPU: the mean return of
     completed episodes rises from ~20 (random play) past 300 within 30
     iterations of 128 steps."""

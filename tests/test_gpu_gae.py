@@ -6,7 +6,7 @@ Tolerance: the kernel evaluates the same fp64 recurrence in the same order;
 only the carries entering each thread's segment are composed with a scan
 (reassociated fp64), so outputs may differ from the oracle by at most one
 fp32 ulp, or by 1e-9 absolute where the fp32 result is a near-cancellation.
-BASELINE's bar (rel 1e-5) is far looser.  Returns = advantages + values must
+The benchmark's stated bar (rel 1e-5) is far looser.  Returns = advantages + values must
 then match bit for bit wherever the advantages do.
 """
 
@@ -148,13 +148,13 @@ def test_gae_nonzero_done_bytes_count_as_done(dev):
 
 
 def test_gae_config2_full_size(dev):
-    """T=2048, N=4096, dones Bernoulli(0.01)."""
+    """Configuration 2: T=2048, N=4096, dones Bernoulli(0.01)."""
     exact = _run(dev, 2048, 4096, 0.01, seed=24)
     assert exact > 0.99
 
 
 def test_gae_config3_full_size(dev):
-    """T=1,048,576, N=16, dones Bernoulli(0.001), gamma .999."""
+    """Configuration 3: T=1,048,576, N=16, dones Bernoulli(0.001), gamma .999."""
     exact = _run(dev, 1_048_576, 16, 0.001, seed=24, gamma=0.999, lam=0.95)
     assert exact > 0.99
 

@@ -2,7 +2,7 @@
 torch autograd on the CPU (oracle.loss_categorical_reference /
 loss_gaussian_reference, which run ppo.py:150-169's own torch calls).
 
-Tolerances (BASELINE): loss scalars rel 1e-5; gradients rel 1e-4 per element
+Tolerances (the benchmark's stated bar): loss scalars rel 1e-5; gradients rel 1e-4 per element
 with an absolute floor of 1e-5 * max|g_ref| for elements near zero (the
 gradient of a softmax row sums to zero, so some entries are cancellations).
 """
@@ -120,7 +120,7 @@ def assert_scalars_close(scalars, o, rtol=1e-5, edge_rows=0):
 
 
 def cat_inputs(B, A, seed, act_dtype=torch.int32):
-    """BASELINE config-4 distributions: logits ~ N(0,1); actions sampled from
+    """Configuration 4's distributions: logits ~ N(0,1); actions sampled from
     softmax(old_logits), old_logits = logits + N(0, 0.05); adv, ret, old
     values ~ N(0,1); values = old values + N(0, 0.1)."""
     g = torch.Generator().manual_seed(seed)
@@ -279,7 +279,7 @@ def test_cat_misaligned_logits(dev):
 
 
 def test_cat_config4_full_size(dev):
-    """B=1,048,576, A=18, vf_clip=0.2."""
+    """Configuration 4: B=1,048,576, A=18, vf_clip=0.2."""
     scalars, dlogits, _ = run_cat(dev, 1_048_576, 18, seed=24, vf_clip=0.2)
     # size-independent invariant: each softmax row of the gradient sums to 0
     rows = dlogits.double().sum(1).abs().max().item()
@@ -316,7 +316,7 @@ def test_cat_out_of_range_action(dev):
 # Gaussian
 # ---------------------------------------------------------------------------
 def gauss_inputs(B, D, seed):
-    """BASELINE config-5 distributions: mu ~ N(0,1); log_std ~ U(-1,0);
+    """Configuration 5's distributions: mu ~ N(0,1); log_std ~ U(-1,0);
     actions ~ N(mu_old, exp(log_std)), mu_old = mu + N(0, 0.05)."""
     g = torch.Generator().manual_seed(seed)
     mu = torch.randn(B, D, generator=g)
@@ -398,7 +398,7 @@ def test_gauss_misaligned_mu(dev):
 
 
 def test_gauss_config5_full_size(dev):
-    """B=2,097,152, D=6, vf_clip=0.2."""
+    """Configuration 5: B=2,097,152, D=6, vf_clip=0.2."""
     run_gauss(dev, 2_097_152, 6, seed=24)
 
 

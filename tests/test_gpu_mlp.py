@@ -74,7 +74,7 @@ def _check(dev, n, D, H, A, act, B, seed, vf_clip=None, act64=False, use_index=T
 @pytest.mark.parametrize(
     "n,D,H,A,act,B",
     [
-        (1024, 4, 64, 2, "tanh", 256),     # BASELINE config 1 minibatch
+        (1024, 4, 64, 2, "tanh", 256),     # configuration 1's minibatch
         (1024, 4, 128, 2, "relu", 128),    # the reference's MLP(4, 128, 2) and batch_size
         (300, 8, 32, 5, "relu", 100),      # B not a multiple of 16
         (200, 17, 64, 18, "tanh", 37),     # odd obs dim, 18 actions

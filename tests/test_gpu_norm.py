@@ -1,7 +1,7 @@
 """GPU parity of advantage normalisation (ppo.py:126-127) against the
 reference's torch-CPU expression, and of the fused GAE+normalise path.
 
-Tolerance: rel 1e-5 (BASELINE) with atol 1e-6 for elements near the mean.
+Tolerance: rel 1e-5 (the benchmark's stated bar) with atol 1e-6 for elements near the mean.
 The kernel's mean/std are fp64 sums rounded to fp32; torch's are fp32
 reductions, so the two can differ by a few fp32 ulps.
 """

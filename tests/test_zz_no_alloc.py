@@ -61,7 +61,7 @@ def _run(lib, dev, B, A, seed, int64, vf_clip):
 def test_noalloc_matches_workspace_entry_point(dev):
     lib = _lib.load()
     for B, A, seed, int64, vf_clip in (
-        (1 << 20, 18, 1, False, 0.2),   # BASELINE config 4's shape, persistent grid
+        (1 << 20, 18, 1, False, 0.2),   # configuration 4's shape, persistent grid
         (10_007, 18, 2, True, 0.0),     # smaller: fewer workgroups than the first call
         (3_001, 64, 3, False, 0.2),     # wave-per-row kernel
         (257, 2, 4, False, 0.0),        # smaller again

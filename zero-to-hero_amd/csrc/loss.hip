@@ -1019,7 +1019,7 @@ __global__ void __launch_bounds__(kBlock) loss_gauss_dense_kernel(LossArgs a, lo
 // ---------------------------------------------------------------------------
 // Gaussian, wave tiles (16-byte-aligned mu/actions/dmu, D <= MAXD <= 8; KD >
 // 0 fixes D at compile time): the categorical wave-tile scheme applied to the
-// Gaussian policy (config 5, D = 6: 48.8 us per call against 49.6-50.0 us for
+// Gaussian policy (B = 2,097,152, D = 6: 48.8 us per call against 49.6-50.0 us for
 // the 256-row dense kernel).  Each wave owns tiles of 64 consecutive rows (one
 // contiguous span of 64*D floats of mu and of actions: 16*D float4 each),
 // staged through its own LDS slice in their global layout, so no workgroup

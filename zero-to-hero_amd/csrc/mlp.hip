@@ -2,7 +2,7 @@
 //
 // Reference: PPOAgent._update_batch, rl/deep/agents/ppo.py:141-169, with the
 // networks of rl/deep/agents/common.py:16-28 (MLP: Linear-act-Linear-act-
-// Linear; the reference uses ReLU, BASELINE's CartPole config tanh):
+// Linear; the reference uses ReLU, the benchmark's CartPole configuration tanh):
 //     values = value(observations).squeeze(1)                     (:147)
 //     logits = policy(observations)                                (:149)
 //     ... the PPO loss of ppo.py:150-167 (row_math.hpp) ...

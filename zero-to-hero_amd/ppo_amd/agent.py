@@ -62,7 +62,7 @@ class PPOConfig:
 # ---------------------------------------------------------------------------
 class MLP(nn.Module):
     """Linear-act-Linear-act-Linear, rl/deep/agents/common.py:16-28.  The
-    reference uses ReLU; `activation="tanh"` gives BASELINE's 4-64-64 tanh
+    reference uses ReLU; `activation="tanh"` gives the benchmark's 4-64-64 tanh
     variant."""
 
     def __init__(self, input_size: int, hidden_size: int, output_size: int,
