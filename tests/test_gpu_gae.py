@@ -570,6 +570,23 @@ def test_gae_resident_normalise_in_place(dev):
     assert torch.equal(out, adv_n) and torch.equal(ret2, ret)
 
 
+def test_gae_out_may_not_alias_inputs_or_each_other(dev):
+    """ops.gae / gae_normalize refuse caller outputs that overlap an input or
+    each other (the passes read the value row after each segment while other
+    workgroups store theirs); disjoint views of one buffer are accepted."""
+    T, N = 64, 32
+    r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.01, seed=9))
+    adv, ret = ppo_amd.gae(r, v, d, lv)
+    with pytest.raises(ValueError, match="overlaps"):
+        ppo_amd.gae(r, v, d, lv, out=(v, torch.empty_like(r)))
+    buf = torch.empty(3, T, N, device=dev)
+    with pytest.raises(ValueError, match="overlaps"):
+        ppo_amd.gae_normalize(r, v, d, lv, out=(buf[0], buf[0], buf[1]))
+    a2, r2, n2 = ppo_amd.gae_normalize(r, v, d, lv, out=(buf[0], buf[1], buf[2]))
+    torch.cuda.synchronize(dev)
+    assert torch.equal(a2, adv) and torch.equal(r2, ret)
+
+
 def test_discounted_returns_resident(dev):
     """values = None (REINFORCE returns) on the resident pass."""
     T, N = 4096, 512

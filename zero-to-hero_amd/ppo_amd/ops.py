@@ -146,9 +146,16 @@ def _gae_inputs(rewards, values, dones, last_value):
     return device, T, N
 
 
-def _outputs(out, count, like: torch.Tensor) -> list:
+def _span(t: torch.Tensor) -> tuple[int, int]:
+    lo = t.data_ptr()
+    return lo, lo + t.numel() * t.element_size()
+
+
+def _outputs(out, count, like: torch.Tensor, inputs: tuple = ()) -> list:
     """Caller-provided output tensors (fp32, contiguous, the shape of `like`,
-    on its device), or new ones."""
+    on its device, overlapping neither each other nor `inputs`), or new ones.
+    (The GAE passes read a row of values after each segment while other
+    workgroups store theirs, so an output may not alias an input.)"""
     if out is None:
         return [torch.empty_like(like) for _ in range(count)]
     if len(out) != count:
@@ -157,6 +164,11 @@ def _outputs(out, count, like: torch.Tensor) -> list:
         _require(t, f"out[{k}]", (torch.float32,), like.device)
         if t.shape != like.shape:
             raise ValueError(f"out[{k}] must have shape {tuple(like.shape)}, got {tuple(t.shape)}")
+    spans = [_span(t) for t in out]
+    others = spans + [_span(t) for t in inputs if t is not None and t.numel() > 0]
+    for k, (lo, hi) in enumerate(spans):
+        if hi > lo and any(j != k and lo < h and l < hi for j, (l, h) in enumerate(others)):
+            raise ValueError(f"out[{k}] overlaps another output or an input")
     return list(out)
 
 
@@ -179,7 +191,7 @@ def gae(
     `out` = (advantages, returns) when given.
     """
     device, T, N = _gae_inputs(rewards, values, dones, last_value)
-    adv, ret = _outputs(out, 2, rewards)
+    adv, ret = _outputs(out, 2, rewards, (rewards, values, dones, last_value))
     if T * N == 0:
         return adv, ret
     stream = _stream(device)
@@ -211,7 +223,7 @@ def gae_normalize(
     [2] fp32 device tensor {mean, std}; the first three are written into
     `out` when given."""
     device, T, N = _gae_inputs(rewards, values, dones, last_value)
-    adv, ret, adv_n = _outputs(out, 3, rewards)
+    adv, ret, adv_n = _outputs(out, 3, rewards, (rewards, values, dones, last_value))
     stats = torch.empty(2, dtype=torch.float32, device=device)
     if T * N > 0:
         stream = _stream(device)
