@@ -49,6 +49,9 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--suite", action="store_true")
+    ap.add_argument("--no-stream", action="store_true",
+                    help="--suite without the back-to-back timing (us_stream), so that "
+                         "profiler passes see only the isolated calls")
     ap.add_argument("--update-suite", action="store_true",
                     help="also time the whole minibatch update loop (VecPPO) vs the CPU oracle")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -244,12 +247,33 @@ def time_events(torch, fn, reps, flush=None):
     return sum(ms) / len(ms) / 1e3
 
 
-def suite(torch, lib, dev):
+def time_stream(torch, calls, passes):
+    """Average duration (s) of one call when `calls` (one per buffer set) run
+    back to back, `passes` times round, between two HIP events on the current
+    stream.  The sets together are well over the 256 MB Infinity Cache, so
+    each call's inputs come from HBM while the previous call's writes drain."""
+    for fn in calls:
+        fn()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(passes):
+        for fn in calls:
+            fn()
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / (passes * len(calls))
+
+
+def suite(torch, lib, dev, stream_timing=True):
     """One line per benchmark configuration's kernel chain (2: GAE+normalise, 3: long-T
     GAE scan, 4: discrete loss, 5: Gaussian loss), each timed through the C
-    ABI with preallocated outputs (HIP events on the launch stream).  Each
-    timed call follows a read of a 512 MiB buffer, so its inputs come from HBM
-    rather than the 256 MB Infinity Cache (configs 2, 4 and 5 fit in it)."""
+    ABI with preallocated outputs (HIP events on the launch stream), two ways:
+    `us`, each timed call alone after a read of a 512 MiB buffer, so that its
+    inputs come from HBM rather than the 256 MB Infinity Cache (configs 2, 4
+    and 5 fit in it); and `us_stream`, calls back to back over several copies
+    of the buffers (time_stream), without the idle time that event records
+    around a single call leave on the device."""
     import ctypes
 
     from ppo_amd import _lib
@@ -268,42 +292,56 @@ def suite(torch, lib, dev):
     def ws(nbytes):
         return torch.empty(nbytes, dtype=torch.uint8, device=dev)
 
+    def measure(name, units, bpu, make, copies):
+        """make(k) -> the call on buffer set k (set 0 also times `us`)."""
+        calls = [make(k) for k in range(copies if stream_timing else 1)]
+        calls[0]()
+        t = time_events(torch, calls[0], 30, flush)
+        out.append((name, units, bpu, t, time_stream(torch, calls, 8) if stream_timing else None))
+        del calls
+
     # config 2 and 3: GAE over [T,N]
-    for name, T, N, pd, gamma, norm in (("config2_gae_norm", 2048, 4096, 0.01, 0.99, True),
-                                        ("config3_long_scan", 1_048_576, 16, 0.001, 0.999, False)):
+    for name, T, N, pd, gamma, norm, copies in (
+            ("config2_gae_norm", 2048, 4096, 0.01, 0.99, True, 4),
+            ("config3_long_scan", 1_048_576, 16, 0.001, 0.999, False, 3)):
         r = torch.randn(T, N, generator=g, **f32)
         v = torch.randn(T, N, generator=g, **f32)
         d = (torch.rand(T, N, device=dev, generator=g) < pd).to(torch.uint8)
         lv = torch.randn(N, generator=g, **f32)
-        adv, ret, advn = (torch.empty(T, N, **f32) for _ in range(3))
         w = ws(lib.ppo_gae_workspace_bytes(T, N))
-        if norm:
-            fn = lambda: lib.ppo_gae_norm_f32(  # noqa: E731
-                r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N, gamma, 0.95,
-                1e-8, adv.data_ptr(), ret.data_ptr(), advn.data_ptr(), None, w.data_ptr(),
-                w.numel(), stream)
-            bpu = GAE_BYTES
-        else:
-            fn = lambda: lib.ppo_gae_f32(  # noqa: E731
+
+        def make(k, r=r, v=v, d=d, lv=lv, T=T, N=N, gamma=gamma, norm=norm, w=w):
+            if k:
+                r, v, d = r.clone(), v.clone(), d.clone()
+            adv, ret, advn = (torch.empty(T, N, **f32) for _ in range(3))
+            if norm:
+                return lambda: lib.ppo_gae_norm_f32(
+                    r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N, gamma, 0.95,
+                    1e-8, adv.data_ptr(), ret.data_ptr(), advn.data_ptr(), None, w.data_ptr(),
+                    w.numel(), stream)
+            return lambda: lib.ppo_gae_f32(
                 r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N, gamma, 0.95,
                 adv.data_ptr(), ret.data_ptr(), w.data_ptr(), w.numel(), stream)
-            bpu = SCAN_BYTES
-        fn()
-        out.append((name, T * N, bpu, time_events(torch, fn, 30, flush)))
-        del r, v, d, adv, ret, advn, w
+
+        measure(name, T * N, GAE_BYTES if norm else SCAN_BYTES, make, copies)
+        del r, v, d, w, make
     # config 4: discrete loss
     x = synthetic_rollout(torch, dev, 256, 4096, 18, seed=25)
     B, A = x["logits"].shape
-    dl, dv, sc = torch.empty(B, A, **f32), torch.empty(B, **f32), torch.empty(6, **f32)
+    sc = torch.empty(6, **f32)
     w = ws(lib.ppo_loss_cat_workspace_bytes(B, A))
-    fn = lambda: lib.ppo_loss_cat_f32(  # noqa: E731
-        x["logits"].data_ptr(), B, A, x["actions"].data_ptr(), 0, x["old_log_probs"].data_ptr(),
-        x["rewards"].data_ptr(), x["values"].data_ptr(), x["new_values"].data_ptr(),
-        x["values"].data_ptr(), ctypes.byref(params), dl.data_ptr(), dv.data_ptr(),
-        sc.data_ptr(), w.data_ptr(), w.numel(), stream)
-    fn()
-    out.append(("config4_loss_cat", B, LOSS_CAT_BYTES, time_events(torch, fn, 30, flush)))
-    del x, dl, dv, w
+
+    def make(k):
+        y = x if k == 0 else {key: t.clone() for key, t in x.items()}
+        dl, dv = torch.empty(B, A, **f32), torch.empty(B, **f32)
+        return lambda: lib.ppo_loss_cat_f32(
+            y["logits"].data_ptr(), B, A, y["actions"].data_ptr(), 0,
+            y["old_log_probs"].data_ptr(), y["rewards"].data_ptr(), y["values"].data_ptr(),
+            y["new_values"].data_ptr(), y["values"].data_ptr(), ctypes.byref(params),
+            dl.data_ptr(), dv.data_ptr(), sc.data_ptr(), w.data_ptr(), w.numel(), stream)
+
+    measure("config4_loss_cat", B, LOSS_CAT_BYTES, make, 4)
+    del x, w, make
     # config 5: Gaussian loss
     B, D = 2_097_152, 6
     mu = torch.randn(B, D, generator=g, **f32)
@@ -311,29 +349,44 @@ def suite(torch, lib, dev):
     acts = mu + 0.05 * torch.randn(B, D, generator=g, **f32) + ls.exp() * torch.randn(
         B, D, generator=g, **f32)
     rows = [torch.randn(B, generator=g, **f32) for _ in range(5)]
-    dmu, dls, dv = torch.empty(B, D, **f32), torch.empty(D, **f32), torch.empty(B, **f32)
     w = ws(lib.ppo_loss_gauss_workspace_bytes(B, D))
-    fn = lambda: lib.ppo_loss_gauss_f32(  # noqa: E731
-        mu.data_ptr(), ls.data_ptr(), B, D, acts.data_ptr(), rows[0].data_ptr(),
-        rows[1].data_ptr(), rows[2].data_ptr(), rows[3].data_ptr(), rows[4].data_ptr(),
-        ctypes.byref(params), dmu.data_ptr(), dls.data_ptr(), dv.data_ptr(), sc.data_ptr(),
-        w.data_ptr(), w.numel(), stream)
-    fn()
-    out.append(("config5_loss_gauss", B, GAUSS_BYTES, time_events(torch, fn, 30, flush)))
-    del mu, acts, rows, dmu, dls, dv, w
+
+    def make(k):
+        m, a_, rs = (mu, acts, rows) if k == 0 else (mu.clone(), acts.clone(),
+                                                     [t.clone() for t in rows])
+        dmu, dls, dv = torch.empty(B, D, **f32), torch.empty(D, **f32), torch.empty(B, **f32)
+        return lambda: lib.ppo_loss_gauss_f32(
+            m.data_ptr(), ls.data_ptr(), B, D, a_.data_ptr(), rs[0].data_ptr(),
+            rs[1].data_ptr(), rs[2].data_ptr(), rs[3].data_ptr(), rs[4].data_ptr(),
+            ctypes.byref(params), dmu.data_ptr(), dls.data_ptr(), dv.data_ptr(), sc.data_ptr(),
+            w.data_ptr(), w.numel(), stream)
+
+    measure("config5_loss_gauss", B, GAUSS_BYTES, make, 4)
+    del mu, acts, rows, w, make
     # the north-star step with A = 2 (CartPole's action count): GAE+norm + loss
     x = synthetic_rollout(torch, dev, T_STEPS, N_ENVS, 2, seed=26)
-    st = Step(torch, lib, x, dev)
+    steps = [Step(torch, lib, x, dev)]
+    if stream_timing:
+        steps.append(Step(torch, lib, {key: t.clone() for key, t in x.items()}, dev))
+    st = steps[0]
     st.gae()
     st.loss()
-    out.append(("north_star_A2_loss", st.B, LOSS_CAT_A2_BYTES, time_events(torch, st.loss, 30, flush)))
+    out.append(("north_star_A2_loss", st.B, LOSS_CAT_A2_BYTES,
+                time_events(torch, st.loss, 30, flush),
+                time_stream(torch, [s_.loss for s_ in steps], 8) if stream_timing else None))
     out.append(("north_star_A2_step", st.B, GAE_BYTES + LOSS_CAT_A2_BYTES,
-                time_events(torch, lambda: (st.gae(), st.loss()), 30, flush)))
-    for name, units, bpu, t in out:
+                time_events(torch, lambda: (st.gae(), st.loss()), 30, flush),
+                time_stream(torch, [lambda s_=s_: (s_.gae(), s_.loss()) for s_ in steps], 8)
+                if stream_timing else None))
+    del steps, st, x
+    for name, units, bpu, t, ts in out:
         gbs = units * bpu / t / 1e9
-        print(json.dumps({"suite": name, "units": units, "bytes_per_unit": bpu,
-                          "us": round(t * 1e6, 2), "GB/s": round(gbs, 1),
-                          "frac": round(gbs / HBM_PEAK_GBS, 4)}), flush=True)
+        line = {"suite": name, "units": units, "bytes_per_unit": bpu, "us": round(t * 1e6, 2),
+                "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        if ts is not None:
+            line["us_stream"] = round(ts * 1e6, 2)
+            line["frac_stream"] = round(units * bpu / ts / 1e9 / HBM_PEAK_GBS, 4)
+        print(json.dumps(line), flush=True)
 
 
 def update_suite(torch, dev, reps=10):
@@ -432,7 +485,7 @@ def main():
     lib = ppo_amd.load_library()
     dev = torch.device("cuda:0")
     if args.suite:
-        suite(torch, lib, dev)
+        suite(torch, lib, dev, stream_timing=not args.no_stream)
         torch.cuda.empty_cache()
     if args.update_suite:
         update_suite(torch, dev)
