@@ -486,6 +486,9 @@ RESIDENT_SHAPES = [
     (15_500, 288, 0.001), # 32-env tiles, 16 steps per thread, ragged
     (2048, 1024, 0.0),    # no dones: every carry crosses every tile
     (1024, 2048, 1.0),    # every step done
+    (32_768, 144, 0.01),  # 16-env tiles (paired rows), 16 steps per thread
+    (16_000, 144, 0.01),  # 16-env tiles, 8 steps per thread, ragged
+    (8_000, 144, 0.02),   # 16-env tiles, 4 steps per thread, ragged
 ]
 
 
@@ -641,6 +644,7 @@ def test_gae_resident_non_finite_carry(dev):
 # at its left edge to the next; one to many env columns, a partial last round.
 ROUND_SHAPES = [
     (1 << 20, 16, 0.001),   # config 3's shape: 16-env tiles, 2 rounds
+    (1_000_003, 16, 0.001), # 16-env tiles, 2 rounds, the last tile ragged
     (600_000, 32, 0.002),   # 32-env tiles, 3 rounds, the last one partial
     (200_000, 128, 0.01),   # 2 columns x 128 tiles per round, 4 rounds
     (300_000, 64, 0.0),     # no dones: every carry crosses every tile and round
