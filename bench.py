@@ -36,6 +36,7 @@ for p in (os.path.join(ROOT, "zero-to-hero_amd"), ROOT):
 
 HBM_PEAK_GBS = 8000.0
 T_STEPS, N_ENVS, N_ACTIONS = 2048, 4096, 18
+ROLLOUT_COPIES = 4  # rollouts the timed steps cycle through (4 x 75 MB > the 256 MB Infinity Cache)
 GAE_BYTES = 21       # r 4 + V 4 + done 1 in; adv 4 + ret 4 + adv_n 4 out
 LOSS_CAT_BYTES = 172  # logits 72 + 6 x 4 per-row inputs in; dlogits 72 + dvalue 4 out
 GAUSS_BYTES = 96     # mu 24 + actions 24 + 5 x 4 in; dmu 24 + dvalue 4 out
@@ -90,16 +91,28 @@ def synthetic_rollout(torch, dev, T, N, A, seed=24):
     return x
 
 
+ROLLOUT_KEYS = ("rewards", "values", "dones", "last_value")
+
+
 class Step:
     """The two C-ABI calls of one update step, on torch's current stream,
-    with preallocated outputs (nothing allocated inside the timed loop)."""
+    with preallocated outputs (nothing allocated inside the timed loop).
 
-    def __init__(self, torch, lib, x, dev):
+    With copies > 1 the step keeps that many copies of the rollout (rewards,
+    values, dones, last value: 75 MB each at T x N = 2048 x 4096) and next()
+    moves to the following one, so that consecutive steps read different
+    rollouts: together they exceed the 256 MB Infinity Cache, and a step's
+    rollout comes from HBM, not from the cache lines the previous step left."""
+
+    def __init__(self, torch, lib, x, dev, copies=1):
         import ctypes
 
         from ppo_amd import _lib
 
         self.torch, self.lib, self.x = torch, lib, x
+        self.rollouts = [x] + [{k: x[k].clone() for k in ROLLOUT_KEYS}
+                               for _ in range(copies - 1)]
+        self.k = 0
         T, N = x["rewards"].shape
         B, A = x["logits"].shape
         self.T, self.N, self.B, self.A = T, N, B, A
@@ -118,8 +131,11 @@ class Step:
         self.params_ref = ctypes.byref(self.params)
         self.stream = torch.cuda.current_stream(dev).cuda_stream
 
+    def next(self):
+        self.k = (self.k + 1) % len(self.rollouts)
+
     def gae(self):
-        x = self.x
+        x = self.rollouts[self.k]
         rc = self.lib.ppo_gae_norm_f32(
             x["rewards"].data_ptr(), x["values"].data_ptr(), x["dones"].data_ptr(),
             x["last_value"].data_ptr(), self.T, self.N, 0.99, 0.95, 1e-8,
@@ -133,7 +149,8 @@ class Step:
         rc = self.lib.ppo_loss_cat_f32(
             x["logits"].data_ptr(), self.B, self.A, x["actions"].data_ptr(), 0,
             x["old_log_probs"].data_ptr(), self.adv_n.data_ptr(), self.ret.data_ptr(),
-            x["new_values"].data_ptr(), x["values"].data_ptr(), self.params_ref,
+            x["new_values"].data_ptr(), self.rollouts[self.k]["values"].data_ptr(),
+            self.params_ref,
             self.dlogits.data_ptr(), self.dvalues.data_ptr(), self.scalars.data_ptr(),
             self.ws_loss.data_ptr(), self.ws_loss.numel(), self.stream)
         if rc:
@@ -223,6 +240,7 @@ def time_step_events(torch, step, reps):
         e[1].record(s)
         step.loss()
         e[2].record(s)
+        step.next()
     torch.cuda.synchronize()
     g = sum(e[0].elapsed_time(e[1]) for e in ev) / reps / 1e3
     loss = sum(e[1].elapsed_time(e[2]) for e in ev) / reps / 1e3
@@ -493,12 +511,13 @@ def main():
     if args.copy_calibration:
         copy_calibration(torch, dev)
     x = synthetic_rollout(torch, dev, T_STEPS, N_ENVS, N_ACTIONS)
-    step = Step(torch, lib, x, dev)
+    step = Step(torch, lib, x, dev, copies=ROLLOUT_COPIES)
     B = step.B
 
     def one_step():
         step.gae()
         step.loss()
+        step.next()
 
     for _ in range(args.warmup):
         one_step()
@@ -510,9 +529,9 @@ def main():
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed / args.steps * 1e3
 
-    # per-call HIP-event timing on the launch stream, inside the step sequence:
-    # each GAE call follows a loss call, so its rollout comes from HBM (back-to-
-    # back GAE calls would find the 75 MB rollout in the 256 MB Infinity Cache)
+    # per-call HIP-event timing on the launch stream, inside the step sequence
+    # (each step reads the next of the rollout copies, so its rollout comes
+    # from HBM)
     t_gae, t_loss = time_step_events(torch, step, max(args.steps, 20))
     achieved = LOSS_CAT_BYTES * B / t_loss / 1e9
     traffic = read_traffic("loss_cat_north_star")
