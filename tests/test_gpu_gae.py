@@ -730,3 +730,53 @@ def test_gae_resident_graph_replays_match_eager(dev, T, N, norm):
         torch.cuda.synchronize(dev)
         for got, w in zip(outs, want):
             assert torch.equal(got, w), f"eager after replay {rep}"
+
+
+# ---------------------------------------------------------------------------
+# Hyperparameter edges on every route, each against the oracle and against a
+# closed form that does not use it: lambda = 0 gives the TD error
+# ((r + (gamma * v') * mask) - v, ppo.py:180-184, in fp64, then fp32) and
+# gamma = 0 gives r - v, both bit-exact; gamma = lambda = 1 with zero values,
+# no dones and no bootstrap gives suffix sums of the rewards (fp64, to 1 ulp).
+# ---------------------------------------------------------------------------
+EDGE_ROUTES = [
+    (2048, 1024, True),     # resident pass
+    (2048, 1024, False),    # the same rollout off the resident pass
+    (1 << 18, 16, True),    # resident pass in rounds
+    (1 << 18, 16, False),   # span passes
+    (300, 7, False),        # unaligned N: tile passes
+]
+
+
+@pytest.mark.parametrize("gamma,lam", [(0.99, 0.0), (0.0, 0.95), (1.0, 1.0), (0.9, 1.0)])
+@pytest.mark.parametrize("T,N,resident", EDGE_ROUTES)
+def test_gae_hyperparameter_edges(dev, monkeypatch, T, N, resident, gamma, lam):
+    if not resident:
+        monkeypatch.setenv("PPO_AMD_GAE_RESIDENT", "0")
+    route = _route(T, N, False)
+    assert (route == "resident") == resident
+    suffix = gamma == 1.0 and lam == 1.0
+    r, v, d, lv = _inputs(T, N, 0.0 if suffix else 0.01, seed=T + N + int(gamma * 10))
+    if suffix:
+        v.zero_()
+        lv = None
+    print(f"gae edges T={T} N={N} route={route} gamma={gamma} lam={lam}", flush=True)
+    adv, _ = ppo_amd.gae(r.to(dev), v.to(dev), d.to(dev), None if lv is None else lv.to(dev),
+                         gamma, lam)
+    got = adv.cpu().numpy()
+    a_ref, _ = ref.gae_c(r.numpy(), v.numpy(), d.numpy(), None if lv is None else lv.numpy(),
+                         gamma, lam)
+    assert_gae_close(got, a_ref)
+    r64, v64 = r.numpy().astype(np.float64), v.numpy().astype(np.float64)
+    mask = 1.0 - d.numpy().astype(np.float64)
+    nv = np.concatenate([v64[1:], (np.zeros((1, N)) if lv is None else
+                                   lv.numpy().astype(np.float64)[None, :])], axis=0)
+    if lam == 0.0:
+        want = ((r64 + (gamma * nv) * mask) - v64).astype(np.float32)
+        np.testing.assert_array_equal(got, want)
+    if gamma == 0.0:
+        np.testing.assert_array_equal(got, (r64 - v64).astype(np.float32))
+    if suffix:
+        # (the carries between segments are composed in another order than
+        # the serial sum, so <= 1 fp32 ulp as against the oracle)
+        assert_gae_close(got, np.cumsum(r64[::-1], axis=0)[::-1])
