@@ -373,11 +373,15 @@ int ppo_mlp_cat_grad_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
  * list(policy.parameters()) + list(value.parameters())).  exp_avg and
  * exp_avg_sq are host arrays of 12 device pointers in that order; the
  * weights and biases of both structs are updated in place (so they must be
- * writable), their gradients hold the clipped gradients afterwards.  Three
- * launches instead of four: the gradient reduction also leaves each
- * tensor's sum of squares in pieces, and increments adam->step_counter when
- * it is set.  grad_norm_out (may be NULL) receives the total norm.  Same
- * limits and workspace as ppo_mlp_cat_grad_f32.
+ * writable), their gradients hold the clipped gradients afterwards.  Two
+ * launches: the gradient kernel, then one kernel that sums the gradient
+ * partials, forms the clip norm and applies Adam (its workgroups wait for
+ * each other, so it runs only when its grid fits on the device at once;
+ * otherwise, or with PPO_AMD_MLP_FUSED_ADAM=0 in the environment, the sums
+ * and the update are two launches, with bit-identical results).
+ * adam->step_counter, when set, is incremented once.  grad_norm_out (may be
+ * NULL) receives the total norm.  Same limits and workspace as
+ * ppo_mlp_cat_grad_f32.
  */
 int ppo_mlp_cat_step_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
                          int32_t obs_dim, int32_t hidden, int32_t A, int32_t activation,

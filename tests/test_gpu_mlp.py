@@ -117,7 +117,7 @@ def test_mlp_grads_match_unfused_gpu_path(dev):
 @pytest.mark.parametrize("capturable", [False, True])
 @pytest.mark.parametrize("max_norm", [0.5, 1e6])
 def test_mlp_step_matches_grads_then_clipped_adam(dev, capturable, max_norm):
-    """ppo_mlp_cat_step_f32 (gradients + clip + Adam in three launches) against
+    """ppo_mlp_cat_step_f32 (gradients + clip + Adam in two or three launches) against
     ppo_mlp_cat_grads followed by ClippedAdam.step(), over four steps: the
     gradients are the same; the clip norm is summed from 64-element pieces
     instead of 1024-element ones (fp64), so parameters, moments and norms
@@ -142,6 +142,42 @@ def test_mlp_step_matches_grads_then_clipped_adam(dev, capturable, max_norm):
             torch.testing.assert_close(a.detach(), b.detach(), rtol=2e-6, atol=1e-7)
     for a, b in zip(opts[0].exp_avg + opts[0].exp_avg_sq, opts[1].exp_avg + opts[1].exp_avg_sq):
         torch.testing.assert_close(a, b, rtol=2e-6, atol=1e-10)
+    assert opts[0].step_count() == opts[1].step_count() == 4
+
+
+@pytest.mark.parametrize("capturable", [False, True])
+@pytest.mark.parametrize("max_norm,n,B", [(0.5, 512, 256), (1e6, 512, 256), (0.5, 8192, 4096)])
+def test_mlp_step_one_launch_matches_two(dev, monkeypatch, capturable, max_norm, n, B):
+    """ppo_mlp_cat_step_f32 sums the gradient partials and applies clip + Adam
+    in one launch when its grid is resident (an in-kernel barrier between the
+    sums of squares and the update); PPO_AMD_MLP_FUSED_ADAM=0 keeps the
+    reduction and the update as two launches.  Both must give bit-identical
+    gradients, parameters, moments, norms, loss scalars and step counts, over
+    four steps (B = 4096 takes the 1024-thread reduction geometry)."""
+    pol, val, cpu, gpu = _case(dev, n, 4, 64, 2, "tanh", seed=41)
+    nets = [(copy.deepcopy(pol).to(dev), copy.deepcopy(val).to(dev)) for _ in range(2)]
+    opts = [ppo_amd.ClippedAdam(list(p.parameters()) + list(v.parameters()), lr=1e-3,
+                                max_grad_norm=max_norm, capturable=capturable)
+            for p, v in nets]
+    args = (gpu["obs"], gpu["actions"], gpu["old_lp"], gpu["adv"], gpu["ret"])
+    g = torch.Generator().manual_seed(42)
+    for step in range(4):
+        idx = torch.randperm(n, generator=g)[:B].to(dev)
+        print(f"mlp step fused-vs-two n={n} B={B} step={step} capturable={capturable}",
+              flush=True)
+        monkeypatch.delenv("PPO_AMD_MLP_FUSED_ADAM", raising=False)
+        s1, n1 = ppo_amd.ppo_mlp_cat_step(nets[0][0], nets[0][1], opts[0], *args, index=idx)
+        monkeypatch.setenv("PPO_AMD_MLP_FUSED_ADAM", "0")
+        s2, n2 = ppo_amd.ppo_mlp_cat_step(nets[1][0], nets[1][1], opts[1], *args, index=idx)
+        torch.cuda.synchronize(dev)
+        assert torch.equal(n1, n2)
+        for k in s2:
+            assert torch.equal(s1[k], s2[k]), k
+        for a, b in zip(opts[0].params, opts[1].params):
+            assert torch.equal(a.grad, b.grad)
+            assert torch.equal(a.detach(), b.detach())
+    for a, b in zip(opts[0].exp_avg + opts[0].exp_avg_sq, opts[1].exp_avg + opts[1].exp_avg_sq):
+        assert torch.equal(a, b)
     assert opts[0].step_count() == opts[1].step_count() == 4
 
 

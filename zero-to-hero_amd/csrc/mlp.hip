@@ -28,9 +28,11 @@
 // is fp32, as torch's; sums over the minibatch differ from torch's GEMM
 // order only by rounding.
 #include <float.h>
+#include <stdlib.h>
 
 #include "common.hpp"
 #include "adam.hpp"
+#include "grid_sync.hpp"
 #include "cartpole_row.hpp"
 #include "row_math.hpp"
 #include "sample_row.hpp"
@@ -757,6 +759,126 @@ __global__ void __launch_bounds__(kWaves * kWave) mlp_grad_reduce_kernel(MlpArgs
   }
 }
 
+// The reduction, clip_grad_norm_ and Adam in one launch (ppo_mlp_cat_step_f32
+// when the reduction grid is resident on the device at once).  Each
+// workgroup sums its parameters' gradient partials as
+// mlp_grad_reduce_kernel does and publishes the sum of squares of the fp32
+// gradients to a slot (grid_sync.hpp: value-tagged 64-bit words, cleared by
+// the owner before a start barrier); then every workgroup reads all slots
+// and forms the per-tensor norms, the total norm and the clip coefficient
+// in the order adam_update_kernel uses (wave w takes tensors w, w + kWaves,
+// ...; lane l sums a tensor's partials l, l + 64, ... in fp64, then the wave
+// tree; adam_coef_from_norms), and updates its parameters from registers.
+// The results are bit-identical to the reduction + adam_update_kernel
+// launches, with one dependent launch fewer per minibatch.
+struct MlpAdamArgs {
+  float* p[kMlpTensors];
+  float* m[kMlpTensors];
+  float* v[kMlpTensors];
+  AdamScalars s;
+  float* norm_out;
+  uint64_t* sync;  // start barrier (kSyncWords words)
+  uint64_t* sq;    // per reduction workgroup: its sum-of-squares slot
+  unsigned nonce;
+};
+
+template <int kWaves, int kRedLoads>
+__global__ void __launch_bounds__(kWaves * kWave) mlp_reduce_adam_kernel(MlpArgs a,
+                                                                         MlpAdamArgs u) {
+  __shared__ double s_sum[kWaves][kRedCols];
+  __shared__ float s_norm[kMlpTensors];
+  __shared__ float s_coef;
+  const int lane = threadIdx.x % kWave;
+  const int w = threadIdx.x / kWave;
+  const long blk = blockIdx.x;
+  int j = 0;
+  while (j + 1 < kMlpTensors && blk >= a.tblk[j + 1]) ++j;
+  const long local = (blk - a.tblk[j]) * kRedCols + lane;
+  const bool valid = local < a.tnum[j];
+  const long li = valid ? local : 0;
+  const long pc = a.toff[j] + li;
+  // wave 0: this workgroup's parameters and moments (they do not depend on
+  // the norm), the step count (read before arriving: workgroup 0 advances it
+  // only once every workgroup has arrived), its slot emptied, arrival
+  float pr = 0.0f, mr = 0.0f, vr = 0.0f;
+  int64_t step0 = 0;
+  if (w == 0) {
+    pr = u.p[j][li];
+    mr = u.m[j][li];
+    vr = u.v[j][li];
+    if (a.step_counter) step0 = *a.step_counter;
+    sync_start(u.sync, u.sq + blk, 1, u.nonce);
+  }
+  double s = 0.0;
+  for (long b0 = w; b0 < a.nblocks; b0 += kRedLoads * kWaves) {
+    float x[kRedLoads];
+#pragma unroll
+    for (int q = 0; q < kRedLoads; ++q) {
+      const long b = b0 + (long)q * kWaves;
+      x[q] = a.gpart[(b < a.nblocks ? b : 0) * a.P + pc];
+    }
+#pragma unroll
+    for (int q = 0; q < kRedLoads; ++q)
+      if (b0 + (long)q * kWaves < a.nblocks) s += (double)x[q];
+  }
+  s_sum[w][lane] = s;
+  __syncthreads();
+  float g = 0.0f;
+  if (w == 0) {
+    double t = s_sum[0][lane];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) t += s_sum[k][lane];
+    g = (float)t;
+    const double sq = wave_sum(valid ? (double)g * (double)g : 0.0);
+    if (lane == 0) slot_put(u.sq + blk, sq);
+  }
+  if (blk == 0) {
+    double tot[kMlpSums];
+    for (int k = 0; k < kMlpSums; ++k) tot[k] = 0.0;
+    for (long b = threadIdx.x; b < a.nblocks; b += kWaves * kWave)
+      for (int k = 0; k < kMlpSums; ++k) tot[k] += a.spart[(long)k * a.nblocks + b];
+    block_sum<kMlpSums>(tot);
+    if (threadIdx.x == 0) {
+      const double nb = (double)a.B;
+      const float pol = (float)(tot[0] / nb);
+      const float vl = (float)(tot[1] / nb);
+      const float ent = (float)(tot[2] / nb);
+      a.scalars[PPO_SCALAR_POLICY] = pol;
+      a.scalars[PPO_SCALAR_VALUE] = vl;
+      a.scalars[PPO_SCALAR_ENTROPY] = ent;
+      a.scalars[PPO_SCALAR_APPROX_KL] = (float)(tot[3] / nb);
+      a.scalars[PPO_SCALAR_CLIPFRAC] = (float)(tot[4] / nb);
+      a.scalars[PPO_SCALAR_LOSS] = (pol + a.vc * vl) - a.ec * ent;
+    }
+  }
+  if (threadIdx.x == 0) res_wait(u.sync, u.nonce, gridDim.x);
+  __syncthreads();
+  if (blk == 0 && threadIdx.x == 0 && a.step_counter) *a.step_counter = step0 + 1;
+  for (int kk = w; kk < kMlpTensors; kk += kWaves) {
+    double acc = 0.0;
+    for (long c = a.tblk[kk] + lane; c < a.tblk[kk + 1]; c += kWave) acc += slot_get(u.sq + c);
+    const double sk = wave_sum(acc);
+    if (lane == 0) s_norm[kk] = (float)sqrt(sk);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float norm;
+    s_coef = adam_coef_from_norms(u.s, s_norm, kMlpTensors, norm);
+    if (blk == 0 && u.norm_out) *u.norm_out = norm;
+  }
+  __syncthreads();
+  if (w == 0 && valid) {
+    AdamScalars sc = u.s;
+    if (a.step_counter) adam_step_scalars_at(sc, (double)(step0 + 1));
+    float gi, mi, vi, pi;
+    adam_elem(sc, s_coef, g, mr, vr, pr, gi, mi, vi, pi);
+    tensor_grad(a, j)[local] = gi;  // (clipped when clipping, as clip_grad_norm_ leaves it)
+    u.p[j][local] = pi;
+    u.m[j][local] = mi;
+    u.v[j][local] = vi;
+  }
+}
+
 long mlp_params(int D, int H, int O) { return (long)H * D + H + (long)H * H + H + (long)O * H + O; }
 
 NetOffsets net_offsets(long base, int D, int H, int O) {
@@ -773,7 +895,7 @@ NetOffsets net_offsets(long base, int D, int H, int O) {
 struct MlpLayout {
   long P, nblocks, rblocks;
   long tblk[kMlpTensors + 1], toff[kMlpTensors], tnum[kMlpTensors];
-  size_t gpart, spart, sqpart, total;
+  size_t gpart, spart, sqpart, sync, total;
 };
 
 MlpLayout mlp_layout(long B, int D, int H, int A) {
@@ -794,7 +916,8 @@ MlpLayout mlp_layout(long B, int D, int H, int A) {
   l.gpart = kHeaderBytes;
   l.spart = l.gpart + align_up((size_t)l.nblocks * l.P * sizeof(float), 256);
   l.sqpart = l.spart + align_up((size_t)kMlpSums * l.nblocks * sizeof(double), 256);
-  l.total = l.sqpart + align_up((size_t)l.rblocks * sizeof(double), 256);
+  l.sync = l.sqpart + align_up((size_t)l.rblocks * sizeof(double), 256);
+  l.total = l.sync + kSyncWords * sizeof(uint64_t);
   return l;
 }
 
@@ -1009,6 +1132,36 @@ extern "C" int ppo_mlp_cat_step_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
   a.sqpart = reinterpret_cast<double*>(static_cast<char*>(workspace) + l.sqpart);
   a.step_counter = adam->step_counter;
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  // one launch for the reduction and the update when its grid is resident
+  // (PPO_AMD_MLP_FUSED_ADAM=0 in the environment keeps two launches)
+  const bool wide = l.nblocks >= kRedWideRows;
+  const void* fused = wide ? (const void*)mlp_reduce_adam_kernel<16, 16>
+                           : (const void*)mlp_reduce_adam_kernel<4, 8>;
+  const int fused_threads = wide ? 1024 : 256;
+  const char* env = getenv("PPO_AMD_MLP_FUSED_ADAM");
+  if (!(env && env[0] == '0') && l.rblocks <= 0x7fffffffL &&
+      resident_blocks(fused, fused_threads, 0, 0) >= l.rblocks) {
+    MlpAdamArgs u = {};
+    for (int j = 0; j < kMlpTensors; ++j) {
+      const ppo_mlp3_f32* net = j < 6 ? actor : critic;
+      const int li = (j % 6) / 2;
+      u.p[j] = const_cast<float*>((j & 1) ? net->bias[li] : net->weight[li]);  // in place
+      u.m[j] = exp_avg[j];
+      u.v[j] = exp_avg_sq[j];
+    }
+    u.s = make_adam_scalars(adam);
+    u.norm_out = grad_norm_out;
+    u.sync = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + l.sync);
+    u.sq = reinterpret_cast<uint64_t*>(a.sqpart);
+    u.nonce = next_nonce();
+    void* gargs[] = {&a};
+    if ((st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(kMlpBlock),
+                                         gargs, 0, stream))))
+      return st;
+    void* fargs[] = {&a, &u};
+    return hip_status(hipLaunchKernel(fused, dim3((unsigned)l.rblocks), dim3(fused_threads),
+                                      fargs, 0, stream));
+  }
   if ((st = mlp_launch(kern, a, l, stream))) return st;
   float* pp[kMlpTensors];
   float* gp[kMlpTensors];

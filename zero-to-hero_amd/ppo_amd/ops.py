@@ -885,8 +885,9 @@ def ppo_mlp_cat_step(
 ) -> tuple[LossStats, torch.Tensor]:
     """ppo_mlp_cat_grads followed by optimizer.step() (a ClippedAdam over
     list(policy.parameters()) + list(value.parameters()), in that order) as
-    three launches (ppo_mlp_cat_step_f32): the gradient reduction also
-    leaves the per-tensor sums of squares that clip_grad_norm_ needs.
+    two launches (ppo_mlp_cat_step_f32: the gradient kernel, then the
+    reduction with clip_grad_norm_ and Adam in one kernel; three launches
+    when that kernel's grid does not fit on the device at once).
     Returns the loss scalars and the pre-clip gradient norm (0-d device
     tensors)."""
     from .optim import ClippedAdam

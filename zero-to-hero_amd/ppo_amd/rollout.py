@@ -389,7 +389,7 @@ class VecPPO:
         if self.fused_mlp and arrays[0].dim() == 2:
             cfg = self.ppo_config
             obs, acts, old_lp, adv, ret, old_v = arrays
-            # gradients, clip to cfg.gradient_clip and Adam: three launches
+            # gradients, clip to cfg.gradient_clip and Adam: two launches
             stats, _ = ops.ppo_mlp_cat_step(
                 self.policy, self.value, self.optimizer, obs, acts, old_lp, adv, ret,
                 old_v if cfg.vf_clip is not None else None, idx, cfg.clip_ratio, cfg.vf_clip,
