@@ -22,7 +22,7 @@ constexpr size_t kHeaderBytes = 256;     // WsHeader at the front of every works
 // agent-scope atomic stores and loads whose completion is awaited explicitly.
 struct WsHeader {
   float stats[4];         // {mean, std, denom, 0} written by the stats finaliser
-  uint64_t epoch;         // Gaussian loss: advanced by one per call (any start value)
+  uint64_t epoch;         // call counter (any start value): Gaussian loss tags, barrier tags
 };
 static_assert(sizeof(WsHeader) <= kHeaderBytes, "header too big");
 

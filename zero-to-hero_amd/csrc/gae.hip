@@ -1762,6 +1762,10 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
   // done, and arrives at the start barrier; no workgroup reads a slot before
   // the barrier is complete, so no reader can see what the slot held before
   // this call.  The other waves start their loads meanwhile.
+  // this launch's barrier tag and the call counter it came from, kept in
+  // LDS by thread 0 (its only user) rather than in registers across step 1
+  __shared__ unsigned s_tag;
+  __shared__ uint64_t s_epoch;
   if (w == 0) {
     for (long rd = 0; rd < rounds; ++rd) {
       const long tt = tile_tt(rd);
@@ -1772,7 +1776,13 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
           slot_clear(bnd + (size_t)rd * a.N + col * E + tid);
       }
     }
-    sync_start(ctr, part + (size_t)blockIdx.x * 3, 3, a.nonce);
+    uint64_t epoch;
+    const unsigned tag = launch_tag(&a.hdr->epoch, a.nonce, epoch);
+    if (tid == 0) {
+      s_tag = tag;
+      s_epoch = epoch;
+    }
+    sync_start(ctr, part + (size_t)blockIdx.x * 3, 3, tag);
   }
 
   const double gl0 = mul(a.gl, 0.0);
@@ -1924,7 +1934,10 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       slot_put(comp + ((size_t)(tt * nc + col) * E + tid) * 2 + 1, tp);
     }
     // the start barrier (once): every workgroup's slots are empty by now
-    if (rd == 0 && tid == 0) res_wait(ctr, a.nonce, gridDim.x);
+    if (rd == 0 && tid == 0) {
+      res_wait(ctr, s_tag, gridDim.x);
+      if (blockIdx.x == 0) epoch_advance(&a.hdr->epoch, s_epoch);
+    }
     __syncthreads();
 
     // ---- look-back: the tiles to the right inside this round (hi down to

@@ -113,6 +113,22 @@ __device__ inline void sync_start(uint64_t* sync, uint64_t* mine, int n, unsigne
   if (lane == 0) res_arrive(ctr, v, nonce, sync_share(i, gridDim.x));
 }
 
+// The tag of a launch's barrier counters: the host's nonce mixed with a call
+// counter kept in the workspace (`epoch`, any start value).  Every workgroup
+// reads the counter before it arrives at the start barrier, and workgroup 0
+// advances it (epoch_advance) once that barrier is complete, so a replay of a
+// captured launch, which repeats the host's nonce, still gets a tag of its
+// own: counters that the previous replay left complete cannot release this
+// replay's waiters early.  `e` receives the counter for epoch_advance.
+__device__ inline unsigned launch_tag(const uint64_t* epoch, unsigned nonce, uint64_t& e) {
+  e = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return nonce ^ (unsigned)((e * 0x9E3779B97F4A7C15ULL) >> 32);
+}
+
+__device__ inline void epoch_advance(uint64_t* epoch, uint64_t e) {
+  __hip_atomic_store(epoch, e + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // A different tag for every launch (zero is skipped).
 inline unsigned next_nonce() {
   static std::atomic<unsigned> calls{0x5bd1e995u};

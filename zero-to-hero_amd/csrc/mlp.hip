@@ -779,6 +779,7 @@ struct MlpAdamArgs {
   float* norm_out;
   uint64_t* sync;  // start barrier (kSyncWords words)
   uint64_t* sq;    // per reduction workgroup: its sum-of-squares slot
+  uint64_t* epoch; // the workspace header's call counter (launch_tag)
   unsigned nonce;
 };
 
@@ -802,12 +803,15 @@ __global__ void __launch_bounds__(kWaves * kWave) mlp_reduce_adam_kernel(MlpArgs
   // only once every workgroup has arrived), its slot emptied, arrival
   float pr = 0.0f, mr = 0.0f, vr = 0.0f;
   int64_t step0 = 0;
+  unsigned tag = 0;  // (wave 0)
+  uint64_t epoch = 0;
   if (w == 0) {
     pr = u.p[j][li];
     mr = u.m[j][li];
     vr = u.v[j][li];
     if (a.step_counter) step0 = *a.step_counter;
-    sync_start(u.sync, u.sq + blk, 1, u.nonce);
+    tag = launch_tag(u.epoch, u.nonce, epoch);
+    sync_start(u.sync, u.sq + blk, 1, tag);
   }
   double s = 0.0;
   for (long b0 = w; b0 < a.nblocks; b0 += kRedLoads * kWaves) {
@@ -851,7 +855,10 @@ __global__ void __launch_bounds__(kWaves * kWave) mlp_reduce_adam_kernel(MlpArgs
       a.scalars[PPO_SCALAR_LOSS] = (pol + a.vc * vl) - a.ec * ent;
     }
   }
-  if (threadIdx.x == 0) res_wait(u.sync, u.nonce, gridDim.x);
+  if (threadIdx.x == 0) {
+    res_wait(u.sync, tag, gridDim.x);
+    if (blk == 0) epoch_advance(u.epoch, epoch);
+  }
   __syncthreads();
   if (blk == 0 && threadIdx.x == 0 && a.step_counter) *a.step_counter = step0 + 1;
   for (int kk = w; kk < kMlpTensors; kk += kWaves) {
@@ -1153,6 +1160,7 @@ extern "C" int ppo_mlp_cat_step_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
     u.norm_out = grad_norm_out;
     u.sync = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + l.sync);
     u.sq = reinterpret_cast<uint64_t*>(a.sqpart);
+    u.epoch = &reinterpret_cast<WsHeader*>(workspace)->epoch;
     u.nonce = next_nonce();
     void* gargs[] = {&a};
     if ((st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(kMlpBlock),
