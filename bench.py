@@ -283,7 +283,7 @@ def time_stream(torch, calls, passes):
     return e0.elapsed_time(e1) / 1e3 / (passes * len(calls))
 
 
-def suite(torch, lib, dev, stream_timing=True):
+def suite(torch, lib, dev, stream_timing=True, cpu=True):
     """One line per benchmark configuration's kernel chain (2: GAE+normalise, 3: long-T
     GAE scan, 4: discrete loss, 5: Gaussian loss), each timed through the C
     ABI with preallocated outputs (HIP events on the launch stream), two ways:
@@ -291,7 +291,10 @@ def suite(torch, lib, dev, stream_timing=True):
     inputs come from HBM rather than the 256 MB Infinity Cache (configs 2, 4
     and 5 fit in it); and `us_stream`, calls back to back over several copies
     of the buffers (time_stream), without the idle time that event records
-    around a single call leave on the device."""
+    around a single call leave on the device.  Unless `cpu` is False, each of
+    configs 2-5 is also run once through the CPU restatement (oracle/) on the
+    same inputs (`cpu_us`; config 3 through the C recurrence on one core, the
+    others through numpy / torch on the host's threads)."""
     import ctypes
 
     from ppo_amd import _lib
@@ -309,6 +312,14 @@ def suite(torch, lib, dev, stream_timing=True):
 
     def ws(nbytes):
         return torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+    cpu_us = {}
+
+    def cpu_time(name, fn):
+        if cpu:
+            t0 = time.perf_counter()
+            fn()
+            cpu_us[name] = (time.perf_counter() - t0) * 1e6
 
     def measure(name, units, bpu, make, copies):
         """make(k) -> the call on buffer set k (set 0 also times `us`)."""
@@ -342,6 +353,16 @@ def suite(torch, lib, dev, stream_timing=True):
                 adv.data_ptr(), ret.data_ptr(), w.data_ptr(), w.numel(), stream)
 
         measure(name, T * N, GAE_BYTES if norm else SCAN_BYTES, make, copies)
+        if cpu:
+            from oracle import ppo_oracle as ref
+
+            rn, vn, dn, ln = (t.cpu().numpy() for t in (r, v, d, lv))
+            if norm:
+                cpu_time(name, lambda: ref.normalize_reference(torch.from_numpy(
+                    ref.gae_numpy(rn, vn, dn, ln, gamma, 0.95)[0]).reshape(-1)))
+            else:
+                ref.build_c()
+                cpu_time(name, lambda: ref.gae_c(rn, vn, dn, ln, gamma, 0.95))
         del r, v, d, w, make
     # config 4: discrete loss
     x = synthetic_rollout(torch, dev, 256, 4096, 18, seed=25)
@@ -359,6 +380,15 @@ def suite(torch, lib, dev, stream_timing=True):
             dl.data_ptr(), dv.data_ptr(), sc.data_ptr(), w.data_ptr(), w.numel(), stream)
 
     measure("config4_loss_cat", B, LOSS_CAT_BYTES, make, 4)
+    if cpu:
+        from oracle import ppo_oracle as ref
+
+        xc = {key: t.cpu() for key, t in x.items()}
+        cpu_time("config4_loss_cat", lambda: ref.loss_categorical_reference(
+            xc["logits"], xc["actions"].long(), xc["old_log_probs"], xc["rewards"].reshape(-1),
+            xc["values"].reshape(-1), xc["new_values"], xc["values"].reshape(-1), 0.2, 0.2,
+            0.5, 0.01))
+        del xc
     del x, w, make
     # config 5: Gaussian loss
     B, D = 2_097_152, 6
@@ -380,6 +410,14 @@ def suite(torch, lib, dev, stream_timing=True):
             w.data_ptr(), w.numel(), stream)
 
     measure("config5_loss_gauss", B, GAUSS_BYTES, make, 4)
+    if cpu:
+        from oracle import ppo_oracle as ref
+
+        mc, lc, ac = mu.cpu(), ls.cpu(), acts.cpu()
+        rc = [t.cpu() for t in rows]
+        cpu_time("config5_loss_gauss", lambda: ref.loss_gaussian_reference(
+            mc, lc, ac, rc[0], rc[1], rc[2], rc[3], rc[4], 0.2, 0.2, 0.5, 0.01))
+        del mc, lc, ac, rc
     del mu, acts, rows, w, make
     # the north-star step with A = 2 (CartPole's action count): GAE+norm + loss
     x = synthetic_rollout(torch, dev, T_STEPS, N_ENVS, 2, seed=26)
@@ -404,6 +442,9 @@ def suite(torch, lib, dev, stream_timing=True):
         if ts is not None:
             line["us_stream"] = round(ts * 1e6, 2)
             line["frac_stream"] = round(units * bpu / ts / 1e9 / HBM_PEAK_GBS, 4)
+        if name in cpu_us:
+            line["cpu_us"] = round(cpu_us[name], 1)
+            line["cpu_threads"] = 1 if name == "config3_long_scan" else torch.get_num_threads()
         print(json.dumps(line), flush=True)
 
 
@@ -503,7 +544,7 @@ def main():
     lib = ppo_amd.load_library()
     dev = torch.device("cuda:0")
     if args.suite:
-        suite(torch, lib, dev, stream_timing=not args.no_stream)
+        suite(torch, lib, dev, stream_timing=not args.no_stream, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
     if args.update_suite:
         update_suite(torch, dev)
