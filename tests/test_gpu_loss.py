@@ -262,6 +262,37 @@ def test_cat_ratio_exactly_on_the_clip_bounds(dev):
     assert_scalars_close(scalars, o)
 
 
+@pytest.mark.parametrize("A", [2, 5, 18, 33, 100])
+def test_cat_masked_logits(dev, A):
+    """Action masking by -inf logits (never at the taken action), as
+    torch.distributions.Categorical accepts it: finite loss, entropy and
+    gradients, zero gradient at the masked logits.  A = 2, 5, 18 take the
+    exact-width wave tiles, 33 the LDS-pass form and 100 the wave-per-row
+    kernel."""
+    B = 1000
+    g = torch.Generator().manual_seed(700 + A)
+    logits = torch.randn(B, A, generator=g)
+    mask = torch.rand(B, A, generator=g) < 0.3
+    old_logits = (logits + 0.05 * torch.randn(B, A, generator=g)).masked_fill(mask, -float("inf"))
+    keep = (~mask).any(1)
+    old_logits[~keep, 0] = 0.0  # (every row keeps at least one action)
+    mask[~keep, 0] = False
+    actions = torch.multinomial(torch.softmax(old_logits, -1), 1, generator=g).squeeze(1)
+    old_lp = torch.log_softmax(old_logits, -1).gather(1, actions[:, None]).squeeze(1)
+    logits = logits.masked_fill(mask, -float("inf"))
+    assert not mask.gather(1, actions[:, None]).any()
+    adv = torch.randn(B, generator=g)
+    ret = torch.randn(B, generator=g)
+    old_v = torch.randn(B, generator=g)
+    val = old_v + 0.1 * torch.randn(B, generator=g)
+    inputs = (logits, actions.to(torch.int32), old_lp, adv, ret, val, old_v)
+    scalars, dlogits, _ = run_cat(dev, B, A, seed=0, inputs=inputs)
+    assert torch.isfinite(scalars).all()
+    dl = dlogits.cpu()
+    assert torch.isfinite(dl).all()
+    assert (dl[mask] == 0).all()
+
+
 def test_cat_misaligned_logits(dev):
     B, A = 300, 18
     inp = cat_inputs(B, A, seed=6)
