@@ -37,6 +37,17 @@ def test_normalize_single_element_is_identity(dev):
     assert out.item() == -4.5
 
 
+@pytest.mark.parametrize("n", [2, 1000, 1_048_579])
+def test_normalize_constant_advantages(dev, n):
+    """Equal advantages: std 0, so (adv - mean) / (0 + eps) is exactly zero in
+    the reference's expression and here (no NaN from the variance)."""
+    a = torch.full((n,), 3.25)
+    out = ppo_amd.normalize_advantages(a.to(dev)).cpu()
+    expect = ref.normalize_reference(a)
+    assert torch.equal(expect, torch.zeros(n))
+    assert torch.equal(out, expect)
+
+
 def test_normalize_misaligned_and_in_place(dev):
     g = torch.Generator().manual_seed(5)
     a = torch.randn(10_001, generator=g)
