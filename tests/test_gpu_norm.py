@@ -90,3 +90,40 @@ def test_fused_matches_separate_ops(dev):
     adv2, ret2 = ppo_amd.gae(r, v, d)
     assert torch.equal(adv, adv2) and torch.equal(ret, ret2)
     torch.testing.assert_close(adv_n, ppo_amd.normalize_advantages(adv2), rtol=1e-6, atol=1e-7)
+
+
+# Advantages whose mean is large against their spread (|mean| / std up to
+# 1e4): the normaliser's statistics must stay exact (the variance is not lost
+# to the rounding of fp32 sums of squares).  Checked against fp64 statistics
+# of the same advantages: the mean within one fp32 ulp (torch's own fp32
+# reduction may land on the neighbouring float), the std within 1e-6
+# relative, and adv_n = (adv - mean) / (std + eps) evaluated with the
+# reported statistics.
+OFFSET_ROUTES = [
+    (2048, 4096, True),    # resident pass
+    (2048, 4096, False),   # strip walk
+    (16_384, 64, False),   # span passes
+    (512, 259, False),     # unaligned N: tile passes
+]
+
+
+@pytest.mark.parametrize("mu", [1e2, 1e3, 1e4])
+@pytest.mark.parametrize("T,N,resident", OFFSET_ROUTES)
+def test_gae_normalize_large_mean(dev, monkeypatch, T, N, resident, mu):
+    if not resident:
+        monkeypatch.setenv("PPO_AMD_GAE_RESIDENT", "0")
+    g = torch.Generator().manual_seed(int(mu) + N)
+    r = mu + torch.randn(T, N, generator=g)
+    v = torch.zeros(T, N)
+    d = torch.ones(T, N, dtype=torch.uint8)  # every step done: adv = r - v
+    print(f"gae_normalize large mean T={T} N={N} resident={resident} mu={mu}", flush=True)
+    adv, _, adv_n, stats = ppo_amd.gae_normalize(r.to(dev), v.to(dev), d.to(dev), None, 0.99,
+                                                 0.95, return_stats=True)
+    a64 = adv.cpu().double()
+    mean64, std64 = a64.mean().item(), a64.std().item()
+    mean_f, std_f = stats.cpu().tolist()
+    assert abs(mean_f - mean64) <= np.spacing(np.float32(abs(mean64))), (mean_f, mean64)
+    assert std_f == pytest.approx(std64, rel=1e-6), (std_f, std64)
+    a = adv.cpu()
+    want = (a - torch.tensor(mean_f)) / (torch.tensor(std_f) + torch.tensor(1e-8))
+    torch.testing.assert_close(adv_n.cpu(), want, rtol=1e-6, atol=1e-6)

@@ -370,10 +370,13 @@ ResPlan res_plan(long T, long N, bool norm) {
 // round one carry per env (the advantage at the round's left edge), then
 // three words (n, sum, sum of squares) per workgroup.
 constexpr size_t kResSlotBase = kSyncWords;
+// per workgroup: n, sum and sum of squares of its advantages, and the centred
+// sum of squares of the exact second pass (gae_resident_kernel, step 4)
+constexpr size_t kResPartWords = 4;
 size_t res_slot_words(const ResPlan& rp) {
   if (!rp.E) return 0;
   return kResSlotBase + (size_t)rp.tiles() * 2 * rp.E + (size_t)rp.rounds * rp.nc * rp.E +
-         (size_t)rp.grid() * 3;
+         (size_t)rp.grid() * kResPartWords;
 }
 size_t res_slot_words_max(long T, long N) {
   return std::max(res_slot_words(res_plan(T, N, true)), res_slot_words(res_plan(T, N, false)));
@@ -1229,7 +1232,9 @@ __device__ __forceinline__ void strip_chunk(const GaeArgs& a, StripShared<kStrip
       adv[i][k] = (float)x;
     }
   }
-  float s1 = 0.0f, s2 = 0.0f;  // this chunk's sums: few terms, fp32
+  // this chunk's sums, fp64 (fp32 sums of squares lose the variance when
+  // |mean| is large against the spread)
+  double s1 = 0.0, s2 = 0.0;
 #pragma unroll
   for (int i = 0; i < L; ++i) {
     if (ok && i < nvalid) {
@@ -1244,8 +1249,9 @@ __device__ __forceinline__ void strip_chunk(const GaeArgs& a, StripShared<kStrip
       if constexpr (kStats) {
 #pragma unroll
         for (int k = 0; k < VW; ++k) {
-          s1 += adv[i][k];
-          s2 += adv[i][k] * adv[i][k];
+          const double x = (double)adv[i][k];
+          s1 += x;
+          s2 += x * x;
         }
       }
     }
@@ -1253,8 +1259,8 @@ __device__ __forceinline__ void strip_chunk(const GaeArgs& a, StripShared<kStrip
   if constexpr (kStats) {
     if (ok) {
       acc[0] += (double)(nvalid * VW);
-      acc[1] += (double)s1;
-      acc[2] += (double)s2;
+      acc[1] += s1;
+      acc[2] += s2;
     }
   }
 }
@@ -1547,7 +1553,7 @@ __global__ void __launch_bounds__(kSpanThreads) gae_span_final_kernel(GaeArgs a)
   // carry entering the span (from the carry scan over the span composites)
   if (tid < E) sh.x[e] = a.carry[sp.span * a.N + col0 + e];
 
-  float s1 = 0.0f, s2 = 0.0f;
+  double s1 = 0.0, s2 = 0.0;  // (fp64: see strip_chunk)
   double cnt = 0.0;
   for (long tile = sp.hi - 1; tile >= sp.lo; --tile) {
     span_stage<E, kHasV>(sh, x);
@@ -1580,8 +1586,8 @@ __global__ void __launch_bounds__(kSpanThreads) gae_span_final_kernel(GaeArgs a)
         sh.r[p] = av;
         sh.v[p] = rt;
         if constexpr (kStats) {
-          s1 += av;
-          s2 += av * av;
+          s1 += (double)av;
+          s2 += (double)av * (double)av;
         }
       }
     }
@@ -1605,7 +1611,7 @@ __global__ void __launch_bounds__(kSpanThreads) gae_span_final_kernel(GaeArgs a)
     __syncthreads();
   }
   if constexpr (kStats) {
-    double acc[3] = {cnt, (double)s1, (double)s2};
+    double acc[3] = {cnt, s1, s2};
     block_sum<3>(acc);
     if (tid == 0) {
       a.partial[blockIdx.x * 4 + 0] = acc[0];
@@ -1721,6 +1727,8 @@ struct ResShared {
   float ssum[5][4][kResBlock];              // per thread and env: sums of a, P, aa, aP, PP
   double carry[E];                          // advantage entering the tile
   float norm[2];                            // mean and denominator
+  double mean, m2;                          // the statistics' fp64 mean and centred sum of squares
+  int exact;                                // the second, exact pass is run
 };
 
 template <int E, int L, bool kStats, bool kHasV, bool kRounds>
@@ -1782,7 +1790,7 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       s_tag = tag;
       s_epoch = epoch;
     }
-    sync_start(ctr, part + (size_t)blockIdx.x * 3, 3, tag);
+    sync_start(ctr, part + (size_t)blockIdx.x * kResPartWords, (int)kResPartWords, tag);
   }
 
   const double gl0 = mul(a.gl, 0.0);
@@ -2027,7 +2035,7 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       }
       block_sum_lds<3>(acc);
       if (tid == 0) {
-        uint64_t* pp = part + (size_t)blockIdx.x * 3;
+        uint64_t* pp = part + (size_t)blockIdx.x * kResPartWords;
         slot_put(pp + 0, acc[0]);
         slot_put(pp + 1, acc[1]);
         slot_put(pp + 2, acc[2]);
@@ -2098,19 +2106,53 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       {
         double tot[3] = {0.0, 0.0, 0.0};
         for (long u = tid; u < (long)gridDim.x; u += kResBlock) {
-          uint64_t* pp = part + (size_t)u * 3;
+          uint64_t* pp = part + (size_t)u * kResPartWords;
           tot[0] += slot_get(pp + 0);
           tot[1] += slot_get(pp + 1);
           tot[2] += slot_get(pp + 2);
         }
         block_sum_lds<3>(tot);
         if (tid == 0) {
+          const double mean = tot[1] / tot[0];
+          const double m2 = tot[2] - tot[1] * mean;
+          sh.mean = mean;
+          sh.m2 = m2;
+          // The workgroups' sums come from fp32 closed forms, whose rounding
+          // (relative ~1e-7 of the sum of squares) swamps the variance once
+          // |mean| is large against the spread.  Past mean^2 > 100 var the
+          // centred sum of squares is therefore formed exactly, in a second
+          // exchange over the advantages held in registers.  Every workgroup
+          // has the same totals, so all take the same branch.
+          sh.exact = tot[0] > 1.0 && mean * mean * tot[0] > 100.0 * (m2 > 0.0 ? m2 : 0.0);
+        }
+        lds_barrier();
+        if (sh.exact) {
+          const double mean = sh.mean;
+          double c[1] = {0.0};
+#pragma unroll
+          for (int i = 0; i < L; ++i) {
+            if (i < nvalid) {
+#pragma unroll
+              for (int k = 0; k < VW; ++k) {
+                const double dx = (double)r[i][k] - mean;
+                c[0] += dx * dx;
+              }
+            }
+          }
+          block_sum_lds<1>(c);
+          if (tid == 0) slot_put(part + (size_t)blockIdx.x * kResPartWords + 3, c[0]);
+          double t2[1] = {0.0};
+          for (long u = tid; u < (long)gridDim.x; u += kResBlock)
+            t2[0] += slot_get(part + (size_t)u * kResPartWords + 3);
+          block_sum_lds<1>(t2);
+          if (tid == 0) sh.m2 = t2[0];
+        }
+        if (tid == 0) {
           // norm_params' formulas on these totals
           const double n = tot[0];
-          const double mean = tot[1] / n;
+          const double mean = sh.mean, m2 = sh.m2;
           float mean_f = (float)mean, std_f, mean_used, denom;
           if (n > 1.0) {
-            const double m2 = tot[2] - tot[1] * mean;
             std_f = (float)sqrt((m2 > 0.0 ? m2 : 0.0) / (n - 1.0));
             mean_used = mean_f;
             denom = std_f + (float)a.eps;
@@ -2257,14 +2299,9 @@ int launch_gae(const GaePlan& p, GaeArgs a, bool norm, hipStream_t stream) {
                             a.stats_out, stream);
   }
   if (p.Tt > 1) {
-    // pass 1: quad tiles when the tile sums are needed (their DPP tree beats
-    // the LDS tree), stacked tiles otherwise (measured faster without sums)
-    PassGeom g1 = p.scan;
-    g1.quad = norm && p.vw == 4 && g1.Qw == 64 && g1.Sw == 4 && p.fin_solo.Tq > 0;
-    if ((st = launch_tile(norm ? tile_kernel<kSummaryStats>(p.vw, g1)
-                               : tile_kernel<kSummary>(p.vw, g1),
-                          g1, a, p.Tt, stream)))
-      return st;
+    // pass 1: tile composites; then the carry scan
+    const PassGeom& g1 = p.scan;
+    if ((st = launch_tile(tile_kernel<kSummary>(p.vw, g1), g1, a, p.Tt, stream))) return st;
     const CarryPlan cp = make_carry_plan(p.Tt, a.N);
     const dim3 cgrid((unsigned)cp.groups, (unsigned)cp.nchunks);
     if (cp.nchunks > 1) {
@@ -2275,17 +2312,22 @@ int launch_gae(const GaePlan& p, GaeArgs a, bool norm, hipStream_t stream) {
     }
     hipLaunchKernelGGL(gae_carry_kernel<false>, cgrid, dim3(cp.Ew * cp.Rw), 0, stream, a.summary,
                        const_cast<double*>(a.carry), a.chunk_sum, p.Tt, a.N, cp.Ew, cp.Rw,
-                       cp.nchunks, norm ? a.tstat : nullptr, a.partial, a.T, p.span);
+                       cp.nchunks, nullptr, a.partial, a.T, p.span);
     if ((st = last_launch_status())) return st;
     if (!norm) {
       const PassGeom& gf = p.final_geom(false);
       return launch_tile(tile_kernel<kFinal>(p.vw, gf), gf, a, p.Tt, stream);
     }
-    // mean/std from the carry-scan partials, then one pass writes adv, ret, adv_n
-    if ((st = launch_finalize_stats(a.partial, cp.groups * cp.nchunks, a.eps, a.hdr, a.stats_out,
-                                    stream)))
+    // the final pass writes adv and ret and leaves fp64 (n, sum, sum of
+    // squares) of its fp32 advantages per block; then the elementwise
+    // normaliser.  (The tile passes used to carry closed-form fp32 sums of
+    // each tile's suffix composites into the carry scan, saving the
+    // normaliser's re-read; their rounding lost the variance once |mean|
+    // exceeded ~100 std.)
+    if ((st = launch_tile(tile_kernel<kFinalPartials>(p.vw, p.fin), p.fin, a, p.Tt, stream)))
       return st;
-    return launch_tile(tile_kernel<kFinalNorm>(p.vw, p.fin), p.fin, a, p.Tt, stream);
+    return launch_normalize(a.partial, p.Tt * p.fin.Tq, a.eps, a.adv, a.adv_n, a.T * a.N, a.hdr,
+                            a.stats_out, stream);
   }
   a.carry = nullptr;
   if (!norm) {
