@@ -18,8 +18,8 @@
 //   * A "segment" is L consecutive steps of VW adjacent envs owned by one
 //     thread (VW=4: float4 row loads, dones read as one 32-bit word).
 //   * A "tile" is Sw consecutive segments x Qw adjacent env-groups owned by
-//     one 256-thread workgroup; segments are composed with a Kogge-Stone scan
-//     in LDS.
+//     one 256-thread workgroup; segments are composed by lane shuffles in each
+//     wave and a fold of the four waves in LDS.
 //   1. gae_tile_kernel<kSummary>: per tile and env, the composite (a, P) of
 //      all its steps -> workspace `summary` [Tt][N].
 //   2. gae_carry_kernel: per env, a reverse scan over the tiles' (a, P) ->
@@ -28,15 +28,10 @@
 //   3. gae_tile_kernel<kFinal>: re-reads the tile, rebuilds the
 //      segment composites, applies the tile carry, and runs the exact serial
 //      recurrence per segment, writing adv and ret.
-// Fused normalisation (ppo_gae_norm_f32): pass 1 also stores, per tile and
-// env, five sums that make the tile's sum of advantages and of their squares
-// closed-form functions of its carry; the carry scan evaluates them as it
-// produces the carries, a one-block finaliser turns the totals into mean and
-// std, and pass 3 writes the normalised advantages beside adv and ret.  The
-// statistics are those of the fp64 advantages before their fp32 rounding
-// (relative difference ~1e-8 from the rounded values' statistics).
-// When the whole horizon fits in one tile (Tt == 1) steps 1-2 are skipped and
-// the final pass emits per-block sums for a separate normalise pass instead.
+// Fused normalisation (ppo_gae_norm_f32): the final pass also leaves per-block
+// fp64 (n, sum, sum of squares) of its fp32 advantages, and the elementwise
+// normaliser runs after it.  When the whole horizon fits in one tile (Tt ==
+// 1) steps 1-2 are skipped.
 //
 // Wide rollouts (N >= 2048, aligned) take a single-pass "strip walk" instead
 // (gae_strip_kernel): a workgroup owns 8-32 adjacent envs for the whole
@@ -70,9 +65,7 @@ struct GaeArgs {
   double2* chunk_sum;  // [nchunks][N] (a, P) of each carry-scan chunk
   const double* carry; // [Tt][N] or null (all-zero carries)
   double* partial;     // [.][4] (n, sum, sum sq) partials of the advantages
-  float* tstat;        // [5][Tt][N] per tile and env: sums over the tile's steps of
-                       // a, P, a*a, a*P, P*P (a, P: composite from the step to the tile end)
-  float* adv_n;        // normalised advantages (fused-normalise, multi-tile path)
+  float* adv_n;        // normalised advantages
   WsHeader* hdr;
   float* stats_out;
   double eps;
@@ -88,10 +81,8 @@ struct GaeArgs {
 // What a gae_tile_kernel launch computes.
 enum GaeMode {
   kSummary = 0,       // pass 1: tile composites
-  kSummaryStats = 1,  // pass 1: tile composites + tile sums for the normaliser
   kFinal = 2,         // pass 2: adv, ret
-  kFinalPartials = 3, // pass 2: adv, ret + per-block (n, sum, sum sq) (single-tile horizon)
-  kFinalNorm = 4,     // pass 2: adv, ret, adv_n with mean/denom from the workspace header
+  kFinalPartials = 3, // pass 2: adv, ret + per-block fp64 (n, sum, sum sq) for the normaliser
 };
 
 // Geometry of one tile pass: L steps x VW envs per thread, Sw segments x Qw
@@ -100,7 +91,6 @@ struct PassGeom {
   int L, Qw, Sw;
   long Tq;
   bool solo;  // Sw == 1: the thread's segment is the tile, no LDS scan
-  bool quad;  // Sw == 4, Qw == 64: segments of a tile in adjacent lanes
 };
 
 struct GaePlan {
@@ -121,7 +111,6 @@ PassGeom make_geom(long Q, int L, int Qw) {
   g.Sw = kBlock / Qw;
   g.Tq = (Q + Qw - 1) / Qw;
   g.solo = g.Sw == 1;
-  g.quad = false;
   return g;
 }
 
@@ -130,12 +119,9 @@ PassGeom make_geom(long Q, int L, int Qw) {
 // rollouts stack Sw = 256/Qw segments per tile (Qw <= 64 env-groups) and
 // compose them with an LDS scan, keeping a workgroup's rows wide enough to
 // coalesce.  Wide rollouts (VW = 4, >= 256 env-groups) have 4 segments of 4
-// steps x 64 env-groups per tile, with two more layouts chosen per pass by
-// measurement at T=2048, N=4096 (kernel us, stacked / quad / solo):
-//   pass 1 with the normaliser's tile sums: 24.3 / 22.1 / 33.1 -> quad
-//   pass 1 without:                          17.9 / 19.3 / -    -> stacked
-//   final pass writing adv, ret, adv_n:      30.5 / 33.6 / 31.7 -> stacked
-//   final pass writing adv, ret:             26.6 / 30.4 / 23.0 -> solo
+// steps x 64 env-groups per tile; their final pass without the normaliser
+// takes solo tiles instead, chosen by measurement at T=2048, N=4096 (kernel
+// us, stacked / solo): pass 1 17.9 / -, final pass 26.6 / 23.0.
 // (solo tiles are 16 steps x 4 envs per thread, 256 env-groups per tile: the
 // same tile boundaries in T, so their carries are interchangeable.)
 GaePlan make_plan(long T, long N, int vw) {
@@ -383,7 +369,7 @@ size_t res_slot_words_max(long T, long N) {
 }
 
 struct GaeLayout {
-  size_t summary, carry, chunk_sum, tstat, partial, slots, total;
+  size_t summary, carry, chunk_sum, partial, slots, total;
 };
 
 GaeLayout make_layout(const GaePlan& p, long N) {
@@ -400,8 +386,6 @@ GaeLayout make_layout(const GaePlan& p, long N) {
   l.chunk_sum = off;
   off += align_up((size_t)std::max(make_carry_plan(p.Tt, N).nchunks,
                                    make_carry_plan(ncarry, N).nchunks) * N * sizeof(double2), 256);
-  l.tstat = off;
-  off += align_up((size_t)5 * p.Tt * N * sizeof(float), 256);
   l.partial = off;
   {
     const CarryPlan cp = make_carry_plan(p.Tt, N);
@@ -529,35 +513,13 @@ __device__ __forceinline__ unsigned load_done_raw(const uint8_t* p) {
 enum TileLayout {
   kStacked = 0,  // segment s of env-group q is thread s*Qw + q; LDS scan across waves
   kSoloTile = 1, // Sw == 1: the thread's segment is the tile
-  kQuadTile = 2, // Sw == 4: segment s of env-group q is thread 4q + s; the scan and
-                 // the tile sums are DPP moves inside each quad of lanes, no LDS
 };
-
-// Lane i of each quad takes lane min(i + off, 3): quad_perm [1,2,3,3] for
-// off = 1, [2,3,3,3] for off = 2.
-template <int kOff>
-struct QuadCtrl {
-  static_assert(kOff == 1 || kOff == 2, "quad offsets 1 and 2");
-  static constexpr int value = kOff == 1 ? 0xF9 : 0xFE;
-};
-template <int kOff>
-__device__ __forceinline__ double quad_down(double x) {
-  return dpp_move<QuadCtrl<kOff>::value>(x);
-}
-template <int kOff>
-__device__ __forceinline__ float quad_down(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
-                                                               QuadCtrl<kOff>::value, 0xF, 0xF,
-                                                               false));
-}
 
 template <int VW, int L, int kLayout, int kMode>
 __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
   constexpr bool kSolo = kLayout == kSoloTile;
-  constexpr bool kQuad = kLayout == kQuadTile;
   constexpr bool kLds = kLayout == kStacked;
   constexpr bool kIsFinal = kMode >= kFinal;
-  constexpr bool kTileStats = kMode == kSummaryStats;
   __shared__ double s_a[kLds ? kBlock * VW : 1];
   __shared__ double s_p[kLds ? kBlock * VW : 1];
 
@@ -565,8 +527,8 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
   const long tile_t = bid / a.Tq;
   const long tile_q = bid - tile_t * a.Tq;
   const int tid = threadIdx.x;
-  const int q = kQuad ? tid >> 2 : tid % a.Qw;
-  const int s = kQuad ? tid & 3 : tid / a.Qw;
+  const int q = tid % a.Qw;
+  const int s = tid / a.Qw;
   const long col = tile_q * a.Qw + q;
   const bool col_ok = col < a.Q;
   const long env0 = col * VW;
@@ -604,18 +566,13 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
     else return ((draw[i] >> (8 * k)) & 0xffu) != 0u;
   };
 
-  // Composite (a, P) of this segment with a zero carry.  With kTileStats also
-  // the sums over the segment's steps of a_t, P_t, a_t^2, a_t P_t, P_t^2, where
-  // (a_t, P_t) is the composite from step t to the segment end, so that the
-  // advantage is adv_t = a_t + P_t * carry.
+  // Composite (a, P) of this segment with a zero carry.
   double ia[VW], ip[VW];
-  float sa[VW], sP[VW], saa[VW], saP[VW], sPP[VW];  // fp32: at most 16 terms each
   {
     double nvd[VW];
 #pragma unroll
     for (int k = 0; k < VW; ++k) {
       ia[k] = 0.0; ip[k] = 1.0; nvd[k] = nv[k];
-      sa[k] = sP[k] = saa[k] = saP[k] = sPP[k] = 0.0f;
     }
 #pragma unroll
     for (int i = L - 1; i >= 0; --i) {
@@ -629,42 +586,19 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
           ia[k] = add(delta, mul(c, ia[k]));
           ip[k] = mul(ip[k], c);
           nvd[k] = vd;
-          if constexpr (kTileStats) {
-            const float fa = (float)ia[k], fp = (float)ip[k];
-            sa[k] += fa;
-            sP[k] += fp;
-            saa[k] += fa * fa;
-            saP[k] += fa * fp;
-            sPP[k] += fp * fp;
-          }
         }
       }
     }
   }
 
-  // Reverse inclusive scan over the Sw segments of the tile:
-  // (a_s, P_s) <- (a_s + P_s*a_{s+off}, P_s*P_{s+off}).  (Solo tiles: the
-  // segment is the tile; quad tiles scan with DPP moves.)
-  if constexpr (kQuad) {
-#pragma unroll
-    for (int k = 0; k < VW; ++k) {
-      {
-        const double pa = quad_down<1>(ia[k]), pp = quad_down<1>(ip[k]);
-        if (s + 1 < 4) { ia[k] = ia[k] + ip[k] * pa; ip[k] = ip[k] * pp; }
-      }
-      {
-        const double pa = quad_down<2>(ia[k]), pp = quad_down<2>(ip[k]);
-        if (s + 2 < 4) { ia[k] = ia[k] + ip[k] * pa; ip[k] = ip[k] * pp; }
-      }
-    }
-  }
-  // Stacked tiles outside the tile-sums pass: reverse scan of the segments
-  // inside each wave by lane moves (segment s + 1 is lane + Qw), the four
+  // Reverse scan over the Sw segments of the tile (solo tiles: the segment is
+  // the tile).  Stacked tiles: reverse scan of the segments inside each wave
+  // by lane moves (segment s + 1 is lane + Qw), the four
   // waves' composites through LDS (one barrier), then each segment's
   // exclusive composite (of the segments after it) = its wave's exclusive
   // part followed by the later waves.  (ex_a, ex_p) is the identity for the
   // tile's last segment; tile_a/tile_p is the whole tile (segment 0).
-  constexpr bool kWaveScan = kLds && kMode != kSummaryStats;
+  constexpr bool kWaveScan = kLds;
   double ex_a[VW], ex_p[VW], tile_a[VW], tile_p[VW];
   if constexpr (kWaveScan) {
     constexpr int kWaves = kBlock / kWave;
@@ -715,123 +649,12 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
       tile_p[k] = ip[k] * lp;
     }
   }
-  if constexpr (kLds && !kWaveScan) {
-#pragma unroll
-  for (int k = 0; k < VW; ++k) { s_a[k * kBlock + tid] = ia[k]; s_p[k * kBlock + tid] = ip[k]; }
-  for (int off = 1; off < a.Sw; off <<= 1) {
-    __syncthreads();
-    const bool has = s + off < a.Sw;
-    double pa[VW], pp[VW];
-    if (has) {
-#pragma unroll
-      for (int k = 0; k < VW; ++k) {
-        pa[k] = s_a[k * kBlock + tid + off * a.Qw];
-        pp[k] = s_p[k * kBlock + tid + off * a.Qw];
-      }
-    }
-    __syncthreads();
-    if (has) {
-#pragma unroll
-      for (int k = 0; k < VW; ++k) {
-        ia[k] = ia[k] + ip[k] * pa[k];
-        ip[k] = ip[k] * pp[k];
-        s_a[k * kBlock + tid] = ia[k];
-        s_p[k * kBlock + tid] = ip[k];
-      }
-    }
-  }
-  __syncthreads();
-  }
-
   if constexpr (!kIsFinal) {
     if (s == 0 && col_ok) {
 #pragma unroll
       for (int k = 0; k < VW; ++k)
         a.summary[tile_t * a.N + env0 + k] =
             kWaveScan ? make_double2(tile_a[k], tile_p[k]) : make_double2(ia[k], ip[k]);
-    }
-    if constexpr (kTileStats && kQuad) {
-      // Re-base on the tile end with the composite (An, Pn) of the later
-      // segments (the scanned value of lane s+1), then sum the four lanes:
-      // (x0 + x2) + (x1 + x3), in lane 0 of the quad.
-      float q5[5][VW];
-#pragma unroll
-      for (int k = 0; k < VW; ++k) {
-        const double na = quad_down<1>(ia[k]), np = quad_down<1>(ip[k]);
-        const float An = s + 1 < 4 ? (float)na : 0.0f;
-        const float Pn = s + 1 < 4 ? (float)np : 1.0f;
-        q5[0][k] = sa[k] + An * sP[k];
-        q5[1][k] = Pn * sP[k];
-        q5[2][k] = saa[k] + 2.0f * An * saP[k] + An * An * sPP[k];
-        q5[3][k] = Pn * (saP[k] + An * sPP[k]);
-        q5[4][k] = Pn * Pn * sPP[k];
-      }
-#pragma unroll
-      for (int j = 0; j < 5; ++j)
-#pragma unroll
-        for (int k = 0; k < VW; ++k) {
-          q5[j][k] += quad_down<2>(q5[j][k]);
-          q5[j][k] += quad_down<1>(q5[j][k]);
-        }
-      if (s == 0 && col_ok) {
-        const long plane = a.Tt * a.N;
-#pragma unroll
-        for (int j = 0; j < 5; ++j) store_f<VW>(a.tstat + j * plane + tile_t * a.N + env0, q5[j]);
-      }
-    } else if constexpr (kTileStats && kSolo) {
-      if (col_ok) {
-        const long plane = a.Tt * a.N;
-        float q5[5][VW];
-#pragma unroll
-        for (int k = 0; k < VW; ++k) {
-          q5[0][k] = sa[k];
-          q5[1][k] = sP[k];
-          q5[2][k] = saa[k];
-          q5[3][k] = saP[k];
-          q5[4][k] = sPP[k];
-        }
-#pragma unroll
-        for (int j = 0; j < 5; ++j) store_f<VW>(a.tstat + j * plane + tile_t * a.N + env0, q5[j]);
-      }
-    } else if constexpr (kTileStats) {
-      // Re-base the segment sums on the tile end: with (An, Pn) the composite
-      // of the later segments of the tile, a' = a + An P and P' = Pn P.
-      float q5[5][VW];
-#pragma unroll
-      for (int k = 0; k < VW; ++k) {
-        float An = 0.0f, Pn = 1.0f;
-        if (s + 1 < a.Sw) {
-          An = (float)s_a[k * kBlock + tid + a.Qw];
-          Pn = (float)s_p[k * kBlock + tid + a.Qw];
-        }
-        q5[0][k] = sa[k] + An * sP[k];
-        q5[1][k] = Pn * sP[k];
-        q5[2][k] = saa[k] + 2.0f * An * saP[k] + An * An * sPP[k];
-        q5[3][k] = Pn * (saP[k] + An * sPP[k]);
-        q5[4][k] = Pn * Pn * sPP[k];
-      }
-      // tree-sum of all five sums over the Sw segments of the tile at once
-      __shared__ float s_q[kTileStats ? 5 * VW * kBlock : 1];
-      const long plane = a.Tt * a.N;
-#pragma unroll
-      for (int j = 0; j < 5; ++j)
-#pragma unroll
-        for (int k = 0; k < VW; ++k) s_q[(j * VW + k) * kBlock + tid] = q5[j][k];
-      for (int h = a.Sw >> 1; h > 0; h >>= 1) {
-        __syncthreads();
-        if (s < h) {
-#pragma unroll
-          for (int j = 0; j < 5 * VW; ++j) s_q[j * kBlock + tid] += s_q[j * kBlock + tid + h * a.Qw];
-        }
-      }
-      __syncthreads();
-      if (s == 0 && col_ok) {
-#pragma unroll
-        for (int j = 0; j < 5; ++j)
-#pragma unroll
-          for (int k = 0; k < VW; ++k)
-            a.tstat[j * plane + tile_t * a.N + env0 + k] = s_q[(j * VW + k) * kBlock + tid];
-      }
     }
     return;
   } else {
@@ -840,19 +663,7 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
 #pragma unroll
     for (int k = 0; k < VW; ++k) {
       const double C = (a.carry && col_ok) ? a.carry[tile_t * a.N + env0 + k] : 0.0;
-      double na = 0.0, np = 1.0;
-      if constexpr (kQuad) {
-        na = quad_down<1>(ia[k]);
-        np = quad_down<1>(ip[k]);
-      }
-      if (kWaveScan)
-        cin[k] = ex_a[k] + ex_p[k] * C;
-      else if (kQuad && s + 1 < 4)
-        cin[k] = na + np * C;
-      else if (kLds && s + 1 < a.Sw)
-        cin[k] = s_a[k * kBlock + tid + a.Qw] + s_p[k * kBlock + tid + a.Qw] * C;
-      else
-        cin[k] = C;
+      cin[k] = kWaveScan ? ex_a[k] + ex_p[k] * C : C;
     }
 
     // Exact serial recurrence over the segment; r[][] is reused for adv.
@@ -875,11 +686,6 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
         }
       }
     }
-    float mean = 0.0f, denom = 1.0f;
-    if constexpr (kMode == kFinalNorm) {
-      mean = a.hdr->stats[0];
-      denom = a.hdr->stats[2];
-    }
 #pragma unroll
     for (int i = 0; i < L; ++i) {
       if (i < nvalid) {
@@ -890,12 +696,6 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
 #pragma unroll
           for (int k = 0; k < VW; ++k) rt[k] = r[i][k] + val(i, k);
           store_f<VW>(a.ret + off, rt);
-        }
-        if constexpr (kMode == kFinalNorm) {
-          float an[VW];
-#pragma unroll
-          for (int k = 0; k < VW; ++k) an[k] = (r[i][k] - mean) / denom;
-          store_f<VW>(a.adv_n + off, an);
         }
       }
     }
@@ -957,21 +757,12 @@ __device__ __forceinline__ void carry_row_scan(double* s_a, double* s_p, int tid
   __syncthreads();
 }
 
-// With tstat (the kCarry launch of the fused-normalise path), each thread also
-// accumulates, for every tile k it writes with carry c_k, the tile's sums of
-// the advantages adv_t = a_t + P_t c_k and of their squares,
-//     sum adv   = S_a + c_k S_P
-//     sum adv^2 = S_aa + 2 c_k S_aP + c_k^2 S_PP,
-// and the block stores (n, sum, sum of squares) in stat_part.
 template <bool kCompose>
 __global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* __restrict__ summary,
                                                                  double* __restrict__ carry,
                                                                  double2* __restrict__ chunk_sum,
                                                                  long Tt, long N, int Ew, int Rw,
-                                                                 long nchunks,
-                                                                 const float* __restrict__ tstat,
-                                                                 double* __restrict__ stat_part,
-                                                                 long T, long span) {
+                                                                 long nchunks) {
   __shared__ double s_a[kCarryBlock];
   __shared__ double s_p[kCarryBlock];
   const int tid = threadIdx.x;
@@ -1027,32 +818,12 @@ __global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* _
     if (g == 0 && ok) chunk_sum[c * N + env] = make_double2(s_a[e], s_p[e]);
   } else {
     double cc = (g + 1 < Rw) ? s_a[tid + Ew] + s_p[tid + Ew] * C : C;
-    double st[3] = {0.0, 0.0, 0.0};
-    const long plane = Tt * N;
 #pragma unroll
     for (int j = kCarryG - 1; j >= 0; --j) {
       const long k = k0 + j;
       if (ok && k < hi) {
         carry[k * N + env] = cc;
-        if (tstat) {
-          const long i = k * N + env;
-          const long len = T - k * span < span ? T - k * span : span;
-          st[0] += (double)len;
-          st[1] += (double)tstat[i] + cc * (double)tstat[plane + i];
-          st[2] += (double)tstat[2 * plane + i] + 2.0 * cc * (double)tstat[3 * plane + i] +
-                   cc * cc * (double)tstat[4 * plane + i];
-        }
         cc = ta[j] + tp[j] * cc;
-      }
-    }
-    if (tstat) {
-      block_sum<3>(st);
-      if (tid == 0) {
-        const long b = c * gridDim.x + blockIdx.x;
-        stat_part[b * 4 + 0] = st[0];
-        stat_part[b * 4 + 1] = st[1];
-        stat_part[b * 4 + 2] = st[2];
-        stat_part[b * 4 + 3] = 0.0;
       }
     }
   }
@@ -1663,13 +1434,11 @@ int launch_span(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
   double* carry = const_cast<double*>(a.carry);
   if (cp.nchunks > 1) {
     hipLaunchKernelGGL(gae_carry_kernel<true>, cgrid, dim3(cp.Ew * cp.Rw), 0, stream, a.summary,
-                       carry, a.chunk_sum, sp.spans, N, cp.Ew, cp.Rw, cp.nchunks, nullptr, nullptr,
-                       T, 0L);
+                       carry, a.chunk_sum, sp.spans, N, cp.Ew, cp.Rw, cp.nchunks);
     if ((st = last_launch_status())) return st;
   }
   hipLaunchKernelGGL(gae_carry_kernel<false>, cgrid, dim3(cp.Ew * cp.Rw), 0, stream, a.summary,
-                     carry, a.chunk_sum, sp.spans, N, cp.Ew, cp.Rw, cp.nchunks, nullptr, nullptr,
-                     T, 0L);
+                     carry, a.chunk_sum, sp.spans, N, cp.Ew, cp.Rw, cp.nchunks);
   if ((st = last_launch_status())) return st;
   if ((st = hip_status(hipLaunchKernel(k2, grid, dim3(kSpanThreads), args, 0, stream)))) return st;
   if (!norm) return PPO_OK;
@@ -2253,7 +2022,6 @@ template <int kMode>
 const void* tile_kernel(int vw, const PassGeom& g) {
   if (vw == 1) return (const void*)gae_tile_kernel<1, 16, kStacked, kMode>;
   if (g.solo) return (const void*)gae_tile_kernel<4, 16, kSoloTile, kMode>;
-  if (g.quad) return (const void*)gae_tile_kernel<4, 4, kQuadTile, kMode>;
   return (const void*)gae_tile_kernel<4, 4, kStacked, kMode>;
 }
 
@@ -2307,12 +2075,12 @@ int launch_gae(const GaePlan& p, GaeArgs a, bool norm, hipStream_t stream) {
     if (cp.nchunks > 1) {
       hipLaunchKernelGGL(gae_carry_kernel<true>, cgrid, dim3(cp.Ew * cp.Rw), 0, stream, a.summary,
                          const_cast<double*>(a.carry), a.chunk_sum, p.Tt, a.N, cp.Ew, cp.Rw,
-                         cp.nchunks, nullptr, nullptr, a.T, p.span);
+                         cp.nchunks);
       if ((st = last_launch_status())) return st;
     }
     hipLaunchKernelGGL(gae_carry_kernel<false>, cgrid, dim3(cp.Ew * cp.Rw), 0, stream, a.summary,
                        const_cast<double*>(a.carry), a.chunk_sum, p.Tt, a.N, cp.Ew, cp.Rw,
-                       cp.nchunks, nullptr, a.partial, a.T, p.span);
+                       cp.nchunks);
     if ((st = last_launch_status())) return st;
     if (!norm) {
       const PassGeom& gf = p.final_geom(false);
@@ -2397,7 +2165,6 @@ int gae_impl(const float* rewards, const float* values, const uint8_t* dones,
   a.stats_out = stats_out;
   a.eps = eps;
   a.adv_n = adv_norm_out;
-  a.tstat = reinterpret_cast<float*>(ws + l.tstat);
   a.slots = reinterpret_cast<uint64_t*>(ws + l.slots);
 
   // Aligned rollouts whose tiles all fit on the device at once take the
