@@ -293,6 +293,22 @@ def test_cat_masked_logits(dev, A):
     assert (dl[mask] == 0).all()
 
 
+@pytest.mark.parametrize("scale", [30.0, 100.0])
+@pytest.mark.parametrize("A", [2, 18, 33])
+def test_cat_peaked_logits(dev, A, scale):
+    """Logits of large magnitude (near-deterministic policies, probabilities
+    underflowing to 0 in fp32): the kernel's max-shifted exponentials and
+    closed-form gradient against torch's log_softmax-based Categorical.  (At
+    |logits| ~ 1e3 the fp32 rounding of z - max itself, an ulp of ~6e-5, moves
+    small probabilities by ~1e-4 relative in either implementation, beyond
+    the 1e-4 gradient tolerance.)"""
+    logits, actions, old_lp, adv, ret, val, old_v = cat_inputs(1000, A, seed=int(scale) + A)
+    logits = logits * scale
+    old_lp = torch.log_softmax(logits, -1).gather(1, actions.long()[:, None]).squeeze(1) + \
+        0.05 * torch.randn(1000, generator=torch.Generator().manual_seed(A))
+    run_cat(dev, 1000, A, seed=0, inputs=(logits, actions, old_lp, adv, ret, val, old_v))
+
+
 def test_cat_misaligned_logits(dev):
     B, A = 300, 18
     inp = cat_inputs(B, A, seed=6)
