@@ -101,17 +101,19 @@ def assert_fixture_scalars(scalars, z):
     assert_scalars_close(scalars, o)
 
 
-def assert_scalars_close(scalars, o, rtol=1e-5, edge_rows=0):
+def assert_scalars_close(scalars, o, rtol=1e-5, edge_rows=0, lp_scale=1.0):
     """The reference's scalars (loss, policy, value, entropy) to rel 1e-5.
     approx_kl = mean(old_lp - lp) is a build-only diagnostic and a
-    cancellation: each fp32 log-prob (magnitude ~log A) carries ~1e-7 of
-    rounding, so it is held to 1e-6 absolute; clipfrac counts rows and may
-    differ by a row whose ratio sits within an ulp of the clip bound."""
+    cancellation: each fp32 log-prob carries rounding of ~1e-7 of its
+    magnitude (lp_scale: the largest |log-prob|, ~log A for categorical
+    policies), so it is held to max(1, lp_scale) x 1e-6 absolute; clipfrac
+    counts rows and may differ by a row whose ratio sits within an ulp of the
+    clip bound."""
     s = scalars.detach().cpu()
     for i, k in enumerate(NAMES):
         e = o[k].item()
         if k == "approx_kl":
-            assert s[i].item() == pytest.approx(e, abs=1e-6), k
+            assert s[i].item() == pytest.approx(e, abs=1e-6 * max(1.0, lp_scale)), k
         elif k == "clipfrac":
             slack = (2.0 + edge_rows) / o["dvalues"].numel()
             assert s[i].item() == pytest.approx(e, abs=slack + 1e-7), k
@@ -378,8 +380,8 @@ def gauss_inputs(B, D, seed):
     return mu, log_std, acts, old_lp, adv, ret, val, old_v
 
 
-def run_gauss(dev, B, D, seed, vf_clip=0.2):
-    inp = gauss_inputs(B, D, seed)
+def run_gauss(dev, B, D, seed, vf_clip=0.2, inputs=None):
+    inp = inputs if inputs is not None else gauss_inputs(B, D, seed)
     print(f"loss_gauss B={B} D={D} vf_clip={vf_clip}", flush=True)
     mu, log_std, acts, old_lp, adv, ret, val, old_v = inp
     scalars, dmu, dls, dv = ppo_amd.ppo_loss_gaussian_fused(
@@ -388,7 +390,8 @@ def run_gauss(dev, B, D, seed, vf_clip=0.2):
     o = ref.loss_gaussian_reference(*inp, 0.2, vf_clip, 0.5, 0.01)
     lp = torch.distributions.Normal(mu, log_std.exp()).log_prob(acts).sum(-1)
     edge = clip_edge_rows(o["ratio"], lp, old_lp)
-    assert_scalars_close(scalars, o, edge_rows=int(edge.sum()))
+    assert_scalars_close(scalars, o, edge_rows=int(edge.sum()),
+                         lp_scale=float(old_lp.abs().max()) / 3.0)
     assert_rows_close(dmu, o["dmu"], edge)
     assert_edge_rows(dmu, gauss_edge_candidates(mu, log_std, acts, adv, o["ratio"], edge), edge,
                      1e-5 * float(o["dmu"].abs().max()))
@@ -422,6 +425,24 @@ def test_golden_fixture_gauss(dev):
 @pytest.mark.parametrize("vf_clip", [None, 0.2])
 def test_gauss(dev, B, D, vf_clip):
     run_gauss(dev, B, D, seed=B * 7 + D, vf_clip=vf_clip)
+
+
+@pytest.mark.parametrize("shift", [-6.0, 3.0])
+@pytest.mark.parametrize("D", [1, 6, 17])
+def test_gauss_extreme_log_std(dev, D, shift):
+    """Very narrow (sigma ~ 1e-3) and very wide (sigma ~ 20) policies: the
+    same checks as test_gauss with log_std shifted by `shift` and the actions
+    drawn at that scale."""
+    B = 1000
+    g = torch.Generator().manual_seed(int(shift * 10) + D)
+    mu = torch.randn(B, D, generator=g)
+    log_std = torch.rand(D, generator=g) - 1.0 + shift
+    mu_old = mu + 0.05 * log_std.exp() * torch.randn(B, D, generator=g)
+    acts = mu_old + log_std.exp() * torch.randn(B, D, generator=g)
+    old_lp = torch.distributions.Normal(mu_old, log_std.exp()).log_prob(acts).sum(-1)
+    adv, ret, old_v = (torch.randn(B, generator=g) for _ in range(3))
+    val = old_v + 0.1 * torch.randn(B, generator=g)
+    run_gauss(dev, B, D, seed=0, inputs=(mu, log_std, acts, old_lp, adv, ret, val, old_v))
 
 
 @pytest.mark.parametrize("D", [1, 2, 3, 4, 5, 6, 7, 8, 9, 13, 16, 17, 24])
