@@ -658,6 +658,47 @@ def test_gae_resident_rounds_match_oracle(dev, T, N, p):
     assert exact > 0.99
 
 
+# Non-finite inputs on the resident pass without the normaliser.  Its
+# look-back walks the composites from the nearest tile outwards and stops at
+# the first whose factor product is zero (a done flag), skipping the tiles
+# beyond; where a skipped tile holds an inf or NaN, the reference carries
+# 0 x inf = NaN into every tile to its left, so the pass must find such tiles
+# afterwards and write NaN there.  Non-finite values late in the horizon, in
+# each round, and (one case) in the bootstrap value.
+NONFINITE_SHAPES = [
+    (16_384, 512, 0.002, False),  # one round, 32 tiles per column: walk window + full fold
+    (1 << 20, 16, 0.001, False),  # config 3's shape: 16-env tiles, 2 rounds
+    (600_000, 32, 0.002, True),   # 3 rounds, the last one partial; inf bootstrap value
+    (300_000, 64, 0.0, False),    # no dones: carries cross every tile (inf, not NaN)
+]
+
+
+@pytest.mark.parametrize("T,N,p,inf_last", NONFINITE_SHAPES)
+def test_gae_resident_no_norm_non_finite(dev, T, N, p, inf_last):
+    assert _route(T, N, False) == "resident"
+    r, v, d, lv = _inputs(T, N, p, seed=T % 977 + N)
+    v[T - 100, 0] = float("inf")
+    v[T - 5000, 1] = float("-inf")
+    v[T // 2 + T // 7, 2] = float("nan")
+    v[T // 3, 3] = float("inf")
+    v[T // 3 + 7, 3] = float("-inf")   # meets the inf above: NaN from there on
+    r[T // 5, N - 1] = float("inf")
+    if inf_last:
+        lv[N // 2] = float("inf")
+    print(f"gae resident no-norm non-finite T={T} N={N} p={p} inf_last={inf_last}", flush=True)
+    adv, ret, _ = _gae_abi(dev, r.to(dev), v.to(dev), d.to(dev), lv.to(dev), 0.99, 0.95)
+    a_ref, _ = ref.gae_c(r.numpy(), v.numpy(), d.numpy(), lv.numpy(), 0.99, 0.95)
+    got = adv.cpu().numpy()
+    assert np.isnan(a_ref).sum() > 1000  # the case is exercised
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(a_ref))
+    np.testing.assert_array_equal(np.isposinf(got), np.isposinf(a_ref))
+    np.testing.assert_array_equal(np.isneginf(got), np.isneginf(a_ref))
+    fin = np.isfinite(a_ref)
+    assert_gae_close(got[fin], a_ref[fin])
+    ret_ref = got + v.numpy()
+    np.testing.assert_array_equal(np.isnan(ret.cpu().numpy()), np.isnan(ret_ref))
+
+
 def test_discounted_returns_resident_rounds(dev):
     """values = None (REINFORCE returns) in rounds."""
     T, N = 1 << 20, 16

@@ -1488,6 +1488,23 @@ __device__ uint64_t g_res_trace[4096 * 32];
 #define RES_MARK(k)
 #endif
 
+// The product of two tiles' factor products, kept nonzero when neither is
+// zero.  In the reference's serial recurrence an infinite advantage becomes
+// NaN only by a zero factor (a done flag, or gamma * lambda = 0): it is
+// multiplied by gamma * lambda once per step and never underflows.  Products
+// composed over many tiles do underflow, and 0 x inf would then give NaN where
+// the reference keeps the infinity; the smallest subnormal in place of such a
+// zero keeps the infinity and changes no finite carry (its terms lie far below
+// an ulp).  Used where tiles are composed (the look-back); inside a tile the
+// products are plain (measured: 0.5-1.5 us per config-3 call on the critical
+// path), so a tile's own product (gamma * lambda)^steps must not underflow for
+// this to hold: gamma * lambda > 2^(-1074 / steps per tile), 0.70 for the
+// 2048-step tiles of 16 envs.
+__device__ __forceinline__ double prod_nz(double x, double y) {
+  const double p = x * y;
+  return (p == 0.0 && x != 0.0 && y != 0.0) ? __builtin_copysign(4.9406564584124654e-324, p) : p;
+}
+
 template <int E>
 struct ResShared {
   static constexpr int Q = kResBlock / E;   // look-back chunks per env
@@ -1498,6 +1515,9 @@ struct ResShared {
   float norm[2];                            // mean and denominator
   double mean, m2;                          // the statistics' fp64 mean and centred sum of squares
   int exact;                                // the second, exact pass is run
+  int rest;                                 // the look-back's full fold is needed
+  int bad;                                  // a composite of this workgroup's tiles is not finite
+  int nanfl[E];                             // the exact carry entering the tile is NaN
 };
 
 template <int E, int L, bool kStats, bool kHasV, bool kRounds>
@@ -1528,8 +1548,46 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
   uint64_t* ctr = a.slots;
   uint64_t* comp = a.slots + kResSlotBase;           // [nt][nc][E][2]
   uint64_t* bnd = comp + (size_t)nt * nc * 2 * E;    // [rounds][N]
-  uint64_t* part = bnd + (size_t)rounds * a.N;       // [grid][3]
+  uint64_t* part = bnd + (size_t)rounds * a.N;       // [grid][kResPartWords]
   auto tile_tt = [&](long rd) { return nt - 1 - (rd * ntr + tl); };  // < 0: no tile
+  // The composite of chunk q (of Q) of tiles lo + 1 .. hi for env e, folded
+  // from the right, LB slot pairs in flight; `base`/`step` address the slot
+  // pair of tile u for env e: word offset ((u * nc + col) * E + e) * 2.
+  auto fold_chunk = [&](int lo, int hi, int q, unsigned base, unsigned step) {
+    const int m = hi - lo;               // tiles to fold
+    const int cs = (m + Q - 1) / Q;      // tiles per chunk
+    const int u_hi = hi - q * cs, u_lo = max(lo + 1, hi - (q + 1) * cs + 1);
+    double A = 0.0, P = 1.0;
+    for (int u0 = u_hi; u0 >= u_lo; u0 -= LB) {
+      uint64_t wa[LB], wp[LB];
+#pragma unroll
+      for (int k = 0; k < LB; ++k) {
+        wa[k] = wp[k] = 0;
+        if (u0 - k >= u_lo) {
+          uint64_t* sl = comp + (base + (unsigned)(u0 - k) * step);
+          wa[k] = slot_peek(sl);
+          wp[k] = slot_peek(sl + 1);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < LB; ++k) {
+        if (u0 - k >= u_lo) {
+          uint64_t* sl = comp + (base + (unsigned)(u0 - k) * step);
+          const double ca = slot_or_get(wa[k], sl);
+          const double cp = slot_or_get(wp[k], sl + 1);
+          A = ca + cp * A;
+          P = prod_nz(cp, P);
+        }
+      }
+    }
+    return make_double2(A, P);
+  };
+  // (without the normaliser) this workgroup's flag of non-finite composites,
+  // published once its last tile's composite is
+  auto publish_bad = [&]() {
+    if (!kStats && tid == 0)
+      slot_put(part + (size_t)blockIdx.x * kResPartWords, sh.bad ? 1.0 : 0.0);
+  };
 #ifdef PPO_GAE_RES_TRACE
   long res_round = 0;
 #endif
@@ -1543,6 +1601,7 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
   // LDS by thread 0 (its only user) rather than in registers across step 1
   __shared__ unsigned s_tag;
   __shared__ uint64_t s_epoch;
+  if (tid == 0) sh.bad = 0;
   if (w == 0) {
     for (long rd = 0; rd < rounds; ++rd) {
       const long tt = tile_tt(rd);
@@ -1709,6 +1768,7 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       }
       slot_put(comp + ((size_t)(tt * nc + col) * E + tid) * 2 + 0, ta);
       slot_put(comp + ((size_t)(tt * nc + col) * E + tid) * 2 + 1, tp);
+      if (!kStats && !(__builtin_isfinite(ta) && __builtin_isfinite(tp))) sh.bad = 1;
     }
     // the start barrier (once): every workgroup's slots are empty by now
     if (rd == 0 && tid == 0) {
@@ -1726,47 +1786,63 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       // kResMaxRounds rounds)
       const int e = tid % E, q = tid / E;
       const int hi = (int)(nt - 1 - rd * ntr);
-      const int m = hi - (int)tt;             // tiles to fold
-      const int cs = (m + Q - 1) / Q;         // tiles per chunk
-      const int u_hi = hi - q * cs, u_lo = max((int)tt + 1, hi - (q + 1) * cs + 1);
       // slot pair of tile u for env e: word offset ((u * nc + col) * E + e) * 2
       const unsigned step = (unsigned)(nc * E * 2), base = (unsigned)((col * E + e) * 2);
-      double A = 0.0, P = 1.0;
-      for (int u0 = u_hi; u0 >= u_lo; u0 -= LB) {
-        uint64_t wa[LB], wp[LB];
-#pragma unroll
-        for (int k = 0; k < LB; ++k) {
-          wa[k] = wp[k] = 0;
-          if (u0 - k >= u_lo) {
-            uint64_t* sl = comp + (base + (unsigned)(u0 - k) * step);
-            wa[k] = slot_peek(sl);
-            wp[k] = slot_peek(sl + 1);
+      // Without the normaliser, the carry is first walked from the nearest
+      // tile outwards, and the walk stops at a tile whose factor product is
+      // zero (a done flag in that env): the tiles beyond it are multiplied by
+      // zero.  The window's words are read at once, one tile per thread.
+      double S = 0.0, M = 1.0;  // (threads tid < E) carry = S + M x (the rest)
+      int lo = (int)tt;         // the full fold covers tiles lo + 1 .. hi
+      if constexpr (!kStats) {
+        {
+          const int u = (int)tt + 1 + q;
+          uint64_t wa = 0, wp = 0;
+          if (u <= hi) {
+            uint64_t* sl = comp + (base + (unsigned)u * step);
+            wa = slot_peek(sl);
+            wp = slot_peek(sl + 1);
           }
+          sh.lb[q][e] = make_double2(__builtin_bit_cast(double, wa), __builtin_bit_cast(double, wp));
+          if (tid == 0) sh.rest = 0;
         }
-#pragma unroll
-        for (int k = 0; k < LB; ++k) {
-          if (u0 - k >= u_lo) {
-            uint64_t* sl = comp + (base + (unsigned)(u0 - k) * step);
-            const double ca = slot_or_get(wa[k], sl);
-            const double cp = slot_or_get(wp[k], sl + 1);
-            A = ca + cp * A;
-            P = cp * P;
+        __syncthreads();
+        if (tid < E) {
+          int u = (int)tt + 1;
+          for (int qq = 0; qq < Q && u <= hi && M != 0.0; ++qq, ++u) {
+            const double2 c = sh.lb[qq][e];
+            uint64_t* sl = comp + (base + (unsigned)u * step);
+            const double ca = slot_or_get(__builtin_bit_cast(uint64_t, c.x), sl);
+            const double cp = slot_or_get(__builtin_bit_cast(uint64_t, c.y), sl + 1);
+            S = S + M * ca;
+            M = prod_nz(M, cp);
           }
+          if (M != 0.0 && u <= hi) sh.rest = 1;
         }
+        __syncthreads();
+        lo = (int)tt + Q;
       }
-      sh.lb[q][e] = make_double2(A, P);
-      __syncthreads();
+      if (kStats || sh.rest) {
+        // (the window's words in sh.lb were read before the last barrier)
+        sh.lb[q][e] = fold_chunk(lo, hi, q, base, step);
+        __syncthreads();
+      }
       if (tid < E) {
-        double xc = rd > 0 ? slot_get(bnd + (size_t)(rd - 1) * a.N + col * E + e) : 0.0;
-        for (int qq = 0; qq < Q; ++qq) {
-          const double2 c = sh.lb[qq][e];
-          xc = c.x + c.y * xc;
+        double xc = 0.0;
+        if (kStats || sh.rest || M != 0.0) {
+          xc = rd > 0 ? slot_get(bnd + (size_t)(rd - 1) * a.N + col * E + e) : 0.0;
+          if (kStats || sh.rest)
+            for (int qq = 0; qq < Q; ++qq) {
+              const double2 c = sh.lb[qq][e];
+              xc = c.x + c.y * xc;
+            }
         }
-        sh.carry[e] = xc;
+        sh.carry[e] = kStats ? xc : S + M * xc;
       }
       __syncthreads();
     }
     RES_MARK(2);
+    if (rd == rounds - 1) publish_bad();
 
     // ---- 3. carry entering each of this thread's segments (one per env)
     double x[VW];
@@ -1959,6 +2035,53 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       RES_MARK(5);
     }
     lds_barrier();  // this round's LDS (composites, carries) is read before the next overwrites it
+  }
+  // (a workgroup without a tile in the last round publishes its flag here)
+  if (tile_tt(rounds - 1) < 0) publish_bad();
+  if constexpr (!kStats) {
+    // The look-back's walk stops at a zero factor product and skips the tiles
+    // beyond it, which is exact unless a skipped composite is not finite: the
+    // reference then carries 0 x inf (or 0 x NaN) = NaN into the tile, and
+    // every advantage and return of that env in the tile is NaN.  Once every
+    // workgroup has published whether its composites are all finite (they
+    // publish before their own look-back), a workgroup that sees any that are
+    // not folds every composite to the right of each of its tiles (all
+    // rounds, in chunks) and writes NaN over the envs whose carry is NaN.  The
+    // same threads wrote those elements, so the NaN is the value that stays.
+    int any = 0;
+    for (long u = tid; u < (long)gridDim.x; u += kResBlock)
+      any |= !(slot_get(part + (size_t)u * kResPartWords) == 0.0);
+    if (__syncthreads_or(any)) {
+      const int e = tid % E, q = tid / E;
+      const unsigned step = (unsigned)(nc * E * 2), base = (unsigned)((col * E + e) * 2);
+      for (long rd = 0; rd < rounds; ++rd) {
+        const long tt = tile_tt(rd);
+        if (tt < 0) break;
+        sh.lb[q][e] = fold_chunk((int)tt, (int)nt - 1, q, base, step);
+        __syncthreads();
+        if (tid < E) {
+          double xc = 0.0;
+          for (int qq = 0; qq < Q; ++qq) {
+            const double2 c = sh.lb[qq][e];
+            xc = c.x + c.y * xc;
+          }
+          sh.nanfl[e] = xc != xc;
+        }
+        __syncthreads();
+        const long t0r = tt * TS + (long)sg * L;
+        const int nvr = t0r >= a.T ? 0 : (a.T - t0r < L ? (int)(a.T - t0r) : L);
+        const float qnan = __builtin_nanf("");
+        for (int k = 0; k < VW; ++k) {
+          if (!sh.nanfl[g * VW + k]) continue;
+          for (int i = 0; i < nvr; ++i) {
+            const unsigned off = ((unsigned)(t0r + i) * n32 + (unsigned)(env0 + k)) * 4u;
+            *(float*)at_byte(a.adv, off) = qnan;
+            if (a.ret) *(float*)at_byte(a.ret, off) = qnan;
+          }
+        }
+        __syncthreads();
+      }
+    }
   }
 }
 
