@@ -673,10 +673,8 @@ NONFINITE_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("T,N,p,inf_last", NONFINITE_SHAPES)
-def test_gae_resident_no_norm_non_finite(dev, T, N, p, inf_last):
-    assert _route(T, N, False) == "resident"
-    r, v, d, lv = _inputs(T, N, p, seed=T % 977 + N)
+def _check_non_finite(dev, T, N, p, inf_last, seed):
+    r, v, d, lv = _inputs(T, N, p, seed=seed)
     v[T - 100, 0] = float("inf")
     v[T - 5000, 1] = float("-inf")
     v[T // 2 + T // 7, 2] = float("nan")
@@ -685,7 +683,6 @@ def test_gae_resident_no_norm_non_finite(dev, T, N, p, inf_last):
     r[T // 5, N - 1] = float("inf")
     if inf_last:
         lv[N // 2] = float("inf")
-    print(f"gae resident no-norm non-finite T={T} N={N} p={p} inf_last={inf_last}", flush=True)
     adv, ret, _ = _gae_abi(dev, r.to(dev), v.to(dev), d.to(dev), lv.to(dev), 0.99, 0.95)
     a_ref, _ = ref.gae_c(r.numpy(), v.numpy(), d.numpy(), lv.numpy(), 0.99, 0.95)
     got = adv.cpu().numpy()
@@ -697,6 +694,28 @@ def test_gae_resident_no_norm_non_finite(dev, T, N, p, inf_last):
     assert_gae_close(got[fin], a_ref[fin])
     ret_ref = got + v.numpy()
     np.testing.assert_array_equal(np.isnan(ret.cpu().numpy()), np.isnan(ret_ref))
+
+
+@pytest.mark.parametrize("T,N,p,inf_last", NONFINITE_SHAPES)
+def test_gae_resident_no_norm_non_finite(dev, T, N, p, inf_last):
+    assert _route(T, N, False) == "resident"
+    print(f"gae resident no-norm non-finite T={T} N={N} p={p} inf_last={inf_last}", flush=True)
+    _check_non_finite(dev, T, N, p, inf_last, seed=T % 977 + N)
+
+
+# The same on the other routes (resident pass off): carries composed over
+# many tiles or spans without a done must keep an infinity as inf.
+@pytest.mark.parametrize("T,N,p,route", [
+    (1 << 17, 16, 0.0, "span"),
+    (1 << 17, 16, 0.001, "span"),
+    (100_000, 64, 0.0, "tiles"),
+    (20_000, 100, 0.002, "tiles"),
+    (16_384, 2048, 0.0, "strip"),
+])
+def test_gae_other_routes_non_finite(no_resident, dev, T, N, p, route):
+    assert _route(T, N, False) == route
+    print(f"gae {route} non-finite T={T} N={N} p={p}", flush=True)
+    _check_non_finite(dev, T, N, p, True, seed=T % 991 + N)
 
 
 def test_discounted_returns_resident_rounds(dev):

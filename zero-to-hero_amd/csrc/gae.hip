@@ -734,6 +734,24 @@ __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
 
 // Reverse inclusive scan over the Rw thread-rows of (ga, gp) in LDS; returns
 // with s_a/s_p holding, for row g, the composite of rows g..Rw-1.
+// The product of two tiles' factor products, kept nonzero when neither is
+// zero.  In the reference's serial recurrence an infinite advantage becomes
+// NaN only by a zero factor (a done flag, or gamma * lambda = 0): it is
+// multiplied by gamma * lambda once per step and never underflows.  Products
+// composed over many tiles do underflow, and 0 x inf would then give NaN where
+// the reference keeps the infinity; the smallest subnormal in place of such a
+// zero keeps the infinity and changes no finite carry (its terms lie far below
+// an ulp).  Used where tiles (spans, chunks) are composed: the carry scan, the
+// span chain and the resident pass's look-back.  Inside a tile the products
+// are plain (measured on the resident pass: 0.5-1.5 us per config-3 call on
+// its critical path), so a tile's own product (gamma * lambda)^steps must not
+// underflow for this to hold: gamma * lambda > 2^(-1074 / steps per tile),
+// e.g. 0.70 for the resident pass's 2048-step tiles of 16 envs.
+__device__ __forceinline__ double prod_nz(double x, double y) {
+  const double p = x * y;
+  return (p == 0.0 && x != 0.0 && y != 0.0) ? __builtin_copysign(4.9406564584124654e-324, p) : p;
+}
+
 __device__ __forceinline__ void carry_row_scan(double* s_a, double* s_p, int tid, int g, int Ew,
                                                int Rw, double ga, double gp) {
   s_a[tid] = ga;
@@ -749,7 +767,7 @@ __device__ __forceinline__ void carry_row_scan(double* s_a, double* s_p, int tid
     __syncthreads();
     if (has) {
       ga = ga + gp * pa;
-      gp = gp * pp;
+      gp = prod_nz(gp, pp);
       s_a[tid] = ga;
       s_p[tid] = gp;
     }
@@ -811,7 +829,7 @@ __global__ void __launch_bounds__(kCarryBlock) gae_carry_kernel(const double2* _
 #pragma unroll
   for (int j = kCarryG - 1; j >= 0; --j) {
     ga = ta[j] + tp[j] * ga;
-    gp = tp[j] * gp;
+    gp = prod_nz(tp[j], gp);
   }
   carry_row_scan(s_a, s_p, tid, g, Ew, Rw, ga, gp);
   if constexpr (kCompose) {
@@ -1303,7 +1321,7 @@ __global__ void __launch_bounds__(kSpanThreads) gae_span_sum_kernel(GaeArgs a) {
     if (tid < E) {
       const double2 t = span_tile_composite<E>(sh, e);
       A = t.x + t.y * A;
-      P = t.y * P;
+      P = prod_nz(t.y, P);
     }
   }
   if (tid < E) a.summary[sp.span * a.N + col0 + e] = make_double2(A, P);
@@ -1487,23 +1505,6 @@ __device__ uint64_t g_res_trace[4096 * 32];
 #else
 #define RES_MARK(k)
 #endif
-
-// The product of two tiles' factor products, kept nonzero when neither is
-// zero.  In the reference's serial recurrence an infinite advantage becomes
-// NaN only by a zero factor (a done flag, or gamma * lambda = 0): it is
-// multiplied by gamma * lambda once per step and never underflows.  Products
-// composed over many tiles do underflow, and 0 x inf would then give NaN where
-// the reference keeps the infinity; the smallest subnormal in place of such a
-// zero keeps the infinity and changes no finite carry (its terms lie far below
-// an ulp).  Used where tiles are composed (the look-back); inside a tile the
-// products are plain (measured: 0.5-1.5 us per config-3 call on the critical
-// path), so a tile's own product (gamma * lambda)^steps must not underflow for
-// this to hold: gamma * lambda > 2^(-1074 / steps per tile), 0.70 for the
-// 2048-step tiles of 16 envs.
-__device__ __forceinline__ double prod_nz(double x, double y) {
-  const double p = x * y;
-  return (p == 0.0 && x != 0.0 && y != 0.0) ? __builtin_copysign(4.9406564584124654e-324, p) : p;
-}
 
 template <int E>
 struct ResShared {
