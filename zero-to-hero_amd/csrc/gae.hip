@@ -1479,7 +1479,10 @@ int launch_span(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
 //   2. a tile publishes its per-env composite; the advantage entering it is
 //      the fold of the composites of the tiles to its right in the same env
 //      column, read in parallel (one composite per thread) and folded in
-//      order from the horizon's end.
+//      order from the horizon's end.  Without the normaliser the fold is
+//      walked from the nearest tile and stops at a zero factor product (a
+//      done flag); a tile skipped that way whose composite is not finite is
+//      found after the stores, and the tiles it makes NaN are rewritten.
 //   3. with the normaliser, the workgroup publishes (n, sum, sum of squares)
 //      of its advantages at once: step 1 also summed each step's suffix
 //      composite (a_t, P_t) and their products, and the advantage at step t
