@@ -841,3 +841,21 @@ def test_gae_hyperparameter_edges(dev, monkeypatch, T, N, resident, gamma, lam):
         # (the carries between segments are composed in another order than
         # the serial sum, so <= 1 fp32 ulp as against the oracle)
         assert_gae_close(got, np.cumsum(r64[::-1], axis=0)[::-1])
+
+
+@pytest.mark.parametrize("T,N", [(0, 8), (5, 0), (0, 0)])
+def test_empty_rollouts(dev, T, N):
+    """Empty rollouts give empty outputs without a launch; the fused
+    normaliser's statistics of no elements are NaN, as torch's mean/std of an
+    empty tensor."""
+    r = torch.empty(T, N, device=dev)
+    v = torch.empty(T, N, device=dev)
+    d = torch.empty(T, N, dtype=torch.uint8, device=dev)
+    lv = torch.empty(N, device=dev)
+    adv, ret = ppo_amd.gae(r, v, d, lv)
+    assert adv.shape == (T, N) and ret.shape == (T, N)
+    adv, ret, adv_n, stats = ppo_amd.gae_normalize(r, v, d, lv, return_stats=True)
+    assert adv_n.shape == (T, N)
+    assert torch.isnan(stats).all()
+    assert ppo_amd.normalize_advantages(adv).shape == (T, N)
+    assert ppo_amd.discounted_returns(r, dones=d).shape == (T, N)

@@ -225,7 +225,9 @@ def gae_normalize(
     device, T, N = _gae_inputs(rewards, values, dones, last_value)
     adv, ret, adv_n = _outputs(out, 3, rewards, (rewards, values, dones, last_value))
     stats = torch.empty(2, dtype=torch.float32, device=device)
-    if T * N > 0:
+    if T * N == 0:
+        stats.fill_(float("nan"))  # torch's mean and std of no elements
+    else:
         stream = _stream(device)
         nbytes = _lib.load().ppo_gae_workspace_bytes(T, N)
         ws = _WORKSPACES.get(device, stream, nbytes)
