@@ -45,6 +45,7 @@ extern "C" {
 #define PPO_ERR_WORKSPACE 2       /* workspace missing or smaller than required */
 #define PPO_ERR_TOO_LARGE 3       /* size beyond what the kernels index (2^31 rows) */
 #define PPO_ERR_UNSUPPORTED 4     /* shape or option the kernels do not implement   */
+#define PPO_ERR_WAIT_TIMEOUT 5    /* a bounded in-kernel wait gave up (ppo_wait_status) */
 #define PPO_ERR_HIP_BASE 1000     /* + hipError_t */
 
 /* Library version, as MAJOR*10000 + MINOR*100 + PATCH. */
@@ -52,6 +53,39 @@ int ppo_amd_version(void);
 
 /* Human-readable text for a return code (static storage). */
 const char* ppo_amd_strerror(int code);
+
+/*
+ * Status of the bounded in-kernel waits (no counterpart in the reference: its
+ * update runs on the CPU in one thread).  Three launches hold workgroups that
+ * wait for one another inside the launch: the resident GAE pass
+ * (ppo_gae_f32 / ppo_gae_norm_f32, PPO_GAE_ROUTE_RESIDENT), the Gaussian loss
+ * with its in-kernel finish (ppo_loss_gauss_f32), and the fused gradient
+ * reduction + clip + Adam of ppo_mlp_cat_step_f32.  Each is launched only when
+ * the occupancy query says its whole grid fits on the device at once; that
+ * query assumes the device's compute units are free.  When another process
+ * or stream keeps part of the grid from running, a wait gives up after its
+ * poll limit instead of hanging; the workgroup then writes NaN over its GAE
+ * outputs or loss scalars, or leaves its share of the parameters, moments,
+ * gradients and step counter unwritten, and raises a status word kept per
+ * device by the library.
+ *
+ * ppo_wait_status enqueues a read of that word on `stream`, synchronises the
+ * stream, clears the word and returns PPO_ERR_WAIT_TIMEOUT if any wait on the
+ * current device gave up since the previous call (on any stream), PPO_OK
+ * otherwise.  It is a host synchronisation point, for callers to place where
+ * they already synchronise (the Python layer checks once per update).
+ * PPO_AMD_GAE_RESIDENT=0, PPO_AMD_GAUSS_FINISH=0 and PPO_AMD_MLP_FUSED_ADAM=0
+ * select launches without in-kernel waits, for callers that share the GPU.
+ */
+int ppo_wait_status(void* stream);
+
+/*
+ * Poll limit of every bounded wait launched after this call (process-wide;
+ * tests and diagnostics).  0 makes every wait give up at once, so that the
+ * failure path can be exercised with every kernel still exiting normally; a
+ * negative value restores the default (2^22 polls).
+ */
+int ppo_set_wait_limit(int64_t polls);
 
 /* ------------------------------------------------------------------------ */
 /* GAE — generalized advantage estimation over a [T,N] rollout.             */

@@ -24,7 +24,7 @@ def declared_functions():
 def test_header_declares_expected_functions():
     names = declared_functions()
     assert "ppo_gae_f32" in names and "ppo_loss_cat_f32" in names
-    assert len(names) == 26
+    assert len(names) == 28
 
 
 def test_library_exports_every_declared_symbol():
@@ -46,7 +46,7 @@ def test_nm_shows_c_linkage():
 
 def test_version_and_strerror():
     lib = _lib.load()
-    assert lib.ppo_amd_version() == 100
+    assert lib.ppo_amd_version() == 200
     assert lib.ppo_amd_strerror(0) == b"ok"
     assert b"workspace" in lib.ppo_amd_strerror(2)
     assert lib.ppo_amd_strerror(12345) != b""

@@ -76,6 +76,7 @@ struct GaeArgs {
   unsigned nonce;      // resident pass: tag of this call in the barrier counter
   long res_nc, res_nt; // resident pass: env columns, time tiles
   long res_ntr, res_rounds;  // resident pass: time tiles per round, rounds
+  WaitCtl wc;          // resident pass: poll limit and the device's wait-status word
 };
 
 // What a gae_tile_kernel launch computes.
@@ -1500,11 +1501,15 @@ int launch_span(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
 // runs while its consumers wait.
 constexpr int kResWaves = kResBlock / kWave;
 #ifdef PPO_GAE_RES_TRACE
-// Phase timestamps of the resident pass (wall clock, 100 MHz), one row of 32
-// per workgroup (6 marks per round): a measurement build only.
-__device__ uint64_t g_res_trace[4096 * 32];
-#define RES_MARK(k) \
-  if (threadIdx.x == 0) g_res_trace[blockIdx.x * 32 + (k) + 6 * res_round] = wall_clock64()
+// Phase timestamps of the resident pass (wall clock, 100 MHz), one row of
+// kResTraceRow words per workgroup (6 marks per round): a measurement build
+// only.
+constexpr int kResTraceRow = 64;
+static_assert(6 * kResMaxRounds <= kResTraceRow, "a trace row holds every round's marks");
+__device__ uint64_t g_res_trace[4096 * kResTraceRow];
+#define RES_MARK(k)                                                                   \
+  if (threadIdx.x == 0)                                                               \
+  g_res_trace[blockIdx.x * kResTraceRow + (k) + 6 * res_round] = wall_clock64()
 #else
 #define RES_MARK(k)
 #endif
@@ -1554,6 +1559,7 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
   uint64_t* bnd = comp + (size_t)nt * nc * 2 * E;    // [rounds][N]
   uint64_t* part = bnd + (size_t)rounds * a.N;       // [grid][kResPartWords]
   auto tile_tt = [&](long rd) { return nt - 1 - (rd * ntr + tl); };  // < 0: no tile
+  int fail = 0;  // one of this thread's bounded waits gave up
   // The composite of chunk q (of Q) of tiles lo + 1 .. hi for env e, folded
   // from the right, LB slot pairs in flight; `base`/`step` address the slot
   // pair of tile u for env e: word offset ((u * nc + col) * E + e) * 2.
@@ -1577,8 +1583,8 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       for (int k = 0; k < LB; ++k) {
         if (u0 - k >= u_lo) {
           uint64_t* sl = comp + (base + (unsigned)(u0 - k) * step);
-          const double ca = slot_or_get(wa[k], sl);
-          const double cp = slot_or_get(wp[k], sl + 1);
+          const double ca = slot_or_get(wa[k], sl, a.wc.spin, fail);
+          const double cp = slot_or_get(wp[k], sl + 1, a.wc.spin, fail);
           A = ca + cp * A;
           P = prod_nz(cp, P);
         }
@@ -1776,7 +1782,7 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
     }
     // the start barrier (once): every workgroup's slots are empty by now
     if (rd == 0 && tid == 0) {
-      res_wait(ctr, s_tag, gridDim.x);
+      if (!res_wait(ctr, s_tag, gridDim.x, a.wc.spin)) fail = 1;
       if (blockIdx.x == 0) epoch_advance(&a.hdr->epoch, s_epoch);
     }
     __syncthreads();
@@ -1816,8 +1822,9 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
           for (int qq = 0; qq < Q && u <= hi && M != 0.0; ++qq, ++u) {
             const double2 c = sh.lb[qq][e];
             uint64_t* sl = comp + (base + (unsigned)u * step);
-            const double ca = slot_or_get(__builtin_bit_cast(uint64_t, c.x), sl);
-            const double cp = slot_or_get(__builtin_bit_cast(uint64_t, c.y), sl + 1);
+            const double ca = slot_or_get(__builtin_bit_cast(uint64_t, c.x), sl, a.wc.spin, fail);
+            const double cp =
+                slot_or_get(__builtin_bit_cast(uint64_t, c.y), sl + 1, a.wc.spin, fail);
             S = S + M * ca;
             M = prod_nz(M, cp);
           }
@@ -1834,7 +1841,8 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
       if (tid < E) {
         double xc = 0.0;
         if (kStats || sh.rest || M != 0.0) {
-          xc = rd > 0 ? slot_get(bnd + (size_t)(rd - 1) * a.N + col * E + e) : 0.0;
+          xc = rd > 0 ? slot_get(bnd + (size_t)(rd - 1) * a.N + col * E + e, a.wc.spin, fail)
+                      : 0.0;
           if (kStats || sh.rest)
             for (int qq = 0; qq < Q; ++qq) {
               const double2 c = sh.lb[qq][e];
@@ -1956,9 +1964,9 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
         double tot[3] = {0.0, 0.0, 0.0};
         for (long u = tid; u < (long)gridDim.x; u += kResBlock) {
           uint64_t* pp = part + (size_t)u * kResPartWords;
-          tot[0] += slot_get(pp + 0);
-          tot[1] += slot_get(pp + 1);
-          tot[2] += slot_get(pp + 2);
+          tot[0] += slot_get(pp + 0, a.wc.spin, fail);
+          tot[1] += slot_get(pp + 1, a.wc.spin, fail);
+          tot[2] += slot_get(pp + 2, a.wc.spin, fail);
         }
         block_sum_lds<3>(tot);
         if (tid == 0) {
@@ -1992,7 +2000,7 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
           if (tid == 0) slot_put(part + (size_t)blockIdx.x * kResPartWords + 3, c[0]);
           double t2[1] = {0.0};
           for (long u = tid; u < (long)gridDim.x; u += kResBlock)
-            t2[0] += slot_get(part + (size_t)u * kResPartWords + 3);
+            t2[0] += slot_get(part + (size_t)u * kResPartWords + 3, a.wc.spin, fail);
           block_sum_lds<1>(t2);
           if (tid == 0) sh.m2 = t2[0];
         }
@@ -2054,7 +2062,7 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
     // same threads wrote those elements, so the NaN is the value that stays.
     int any = 0;
     for (long u = tid; u < (long)gridDim.x; u += kResBlock)
-      any |= !(slot_get(part + (size_t)u * kResPartWords) == 0.0);
+      any |= !(slot_get(part + (size_t)u * kResPartWords, a.wc.spin, fail) == 0.0);
     if (__syncthreads_or(any)) {
       const int e = tid % E, q = tid / E;
       const unsigned step = (unsigned)(nc * E * 2), base = (unsigned)((col * E + e) * 2);
@@ -2085,6 +2093,27 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
         }
         __syncthreads();
       }
+    }
+  }
+  // A wait that gave up (grid not co-resident) may have read slots another
+  // workgroup had not yet emptied or filled: this workgroup writes NaN over
+  // every output element it wrote (its own threads' elements, so the NaN is
+  // the value that stays) and raises the device's wait-status word.
+  if (__syncthreads_or(fail)) {
+    if (tid == 0) wait_report(a.wc.status);
+    const float qnan = __builtin_nanf("");
+    for (long rd = 0; rd < rounds; ++rd) {
+      const long tt = tile_tt(rd);
+      if (tt < 0) break;
+      const long t0r = tt * TS + (long)sg * L;
+      const int nvr = t0r >= a.T ? 0 : (a.T - t0r < L ? (int)(a.T - t0r) : L);
+      for (int i = 0; i < nvr; ++i)
+        for (int k = 0; k < VW; ++k) {
+          const unsigned off = ((unsigned)(t0r + i) * n32 + (unsigned)(env0 + k)) * 4u;
+          *(float*)at_byte(a.adv, off) = qnan;
+          if (a.ret) *(float*)at_byte(a.ret, off) = qnan;
+          if constexpr (kStats) *(float*)at_byte(a.adv_n, off) = qnan;
+        }
     }
   }
 }
@@ -2139,6 +2168,8 @@ int launch_resident(long T, long N, GaeArgs a, bool norm, hipStream_t stream) {
   a.res_ntr = rp.ntr;
   a.res_rounds = rp.rounds;
   a.nonce = next_nonce();
+  int st = wait_ctl(a.wc);
+  if (st) return st;
   void* args[] = {&a};
   return hip_status(
       hipLaunchKernel(kern, dim3((unsigned)rp.grid()), dim3(kResBlock), args, 0, stream));

@@ -19,7 +19,18 @@
 namespace ppo {
 
 constexpr uint64_t kSlotTag = 0x7FF4A5A55A5A0F0FULL;  // a signalling-NaN pattern
-constexpr long kSlotSpin = 1L << 22;                  // polls before giving up
+constexpr long kSlotSpin = 1L << 22;                  // polls before giving up (default)
+
+// Bounded-wait control of one launch: the poll limit of every wait and the
+// current device's wait-status word (library-owned, see wait_ctl).
+struct WaitCtl {
+  unsigned* status;
+  long spin;
+};
+
+// Host: fills `w` for a launch on the current device (abi.hip).  Returns a
+// PPO code.
+int wait_ctl(WaitCtl& w);
 // The start barrier counts arrivals on kSyncCounters counters, kSyncStride
 // words (256 bytes) apart: atomics on one address are serialised by the
 // memory (measured ~35 ns each on MI355X, so 1024 arrivals on one counter
@@ -42,18 +53,26 @@ __device__ __forceinline__ uint64_t slot_peek(uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ double slot_get(uint64_t* p) {
-  for (long it = 0; it < kSlotSpin; ++it) {
+// Polls slot `p` up to `spin` times; a slot still empty then reads as NaN
+// and sets `fail` (spin 0: gives up at once).
+__device__ __forceinline__ double slot_get(uint64_t* p, long spin, int& fail) {
+  for (long it = 0; it < spin; ++it) {
     const uint64_t w = slot_peek(p);
     if (w != 0) return slot_value(w);
     __builtin_amdgcn_s_sleep(1);
   }
+  fail = 1;
   return __builtin_nan("");
 }
 
 // A word already read (w) or, when it was still empty, the polled value.
-__device__ __forceinline__ double slot_or_get(uint64_t w, uint64_t* p) {
-  return w ? slot_value(w) : slot_get(p);
+__device__ __forceinline__ double slot_or_get(uint64_t w, uint64_t* p, long spin, int& fail) {
+  return w ? slot_value(w) : slot_get(p, spin, fail);
+}
+
+// Raises the device's wait-status word (one vector atomic; failure path only).
+__device__ __forceinline__ void wait_report(unsigned* status) {
+  __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void slot_clear(uint64_t* p) {
@@ -82,11 +101,11 @@ __device__ inline void res_arrive(uint64_t* ctr, uint64_t v, unsigned nonce, uns
   __hip_atomic_fetch_add(ctr, (uint64_t)1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Waits (bounded) until every counter of the barrier at `sync` is complete.
-// (All counters are read together, so a complete barrier costs one round
-// trip.)
-__device__ inline void res_wait(uint64_t* sync, unsigned nonce, unsigned nblocks) {
-  for (long it = 0; it < kSlotSpin; ++it) {
+// Waits (at most `spin` polls) until every counter of the barrier at `sync`
+// is complete; false when it gave up.  (All counters are read together, so a
+// complete barrier costs one round trip.)
+__device__ inline bool res_wait(uint64_t* sync, unsigned nonce, unsigned nblocks, long spin) {
+  for (long it = 0; it < spin; ++it) {
     uint64_t v[kSyncCounters];
 #pragma unroll
     for (int i = 0; i < kSyncCounters; ++i) v[i] = slot_peek(sync + i * kSyncStride);
@@ -95,9 +114,10 @@ __device__ inline void res_wait(uint64_t* sync, unsigned nonce, unsigned nblocks
     for (int i = 0; i < kSyncCounters; ++i)
       done = done && (i >= (int)nblocks ||
                       ((v[i] >> 32) == nonce && (unsigned)v[i] >= sync_share(i, nblocks)));
-    if (done) return;
+    if (done) return true;
     __builtin_amdgcn_s_sleep(1);
   }
+  return false;
 }
 
 // Called by wave 0 of every workgroup at its start: empties the `n` slots at

@@ -72,6 +72,8 @@ struct LossArgs {
   double* partial;
   uint64_t* epoch;  // Gaussian: the workspace header's call counter
   int tag_slot;     // Gaussian: partial slot holding each workgroup's arrival tag
+  int finish;       // Gaussian: 1 = collect in-kernel, 0 = loss_gauss_finish_kernel does
+  WaitCtl wc;       // Gaussian in-kernel finish: poll limit, the device's wait-status word
 };
 
 // Streamed arrays are touched once: nontemporal loads/stores keep them from
@@ -267,9 +269,9 @@ __device__ __forceinline__ uint64_t loss_tag(uint64_t epoch) {
 // (K = 5: the loss sums; K = 1: one dlog_std column); the totals end in
 // every lane of wave 0.
 template <int K>
-__device__ void collect_slots(const LossArgs& a, int slot0, uint64_t tag, double (&tot)[K]) {
+__device__ void collect_slots(const LossArgs& a, long nb, int slot0, uint64_t tag,
+                              double (&tot)[K]) {
   constexpr int kPer = 4;  // blocks a thread polls and loads together
-  const long nb = gridDim.x;
   const uint64_t* part = reinterpret_cast<const uint64_t*>(a.partial);
   const uint64_t* tags = part + (long)a.tag_slot * nb;
 #pragma unroll
@@ -277,6 +279,10 @@ __device__ void collect_slots(const LossArgs& a, int slot0, uint64_t tag, double
   bool ok = true;
   for (long b0 = threadIdx.x; b0 < nb; b0 += kPer * kBlock) {
     for (long it = 0;; ++it) {
+      if (it >= a.wc.spin) {
+        ok = false;
+        break;
+      }
       uint64_t w[kPer];
 #pragma unroll
       for (int h = 0; h < kPer; ++h) {
@@ -287,10 +293,6 @@ __device__ void collect_slots(const LossArgs& a, int slot0, uint64_t tag, double
 #pragma unroll
       for (int h = 0; h < kPer; ++h) all = all && w[h] == tag;
       if (all) break;
-      if (it >= kSlotSpin) {
-        ok = false;
-        break;
-      }
       __builtin_amdgcn_s_sleep(1);
     }
     // every load issued before any is consumed (blocks past the grid
@@ -313,46 +315,40 @@ __device__ void collect_slots(const LossArgs& a, int slot0, uint64_t tag, double
   if (!ok) {
 #pragma unroll
     for (int k = 0; k < K; ++k) tot[k] = __builtin_nan("");
+    wait_report(a.wc.status);
   }
   block_sum<K>(tot);
 }
 
+// Collector `b` of `ncoll` sums the slot groups it owns over the `nb`
+// publishing workgroups, all tagged loss_tag(epn): groups 1 + d (dlog_std
+// column d) go round-robin from collector 1, and collector 0 takes the
+// groups left over and then group 0, the loss sums, forms the scalars and
+// stores epn as the call counter.
 template <int MAXD>
-__device__ void loss_publish(const LossArgs& a) {
-  __shared__ uint64_t s_ep;
+__device__ void loss_collect(const LossArgs& a, long nb, uint64_t epn, long b, long ncoll) {
   __shared__ float s_hterm[MAXD > 0 ? MAXD : 1];
   const int tid = threadIdx.x;
-  const long nb = gridDim.x;
-  uint64_t ep = 0;
-  if (tid == 0) ep = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial stores are complete
-  __syncthreads();
-  if (tid == 0) {
-    uint64_t* tags = reinterpret_cast<uint64_t*>(a.partial) + (long)a.tag_slot * nb;
-    __hip_atomic_store(tags + blockIdx.x, loss_tag(ep + 1), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    s_ep = ep + 1;
-  }
   const int D = MAXD > 0 ? a.A : 0;
-  if ((long)blockIdx.x > (long)D) return;  // no slot group here
-  if (blockIdx.x == 0 && MAXD > 0 && tid < D) {
+  if (b > (long)D) return;  // no slot group here
+  if (b == 0 && MAXD > 0 && tid < D) {
     // Gaussian entropy term per dim, summed in dim order below
     const float kEntConst = 1.41893853320467274178f;  // 0.5 + 0.5*log(2*pi)
     s_hterm[tid] = kEntConst + logf(expf(a.log_std[tid]));
   }
   __syncthreads();
-  const uint64_t epn = s_ep, tag = loss_tag(epn);
+  const uint64_t tag = loss_tag(epn);
   if (MAXD > 0) {
-    for (long grp = (long)blockIdx.x + (blockIdx.x == 0 ? nb : 0); grp <= D; grp += nb) {
+    for (long grp = b + (b == 0 ? ncoll : 0); grp <= D; grp += ncoll) {
       if (grp == 0) continue;
       double col[1];
-      collect_slots<1>(a, kLossSums + (int)grp - 1, tag, col);
+      collect_slots<1>(a, nb, kLossSums + (int)grp - 1, tag, col);
       if (tid == 0) a.dlog_std[grp - 1] = (float)col[0] - a.ec;
     }
   }
-  if (blockIdx.x != 0) return;
+  if (b != 0) return;
   double tot[kLossSums];
-  collect_slots<kLossSums>(a, 0, tag, tot);
+  collect_slots<kLossSums>(a, nb, 0, tag, tot);
   if (tid == 0) {
     float ent;
     if (MAXD > 0) {
@@ -374,6 +370,39 @@ __device__ void loss_publish(const LossArgs& a) {
     a.scalars[PPO_SCALAR_LOSS] = (pol + a.vc * vl) - a.ec * ent;
     __hip_atomic_store(a.epoch, epn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+template <int MAXD>
+__device__ void loss_publish(const LossArgs& a) {
+  __shared__ uint64_t s_ep;
+  const int tid = threadIdx.x;
+  const long nb = gridDim.x;
+  uint64_t ep = 0;
+  if (tid == 0) ep = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial stores are complete
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t* tags = reinterpret_cast<uint64_t*>(a.partial) + (long)a.tag_slot * nb;
+    __hip_atomic_store(tags + blockIdx.x, loss_tag(ep + 1), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    s_ep = ep + 1;
+  }
+  if (!a.finish) return;  // (loss_gauss_finish_kernel collects after the launch)
+  __syncthreads();
+  loss_collect<MAXD>(a, nb, s_ep, blockIdx.x, nb);
+}
+
+// The Gaussian finish as a launch of its own, for grids whose co-residency
+// the host could not establish: one workgroup collects every slot group of
+// the `nb` workgroups of the loss launch before it, whose tags are complete
+// by then (the waits find them at the first poll).
+template <int MAXD>
+__global__ void __launch_bounds__(kBlock) loss_gauss_finish_kernel(LossArgs a, long nb) {
+  __shared__ uint64_t s_ep;
+  if (threadIdx.x == 0)
+    s_ep = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+  __syncthreads();
+  loss_collect<MAXD>(a, nb, s_ep, 0, 1);
 }
 
 // Action index of a row, or -1 when it lies outside [0, A).
@@ -1476,10 +1505,24 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
   } else {
     kern = (const void*)loss_gauss_kernel<false>;
   }
-  blocks = std::min(blocks, resident_blocks(kern, kBlock, lds_used, blocks));
+  // The in-kernel finish needs the whole grid resident at once: the grid is
+  // capped at the occupancy query's answer.  When the runtime cannot answer
+  // (or PPO_AMD_GAUSS_FINISH=0 is set, for callers that share the GPU), the
+  // workgroups only publish and a one-workgroup launch collects after them.
+  const long resident = resident_blocks(kern, kBlock, lds_used, 0);
+  const char* env = getenv("PPO_AMD_GAUSS_FINISH");
+  a.finish = resident > 0 && !(env && env[0] == '0');
+  if (a.finish) {
+    blocks = std::min(blocks, resident);
+    if ((st = wait_ctl(a.wc))) return st;
+  }
   void* args[] = {&a, const_cast<long*>(wave_tiles ? &wfull : &tiles)};
   if ((st = hip_status(
            hipLaunchKernel(kern, grid_of(blocks), dim3(kBlock), args, lds_used, stream))))
     return st;
-  return PPO_OK;
+  if (a.finish) return PPO_OK;
+  if ((st = wait_ctl(a.wc))) return st;
+  hipLaunchKernelGGL(loss_gauss_finish_kernel<kMaxGaussDim>, dim3(1), dim3(kBlock), 0, stream, a,
+                     blocks);
+  return last_launch_status();
 }

@@ -781,6 +781,7 @@ struct MlpAdamArgs {
   uint64_t* sq;    // per reduction workgroup: its sum-of-squares slot
   uint64_t* epoch; // the workspace header's call counter (launch_tag)
   unsigned nonce;
+  WaitCtl wc;      // poll limit and the device's wait-status word
 };
 
 template <int kWaves, int kRedLoads>
@@ -855,19 +856,38 @@ __global__ void __launch_bounds__(kWaves * kWave) mlp_reduce_adam_kernel(MlpArgs
       a.scalars[PPO_SCALAR_LOSS] = (pol + a.vc * vl) - a.ec * ent;
     }
   }
+  // A wait that gives up (grid not co-resident) may leave slots unread or
+  // read before their owner emptied them: this workgroup then writes none of
+  // its parameters, moments or gradients (and workgroup 0 neither the step
+  // counter; the norm output reads NaN), and raises the wait-status word.
+  int fail = 0;
   if (threadIdx.x == 0) {
-    res_wait(u.sync, tag, gridDim.x);
+    if (!res_wait(u.sync, tag, gridDim.x, u.wc.spin)) fail = 1;
     if (blk == 0) epoch_advance(u.epoch, epoch);
   }
-  __syncthreads();
-  if (blk == 0 && threadIdx.x == 0 && a.step_counter) *a.step_counter = step0 + 1;
+  // (after the barrier every workgroup has arrived and emptied its slot)
+  if (__syncthreads_or(fail)) {
+    if (threadIdx.x == 0) {
+      wait_report(u.wc.status);
+      if (blk == 0 && u.norm_out) *u.norm_out = __builtin_nanf("");
+    }
+    return;
+  }
   for (int kk = w; kk < kMlpTensors; kk += kWaves) {
     double acc = 0.0;
-    for (long c = a.tblk[kk] + lane; c < a.tblk[kk + 1]; c += kWave) acc += slot_get(u.sq + c);
+    for (long c = a.tblk[kk] + lane; c < a.tblk[kk + 1]; c += kWave)
+      acc += slot_get(u.sq + c, u.wc.spin, fail);
     const double sk = wave_sum(acc);
     if (lane == 0) s_norm[kk] = (float)sqrt(sk);
   }
-  __syncthreads();
+  if (__syncthreads_or(fail)) {
+    if (threadIdx.x == 0) {
+      wait_report(u.wc.status);
+      if (blk == 0 && u.norm_out) *u.norm_out = __builtin_nanf("");
+    }
+    return;
+  }
+  if (blk == 0 && threadIdx.x == 0 && a.step_counter) *a.step_counter = step0 + 1;
   if (threadIdx.x == 0) {
     float norm;
     s_coef = adam_coef_from_norms(u.s, s_norm, kMlpTensors, norm);
@@ -1162,6 +1182,7 @@ extern "C" int ppo_mlp_cat_step_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
     u.sq = reinterpret_cast<uint64_t*>(a.sqpart);
     u.epoch = &reinterpret_cast<WsHeader*>(workspace)->epoch;
     u.nonce = next_nonce();
+    if ((st = wait_ctl(u.wc))) return st;
     void* gargs[] = {&a};
     if ((st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(kMlpBlock),
                                          gargs, 0, stream))))

@@ -60,6 +60,7 @@ GAE_ROUTES = {0: "none", 1: "resident", 2: "strip", 3: "span", 4: "tiles"}
 PPO_ACT_RELU = 0
 PPO_ACT_TANH = 1
 PPO_ERR_UNSUPPORTED = 4
+PPO_ERR_WAIT_TIMEOUT = 5
 
 GATHER_MAX_ARRAYS = 8
 ADAM_MAX_TENSORS = 32
@@ -75,6 +76,8 @@ _int = ctypes.c_int
 SIGNATURES = {
     "ppo_amd_version": (_int, []),
     "ppo_amd_strerror": (ctypes.c_char_p, [_int]),
+    "ppo_wait_status": (_int, [_vp]),
+    "ppo_set_wait_limit": (_int, [_i64]),
     "ppo_gae_workspace_bytes": (_sz, [_i64, _i64]),
     "ppo_gae_route": (_int, [_i64, _i64, _int, _int]),
     "ppo_gae_f32": (

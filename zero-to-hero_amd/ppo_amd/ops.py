@@ -40,6 +40,8 @@ __all__ = [
     "ppo_mlp_cat_grads",
     "mlp_act_categorical",
     "mlp_fusable",
+    "check_waits",
+    "set_wait_limit",
     "LossStats",
 ]
 
@@ -110,6 +112,28 @@ def _call(name: str, device: torch.device, stream: int, *args) -> None:
     if code != _lib.PPO_OK:
         _WORKSPACES.drop(device, stream)
         _lib.check(name, code)
+
+
+def check_waits(device: Optional[torch.device] = None) -> None:
+    """Synchronises torch's current stream on `device` (default: the current
+    device) and raises PPOLibraryError with code PPO_ERR_WAIT_TIMEOUT if a
+    bounded in-kernel wait on that device gave up since the last check (on
+    any stream).  The launches with such waits (the resident GAE pass, the
+    Gaussian loss's in-kernel finish, the fused clip + Adam of
+    ppo_mlp_cat_step) assume their whole grid runs at once; when another
+    process or stream on the GPU prevents that, the affected outputs are NaN
+    or the affected parameters unwritten, and this check reports it.
+    VecPPO.update and PPOAgent._update call it once per update."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    with torch.cuda.device(device):
+        _lib.check("ppo_wait_status", _lib.load().ppo_wait_status(_stream(device)))
+
+
+def set_wait_limit(polls: Optional[int]) -> None:
+    """Poll limit of the bounded in-kernel waits launched from now on
+    (process-wide): 0 makes every wait give up at once (tests of the failure
+    path), None restores the default."""
+    _lib.load().ppo_set_wait_limit(-1 if polls is None else int(polls))
 
 
 def _as_2d(t: torch.Tensor) -> torch.Tensor:

@@ -142,6 +142,10 @@ class VecPPO:
     buffer only replay.  Graphs are kept for the two most recent buffers.
     The results equal the eager fused path's: the same kernels run on the
     same data.
+
+    With `check_waits` (default) each update ends with ops.check_waits(),
+    one host synchronisation that raises if an in-kernel wait of the update
+    (GAE resident pass, fused clip + Adam) gave up.
     """
 
     def __init__(
@@ -158,8 +162,10 @@ class VecPPO:
         graphs: bool = False,
         graph_chunk: int = 64,
         fused_mlp: Optional[bool] = None,
+        check_waits: bool = True,
     ) -> None:
         self.policy, self.value = policy, value
+        self.check_waits = check_waits
         self.ppo_config, self.gamma, self.batch_size = ppo_config, gamma, batch_size
         self.log_std = log_std
         self.generator = generator
@@ -374,13 +380,16 @@ class VecPPO:
         adv_f, ret_f = adv_n.reshape(n).contiguous(), ret.reshape(n).contiguous()
         arrays = (obs, acts, old_lp, adv_f, ret_f, old_v)
         if self.graphs:
-            return self._update_graphed(buffer.device, arrays)
-        stats: dict = {}
-        for _ in range(cfg.epochs):
-            indices = torch.randperm(n, generator=self.generator)
-            for start in range(0, n, self.batch_size):
-                idx = indices[start : start + self.batch_size].to(buffer.device)
-                stats = self._minibatch(idx, arrays)
+            stats = self._update_graphed(buffer.device, arrays)
+        else:
+            stats = {}
+            for _ in range(cfg.epochs):
+                indices = torch.randperm(n, generator=self.generator)
+                for start in range(0, n, self.batch_size):
+                    idx = indices[start : start + self.batch_size].to(buffer.device)
+                    stats = self._minibatch(idx, arrays)
+        if self.check_waits:
+            ops.check_waits(buffer.device)
         return stats
 
     def _minibatch(self, idx: torch.Tensor, arrays: tuple) -> dict:
