@@ -514,6 +514,75 @@ def update_suite(torch, dev, reps=10):
         out["cpu_ms"] = round((time.perf_counter() - t0) / creps * 1e3, 3)
         out["cpu_threads"] = torch.get_num_threads()
         print(json.dumps(out), flush=True)
+    dropin_agent_suite(torch, dev, reps)
+
+
+def dropin_agent_suite(torch, dev, reps=10, T=500):
+    """The drop-in PPOAgent as the reference's runner uses it, at the
+    reference's defaults (TrainingConfig: hidden 128, ReLU, batch 128, 4
+    epochs): `_update` over one T-step CartPole episode (ppo.py:113-171,
+    steady state: every episode of a converged agent lasts 500 steps) and
+    `select_action` (ppo.py:65-79), against oracle.ReferenceAgent (the same
+    code path on the CPU, torch CPU ops) on the same rollout."""
+    import numpy as np
+
+    from oracle import ppo_oracle as ref
+    from ppo_amd.agent import PPOAgent, TrainingConfig
+
+    config = TrainingConfig()
+    env = ref.CartPoleHost()
+    gpu = PPOAgent(env, config, device=dev)
+    cpu = ref.ReferenceAgent(hidden_size=config.hidden_size, batch_size=config.batch_size,
+                             seed=config.seed)
+    # one episode's rollout, collected by the CPU agent's own policy
+    obs, _ = env.reset(seed=0)
+    steps = []
+    for t in range(T):
+        a = cpu.select_action(obs)
+        lp, v = cpu.pending
+        nxt, r, term, trunc, _ = env.step(a)
+        steps.append((obs, a, float(r), bool(term or trunc or t == T - 1), lp, v))
+        obs = nxt if not (term or trunc) else env.reset(seed=t)[0]
+    from ppo_amd.agent import RolloutStep, Transition
+    gpu_rollout = [RolloutStep(Transition(o, a, r, o, d, False), lp, v)
+                   for o, a, r, d, lp, v in steps]
+    out = {"update_suite": "dropin_agent", "T": T, "hidden": config.hidden_size,
+           "activation": "relu", "batch_size": config.batch_size, "epochs": 4,
+           "fused_update": gpu.fused_update, "graphs": gpu.graphs}
+
+    def gpu_update():
+        gpu.rollout = gpu_rollout
+        gpu._update()
+
+    for _ in range(3):  # eager, capture, replay
+        gpu_update()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        gpu_update()
+    torch.cuda.synchronize()
+    out["gpu_update_ms"] = round((time.perf_counter() - t0) / reps * 1e3, 3)
+    t0 = time.perf_counter()
+    creps = max(1, reps // 2)
+    for _ in range(creps):
+        cpu.rollout = list(steps)
+        cpu.end_episode()
+    out["cpu_update_ms"] = round((time.perf_counter() - t0) / creps * 1e3, 3)
+    out["update_speedup"] = round(out["cpu_update_ms"] / out["gpu_update_ms"], 2)
+    o = np.zeros(4, np.float32)
+    for _ in range(20):
+        gpu.select_action(o)
+    n_act = 500
+    t0 = time.perf_counter()
+    for _ in range(n_act):
+        gpu.select_action(o)
+    out["gpu_select_action_us"] = round((time.perf_counter() - t0) / n_act * 1e6, 1)
+    t0 = time.perf_counter()
+    for _ in range(n_act):
+        cpu.select_action(o)
+    out["cpu_select_action_us"] = round((time.perf_counter() - t0) / n_act * 1e6, 1)
+    out["cpu_threads"] = torch.get_num_threads()
+    print(json.dumps(out), flush=True)
 
 
 def copy_calibration(torch, dev, reps=3):

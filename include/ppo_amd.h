@@ -442,6 +442,23 @@ int ppo_mlp_act_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
                         float* observations_out, int32_t* actions_out, float* log_probs_out,
                         float* values_out, void* stream);
 
+/*
+ * The forward half of PPOAgent.select_action (ppo.py:65-79, lines 66 and
+ * 73-77): logits_out [N,A] = actor(obs) and values_out [N] = critic(obs)
+ * through the networks of ppo_mlp_cat_grad_f32, in one launch, so that a
+ * caller sampling on the host (the reference's CPU Categorical, which
+ * consumes torch's global generator) copies both back to the host at once.
+ * observations, logits_out and values_out may be device memory or pinned
+ * host memory (hipHostMalloc, torch pin_memory): the kernel then reads and
+ * writes the host memory over the bus, and the caller reads the results
+ * after synchronising the stream, with no copy launched.  Same size limits
+ * as ppo_mlp_cat_grad_f32.
+ */
+int ppo_mlp_forward_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
+                            int32_t obs_dim, int32_t hidden, int32_t A, int32_t activation,
+                            const float* observations, int64_t N, float* logits_out,
+                            float* values_out, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Vectorised CartPole-v1 (the reference's environment, rl/deep/cli.py:    */
 /* 179-180, stepped by rl/deep/runner.py:56-74).                            */

@@ -45,10 +45,13 @@ def test_ppo_advantages_use_next_step_value(dev):
     assert advantages.tolist() == pytest.approx([2.1, 2.0])
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("T,activation", [(37, "relu"), (200, "tanh")])
-def test_agent_update_matches_reference(dev, T, activation):
+def test_agent_update_matches_reference(dev, T, activation, fused):
     config = TrainingConfig(hidden_size=64, batch_size=32)
-    agent = PPOAgent(cartpole_like(), config, device=dev, activation=activation)
+    agent = PPOAgent(cartpole_like(), config, device=dev, activation=activation,
+                     fused_update=fused)
+    assert agent.fused_update == fused
     torch.manual_seed(config.seed)
     policy = MLP(4, config.hidden_size, 2, activation)
     value = MLP(4, config.hidden_size, 1, activation)
@@ -126,7 +129,8 @@ def test_vec_update_matches_reference(dev):
 # ---------------------------------------------------------------------------
 # The drop-in agent driven the way the reference's runner drives it
 # ---------------------------------------------------------------------------
-def test_agent_drives_like_reference_runner(dev):
+@pytest.mark.parametrize("fused,atol", [(True, 2e-5), (False, 1e-6)])
+def test_agent_drives_like_reference_runner(dev, fused, atol):
     """rl/deep/tests/test_runner.py:9-25 for the GPU agent: 16 training
     episodes and 4 evaluation episodes of single-env CartPole through
     start_episode / select_action / update / end_episode (runner.py:42-84),
@@ -134,11 +138,14 @@ def test_agent_drives_like_reference_runner(dev):
     The same episodes are then run by the CPU restatement of the reference
     agent (oracle.ReferenceAgent) from the same seed: both consume the global
     CPU generator identically (Categorical sampling, torch.randperm), so the
-    trajectories agree step for step and the parameters to fp32 noise."""
+    trajectories agree step for step and the parameters to fp32 noise
+    (the fused update sums gradients in another order than torch and
+    applies Adam in one kernel: 2e-5; torch's MLPs + the fused loss: 1e-6).""" 
     config = TrainingConfig(batch_size=4, warmup_steps=4, hidden_size=16, seed=24)
     print("runner-style: GPU agent", flush=True)
     env = ref.CartPoleHost()
-    agent = PPOAgent(env, config, device=dev)
+    agent = PPOAgent(env, config, device=dev, fused_update=fused)
+    assert agent.fused_update == fused
     train = [ref.run_episode(env, agent, ep, config.seed, training=True) for ep in range(16)]
     evals = [ref.run_episode(ref.CartPoleHost(), agent, ep, config.seed, training=False)
              for ep in range(4)]
@@ -162,7 +169,7 @@ def test_agent_drives_like_reference_runner(dev):
     print(f"  {sum(t[1] for t in train)} training steps; max |param diff| {worst:.2e}",
           flush=True)
     for a, b in zip(agent.parameters, cpu_params):
-        torch.testing.assert_close(a.detach().cpu(), b.detach(), rtol=0, atol=1e-6)
+        torch.testing.assert_close(a.detach().cpu(), b.detach(), rtol=0, atol=atol)
 
 
 def test_agent_minibatch_indices_follow_randperm(dev, monkeypatch):
@@ -189,6 +196,87 @@ def test_agent_minibatch_indices_follow_randperm(dev, monkeypatch):
     assert len(seen) == len(expected)
     for a, b in zip(seen, expected):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("T,B", [(30, 7), (500, 128)])
+def test_fused_agent_minibatch_indices_follow_randperm(dev, monkeypatch, T, B):
+    """The fused loop draws every epoch's torch.randperm before the first
+    minibatch and slices them on the device: the rows of each minibatch are
+    still the reference's slices, bit for bit, and the loop consumes the
+    global generator exactly as ppo.py:129-131 does (the next draw after the
+    update is the same)."""
+    config = TrainingConfig(hidden_size=16, batch_size=B)
+    agent = PPOAgent(cartpole_like(), config, device=dev)
+    assert agent.fused_update
+    agent.rollout = [
+        _rollout_step(1.0, t == T - 1, np.array([t, 0, 0, 0], np.float32), t % 2, -0.7, 0.1)
+        for t in range(T)
+    ]
+    seen = []
+    monkeypatch.setattr(agent._vec, "_minibatch",
+                        lambda idx, arrays: seen.append(idx.cpu().clone()) or {})
+    torch.manual_seed(99)
+    agent._update()
+    after = torch.randint(0, 1 << 30, (4,))
+    torch.manual_seed(99)
+    expected = []
+    for _ in range(agent.ppo_config.epochs):
+        idx = torch.randperm(T)
+        expected += [idx[s : s + B] for s in range(0, T, B)]
+    assert torch.equal(after, torch.randint(0, 1 << 30, (4,)))
+    assert len(seen) == len(expected)
+    for a, b in zip(seen, expected):
+        assert torch.equal(a, b)
+
+
+def test_fused_agent_repeated_lengths_replay_graphs(dev):
+    """Episodes of the previous episode's length replay the captured update
+    (graphs): two agents from one seed, one with graphs and one without,
+    stay identical bit for bit over episodes of lengths 40, 40, 40, 17, 40."""
+    config = TrainingConfig(hidden_size=32, batch_size=16)
+    agents = [PPOAgent(cartpole_like(), config, device=dev) for _ in range(2)]
+    agents[1].graphs = False  # (same optimizer kind: a device step counter)
+    g = torch.Generator().manual_seed(8)
+    for ep, T in enumerate([40, 40, 40, 17, 40]):
+        obs = (torch.rand(T, 4, generator=g) - 0.5) * 0.1
+        acts = torch.randint(0, 2, (T,), generator=g)
+        lps = -0.69 + 0.05 * torch.randn(T, generator=g)
+        vals = torch.randn(T, generator=g)
+        for agent in agents:
+            agent.rollout = [_rollout_step(1.0, t == T - 1, obs[t].numpy(), int(acts[t]),
+                                           float(lps[t]), float(vals[t])) for t in range(T)]
+            torch.manual_seed(100 + ep)
+            agent._update()
+        torch.cuda.synchronize()
+        for a, b in zip(agents[0].parameters, agents[1].parameters):
+            assert torch.equal(a, b), ep
+    assert agents[0]._vec.update_graphed_ready()
+
+
+def test_select_action_one_copy_matches_torch_forward(dev):
+    """select_action's fused forward (both networks in one launch, logits and
+    value in one buffer) gives torch's forward within fp32 noise, and the
+    same draw from the global generator."""
+    config = TrainingConfig(hidden_size=128)
+    agent = PPOAgent(cartpole_like(), config, device=dev)
+    g = torch.Generator().manual_seed(2)
+    for k in range(20):
+        o = ((torch.rand(4, generator=g) - 0.5) * 0.2).numpy()
+        torch.manual_seed(k)
+        a = agent.select_action(o)
+        step = agent.pending_step
+        with torch.no_grad():
+            x = torch.as_tensor(o).to(dev)
+            logits = agent.policy(x).cpu()
+            value = agent.value(x).squeeze().cpu()
+        torch.manual_seed(k)
+        dist = torch.distributions.Categorical(logits=logits)
+        assert int(dist.sample()) == a
+        torch.testing.assert_close(step.log_prob, dist.log_prob(torch.tensor(a)),
+                                   rtol=1e-5, atol=1e-6)
+        torch.testing.assert_close(step.value, value, rtol=1e-5, atol=1e-6)
+        assert step.value.dim() == 0 and step.log_prob.dim() == 0
+        assert agent.select_action(o, training=False) == int(torch.argmax(logits))
 
 
 def test_agent_rejects_out_of_range_actions_without_syncing(dev):
@@ -223,7 +311,8 @@ def test_agent_advantages_with_non_representable_rewards(dev):
     assert bool((err <= bound + ulp).all())
 
 
-def test_agent_vf_clip_uses_rollout_values(dev, monkeypatch):
+@pytest.mark.parametrize("fused", [True, False])
+def test_agent_vf_clip_uses_rollout_values(dev, monkeypatch, fused):
     """PPOConfig.vf_clip (a field the reference does not have) carries the
     rollout's values into _update_batch: one minibatch's raw gradients match
     update_batch_grads_reference with value clipping; without the old values
@@ -231,7 +320,7 @@ def test_agent_vf_clip_uses_rollout_values(dev, monkeypatch):
     T, H = 64, 32
     config = TrainingConfig(hidden_size=H, batch_size=T)
     pcfg = PPOConfig(vf_clip=0.2, gradient_clip=1e9)
-    agent = PPOAgent(cartpole_like(), config, pcfg, device=dev)
+    agent = PPOAgent(cartpole_like(), config, pcfg, device=dev, fused_update=fused)
     cpu_policy = copy.deepcopy(agent.policy).cpu()
     cpu_value = copy.deepcopy(agent.value).cpu()
     g = torch.Generator().manual_seed(4)

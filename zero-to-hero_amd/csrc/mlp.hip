@@ -509,7 +509,9 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
 // the forward of mlp_cat_grad_kernel, then per row the inverse-CDF draw of
 // sample_row.hpp at the caller's uniform.  Writes actions (int32), their
 // log-probabilities and the critic's values, and copies the observations to
-// obs_out when given (a rollout buffer row).
+// obs_out when given (a rollout buffer row).  With `logits` set instead of
+// `u` (ppo_mlp_forward_cat_f32), writes the actor's logits and the critic's
+// values and draws nothing.
 struct ActArgs {
   MlpNet actor, critic;
   int D, A;
@@ -520,6 +522,7 @@ struct ActArgs {
   int32_t* act;
   float* logp;
   float* val;
+  float* logits;
 };
 
 template <int H, int kAct>
@@ -543,9 +546,17 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_act_cat_kernel(ActArgs a) {
     }
     s_x[r * kXld + c] = x;
   }
-  const float u = tid < R && row0 + tid < a.N ? a.u[row0 + tid] : 0.0f;
+  const float u = a.u && tid < R && row0 + tid < a.N ? a.u[row0 + tid] : 0.0f;
   lds_barrier();
   mlp_forward<H, kAct>(a.actor, a.critic, s_x, D, a.A, s_a1, s_a2, s_c1, s_c2, s_z, s_v);
+  if (a.logits) {
+    for (int e = tid; e < R * a.A; e += kMlpBlock) {
+      const int r = e / a.A, j = e - r * a.A;
+      if (row0 + r < a.N) a.logits[(row0 + r) * a.A + j] = s_z[r * kZld + j];
+    }
+    if (tid < R && row0 + tid < a.N) a.val[row0 + tid] = s_v[tid];
+    return;
+  }
   if (tid < R && row0 + tid < a.N) {
     int act;
     float lp;
@@ -1206,6 +1217,53 @@ extern "C" int ppo_mlp_cat_step_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
                                l.tblk, grad_norm_out, stream);
 }
 
+namespace ppo {
+namespace {
+
+// The device's address of `p`: itself for device memory, the mapped address
+// for pinned host memory (hipHostMalloc / torch pin_memory), so that a kernel
+// reads and writes it over the bus.
+void* device_view(const void* p) {
+  if (!p) return nullptr;
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return const_cast<void*>(p);
+  }
+  if (attr.type != hipMemoryTypeHost) return const_cast<void*>(p);
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, const_cast<void*>(p), 0) != hipSuccess || !d) {
+    (void)hipGetLastError();
+    return const_cast<void*>(p);
+  }
+  return d;
+}
+
+int launch_act(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic, int32_t obs_dim,
+               int32_t hidden, int32_t A, int32_t activation, ActArgs& a, void* stream_ptr) {
+  if (a.N < 0) return PPO_ERR_INVALID_ARG;
+  if (obs_dim <= 0 || obs_dim > kMlpMaxIn || A <= 0 || A > kMlpMaxA) return PPO_ERR_UNSUPPORTED;
+  if (activation != PPO_ACT_RELU && activation != PPO_ACT_TANH) return PPO_ERR_INVALID_ARG;
+  const void* kern = activation == PPO_ACT_TANH ? act_kernel_act<PPO_ACT_TANH>(hidden)
+                                                : act_kernel_act<PPO_ACT_RELU>(hidden);
+  if (!kern) return PPO_ERR_UNSUPPORTED;
+  if (!mlp_net_weights_ok(actor) || !mlp_net_weights_ok(critic)) return PPO_ERR_INVALID_ARG;
+  if (a.N == 0) return PPO_OK;
+  if (!a.obs || !a.val) return PPO_ERR_INVALID_ARG;
+  if (a.N > (1L << 31)) return PPO_ERR_TOO_LARGE;
+  a.actor = to_net(actor, obs_dim, hidden);
+  a.critic = to_net(critic, obs_dim, hidden);
+  a.D = obs_dim;
+  a.A = A;
+  void* args[] = {&a};
+  const long blocks = (a.N + kMlpRows - 1) / kMlpRows;
+  return hip_status(hipLaunchKernel(kern, dim3((unsigned)blocks), dim3(kMlpBlock), args, 0,
+                                    reinterpret_cast<hipStream_t>(stream_ptr)));
+}
+
+}  // namespace
+}  // namespace ppo
+
 extern "C" int ppo_mlp_act_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
                                    int32_t obs_dim, int32_t hidden, int32_t A,
                                    int32_t activation, const float* observations, int64_t N,
@@ -1213,22 +1271,8 @@ extern "C" int ppo_mlp_act_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32
                                    int32_t* actions_out, float* log_probs_out,
                                    float* values_out, void* stream_ptr) {
   using namespace ppo;
-  if (N < 0) return PPO_ERR_INVALID_ARG;
-  if (obs_dim <= 0 || obs_dim > kMlpMaxIn || A <= 0 || A > kMlpMaxA) return PPO_ERR_UNSUPPORTED;
-  if (activation != PPO_ACT_RELU && activation != PPO_ACT_TANH) return PPO_ERR_INVALID_ARG;
-  const void* kern = activation == PPO_ACT_TANH ? act_kernel_act<PPO_ACT_TANH>(hidden)
-                                                : act_kernel_act<PPO_ACT_RELU>(hidden);
-  if (!kern) return PPO_ERR_UNSUPPORTED;
-  if (!mlp_net_weights_ok(actor) || !mlp_net_weights_ok(critic)) return PPO_ERR_INVALID_ARG;
-  if (N == 0) return PPO_OK;
-  if (!observations || !uniforms || !actions_out || !log_probs_out || !values_out)
-    return PPO_ERR_INVALID_ARG;
-  if (N > (1L << 31)) return PPO_ERR_TOO_LARGE;
+  if (N > 0 && (!uniforms || !actions_out || !log_probs_out)) return PPO_ERR_INVALID_ARG;
   ActArgs a = {};
-  a.actor = to_net(actor, obs_dim, hidden);
-  a.critic = to_net(critic, obs_dim, hidden);
-  a.D = obs_dim;
-  a.A = A;
   a.obs = observations;
   a.N = N;
   a.u = uniforms;
@@ -1236,10 +1280,22 @@ extern "C" int ppo_mlp_act_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32
   a.act = actions_out;
   a.logp = log_probs_out;
   a.val = values_out;
-  void* args[] = {&a};
-  const long blocks = (N + kMlpRows - 1) / kMlpRows;
-  return hip_status(hipLaunchKernel(kern, dim3((unsigned)blocks), dim3(kMlpBlock), args, 0,
-                                    reinterpret_cast<hipStream_t>(stream_ptr)));
+  return launch_act(actor, critic, obs_dim, hidden, A, activation, a, stream_ptr);
+}
+
+extern "C" int ppo_mlp_forward_cat_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic,
+                                       int32_t obs_dim, int32_t hidden, int32_t A,
+                                       int32_t activation, const float* observations,
+                                       int64_t N, float* logits_out, float* values_out,
+                                       void* stream_ptr) {
+  using namespace ppo;
+  if (N > 0 && !logits_out) return PPO_ERR_INVALID_ARG;
+  ActArgs a = {};
+  a.obs = static_cast<const float*>(device_view(observations));
+  a.N = N;
+  a.logits = static_cast<float*>(device_view(logits_out));
+  a.val = static_cast<float*>(device_view(values_out));
+  return launch_act(actor, critic, obs_dim, hidden, A, activation, a, stream_ptr);
 }
 
 extern "C" int ppo_cartpole_rollout_f32(

@@ -126,6 +126,11 @@ SIGNATURES = {
         [ctypes.POINTER(Mlp3), ctypes.POINTER(Mlp3), _i32, _i32, _i32, _i32, _vp, _i64, _vp, _vp,
          _vp, _vp, _vp, _vp],
     ),
+    "ppo_mlp_forward_cat_f32": (
+        _int,
+        [ctypes.POINTER(Mlp3), ctypes.POINTER(Mlp3), _i32, _i32, _i32, _i32, _vp, _i64, _vp, _vp,
+         _vp],
+    ),
     "ppo_sample_cat_f32": (_int, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ppo_sample_gauss_f32": (_int, [_vp, _vp, _i64, _i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "ppo_mlp_cat_grad_workspace_bytes": (_sz, [_i64, _i32, _i32, _i32]),

@@ -7,14 +7,24 @@ this one unchanged.  Differences, all on the device side:
   * `_advantages` runs the GAE kernel (fp64 recurrence, the reference's
     operation order) instead of a Python loop;
   * `_update` normalises with the fused normalisation kernel;
-  * `_update_batch` computes the loss and its gradient with the fused loss
-    kernel; the MLPs, clip_grad_norm_ and Adam stay in torch on the GPU.
+  * when the networks are MLPs the fused kernels support (the reference's
+    own 4-128-128 ReLU networks are), `_update` runs every minibatch as the
+    fused MLP step (gather + both forwards + loss + backward, then the
+    gradient reduction with clip_grad_norm_ and Adam: two launches), with the
+    permutations of all epochs uploaded in one copy, and replays the
+    minibatch loop from HIP graphs when an episode has the previous one's
+    length; `optimizer` is then a ClippedAdam (clip + Adam fused);
+  * otherwise `_update_batch` computes the loss and its gradient with the
+    fused loss kernel and the MLPs, clip_grad_norm_ and Adam stay in torch;
+  * `select_action` brings the logits and the value to the host in one copy
+    (one forward launch for both networks when fused).
 The environment is duck-typed (anything with observation_space.shape and
 action_space.n), since gymnasium is not a dependency here.
 """
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Optional
 
@@ -127,6 +137,16 @@ def cartpole_sizes(env) -> tuple[int, int]:
 # The agent (rl/deep/agents/ppo.py:38-193)
 # ---------------------------------------------------------------------------
 class PPOAgent:
+    """rl/deep/agents/ppo.py:38-193 with the update on the GPU.
+
+    `fused_update` (default: whenever ops.mlp_fusable accepts the networks)
+    takes the fused minibatch step described in the module docstring;
+    `graphs` (default True) lets the fused loop replay captured graphs for
+    episodes of a length seen in the previous update.  Both follow the
+    reference's randomness: actions are sampled by a CPU Categorical and the
+    minibatches come from torch.randperm, both on the global CPU generator,
+    so one seed gives the reference's trajectories and index stream."""
+
     name = "ppo"
 
     def __init__(
@@ -136,6 +156,8 @@ class PPOAgent:
         ppo_config: PPOConfig = PPOConfig(),
         device: str | torch.device = "cuda",
         activation: str = "relu",
+        fused_update: Optional[bool] = None,
+        graphs: bool = True,
     ) -> None:
         torch.manual_seed(config.seed)                                    # ppo.py:47
 
@@ -143,6 +165,7 @@ class PPOAgent:
         self.ppo_config = ppo_config
         self.device = torch.device(device)
         observation_size, action_count = cartpole_sizes(env)
+        self.action_count = action_count
 
         # initialised on the CPU generator exactly as the reference does, then
         # moved, so both start from identical weights for one seed
@@ -151,7 +174,25 @@ class PPOAgent:
         self.policy.to(self.device)
         self.value.to(self.device)
         self.parameters = list(self.policy.parameters()) + list(self.value.parameters())
-        self.optimizer = torch.optim.Adam(self.parameters, lr=config.lr)
+        fusable = ops.mlp_fusable(self.policy, self.value)
+        if fused_update and not fusable:
+            raise ValueError("fused_update needs MLPs on the GPU that ops.mlp_fusable accepts")
+        self.fused_update = fusable if fused_update is None else bool(fused_update)
+        self._fused_act = fusable
+        self._vec = None
+        if self.fused_update:
+            from .rollout import VecPPO
+
+            self._vec = VecPPO(self.policy, self.value, ppo_config, gamma=config.gamma,
+                               lr=config.lr, batch_size=config.batch_size, fused_update=True,
+                               graphs=graphs, fused_mlp=True)
+            self.optimizer = self._vec.optimizer
+        else:
+            self.optimizer = torch.optim.Adam(self.parameters, lr=config.lr)
+        self.graphs = graphs
+        self._stage: dict = {}  # rollout length -> persistent device arrays (graph replays)
+        self._last_n = -1
+        self._act_ctx = None  # select_action's launch arguments and pinned buffer
 
         self.rollout: list[RolloutStep] = []
         self.pending_step: PendingStep | None = None
@@ -162,21 +203,67 @@ class PPOAgent:
 
     @torch.no_grad()
     def select_action(self, observation: np.ndarray, training: bool = True) -> int:
-        """ppo.py:65-79.  The policy runs on the device; sampling uses a CPU
+        """ppo.py:65-79.  The networks run on the device and the logits and
+        the value come back to the host in one copy; sampling uses a CPU
         Categorical so the global CPU generator is consumed as in the
         reference.  log_prob and value are 0-d CPU tensors, as there."""
-        obs = torch.as_tensor(observation, dtype=torch.float32, device=self.device)
-        logits = self.policy(obs).cpu()
+        A = self.action_count
+        if self._fused_act and np.ndim(observation) == 1:
+            logits, value = self._forward_pinned(observation)
+        else:
+            obs = torch.as_tensor(observation, dtype=torch.float32).to(self.device)
+            host = torch.cat([self.policy(obs).reshape(-1), self.value(obs).reshape(-1)]).cpu()
+            logits, value = host[:A], host[A]
         if not training:
             return int(torch.argmax(logits).item())
 
-        distribution = Categorical(logits=logits)
+        # (validation only raises on invalid logits; skipping it changes no
+        # result and no generator draw)
+        distribution = Categorical(logits=logits, validate_args=False)
         action = distribution.sample()
         self.pending_step = PendingStep(
             log_prob=distribution.log_prob(action),
-            value=self.value(obs).squeeze().cpu(),
+            value=value,
         )
         return int(action.item())
+
+    def _forward_pinned(self, observation) -> tuple[torch.Tensor, torch.Tensor]:
+        """Both networks on one observation through ppo_mlp_forward_cat_f32,
+        reading it from and writing the logits and value to pinned host
+        memory (no copy launches), then one stream synchronisation.  The
+        launch arguments are built once and rebuilt when a network or its
+        parameter storage changes."""
+        key = (id(self.policy), id(self.value),
+               tuple(p.data_ptr() for p in self.parameters))
+        if self._act_ctx is None or self._act_ctx[0] != key:
+            from . import _lib
+
+            lp, act = ops.mlp_structure(self.policy)
+            lv, _ = ops.mlp_structure(self.value)
+            D, H, A = lp[0].in_features, lp[0].out_features, lp[2].out_features
+            structs = (_lib.Mlp3(), _lib.Mlp3())
+            for st, layers in zip(structs, (lp, lv)):
+                for i, m in enumerate(layers):
+                    st.weight[i] = m.weight.data_ptr()
+                    st.bias[i] = m.bias.data_ptr()
+            io = torch.zeros(D + A + 1, dtype=torch.float32, pin_memory=True)
+            ptr = io.data_ptr()
+            head = (ctypes.byref(structs[0]), ctypes.byref(structs[1]), D, H, A,
+                    _lib.PPO_ACT_TANH if act == "tanh" else _lib.PPO_ACT_RELU, ptr, 1,
+                    ptr + 4 * D, ptr + 4 * (D + A))
+            self._act_ctx = (key, structs, io, io.numpy(), head, D, A,
+                             _lib.load().ppo_mlp_forward_cat_f32)
+        _, _, io, io_np, head, D, A, fn = self._act_ctx
+        io_np[:D] = observation
+        stream = torch.cuda.current_stream(self.device)
+        code = fn(*head, stream.cuda_stream)
+        if code:
+            from . import _lib
+
+            _lib.check("ppo_mlp_forward_cat_f32", code)
+        stream.synchronize()
+        out = torch.from_numpy(io_np[D:].copy())
+        return out[:A], out[A]
 
     def update(
         self,
@@ -243,6 +330,15 @@ class PPOAgent:
         if len(advantages) > 1:
             advantages = ops.normalize_advantages(advantages)
 
+        # The fused loop stands in for the minibatch loop below unless
+        # _update_batch was replaced (a subclass or an instance attribute),
+        # in which case that method is what must run per minibatch.
+        if self.fused_update and "_update_batch" not in self.__dict__ and (
+                type(self)._update_batch is PPOAgent._update_batch):
+            self._update_fused(observations, actions, old_log_probs.reshape(-1),
+                               advantages, returns, old_values)
+            return
+
         for _ in range(self.ppo_config.epochs):
             indices = torch.randperm(len(actions))
             for start in range(0, len(actions), self.config.batch_size):
@@ -260,6 +356,31 @@ class PPOAgent:
                     **extra,
                 )
 
+    def _update_fused(self, observations, actions, old_log_probs, advantages, returns,
+                      old_values) -> None:
+        """ppo.py:129-171 as VecPPO's fused minibatch loop over the episode's
+        arrays: the same torch.randperm draws on the global CPU generator
+        (all epochs drawn before the first minibatch, which consumes the
+        generator identically: nothing between the reference's draws uses
+        it), one upload, two launches per minibatch, one wait-status check.
+        An episode as long as the previous one is copied into that length's
+        persistent arrays and its loop replayed from graphs."""
+        n = observations.shape[0]
+        arrays = (observations, actions, old_log_probs, advantages, returns, old_values)
+        use_graphs = self.graphs and n == self._last_n
+        if self.graphs:
+            stage = self._stage.pop(n, None)
+            if stage is None:
+                stage = tuple(torch.empty_like(x) for x in arrays)
+            self._stage[n] = stage  # most recent last
+            while len(self._stage) > 2:
+                self._stage.pop(next(iter(self._stage)))
+            for dst, src in zip(stage, arrays):
+                dst.copy_(src)
+            arrays = stage
+        self._last_n = n
+        self._vec.update_flat(arrays, self.device, graphs=use_graphs)
+
     def _update_batch(
         self,
         observations: torch.Tensor,
@@ -269,13 +390,23 @@ class PPOAgent:
         returns: torch.Tensor,
         old_values: Optional[torch.Tensor] = None,
     ) -> None:
-        """ppo.py:141-171: MLP forwards in torch, the fused loss kernel for
-        the loss and its gradient, then backward through the MLPs,
-        clip_grad_norm_ and Adam.  `old_values` (the rollout's values of the
-        minibatch rows) is needed only with PPOConfig.vf_clip, which the
-        reference does not have; ValueError if it is missing then."""
-        if self.ppo_config.vf_clip is not None and old_values is None:
+        """ppo.py:141-171.  With the fused update: one fused MLP step over
+        the given rows (forward, loss, backward, clip_grad_norm_ and Adam).
+        Otherwise: MLP forwards in torch, the fused loss kernel for the loss
+        and its gradient, then backward through the MLPs, clip_grad_norm_ and
+        Adam.  `old_values` (the rollout's values of the minibatch rows) is
+        needed only with PPOConfig.vf_clip, which the reference does not
+        have; ValueError if it is missing then."""
+        cfg = self.ppo_config
+        if cfg.vf_clip is not None and old_values is None:
             raise ValueError("PPOConfig.vf_clip needs the minibatch's old_values")
+        if self.fused_update:
+            ops.ppo_mlp_cat_step(
+                self.policy, self.value, self.optimizer, observations.contiguous(),
+                actions.contiguous(), old_log_probs.contiguous(), advantages.contiguous(),
+                returns.contiguous(), None if old_values is None else old_values.contiguous(),
+                None, cfg.clip_ratio, cfg.vf_clip, cfg.value_coef, cfg.entropy_coef)
+            return
         logits = self.policy(observations)
         values = self.value(observations).squeeze(1)
         loss, _ = ops.ppo_loss_discrete(
@@ -285,15 +416,15 @@ class PPOAgent:
             advantages.contiguous(),
             returns.contiguous(),
             values.contiguous(),
-            clip_ratio=self.ppo_config.clip_ratio,
-            vf_clip=self.ppo_config.vf_clip,
-            value_coef=self.ppo_config.value_coef,
-            entropy_coef=self.ppo_config.entropy_coef,
+            clip_ratio=cfg.clip_ratio,
+            vf_clip=cfg.vf_clip,
+            value_coef=cfg.value_coef,
+            entropy_coef=cfg.entropy_coef,
             old_values=None if old_values is None else old_values.contiguous(),
         )
         self.optimizer.zero_grad()
         loss.backward()
-        nn.utils.clip_grad_norm_(self.parameters, self.ppo_config.gradient_clip)
+        nn.utils.clip_grad_norm_(self.parameters, cfg.gradient_clip)
         self.optimizer.step()
 
     def _advantages(self, values: torch.Tensor) -> torch.Tensor:

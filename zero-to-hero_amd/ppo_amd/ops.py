@@ -39,6 +39,7 @@ __all__ = [
     "ppo_loss_gaussian_fused",
     "ppo_mlp_cat_grads",
     "mlp_act_categorical",
+    "mlp_forward_categorical",
     "mlp_fusable",
     "check_waits",
     "set_wait_limit",
@@ -988,6 +989,44 @@ def mlp_act_categorical(
           observations.data_ptr(), N, uniforms.data_ptr(), _ptr(observations_out),
           actions_out.data_ptr(), log_probs_out.data_ptr(), values_out.data_ptr(), stream)
     return actions_out, log_probs_out, values_out
+
+
+def mlp_forward_categorical(
+    policy: torch.nn.Module,
+    value: torch.nn.Module,
+    observations: torch.Tensor,
+    logits_out: Optional[torch.Tensor] = None,
+    values_out: Optional[torch.Tensor] = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """policy(observations) and value(observations).squeeze(-1) for
+    observations [N,D] in one launch (ppo_mlp_forward_cat_f32; networks as in
+    ppo_mlp_cat_grads).  Returns (logits [N,A], values [N]), written into
+    logits_out / values_out when given: two views of one buffer let one
+    copy bring both to the host (the forward half of PPOAgent.select_action,
+    ppo.py:65-79)."""
+    if not mlp_fusable(policy, value):
+        raise ValueError("policy/value are not MLPs the fused kernel supports (see mlp_fusable)")
+    lp, act = mlp_structure(policy)
+    lv, _ = mlp_structure(value)
+    D, H, A = lp[0].in_features, lp[0].out_features, lp[2].out_features
+    device = lp[0].weight.device
+    _require(observations, "observations", (torch.float32,), device)
+    if observations.dim() != 2 or observations.shape[1] != D:
+        raise ValueError(f"observations must be [N,{D}], got {tuple(observations.shape)}")
+    N = observations.shape[0]
+    logits_out = _out(logits_out, "logits_out", (N, A), torch.float32, device)
+    values_out = _out(values_out, "values_out", (N,), torch.float32, device)
+    s_actor, s_critic = _lib.Mlp3(), _lib.Mlp3()
+    for st, layers in ((s_actor, lp), (s_critic, lv)):
+        for i, m in enumerate(layers):
+            st.weight[i] = m.weight.data_ptr()
+            st.bias[i] = m.bias.data_ptr()
+    stream = _stream(device)
+    _call("ppo_mlp_forward_cat_f32", device, stream, ctypes.byref(s_actor),
+          ctypes.byref(s_critic), D, H, A,
+          _lib.PPO_ACT_TANH if act == "tanh" else _lib.PPO_ACT_RELU,
+          observations.data_ptr(), N, logits_out.data_ptr(), values_out.data_ptr(), stream)
+    return logits_out, values_out
 
 
 def mlp_cartpole_rollout(

@@ -183,6 +183,7 @@ class VecPPO:
         self._rollout_u: Optional[torch.Tensor] = None  # uniforms of the fused rollout
         self._plan: Optional[_GraphPlan] = None  # the most recently used
         self._side_stream: Optional[torch.cuda.Stream] = None
+        self._perms = _PermUploader()
         can_fuse = fused_update and log_std is None and ops.mlp_fusable(policy, value)
         if fused_mlp and not can_fuse:
             raise ValueError("fused_mlp needs fused_update, a categorical policy and MLPs that "
@@ -378,18 +379,33 @@ class VecPPO:
         old_lp = buffer.log_probs[:T].reshape(n).contiguous()
         old_v = buffer.values[:T].reshape(n).contiguous()
         adv_f, ret_f = adv_n.reshape(n).contiguous(), ret.reshape(n).contiguous()
-        arrays = (obs, acts, old_lp, adv_f, ret_f, old_v)
-        if self.graphs:
-            stats = self._update_graphed(buffer.device, arrays)
+        return self.update_flat((obs, acts, old_lp, adv_f, ret_f, old_v), buffer.device)
+
+    def update_flat(self, arrays: tuple, device: torch.device,
+                    graphs: Optional[bool] = None) -> dict:
+        """The epoch/minibatch loop (ppo.py:129-171) over flattened rollout
+        arrays (observations [n,...], actions [n(,D)], old_log_probs,
+        advantages (normalised), returns, old_values [n]): `epochs`
+        permutations from torch.randperm on `generator`, drawn together on
+        the host and uploaded in one copy, sliced into minibatches on the
+        device.  `graphs` overrides the constructor's choice for this call;
+        graph plans are keyed on the arrays' storage, so repeated calls replay
+        only when the same tensors are passed again."""
+        use_graphs = self.graphs if graphs is None else graphs
+        if use_graphs and not self.fused:
+            raise ValueError("graphs need fused_update=True")
+        if use_graphs:
+            stats = self._update_graphed(device, arrays)
         else:
+            cfg = self.ppo_config
+            n = arrays[0].shape[0]
+            perms = self._perms.upload(n, cfg.epochs, self.generator, arrays[0].device)
             stats = {}
-            for _ in range(cfg.epochs):
-                indices = torch.randperm(n, generator=self.generator)
+            for e in range(cfg.epochs):
                 for start in range(0, n, self.batch_size):
-                    idx = indices[start : start + self.batch_size].to(buffer.device)
-                    stats = self._minibatch(idx, arrays)
+                    stats = self._minibatch(perms[e, start : start + self.batch_size], arrays)
         if self.check_waits:
-            ops.check_waits(buffer.device)
+            ops.check_waits(device)
         return stats
 
     def _minibatch(self, idx: torch.Tensor, arrays: tuple) -> dict:
@@ -511,6 +527,40 @@ class VecPPO:
             nn.utils.clip_grad_norm_(self.parameters, cfg.gradient_clip)
             self.optimizer.step()
         return stats
+
+
+class _PermUploader:
+    """The eager loop's permutations: `epochs` rows of torch.randperm(n) drawn
+    on the host into one of two pinned buffers (the other may still be read
+    by the previous upload) and copied to one device buffer in one launch.
+    The device buffer is reused: the next upload is ordered after the
+    previous update's kernels on the same stream."""
+
+    def __init__(self) -> None:
+        self.host: list = [None, None]
+        self.events: list = [None, None]
+        self.dev: Optional[torch.Tensor] = None
+        self.flip = 0
+
+    def upload(self, n: int, epochs: int, generator, device) -> torch.Tensor:
+        k = self.flip
+        self.flip ^= 1
+        if self.events[k] is not None:
+            self.events[k].synchronize()
+        need = epochs * n
+        if self.host[k] is None or self.host[k].numel() < need:
+            self.host[k] = torch.empty(max(need, 1024), dtype=torch.int64, pin_memory=True)
+        if self.dev is None or self.dev.numel() < need or self.dev.device != device:
+            self.dev = torch.empty(max(need, 1024), dtype=torch.int64, device=device)
+        host = self.host[k][:need].view(epochs, n)
+        for e in range(epochs):
+            torch.randperm(n, generator=generator, out=host[e])
+        dev = self.dev[:need].view(epochs, n)
+        ops.copy_pinned_to_device(dev, host)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(device))
+        self.events[k] = ev
+        return dev
 
 
 class _GraphPlan:
