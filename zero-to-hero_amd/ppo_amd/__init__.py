@@ -11,12 +11,14 @@ include/ppo_amd.h) behind the reference's own PPO surface:
             and common.py, same names and signatures
   rollout   RolloutBuffer ([T,N] env-contiguous, on device) and VecPPO
   optim     ClippedAdam (clip_grad_norm_ + Adam, two launches)
+  reference_patch  _advantages / _update_batch for the reference's own
+            PPOAgent class (reference_patch.apply(PPOAgent))
   torch_ops the hot path as registered operators, torch.ops.ppo_amd.*
             (gae, gae_normalize, normalize_advantages, ppo_loss_discrete,
             ppo_loss_gaussian), visible to torch.compile and the dispatcher
 """
 
-from . import _lib
+from . import _lib, reference_patch
 from .agent import (
     MLP,
     PendingStep,
@@ -33,7 +35,9 @@ from .ops import (
     gae,
     gather_rows,
     gae_normalize,
+    check_waits,
     mlp_act_categorical,
+    mlp_forward_categorical,
     mlp_fusable,
     normalize_advantages,
     ppo_loss_discrete,
@@ -73,13 +77,16 @@ __all__ = [
     "Transition",
     "VecPPO",
     "cartpole_sizes",
+    "check_waits",
     "discounted_returns",
     "gae",
     "gae_normalize",
     "gather_rows",
     "load_library",
     "mlp_act_categorical",
+    "mlp_forward_categorical",
     "mlp_fusable",
+    "reference_patch",
     "normalize_advantages",
     "ppo_loss_discrete",
     "ppo_loss_discrete_fused",
