@@ -56,11 +56,13 @@ const char* ppo_amd_strerror(int code);
 
 /*
  * Status of the bounded in-kernel waits (no counterpart in the reference: its
- * update runs on the CPU in one thread).  Three launches hold workgroups that
+ * update runs on the CPU in one thread).  Four launches hold workgroups that
  * wait for one another inside the launch: the resident GAE pass
  * (ppo_gae_f32 / ppo_gae_norm_f32, PPO_GAE_ROUTE_RESIDENT), the Gaussian loss
- * with its in-kernel finish (ppo_loss_gauss_f32), and the fused gradient
- * reduction + clip + Adam of ppo_mlp_cat_step_f32.  Each is launched only when
+ * with its in-kernel finish (ppo_loss_gauss_f32), the categorical loss of at
+ * most 2^22 rows, which also finishes in-kernel (ppo_loss_cat_f32 and its
+ * _noalloc form), and the fused gradient reduction + clip + Adam of
+ * ppo_mlp_cat_step_f32.  Each is launched only when
  * the occupancy query says its whole grid fits on the device at once; that
  * query assumes the device's compute units are free.  When another process
  * or stream keeps part of the grid from running, a wait gives up after its
@@ -74,8 +76,9 @@ const char* ppo_amd_strerror(int code);
  * current device gave up since the previous call (on any stream), PPO_OK
  * otherwise.  It is a host synchronisation point, for callers to place where
  * they already synchronise (the Python layer checks once per update).
- * PPO_AMD_GAE_RESIDENT=0, PPO_AMD_GAUSS_FINISH=0 and PPO_AMD_MLP_FUSED_ADAM=0
- * select launches without in-kernel waits, for callers that share the GPU.
+ * PPO_AMD_GAE_RESIDENT=0, PPO_AMD_GAUSS_FINISH=0, PPO_AMD_CAT_FINISH_MAX_ROWS=0
+ * and PPO_AMD_MLP_FUSED_ADAM=0 select launches without in-kernel waits, for
+ * callers that share the GPU.
  */
 int ppo_wait_status(void* stream);
 

@@ -489,6 +489,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_kernel(LossArgs a, long ntile
     __syncthreads();
   }
   store_scalar_partials(a, acc);
+  if (a.finish) loss_publish<0>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -624,6 +625,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_pipe_kernel(LossArgs a, long 
     __syncthreads();
   }
   store_scalar_partials(a, acc);
+  if (a.finish) loss_publish<0>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -768,6 +770,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_wtile_kernel(LossArgs a, long
     if (lane < count - (m4 << 2)) a.dx[row0 * A + (m4 << 2) + lane] = s_tile[(m4 << 2) + lane];
   }
   store_scalar_partials(a, acc);
+  if (a.finish) loss_publish<0>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -826,6 +829,7 @@ __global__ void __launch_bounds__(kBlock) loss_cat_wave_kernel(LossArgs a) {
     if (lane == 0) accumulate(acc, o, H);
   }
   store_scalar_partials(a, acc);
+  if (a.finish) loss_publish<0>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -1241,6 +1245,19 @@ int fill_common(LossArgs& a, long B, const ppo_loss_params* p, const float* old_
 
 long row_tiles(long B) { return (B + kBlock - 1) / kBlock; }
 
+// Batches of at most this many rows finish in-kernel (loss_publish) rather
+// than by the one-block finaliser launch.  Measured on MI355X (A = 18, each
+// call after a cache-evicting read): B = 1,048,576 40.9 against 42.4 us; B =
+// 8,388,608 273.2-273.8 against 273.9 us cold, but inside the PPO step the
+// in-kernel finish measured slower at that size (260.6 against 257.5 us: the
+// collecting workgroup's polls wait behind 0.6 GB of gradient write-back), so
+// large batches keep the launch.  PPO_AMD_CAT_FINISH_MAX_ROWS overrides the
+// limit (0: always the launch, which has no in-kernel wait).
+long cat_finish_max_rows() {
+  const char* env = getenv("PPO_AMD_CAT_FINISH_MAX_ROWS");
+  return env ? atol(env) : (1L << 22);
+}
+
 long cat_blocks(long B, int A) {
   if (A <= kMaxCatRowWidth) return std::min(row_tiles(B), kLossGridCap);
   return std::max(1L, std::min((B + 3) / 4, kWaveRowBlocks));
@@ -1339,7 +1356,19 @@ int loss_cat_launch(const float* logits, int64_t B, int32_t A, const void* actio
                                : (const void*)loss_cat_kernel<int32_t, false>;
     if (dense) lds = (size_t)kBlock * A * sizeof(float);
     // one wave of resident workgroups looping over the tiles
-    blocks = std::min(blocks, resident_blocks(kern, kBlock, lds, blocks));
+    const long resident = resident_blocks(kern, kBlock, lds, 0);
+    blocks = std::min(blocks, resident > 0 ? resident : blocks);
+    // Below cat_finish_max_rows() rows (and with the whole grid known to be
+    // resident) the kernel finishes in-kernel as the Gaussian kernels do
+    // (loss_publish: workgroup 0 collects every workgroup's tagged partials)
+    // instead of a one-block finaliser launch.
+    if (resident > 0 && B <= cat_finish_max_rows()) {
+      int wst = wait_ctl(a.wc);
+      if (wst) return wst;
+      a.finish = 1;
+      a.epoch = &static_cast<WsHeader*>(workspace)->epoch;
+      a.tag_slot = kScalarSlots - 1;
+    }
     const long wfull = B / kWave;  // full wave tiles
     void* args[] = {&a, const_cast<long*>(dense ? &wfull : &tiles)};
     st = hip_status(hipLaunchKernel(kern, grid_of(blocks), dim3(kBlock), args, lds, stream));
@@ -1353,6 +1382,7 @@ int loss_cat_launch(const float* logits, int64_t B, int32_t A, const void* actio
                          stream, a);
   }
   if ((st = last_launch_status())) return st;
+  if (a.finish) return PPO_OK;
   hipLaunchKernelGGL(loss_finalize_kernel, dim3(1), dim3(kFinalBlock), 0, stream, a, blocks);
   return last_launch_status();
 }
