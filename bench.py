@@ -58,6 +58,10 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="wall-clock budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gae-phases", metavar="LIB",
+                    help="phase timestamps of the resident GAE pass (configs 2 and 3) from a "
+                         "trace build of the library at LIB (make -C zero-to-hero_amd/csrc "
+                         "EXTRA=-DPPO_GAE_RES_TRACE OBJDIR=_build_trace OUT=<LIB>); then exit")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (for rocprofv3 --pmc scaling)")
     return ap.parse_args()
@@ -585,6 +589,84 @@ def dropin_agent_suite(torch, dev, reps=10, T=500):
     print(json.dumps(out), flush=True)
 
 
+def gae_phases(torch, dev, lib_path, reps=4):
+    """Phase timestamps of gae_resident_kernel from a trace build (each
+    workgroup's thread 0 stores the wall clock, 100 MHz, at 6 marks per
+    round into a device array the build exports): per config, per call
+    after a cache-evicting read, the p50 and max over the workgroups of each
+    mark, in us from the first workgroup's start, and the call's event
+    interval."""
+    import ctypes
+
+    import numpy as np
+
+    from ppo_amd import _lib
+
+    lib = ctypes.CDLL(lib_path)
+    for name, (res, argt) in _lib.SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, argt
+    lib.ppo_debug_res_trace.restype = ctypes.c_void_p
+    hip = ctypes.CDLL("libamdhip64.so")
+    row = 64  # trace words per workgroup (6 marks per round, up to 8 rounds)
+    names = ["start", "phase1", "carry", "phase3", "stats", "end"]
+    f32 = dict(dtype=torch.float32, device=dev)
+    evict = torch.empty(128 * 1024 * 1024, **f32)
+    es = torch.empty((), **f32)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    for cfg, T, N, norm, gamma, p_done, rounds in (("config2", 2048, 4096, True, 0.99, 0.01, 1),
+                                                   ("config3", 1 << 20, 16, False, 0.999, 0.001, 2)):
+        g = torch.Generator(device=dev).manual_seed(24)
+        r = torch.randn(T, N, generator=g, **f32)
+        v = torch.randn(T, N, generator=g, **f32)
+        d = (torch.rand(T, N, device=dev, generator=g) < p_done).to(torch.uint8)
+        lv = torch.randn(N, generator=g, **f32)
+        adv, ret, advn = (torch.empty(T, N, **f32) for _ in range(3))
+        w = torch.empty(lib.ppo_gae_workspace_bytes(T, N), dtype=torch.uint8, device=dev)
+        grid = None
+        for rep in range(reps):
+            # (marks a configuration does not write must not keep an earlier call's values)
+            if hip.hipMemset(ctypes.c_void_p(lib.ppo_debug_res_trace()), 0,
+                             ctypes.c_size_t(4096 * row * 8)):
+                raise RuntimeError("hipMemset of the trace failed")
+            torch.sum(evict, dim=0, out=es)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            if norm:
+                rc = lib.ppo_gae_norm_f32(r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T,
+                                          N, gamma, 0.95, 1e-8, adv.data_ptr(), ret.data_ptr(),
+                                          advn.data_ptr(), None, w.data_ptr(), w.numel(), stream)
+            else:
+                rc = lib.ppo_gae_f32(r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N,
+                                     gamma, 0.95, adv.data_ptr(), ret.data_ptr(), w.data_ptr(),
+                                     w.numel(), stream)
+            e1.record()
+            torch.cuda.synchronize()
+            if rc:
+                raise RuntimeError(f"GAE call returned {rc}")
+            buf = np.zeros(4096 * row, dtype=np.uint64)
+            if hip.hipMemcpy(buf.ctypes.data_as(ctypes.c_void_p),
+                             ctypes.c_void_p(lib.ppo_debug_res_trace()),
+                             ctypes.c_size_t(buf.nbytes), 2):
+                raise RuntimeError("hipMemcpy of the trace failed")
+            tr = buf.reshape(-1, row).astype(np.int64)
+            if grid is None:
+                grid = int((tr[:, 0] != 0).sum())
+            tr = tr[:grid]
+            rel = (tr - tr[:, 0].min()) / 100.0
+            out = {"gae_phases": cfg, "T": T, "N": N, "rep": rep, "workgroups": grid,
+                   "event_us": round(e0.elapsed_time(e1) * 1e3, 2)}
+            for rd in range(rounds):
+                for k, name in enumerate(names):
+                    col = tr[:, k + 6 * rd]
+                    if (rd > 0 and k == 0) or (col == 0).all():
+                        continue
+                    c = rel[:, k + 6 * rd]
+                    out[f"r{rd}_{name}"] = [round(float(np.median(c)), 2), round(float(c.max()), 2)]
+            print(json.dumps(out), flush=True)
+        del r, v, d, adv, ret, advn, w
+
+
 def copy_calibration(torch, dev, reps=3):
     """A plain device-to-device copy of exactly 1 GiB (torch copy_), run
     `reps` times so that a rocprofv3 --pmc pass over this command records what
@@ -612,6 +694,9 @@ def main():
         sys.exit(2)
     lib = ppo_amd.load_library()
     dev = torch.device("cuda:0")
+    if args.gae_phases:
+        gae_phases(torch, dev, args.gae_phases)
+        return
     if args.suite:
         suite(torch, lib, dev, stream_timing=not args.no_stream, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
