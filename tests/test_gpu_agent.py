@@ -402,3 +402,40 @@ def test_vec_update_config1_matches_reference(dev, mode):
             torch.testing.assert_close(a.detach().cpu(), b.detach(), rtol=0, atol=2e-5)
     if mode == "graphs":
         assert vec.update_graphed_ready()
+
+
+@pytest.mark.parametrize("H,A,act", [(128, 2, "relu"), (64, 18, "tanh"), (16, 5, "relu")])
+def test_mlp_forward_categorical_matches_torch(dev, H, A, act):
+    """ppo_mlp_forward_cat_f32 on device tensors (N rows) and on pinned host
+    memory (one row, the path select_action takes): torch's forward of both
+    networks within fp32 noise."""
+    torch.manual_seed(H + A)
+    pol, val = MLP(6, H, A, act).to(dev), MLP(6, H, 1, act).to(dev)
+    obs = torch.randn(1000, 6, device=dev)
+    logits, values = ppo_amd.mlp_forward_categorical(pol, val, obs)
+    with torch.no_grad():
+        torch.testing.assert_close(logits, pol(obs), rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(values, val(obs).squeeze(1), rtol=1e-5, atol=1e-5)
+    io = torch.zeros(6 + A + 1, dtype=torch.float32, pin_memory=True)
+    io[:6] = obs[7].cpu()
+    lo, vo = io[6:6 + A].view(1, A), io[6 + A:]
+    ppo_amd.mlp_forward_categorical(pol, val, io[:6].view(1, 6), logits_out=lo, values_out=vo)
+    torch.cuda.synchronize(dev)
+    torch.testing.assert_close(lo[0], logits[7].cpu(), rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(vo[0], values[7].cpu(), rtol=1e-6, atol=1e-6)
+
+
+def test_select_action_after_network_replaced(dev):
+    """A network object replaced by one the fused forward does not run
+    (here: a GELU MLP) makes select_action fall back to torch's forward."""
+    agent = PPOAgent(cartpole_like(), TrainingConfig(hidden_size=32), device=dev)
+    o = np.zeros(4, np.float32)
+    agent.select_action(o)
+    agent.policy = torch.nn.Sequential(torch.nn.Linear(4, 32), torch.nn.GELU(),
+                                       torch.nn.Linear(32, 2)).to(dev)
+    torch.manual_seed(3)
+    a = agent.select_action(o)
+    with torch.no_grad():
+        logits = agent.policy(torch.as_tensor(o).to(dev)).cpu()
+    torch.manual_seed(3)
+    assert a == int(torch.distributions.Categorical(logits=logits).sample())

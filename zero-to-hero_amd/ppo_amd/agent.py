@@ -193,6 +193,8 @@ class PPOAgent:
         self._stage: dict = {}  # rollout length -> persistent device arrays (graph replays)
         self._last_n = -1
         self._act_ctx = None  # select_action's launch arguments and pinned buffer
+        self._act_ids: tuple = ()
+        self._act_ok = False
 
         self.rollout: list[RolloutStep] = []
         self.pending_step: PendingStep | None = None
@@ -208,7 +210,7 @@ class PPOAgent:
         Categorical so the global CPU generator is consumed as in the
         reference.  log_prob and value are 0-d CPU tensors, as there."""
         A = self.action_count
-        if self._fused_act and np.ndim(observation) == 1:
+        if self._fused_act and np.ndim(observation) == 1 and self._act_ready():
             logits, value = self._forward_pinned(observation)
         else:
             obs = torch.as_tensor(observation, dtype=torch.float32).to(self.device)
@@ -226,6 +228,15 @@ class PPOAgent:
             value=value,
         )
         return int(action.item())
+
+    def _act_ready(self) -> bool:
+        """The networks are still ones the fused forward runs (checked again
+        only when a network object was replaced)."""
+        ids = (id(self.policy), id(self.value))
+        if self._act_ids != ids:
+            self._act_ids = ids
+            self._act_ok = ops.mlp_fusable(self.policy, self.value)
+        return self._act_ok
 
     def _forward_pinned(self, observation) -> tuple[torch.Tensor, torch.Tensor]:
         """Both networks on one observation through ppo_mlp_forward_cat_f32,

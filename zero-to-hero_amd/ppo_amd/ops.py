@@ -1001,21 +1001,38 @@ def mlp_forward_categorical(
     """policy(observations) and value(observations).squeeze(-1) for
     observations [N,D] in one launch (ppo_mlp_forward_cat_f32; networks as in
     ppo_mlp_cat_grads).  Returns (logits [N,A], values [N]), written into
-    logits_out / values_out when given: two views of one buffer let one
-    copy bring both to the host (the forward half of PPOAgent.select_action,
-    ppo.py:65-79)."""
+    logits_out / values_out when given.  Any of the three tensors may be
+    pinned host memory, which the kernel reads and writes over the bus (the
+    forward half of PPOAgent.select_action, ppo.py:65-79: observation in,
+    logits and value out, one synchronisation and no copy launch); results in
+    host memory are valid once the stream is synchronised."""
     if not mlp_fusable(policy, value):
         raise ValueError("policy/value are not MLPs the fused kernel supports (see mlp_fusable)")
     lp, act = mlp_structure(policy)
     lv, _ = mlp_structure(value)
     D, H, A = lp[0].in_features, lp[0].out_features, lp[2].out_features
     device = lp[0].weight.device
-    _require(observations, "observations", (torch.float32,), device)
-    if observations.dim() != 2 or observations.shape[1] != D:
-        raise ValueError(f"observations must be [N,{D}], got {tuple(observations.shape)}")
+
+    def check(t, name, shape):
+        # a device tensor on the networks' GPU, or pinned host memory
+        if isinstance(t, torch.Tensor) and t.device.type == "cpu" and t.is_pinned():
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise TypeError(f"{name} must be contiguous fp32")
+        else:
+            _require(t, name, (torch.float32,), device)
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name} must be {shape}, got {tuple(t.shape)}")
+
+    if not isinstance(observations, torch.Tensor) or observations.dim() != 2:
+        raise ValueError("observations must be a [N,D] tensor")
     N = observations.shape[0]
-    logits_out = _out(logits_out, "logits_out", (N, A), torch.float32, device)
-    values_out = _out(values_out, "values_out", (N,), torch.float32, device)
+    check(observations, "observations", (N, D))
+    if logits_out is None:
+        logits_out = torch.empty((N, A), dtype=torch.float32, device=device)
+    if values_out is None:
+        values_out = torch.empty((N,), dtype=torch.float32, device=device)
+    check(logits_out, "logits_out", (N, A))
+    check(values_out, "values_out", (N,))
     s_actor, s_critic = _lib.Mlp3(), _lib.Mlp3()
     for st, layers in ((s_actor, lp), (s_critic, lv)):
         for i, m in enumerate(layers):
