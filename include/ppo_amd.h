@@ -59,10 +59,11 @@ const char* ppo_amd_strerror(int code);
  * update runs on the CPU in one thread).  Four launches hold workgroups that
  * wait for one another inside the launch: the resident GAE pass
  * (ppo_gae_f32 / ppo_gae_norm_f32, PPO_GAE_ROUTE_RESIDENT), the Gaussian loss
- * with its in-kernel finish (ppo_loss_gauss_f32), the categorical loss of at
- * most 2^22 rows, which also finishes in-kernel (ppo_loss_cat_f32 and its
- * _noalloc form), and the fused gradient reduction + clip + Adam of
- * ppo_mlp_cat_step_f32.  Each is launched only when
+ * with its in-kernel finish (ppo_loss_gauss_f32), the categorical loss, which
+ * also finishes in-kernel (ppo_loss_cat_f32 and its _noalloc form: every batch
+ * on the wave-tile kernels, whose workgroup 0 only collects, batches of at
+ * most 2^22 rows on the other forms), and the fused gradient reduction + clip
+ * + Adam of ppo_mlp_cat_step_f32.  Each is launched only when
  * the occupancy query says its whole grid fits on the device at once; that
  * query assumes the device's compute units are free.  When another process
  * or stream keeps part of the grid from running, a wait gives up after its
@@ -76,8 +77,15 @@ const char* ppo_amd_strerror(int code);
  * current device gave up since the previous call (on any stream), PPO_OK
  * otherwise.  It is a host synchronisation point, for callers to place where
  * they already synchronise (the Python layer checks once per update).
- * PPO_AMD_GAE_RESIDENT=0, PPO_AMD_GAUSS_FINISH=0, PPO_AMD_CAT_FINISH_MAX_ROWS=0
- * and PPO_AMD_MLP_FUSED_ADAM=0 select launches without in-kernel waits, for
+ * After a give-up, a workgroup that was late may have left arrival tags and
+ * counters that a later call on the same workspace would take for its own:
+ * when it returns PPO_ERR_WAIT_TIMEOUT the library has zeroed the scratch of
+ * ppo_loss_cat_f32_noalloc, and the caller must zero (or discard) every
+ * workspace used since the previous PPO_OK before passing it again (the
+ * Python layer zeroes its pooled workspaces).  A zeroed workspace is always
+ * valid.
+ * PPO_AMD_GAE_RESIDENT=0, PPO_AMD_GAUSS_FINISH=0, PPO_AMD_CAT_FINISH=0 and
+ * PPO_AMD_MLP_FUSED_ADAM=0 select launches without in-kernel waits, for
  * callers that share the GPU.
  */
 int ppo_wait_status(void* stream);

@@ -1,8 +1,8 @@
 """Bounded in-kernel waits that give up fail loudly.
 
 Four launches hold workgroups that wait for one another: the resident GAE
-pass, the in-kernel finish of the Gaussian loss and of the categorical loss
-(up to 2^22 rows), and the fused clip + Adam of ppo_mlp_cat_step.  The give-up is forced from the host with a poll limit of
+pass, the in-kernel finish of the Gaussian loss and of the categorical loss,
+and the fused clip + Adam of ppo_mlp_cat_step.  The give-up is forced from the host with a poll limit of
 zero (ppo_set_wait_limit), so every wait gives up at once and every kernel
 still exits normally.  Then:
   - ppo_wait_status / ops.check_waits raise PPO_ERR_WAIT_TIMEOUT, once (the
@@ -139,11 +139,12 @@ def test_gauss_finish_giveup_and_launch_route(dev, giveup, monkeypatch, B, D):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("B,A", [(1_048_576, 18), (70_001, 5), (4096, 2)])
+@pytest.mark.parametrize("B,A", [(8_388_608, 18), (1_048_576, 18), (70_001, 5), (4096, 2),
+                                 (5_000_001, 8), (3000, 24)])
 def test_categorical_finish_giveup_and_launch_route(dev, giveup, monkeypatch, B, A):
-    """Batches up to 2^22 rows finish in-kernel (workgroup 0 collects the
-    tagged partials); PPO_AMD_CAT_FINISH_MAX_ROWS=0 selects the finaliser
-    launch instead.  Both give the same results bit for bit; a give-up
+    """The categorical loss finishes in-kernel (workgroup 0 collects the
+    tagged partials; on the wave-tile kernels it takes no tiles itself);
+    PPO_AMD_CAT_FINISH=0 selects the finaliser launch instead.  Both give the same results bit for bit; a give-up
     leaves NaN scalars, intact gradients and the status raised."""
     print(f"waits cat B={B} A={A}", flush=True)
     g = torch.Generator().manual_seed(B)
@@ -151,20 +152,28 @@ def test_categorical_finish_giveup_and_launch_route(dev, giveup, monkeypatch, B,
     acts = torch.randint(0, A, (B,), generator=g, dtype=torch.int32)
     rows = [torch.randn(B, generator=g) for _ in range(5)]
     args = [x.to(dev) for x in [logits, acts] + rows]
-    monkeypatch.delenv("PPO_AMD_CAT_FINISH_MAX_ROWS", raising=False)
+    monkeypatch.delenv("PPO_AMD_CAT_FINISH", raising=False)
     good = [x.clone() for x in ops.ppo_loss_discrete_fused(*args, 0.2, 0.2, 0.5, 0.01)]
-    monkeypatch.setenv("PPO_AMD_CAT_FINISH_MAX_ROWS", "0")
+    monkeypatch.setenv("PPO_AMD_CAT_FINISH", "0")
     sep = ops.ppo_loss_discrete_fused(*args, 0.2, 0.2, 0.5, 0.01)
     for a, b in zip(good, sep):
         assert torch.equal(a, b)
-    monkeypatch.delenv("PPO_AMD_CAT_FINISH_MAX_ROWS", raising=False)
+    monkeypatch.delenv("PPO_AMD_CAT_FINISH", raising=False)
     ops.check_waits(dev)
+    # the wave-tile forms (A % 4 != 0, A <= 20) finish in-kernel at every B,
+    # the other forms up to 2^22 rows; above that the finaliser launch waits
+    # for nothing
+    in_kernel = (A % 4 != 0 and A <= 20) or B <= (1 << 22)
     with giveup:
         scalars, dlogits, dv = ops.ppo_loss_discrete_fused(*args, 0.2, 0.2, 0.5, 0.01)
         torch.cuda.synchronize(dev)
-    assert bool(torch.isnan(scalars).all())
     assert torch.equal(dlogits, good[1]) and torch.equal(dv, good[2])
-    _expect_timeout(dev)
+    if in_kernel:
+        assert bool(torch.isnan(scalars).all())
+        _expect_timeout(dev)
+    else:
+        assert torch.equal(scalars, good[0])
+        ops.check_waits(dev)
     again = ops.ppo_loss_discrete_fused(*args, 0.2, 0.2, 0.5, 0.01)
     ops.check_waits(dev)
     for a, b in zip(good, again):

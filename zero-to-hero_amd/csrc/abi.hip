@@ -92,7 +92,10 @@ extern "C" int ppo_wait_status(void* stream_ptr) {
                                       stream))))
     return st;
   if ((st = hip_status(hipStreamSynchronize(stream)))) return st;
-  return host ? PPO_ERR_WAIT_TIMEOUT : PPO_OK;
+  if (!host) return PPO_OK;
+  if ((st = scratch_clear(stream))) return st;
+  if ((st = hip_status(hipStreamSynchronize(stream)))) return st;
+  return PPO_ERR_WAIT_TIMEOUT;
 }
 
 extern "C" int ppo_set_wait_limit(int64_t polls) {

@@ -31,6 +31,12 @@ struct WaitCtl {
 // Host: fills `w` for a launch on the current device (abi.hip).  Returns a
 // PPO code.
 int wait_ctl(WaitCtl& w);
+
+// Host: zeroes the allocation-free entry point's scratch on the current
+// device, on `stream` (loss.hip).  A wait that gave up can leave arrival
+// tags and counters that a later call on the same memory would take for its
+// own; ppo_wait_status clears that memory when it reports a give-up.
+int scratch_clear(hipStream_t stream);
 // The start barrier counts arrivals on kSyncCounters counters, kSyncStride
 // words (256 bytes) apart: atomics on one address are serialised by the
 // memory (measured ~35 ns each on MI355X, so 1024 arrivals on one counter

@@ -73,6 +73,7 @@ struct LossArgs {
   uint64_t* epoch;  // Gaussian: the workspace header's call counter
   int tag_slot;     // Gaussian: partial slot holding each workgroup's arrival tag
   int finish;       // Gaussian: 1 = collect in-kernel, 0 = loss_gauss_finish_kernel does
+  int collector;    // categorical wave-tile kernel: workgroup 0 only collects (no tiles)
   WaitCtl wc;       // Gaussian in-kernel finish: poll limit, the device's wait-status word
 };
 
@@ -204,13 +205,11 @@ __device__ __forceinline__ void accumulate(double (&acc)[5], const RowOut& o, fl
 // One-block finaliser of the categorical loss, launched after the loss kernel
 // on the same stream: sums the per-block partials in a fixed order (thread t
 // takes blocks t, t + kFinalBlock, ...; then the block tree), so results are
-// deterministic, and forms the means and the total loss.  (The Gaussian
-// kernels finish in-kernel, loss_publish below.  Measured on MI355X: the
-// in-kernel finish takes the Gaussian loss of B = 2,097,152, D = 6 from 49.0
-// to 45.2 us, but the north-star categorical loss (B = 8,388,608, A = 18) from
-// 253.0 + 4.5 us to 260.6 us: its collecting workgroup's round trips run while
-// the kernel's 0.6 GB of gradients are still being written back, at several
-// us each; after the kernel boundary the finaliser's loads return quickly.)
+// deterministic, and forms the means and the total loss.  The categorical
+// and Gaussian kernels normally finish in-kernel (loss_publish below; see
+// cat_finish_in_kernel for when the categorical loss does); this launch is
+// the route without in-kernel waits.  Measured on MI355X: the in-kernel
+// finish takes the Gaussian loss of B = 2,097,152, D = 6 from 49.0 to 45.2 us.
 __global__ void __launch_bounds__(kFinalBlock) loss_finalize_kernel(LossArgs a, long nblocks) {
   constexpr int K = kLossSums;
   double tot[K];
@@ -723,8 +722,10 @@ __global__ void __launch_bounds__(kBlock) loss_cat_wtile_kernel(LossArgs a, long
   f4* s_tile4 = reinterpret_cast<f4*>(s_tile);
   double acc[5] = {0, 0, 0, 0, 0};
   WavePrefetch<ActT, PF> pf;
-  const long wstride = (long)gridDim.x * kWavesPerBlock;
-  long wt = (long)blockIdx.x * kWavesPerBlock + wid;
+  // (with a.collector, workgroup 0 takes no tiles: it only collects the others' partials)
+  const long c0 = a.collector;
+  const long wstride = ((long)gridDim.x - c0) * kWavesPerBlock;
+  long wt = (long)blockIdx.x < c0 ? nfull + 1 : ((long)blockIdx.x - c0) * kWavesPerBlock + wid;
   if (wt < nfull) wave_prefetch<ActT, PF, kVclip>(a, wt, lane, n4, pf);
 
   for (; wt < nfull; wt += wstride) {
@@ -1245,17 +1246,27 @@ int fill_common(LossArgs& a, long B, const ppo_loss_params* p, const float* old_
 
 long row_tiles(long B) { return (B + kBlock - 1) / kBlock; }
 
-// Batches of at most this many rows finish in-kernel (loss_publish) rather
-// than by the one-block finaliser launch.  Measured on MI355X (A = 18, each
-// call after a cache-evicting read): B = 1,048,576 40.9 against 42.4 us; B =
-// 8,388,608 273.2-273.8 against 273.9 us cold, but inside the PPO step the
-// in-kernel finish measured slower at that size (260.6 against 257.5 us: the
-// collecting workgroup's polls wait behind 0.6 GB of gradient write-back), so
-// large batches keep the launch.  PPO_AMD_CAT_FINISH_MAX_ROWS overrides the
-// limit (0: always the launch, which has no in-kernel wait).
-long cat_finish_max_rows() {
-  const char* env = getenv("PPO_AMD_CAT_FINISH_MAX_ROWS");
-  return env ? atol(env) : (1L << 22);
+// How the categorical loss forms its scalars: in-kernel (loss_publish:
+// every workgroup tags its partials and workgroup 0 collects them) or by the
+// one-block finaliser launch after the kernel.  Measured on MI355X (A = 18):
+//  - collected by a working workgroup, in-kernel beats the launch at B =
+//    1,048,576 (40.9 against 42.4 us per call) but not inside the PPO step
+//    at B = 8,388,608 (260.6 against 257.5 us): the collector's polls are
+//    queued behind its own wave's outstanding gradient stores (one in-order
+//    counter per wave for loads and stores);
+//  - collected by a workgroup that takes no tiles (wave-tile kernels, the
+//    other workgroups share its tiles), the polls return at once: B =
+//    8,388,608 in the step 258.2-258.4 against 261.2-262.4 us, step 291.9-292.4
+//    against 295.3-296.0 us; B = 1,048,576 40.4-40.5 against 40.7-41.0 us.
+// So the wave-tile kernels finish in-kernel with a dedicated collector at
+// every batch size, the other forms in-kernel up to kCatFinishRows rows.
+// PPO_AMD_CAT_FINISH=0 selects the finaliser launch everywhere (no
+// in-kernel wait: for callers that share the GPU).
+constexpr long kCatFinishRows = 1L << 22;
+
+bool cat_finish_in_kernel() {
+  const char* env = getenv("PPO_AMD_CAT_FINISH");
+  return !(env && env[0] == '0');
 }
 
 long cat_blocks(long B, int A) {
@@ -1358,11 +1369,9 @@ int loss_cat_launch(const float* logits, int64_t B, int32_t A, const void* actio
     // one wave of resident workgroups looping over the tiles
     const long resident = resident_blocks(kern, kBlock, lds, 0);
     blocks = std::min(blocks, resident > 0 ? resident : blocks);
-    // Below cat_finish_max_rows() rows (and with the whole grid known to be
-    // resident) the kernel finishes in-kernel as the Gaussian kernels do
-    // (loss_publish: workgroup 0 collects every workgroup's tagged partials)
-    // instead of a one-block finaliser launch.
-    if (resident > 0 && B <= cat_finish_max_rows()) {
+    // in-kernel finish (cat_finish_in_kernel), for a grid resident at once
+    if (resident > 0 && cat_finish_in_kernel() && (dense ? blocks > 1 : B <= kCatFinishRows)) {
+      a.collector = dense ? 1 : 0;
       int wst = wait_ctl(a.wc);
       if (wst) return wst;
       a.finish = 1;
@@ -1424,6 +1433,14 @@ int scratch_address(void** out) {
 }
 
 }  // namespace
+
+int scratch_clear(hipStream_t stream) {
+  void* p = nullptr;
+  int st = scratch_address(&p);
+  if (st) return st;
+  return hip_status(hipMemsetAsync(p, 0, kLossScratchBytes, stream));
+}
+
 }  // namespace ppo
 
 extern "C" int ppo_loss_cat_f32(const float* logits, int64_t B, int32_t A, const void* actions,

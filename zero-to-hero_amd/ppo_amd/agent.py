@@ -366,6 +366,8 @@ class PPOAgent:
                     returns[batch_indices],
                     **extra,
                 )
+        if dev.type == "cuda":
+            ops.check_waits(dev)
 
     def _update_fused(self, observations, actions, old_log_probs, advantages, returns,
                       old_values) -> None:

@@ -103,6 +103,13 @@ class _WorkspacePool:
     def drop(self, device: torch.device, stream: int) -> None:
         self._bufs.pop((device.index, stream), None)
 
+    def zero(self, device: torch.device) -> None:
+        """Zeroes every buffer of `device` (a zeroed workspace is valid for
+        every entry point), on the current stream."""
+        for (index, _), buf in self._bufs.items():
+            if index == device.index:
+                buf.zero_()
+
 
 _WORKSPACES = _WorkspacePool()
 
@@ -123,11 +130,21 @@ def check_waits(device: Optional[torch.device] = None) -> None:
     Gaussian loss's in-kernel finish, the fused clip + Adam of
     ppo_mlp_cat_step) assume their whole grid runs at once; when another
     process or stream on the GPU prevents that, the affected outputs are NaN
-    or the affected parameters unwritten, and this check reports it.
-    VecPPO.update and PPOAgent._update call it once per update."""
+    or the affected parameters unwritten, and this check reports it (and
+    zeroes the pooled workspaces, which a late workgroup of the failed call
+    may have left with stale arrival tags).  VecPPO.update and
+    PPOAgent._update call it once per update."""
     device = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    if device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
     with torch.cuda.device(device):
-        _lib.check("ppo_wait_status", _lib.load().ppo_wait_status(_stream(device)))
+        code = _lib.load().ppo_wait_status(_stream(device))
+        if code == _lib.PPO_ERR_WAIT_TIMEOUT:
+            # a late workgroup of the failed call may have left arrival tags
+            # and counters in the workspaces: start them afresh
+            _WORKSPACES.zero(device)
+            torch.cuda.current_stream(device).synchronize()
+        _lib.check("ppo_wait_status", code)
 
 
 def set_wait_limit(polls: Optional[int]) -> None:
