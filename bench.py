@@ -752,7 +752,7 @@ def main():
             "T": T_STEPS, "N": N_ENVS, "A": N_ACTIONS, "samples_per_step": B,
         },
         "roofline": {
-            "kernel": "ppo_loss_cat_f32 (loss_cat_wtile_kernel + loss_finalize_kernel)",
+            "kernel": "ppo_loss_cat_f32 (loss_cat_wtile_kernel, finished in-kernel)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -108,7 +108,8 @@ def _gauss(dev, B, D, seed):
     return [x.to(dev) for x in (mu, log_std, acts, old_lp, adv, ret, val, old_v)]
 
 
-@pytest.mark.parametrize("B,D", [(2_097_152, 6), (100_003, 3), (4096, 17)])
+@pytest.mark.parametrize("B,D", [(8_388_608, 6), (2_097_152, 6), (100_003, 3), (4096, 17),
+                                 (5_000_003, 8)])
 def test_gauss_finish_giveup_and_launch_route(dev, giveup, monkeypatch, B, D):
     print(f"waits gauss B={B} D={D}", flush=True)
     args = _gauss(dev, B, D, 9)

@@ -73,7 +73,7 @@ struct LossArgs {
   uint64_t* epoch;  // Gaussian: the workspace header's call counter
   int tag_slot;     // Gaussian: partial slot holding each workgroup's arrival tag
   int finish;       // Gaussian: 1 = collect in-kernel, 0 = loss_gauss_finish_kernel does
-  int collector;    // categorical wave-tile kernel: workgroup 0 only collects (no tiles)
+  int collector;    // wave-tile kernels: workgroups 0 .. collector-1 only collect (no tiles)
   WaitCtl wc;       // Gaussian in-kernel finish: poll limit, the device's wait-status word
 };
 
@@ -1143,8 +1143,10 @@ __global__ void __launch_bounds__(kBlock) loss_gauss_wtile_kernel(LossArgs a, lo
   for (int d = 0; d < MAXD; ++d) col[d] = 0.0;
   double acc[5] = {0, 0, 0, 0, 0};
   GaussWavePrefetch<PF> pf;
-  const long wstride = (long)gridDim.x * kWavesPerBlock;
-  long wt = (long)blockIdx.x * kWavesPerBlock + wid;
+  // (with a.collector = c, workgroups 0 .. c-1 take no tiles: they only collect)
+  const long c0 = a.collector;
+  const long wstride = ((long)gridDim.x - c0) * kWavesPerBlock;
+  long wt = (long)blockIdx.x < c0 ? nfull + 1 : ((long)blockIdx.x - c0) * kWavesPerBlock + wid;
   if (wt < nfull) gauss_wave_prefetch<PF, kVclip>(a, wt, lane, D, pf);
 
   for (; wt < nfull; wt += wstride) {
@@ -1562,6 +1564,13 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
   if (a.finish) {
     blocks = std::min(blocks, resident);
     if ((st = wait_ctl(a.wc))) return st;
+    // Above 2^22 rows the D + 1 collecting workgroups take no tiles (as the
+    // categorical wave-tile kernels' workgroup 0): their polls are then not
+    // queued behind their own gradient stores.  Measured on MI355X (D = 6,
+    // one call after a cache-evicting read): B = 8,388,608 151.9-152.5 us
+    // against 155.0-156.5; B = 2,097,152 45.0-45.1 against 44.7-45.0, so
+    // smaller batches keep working collectors.
+    if (wave_tiles && blocks > D + 1 && B > (1L << 22)) a.collector = D + 1;
   }
   void* args[] = {&a, const_cast<long*>(wave_tiles ? &wfull : &tiles)};
   if ((st = hip_status(
