@@ -91,6 +91,23 @@ const char* ppo_amd_strerror(int code);
 int ppo_wait_status(void* stream);
 
 /*
+ * The same take of the status word without a host synchronisation: enqueues
+ * on `stream` the read-and-clear of the word and a copy of its value (0 = no
+ * give-up) to *host_word, which must be pinned host memory (hipHostMalloc,
+ * torch pin_memory) and is valid once the stream has passed this call (an
+ * event).  For loops that check the previous iteration's status while the
+ * next one runs; on a non-zero value the caller must treat every output since
+ * its previous clean check as invalid, and zero its workspaces and (ppo_wait_reset)
+ * the library's scratch as above.
+ */
+int ppo_wait_status_async(uint32_t* host_word, void* stream);
+
+/* Zeroes the library's scratch on the current device (ordered on `stream`,
+   then synchronised): what ppo_wait_status does on a give-up, for callers
+   that learn of it through ppo_wait_status_async. */
+int ppo_wait_reset(void* stream);
+
+/*
  * Poll limit of every bounded wait launched after this call (process-wide;
  * tests and diagnostics).  0 makes every wait give up at once, so that the
  * failure path can be exercised with every kernel still exiting normally; a

@@ -24,7 +24,7 @@ def declared_functions():
 def test_header_declares_expected_functions():
     names = declared_functions()
     assert "ppo_gae_f32" in names and "ppo_loss_cat_f32" in names
-    assert len(names) == 29
+    assert len(names) == 31
 
 
 def test_library_exports_every_declared_symbol():

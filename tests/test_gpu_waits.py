@@ -236,12 +236,15 @@ def test_fused_adam_giveup_leaves_parameters(dev, giveup, monkeypatch, capturabl
         assert torch.equal(a.detach(), b.detach())
 
 
-def test_vecppo_update_raises_on_giveup(dev, giveup):
-    """VecPPO.update checks the wait status once per update."""
+@pytest.mark.parametrize("mode", ["deferred", "sync"])
+def test_vecppo_update_raises_on_giveup(dev, giveup, mode):
+    """VecPPO.update checks the wait status once per update: "sync" at the
+    end of the update that gave up, "deferred" at the end of the next update
+    (or at flush_waits)."""
     torch.manual_seed(3)
     T, N = 64, 64
     pol, val = MLP(4, 64, 2, "tanh").to(dev), MLP(4, 64, 1, "tanh").to(dev)
-    agent = VecPPO(pol, val, PPOConfig(), batch_size=1024)
+    agent = VecPPO(pol, val, PPOConfig(), batch_size=1024, check_waits=mode)
     assert agent.fused_mlp
     buf = RolloutBuffer(T, N, (4,), device=dev)
     g = torch.Generator(device=dev).manual_seed(4)
@@ -251,8 +254,43 @@ def test_vecppo_update_raises_on_giveup(dev, giveup):
         buf.add_outcome(torch.ones(N, device=dev),
                         (torch.rand(N, device=dev, generator=g) < 0.02).to(torch.uint8))
     buf.finish()
+    before = [p.detach().clone() for p in agent.parameters]
     with giveup:
-        with pytest.raises(_lib.PPOLibraryError) as ei:
-            agent.update(buf)
+        if mode == "deferred":
+            agent.update(buf)  # (reported by the next check)
+            with pytest.raises(_lib.PPOLibraryError) as ei:
+                agent.flush_waits()
+        else:
+            with pytest.raises(_lib.PPOLibraryError) as ei:
+                agent.update(buf)
     assert ei.value.code == _lib.PPO_ERR_WAIT_TIMEOUT
+    for a, b in zip(before, agent.parameters):
+        assert torch.equal(a, b.detach())  # every minibatch's Adam step gave up
     ops.check_waits(dev)
+    agent.flush_waits()
+    # a clean update after the reset, then a deferred report of nothing
+    agent.update(buf)
+    agent.update(buf)
+    agent.flush_waits()
+    assert any(not torch.equal(a, b.detach()) for a, b in zip(before, agent.parameters))
+
+
+def test_wait_poller_reports_previous_iteration(dev, giveup):
+    """WaitPoller.check reports a give-up of the previous iteration, clears
+    the workspaces, and then runs clean."""
+    poller = ops.WaitPoller()
+    r, v, d, lv = (x.to(dev) for x in _rollout(2048, 4096, 0.01, 5))
+    good = [x.clone() for x in ops.gae_normalize(r, v, d, lv, 0.99, 0.95)]
+    poller.check(dev)
+    with giveup:
+        ops.gae_normalize(r, v, d, lv, 0.99, 0.95)
+    poller.check(dev)  # takes the give-up, reports the clean iteration before
+    ops.gae_normalize(r, v, d, lv, 0.99, 0.95)  # (invalid until the report: may be stale)
+    with pytest.raises(_lib.PPOLibraryError) as ei:
+        poller.check(dev)
+    assert ei.value.code == _lib.PPO_ERR_WAIT_TIMEOUT
+    again = ops.gae_normalize(r, v, d, lv, 0.99, 0.95)
+    poller.check(dev)
+    poller.flush(dev)
+    for a, b in zip(good, again):
+        assert torch.equal(a, b)

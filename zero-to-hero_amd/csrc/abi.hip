@@ -98,6 +98,27 @@ extern "C" int ppo_wait_status(void* stream_ptr) {
   return PPO_ERR_WAIT_TIMEOUT;
 }
 
+extern "C" int ppo_wait_status_async(uint32_t* host_word, void* stream_ptr) {
+  using namespace ppo;
+  if (!host_word) return PPO_ERR_INVALID_ARG;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  unsigned* words = nullptr;
+  int st = words_address(&words);
+  if (st) return st;
+  hipLaunchKernelGGL(wait_take_kernel, dim3(1), dim3(1), 0, stream, words);
+  if ((st = last_launch_status())) return st;
+  return hip_status(hipMemcpyAsync(host_word, words + 1, sizeof(unsigned), hipMemcpyDeviceToHost,
+                                   stream));
+}
+
+extern "C" int ppo_wait_reset(void* stream_ptr) {
+  using namespace ppo;
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_ptr);
+  int st = scratch_clear(stream);
+  if (st) return st;
+  return hip_status(hipStreamSynchronize(stream));
+}
+
 extern "C" int ppo_set_wait_limit(int64_t polls) {
   ppo::g_spin.store(polls < 0 ? ppo::kSlotSpin : (long)polls, std::memory_order_relaxed);
   return PPO_OK;

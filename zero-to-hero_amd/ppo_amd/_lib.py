@@ -77,6 +77,8 @@ SIGNATURES = {
     "ppo_amd_version": (_int, []),
     "ppo_amd_strerror": (ctypes.c_char_p, [_int]),
     "ppo_wait_status": (_int, [_vp]),
+    "ppo_wait_status_async": (_int, [_vp, _vp]),
+    "ppo_wait_reset": (_int, [_vp]),
     "ppo_set_wait_limit": (_int, [_i64]),
     "ppo_gae_workspace_bytes": (_sz, [_i64, _i64]),
     "ppo_gae_route": (_int, [_i64, _i64, _int, _int]),

@@ -187,6 +187,8 @@ class PPOAgent:
                                lr=config.lr, batch_size=config.batch_size, fused_update=True,
                                graphs=graphs, fused_mlp=True)
             self.optimizer = self._vec.optimizer
+            # (the reference's update is synchronous: report a give-up at once)
+            self._vec.check_waits = "sync"
         else:
             self.optimizer = torch.optim.Adam(self.parameters, lr=config.lr)
         self.graphs = graphs

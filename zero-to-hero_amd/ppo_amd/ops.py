@@ -43,6 +43,7 @@ __all__ = [
     "mlp_fusable",
     "check_waits",
     "set_wait_limit",
+    "WaitPoller",
     "LossStats",
 ]
 
@@ -145,6 +146,64 @@ def check_waits(device: Optional[torch.device] = None) -> None:
             _WORKSPACES.zero(device)
             torch.cuda.current_stream(device).synchronize()
         _lib.check("ppo_wait_status", code)
+
+
+class WaitPoller:
+    """Wait-status checks for a loop without a synchronisation per
+    iteration (ppo_wait_status_async): check() enqueues this iteration's take
+    of the device's status word into pinned host memory and reports the
+    previous iteration's, waiting only for that earlier take (normally done:
+    the GPU is then running this iteration's work).  A give-up is therefore
+    reported by the check of the iteration after it, as a PPOLibraryError
+    with code PPO_ERR_WAIT_TIMEOUT that covers every output since the last
+    clean check; the pooled workspaces and the library's scratch are zeroed
+    before it is raised.  flush() reports everything pending, synchronously."""
+
+    def __init__(self) -> None:
+        self._words: list = [None, None]
+        self._events: list = [None, None]
+        self._k = 0
+
+    def _take(self, device: torch.device) -> None:
+        k = self._k
+        self._k ^= 1
+        if self._words[k] is None:
+            self._words[k] = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        stream = _stream(device)
+        _lib.check("ppo_wait_status_async",
+                   _lib.load().ppo_wait_status_async(self._words[k].data_ptr(), stream))
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(device))
+        self._events[k] = ev
+
+    def _pending(self, k: int) -> int:
+        ev = self._events[k]
+        if ev is None:
+            return 0
+        ev.synchronize()
+        self._events[k] = None
+        return int(self._words[k][0])
+
+    def _fail(self, device: torch.device) -> None:
+        for k in (0, 1):  # (a later take is covered by the same error)
+            self._pending(k)
+        _WORKSPACES.zero(device)
+        _lib.check("ppo_wait_reset", _lib.load().ppo_wait_reset(_stream(device)))
+        _lib.check("ppo_wait_status", _lib.PPO_ERR_WAIT_TIMEOUT)
+
+    def check(self, device: torch.device) -> None:
+        prev = self._k ^ 1
+        with torch.cuda.device(device):
+            self._take(device)
+            if self._pending(prev):
+                self._fail(device)
+
+    def flush(self, device: torch.device) -> None:
+        with torch.cuda.device(device):
+            self._take(device)
+            bad = self._pending(0) | self._pending(1)
+            if bad:
+                self._fail(device)
 
 
 def set_wait_limit(polls: Optional[int]) -> None:

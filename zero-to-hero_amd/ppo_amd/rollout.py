@@ -143,9 +143,13 @@ class VecPPO:
     The results equal the eager fused path's: the same kernels run on the
     same data.
 
-    With `check_waits` (default) each update ends with ops.check_waits(),
-    one host synchronisation that raises if an in-kernel wait of the update
-    (GAE resident pass, fused clip + Adam) gave up.
+    `check_waits` reports in-kernel waits that gave up (GAE resident pass,
+    the losses' in-kernel finish, fused clip + Adam) as PPOLibraryError
+    (PPO_ERR_WAIT_TIMEOUT): "deferred" (default, also True) checks each
+    update's status at the end of the next update (ops.WaitPoller: no
+    synchronisation per update) and `flush_waits()` checks at once; "sync"
+    synchronises at the end of every update (ops.check_waits); False does
+    not check.
     """
 
     def __init__(
@@ -162,10 +166,14 @@ class VecPPO:
         graphs: bool = False,
         graph_chunk: int = 64,
         fused_mlp: Optional[bool] = None,
-        check_waits: bool = True,
+        check_waits: bool | str = "deferred",
     ) -> None:
         self.policy, self.value = policy, value
+        if check_waits not in (True, False, "deferred", "sync"):
+            raise ValueError(f"check_waits must be True, False, 'deferred' or 'sync', got "
+                             f"{check_waits!r}")
         self.check_waits = check_waits
+        self._poller = ops.WaitPoller()
         self.ppo_config, self.gamma, self.batch_size = ppo_config, gamma, batch_size
         self.log_std = log_std
         self.generator = generator
@@ -404,9 +412,16 @@ class VecPPO:
             for e in range(cfg.epochs):
                 for start in range(0, n, self.batch_size):
                     stats = self._minibatch(perms[e, start : start + self.batch_size], arrays)
-        if self.check_waits:
+        if self.check_waits == "sync":
             ops.check_waits(device)
+        elif self.check_waits:
+            self._poller.check(arrays[0].device)
         return stats
+
+    def flush_waits(self) -> None:
+        """Reports at once (synchronising) any in-kernel wait that gave up in
+        the updates not yet checked."""
+        self._poller.flush(self.parameters[0].device)
 
     def _minibatch(self, idx: torch.Tensor, arrays: tuple) -> dict:
         """One minibatch (rows idx of the flattened rollout arrays): forward,
