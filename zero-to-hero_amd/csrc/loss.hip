@@ -73,6 +73,7 @@ struct LossArgs {
   uint64_t* epoch;  // Gaussian: the workspace header's call counter
   int tag_slot;     // Gaussian: partial slot holding each workgroup's arrival tag
   int finish;       // Gaussian: 1 = collect in-kernel, 0 = loss_gauss_finish_kernel does
+  int nopoll;       // the collection follows the loss launch: read the partials without polling
   int collector;    // wave-tile kernels: workgroups 0 .. collector-1 only collect (no tiles)
   WaitCtl wc;       // Gaussian in-kernel finish: poll limit, the device's wait-status word
 };
@@ -277,7 +278,7 @@ __device__ void collect_slots(const LossArgs& a, long nb, int slot0, uint64_t ta
   for (int k = 0; k < K; ++k) tot[k] = 0.0;
   bool ok = true;
   for (long b0 = threadIdx.x; b0 < nb; b0 += kPer * kBlock) {
-    for (long it = 0;; ++it) {
+    for (long it = 0; !a.nopoll; ++it) {
       if (it >= a.wc.spin) {
         ok = false;
         break;
@@ -391,17 +392,21 @@ __device__ void loss_publish(const LossArgs& a) {
   loss_collect<MAXD>(a, nb, s_ep, blockIdx.x, nb);
 }
 
-// The Gaussian finish as a launch of its own, for grids whose co-residency
-// the host could not establish: one workgroup collects every slot group of
-// the `nb` workgroups of the loss launch before it, whose tags are complete
-// by then (the waits find them at the first poll).
+// The Gaussian finish as a launch of its own (no in-kernel wait: for grids
+// whose co-residency the host could not establish, or PPO_AMD_GAUSS_FINISH=0):
+// workgroup g sums slot group g of the `nb` workgroups of the loss launch
+// before it, in the in-kernel collectors' order (same results bit for bit),
+// reading the partials without polling their tags (the launch boundary
+// orders them); workgroup 0 then forms the scalars and advances the call
+// counter past the tags that launch stored.
 template <int MAXD>
 __global__ void __launch_bounds__(kBlock) loss_gauss_finish_kernel(LossArgs a, long nb) {
   __shared__ uint64_t s_ep;
   if (threadIdx.x == 0)
     s_ep = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
   __syncthreads();
-  loss_collect<MAXD>(a, nb, s_ep, 0, 1);
+  a.nopoll = 1;
+  loss_collect<MAXD>(a, nb, s_ep, blockIdx.x, gridDim.x);
 }
 
 // Action index of a row, or -1 when it lies outside [0, A).
@@ -1578,7 +1583,7 @@ extern "C" int ppo_loss_gauss_f32(const float* mu, const float* log_std, int64_t
     return st;
   if (a.finish) return PPO_OK;
   if ((st = wait_ctl(a.wc))) return st;
-  hipLaunchKernelGGL(loss_gauss_finish_kernel<kMaxGaussDim>, dim3(1), dim3(kBlock), 0, stream, a,
-                     blocks);
+  hipLaunchKernelGGL(loss_gauss_finish_kernel<kMaxGaussDim>, dim3((unsigned)(D + 1)),
+                     dim3(kBlock), 0, stream, a, blocks);
   return last_launch_status();
 }
