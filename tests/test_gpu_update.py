@@ -109,3 +109,51 @@ def test_copy_from_pinned(dev):
                                           64, torch.cuda.current_stream().cuda_stream)
     assert rc == _lib.PPO_OK + 1  # PPO_ERR_INVALID_ARG: not pinned, nothing launched
     assert torch.equal(dst.cpu(), src)
+
+
+@pytest.mark.parametrize("capturable", [False, True])
+def test_clipped_adam_state_dict_round_trip_with_torch_adam(dev, capturable):
+    """ClippedAdam.state_dict() has torch.optim.Adam's layout: a torch Adam
+    loads it and continues with the same steps (and the reverse), and
+    load_state_dict copies into the existing moment buffers."""
+    torch.manual_seed(0)
+    shapes = [(8, 4), (8,), (3, 8), (3,)]
+    p1 = [torch.randn(s, device=dev, requires_grad=True) for s in shapes]
+    p2 = [p.detach().clone().requires_grad_(True) for p in p1]
+    opt = ppo_amd.ClippedAdam(p1, lr=1e-2, max_grad_norm=0.0, capturable=capturable)
+    ref_opt = torch.optim.Adam(p2, lr=1e-2)
+    for _ in range(3):
+        grads = [torch.randn(s, device=dev) for s in shapes]
+        for p, g in zip(p1, grads):
+            p.grad = g.clone()
+        for p, g in zip(p2, grads):
+            p.grad = g.clone()
+        opt.step()
+        ref_opt.step()
+    sd = opt.state_dict()
+    assert sd["param_groups"][0]["params"] == [0, 1, 2, 3]
+    fresh = torch.optim.Adam([p.detach().clone().requires_grad_(True) for p in p1], lr=1e-2)
+    fresh.load_state_dict(sd)
+    for i in range(4):
+        torch.testing.assert_close(fresh.state[fresh.param_groups[0]["params"][i]]["exp_avg"],
+                                   ref_opt.state[p2[i]]["exp_avg"], rtol=1e-5, atol=1e-7)
+    buf = opt.exp_avg[0]
+    opt2 = ppo_amd.ClippedAdam(p1, lr=1e-3, max_grad_norm=0.0, capturable=capturable)
+    keep = opt2.exp_avg[0]
+    opt2.load_state_dict(ref_opt.state_dict())
+    assert opt2.exp_avg[0] is keep and opt2.lr == 1e-2
+    assert opt2.step_count() == 3
+    torch.testing.assert_close(opt2.exp_avg[0], buf, rtol=1e-5, atol=1e-7)
+
+
+def test_keep_grads_zeroes_in_place(dev):
+    p = torch.randn(4, device=dev, requires_grad=True)
+    opt = ppo_amd.ClippedAdam([p])
+    p.grad = torch.ones(4, device=dev)
+    g = p.grad
+    opt.keep_grads = True
+    opt.zero_grad()
+    assert p.grad is g and bool((g == 0).all())
+    opt.keep_grads = False
+    opt.zero_grad()
+    assert p.grad is None

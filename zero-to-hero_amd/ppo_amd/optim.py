@@ -71,13 +71,66 @@ class ClippedAdam:
             return int(self.step_t.item())
         return max(self.steps)
 
+    # True when the parameters' gradient buffers must keep their storage
+    # (captured graphs and the fused MLP step write into them): zero_grad then
+    # zeroes them in place whatever set_to_none says.
+    keep_grads = False
+
     def zero_grad(self, set_to_none: bool = True) -> None:
         for p in self.params:
             if p.grad is not None:
-                if set_to_none:
+                if set_to_none and not self.keep_grads:
                     p.grad = None
                 else:
                     p.grad.zero_()
+
+    def state_dict(self) -> dict:
+        """The state in torch.optim.Adam's layout (per parameter index:
+        step, exp_avg, exp_avg_sq; one param group), so that it can be saved,
+        and loaded into either optimizer."""
+        if self.capturable:
+            steps = [self.step_t.detach().to(torch.float32).cpu()] * len(self.params)
+        else:
+            steps = [torch.tensor(float(k)) for k in self.steps]
+        state = {i: {"step": steps[i].clone(), "exp_avg": self.exp_avg[i].detach().clone(),
+                     "exp_avg_sq": self.exp_avg_sq[i].detach().clone()}
+                 for i in range(len(self.params))}
+        group = {"lr": self.lr, "betas": tuple(self.betas), "eps": self.eps,
+                 "weight_decay": 0.0, "amsgrad": False, "max_grad_norm": self.max_grad_norm,
+                 "params": list(range(len(self.params)))}
+        return {"state": state, "param_groups": [group]}
+
+    @torch.no_grad()
+    def load_state_dict(self, state_dict: dict) -> None:
+        """Loads a state_dict() of this class or of torch.optim.Adam over the
+        same parameters (one group, no weight decay, no amsgrad), copying the
+        moments into the existing buffers (their storage stays, as captured
+        graphs need).  Parameters absent from the state start at step 0."""
+        groups = state_dict["param_groups"]
+        if len(groups) != 1 or len(groups[0]["params"]) != len(self.params):
+            raise ValueError("expected one parameter group over the same parameters")
+        g = groups[0]
+        if g.get("weight_decay", 0.0) or g.get("amsgrad", False):
+            raise ValueError("ClippedAdam has no weight decay and no amsgrad")
+        self.lr, self.betas, self.eps = g["lr"], tuple(g["betas"]), g["eps"]
+        self.max_grad_norm = g.get("max_grad_norm", self.max_grad_norm)
+        steps = []
+        for i, key in enumerate(g["params"]):
+            st = state_dict["state"].get(key)
+            if st is None:
+                self.exp_avg[i].zero_()
+                self.exp_avg_sq[i].zero_()
+                steps.append(0)
+                continue
+            self.exp_avg[i].copy_(st["exp_avg"])
+            self.exp_avg_sq[i].copy_(st["exp_avg_sq"])
+            steps.append(int(float(st["step"])))
+        if self.capturable:
+            if len(set(steps)) != 1:
+                raise ValueError("capturable mode keeps one step count for all parameters")
+            self.step_t.fill_(steps[0])
+        else:
+            self.steps = steps
 
     def _fused_params(self) -> tuple:
         """Adam parameters for a fused step of all tensors together (the

@@ -208,6 +208,8 @@ class VecPPO:
             self.optimizer = ClippedAdam(self.parameters, lr=lr,
                                          max_grad_norm=ppo_config.gradient_clip,
                                          capturable=graphs)
+            # the fused MLP step and captured graphs write into the gradient buffers
+            self.optimizer.keep_grads = self.fused_mlp or graphs
         else:
             self.optimizer = torch.optim.Adam(self.parameters, lr=lr)
 
