@@ -298,7 +298,10 @@ def suite(torch, lib, dev, stream_timing=True, cpu=True):
     around a single call leave on the device.  Unless `cpu` is False, each of
     configs 2-5 is also run once through the CPU restatement (oracle/) on the
     same inputs (`cpu_us`; config 3 through the C recurrence on one core, the
-    others through numpy / torch on the host's threads)."""
+    others through numpy / torch on the host's threads).  `copy_us` /
+    `copy_frac`: torch's device copy_ moving the same bytes, timed like `us`
+    (the floor of a single timed call at that size); an `event_floor` line
+    gives the event pair around no work."""
     import ctypes
 
     from ppo_amd import _lib
@@ -439,10 +442,26 @@ def suite(torch, lib, dev, stream_timing=True, cpu=True):
                 time_stream(torch, [lambda s_=s_: (s_.gae(), s_.loss()) for s_ in steps], 8)
                 if stream_timing else None))
     del steps, st, x
+    # The floor of this timing at each byte count: torch's device copy_ moving
+    # the same bytes (half read, half written), and an event pair around no
+    # work, each after the same cache-evicting read.
+    copy_us = {}
+    for name, units, bpu, t, ts in out:
+        n = units * bpu // 8
+        src = torch.ones(n, **f32)
+        dst = torch.empty_like(src)
+        copy_us[name] = time_events(torch, lambda: dst.copy_(src), 30, flush)
+        del src, dst
+    floor = time_events(torch, lambda: None, 30, flush)
+    print(json.dumps({"suite": "event_floor", "us": round(floor * 1e6, 2),
+                      "what": "an event pair around no work, after the cache-evicting read"}),
+          flush=True)
     for name, units, bpu, t, ts in out:
         gbs = units * bpu / t / 1e9
         line = {"suite": name, "units": units, "bytes_per_unit": bpu, "us": round(t * 1e6, 2),
-                "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+                "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "copy_us": round(copy_us[name] * 1e6, 2),
+                "copy_frac": round(units * bpu / copy_us[name] / 1e9 / HBM_PEAK_GBS, 4)}
         if ts is not None:
             line["us_stream"] = round(ts * 1e6, 2)
             line["frac_stream"] = round(units * bpu / ts / 1e9 / HBM_PEAK_GBS, 4)
