@@ -518,7 +518,6 @@ enum TileLayout {
 
 template <int VW, int L, int kLayout, int kMode>
 __global__ void __launch_bounds__(kBlock) gae_tile_kernel(GaeArgs a) {
-  constexpr bool kSolo = kLayout == kSoloTile;
   constexpr bool kLds = kLayout == kStacked;
   constexpr bool kIsFinal = kMode >= kFinal;
   __shared__ double s_a[kLds ? kBlock * VW : 1];
