@@ -3,7 +3,8 @@
 A "step" is one pass of the PPO update hot path over one synthetic rollout of
 T x N = 2048 x 4096 = 8,388,608 samples (the benchmark's GAE + normalise rollout):
   1. ppo_gae_norm_f32  — GAE with bootstrap + returns + advantage
-                         normalisation (rl/deep/agents/ppo.py:123-127)
+                         normalisation (rl/deep/agents/ppo.py:123-127), the
+                         normalised advantages written over the raw ones
   2. ppo_loss_cat_f32  — fused categorical PPO loss forward+backward over all
                          B = T*N samples, A = 18 actions, vf_clip = 0.2
                          (ppo.py:150-169; A = 18, value clipping 0.2)
@@ -38,6 +39,7 @@ HBM_PEAK_GBS = 8000.0
 T_STEPS, N_ENVS, N_ACTIONS = 2048, 4096, 18
 ROLLOUT_COPIES = 4  # rollouts the timed steps cycle through (4 x 75 MB > the 256 MB Infinity Cache)
 GAE_BYTES = 21       # r 4 + V 4 + done 1 in; adv 4 + ret 4 + adv_n 4 out
+GAE_INPLACE_BYTES = 17  # the same, normalised in place: ret 4 + adv_n 4 out
 LOSS_CAT_BYTES = 172  # logits 72 + 6 x 4 per-row inputs in; dlogits 72 + dvalue 4 out
 GAUSS_BYTES = 96     # mu 24 + actions 24 + 5 x 4 in; dmu 24 + dvalue 4 out
 SCAN_BYTES = 17      # r, V, done in; adv, ret out
@@ -101,6 +103,9 @@ ROLLOUT_KEYS = ("rewards", "values", "dones", "last_value")
 class Step:
     """The two C-ABI calls of one update step, on torch's current stream,
     with preallocated outputs (nothing allocated inside the timed loop).
+    The advantages are normalised in place, as ppo.py:127 keeps only the
+    normalised ones: the GAE call writes the returns and the normalised
+    advantages (17 bytes per sample with its inputs).
 
     With copies > 1 the step keeps that many copies of the rollout (rewards,
     values, dones, last value: 75 MB each at T x N = 2048 x 4096) and next()
@@ -121,7 +126,6 @@ class Step:
         B, A = x["logits"].shape
         self.T, self.N, self.B, self.A = T, N, B, A
         f32 = dict(dtype=torch.float32, device=dev)
-        self.adv = torch.empty(T, N, **f32)
         self.ret = torch.empty(T, N, **f32)
         self.adv_n = torch.empty(T, N, **f32)
         self.stats = torch.empty(2, **f32)
@@ -143,7 +147,7 @@ class Step:
         rc = self.lib.ppo_gae_norm_f32(
             x["rewards"].data_ptr(), x["values"].data_ptr(), x["dones"].data_ptr(),
             x["last_value"].data_ptr(), self.T, self.N, 0.99, 0.95, 1e-8,
-            self.adv.data_ptr(), self.ret.data_ptr(), self.adv_n.data_ptr(),
+            self.adv_n.data_ptr(), self.ret.data_ptr(), self.adv_n.data_ptr(),
             self.stats.data_ptr(), self.ws_gae.data_ptr(), self.ws_gae.numel(), self.stream)
         if rc:
             raise RuntimeError(f"ppo_gae_norm_f32 returned {rc}")
@@ -337,19 +341,23 @@ def suite(torch, lib, dev, stream_timing=True, cpu=True):
         del calls
 
     # config 2 and 3: GAE over [T,N]
-    for name, T, N, pd, gamma, norm, copies in (
-            ("config2_gae_norm", 2048, 4096, 0.01, 0.99, True, 4),
-            ("config3_long_scan", 1_048_576, 16, 0.001, 0.999, False, 3)):
+    for name, T, N, pd, gamma, norm, inplace, copies in (
+            ("config2_gae_norm", 2048, 4096, 0.01, 0.99, True, False, 4),
+            ("config2_gae_norm_in_place", 2048, 4096, 0.01, 0.99, True, True, 4),
+            ("config3_long_scan", 1_048_576, 16, 0.001, 0.999, False, False, 3)):
         r = torch.randn(T, N, generator=g, **f32)
         v = torch.randn(T, N, generator=g, **f32)
         d = (torch.rand(T, N, device=dev, generator=g) < pd).to(torch.uint8)
         lv = torch.randn(N, generator=g, **f32)
         w = ws(lib.ppo_gae_workspace_bytes(T, N))
 
-        def make(k, r=r, v=v, d=d, lv=lv, T=T, N=N, gamma=gamma, norm=norm, w=w):
+        def make(k, r=r, v=v, d=d, lv=lv, T=T, N=N, gamma=gamma, norm=norm, inplace=inplace,
+                 w=w):
             if k:
                 r, v, d = r.clone(), v.clone(), d.clone()
             adv, ret, advn = (torch.empty(T, N, **f32) for _ in range(3))
+            if inplace:
+                advn = adv
             if norm:
                 return lambda: lib.ppo_gae_norm_f32(
                     r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N, gamma, 0.95,
@@ -359,8 +367,9 @@ def suite(torch, lib, dev, stream_timing=True, cpu=True):
                 r.data_ptr(), v.data_ptr(), d.data_ptr(), lv.data_ptr(), T, N, gamma, 0.95,
                 adv.data_ptr(), ret.data_ptr(), w.data_ptr(), w.numel(), stream)
 
-        measure(name, T * N, GAE_BYTES if norm else SCAN_BYTES, make, copies)
-        if cpu:
+        measure(name, T * N,
+                (GAE_INPLACE_BYTES if inplace else GAE_BYTES) if norm else SCAN_BYTES, make, copies)
+        if cpu and not inplace:
             from oracle import ppo_oracle as ref
 
             rn, vn, dn, ln = (t.cpu().numpy() for t in (r, v, d, lv))
@@ -437,7 +446,7 @@ def suite(torch, lib, dev, stream_timing=True, cpu=True):
     out.append(("north_star_A2_loss", st.B, LOSS_CAT_A2_BYTES,
                 time_events(torch, st.loss, 30, flush),
                 time_stream(torch, [s_.loss for s_ in steps], 8) if stream_timing else None))
-    out.append(("north_star_A2_step", st.B, GAE_BYTES + LOSS_CAT_A2_BYTES,
+    out.append(("north_star_A2_step", st.B, GAE_INPLACE_BYTES + LOSS_CAT_A2_BYTES,
                 time_events(torch, lambda: (st.gae(), st.loss()), 30, flush),
                 time_stream(torch, [lambda s_=s_: (s_.gae(), s_.loss()) for s_ in steps], 8)
                 if stream_timing else None))
@@ -783,8 +792,9 @@ def main():
         },
         "gae_norm": {
             "avg_call_us": round(t_gae * 1e6, 2),
-            "achieved_GBs": round(GAE_BYTES * B / t_gae / 1e9, 1),
-            "frac": round(GAE_BYTES * B / t_gae / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_sample": GAE_INPLACE_BYTES,
+            "achieved_GBs": round(GAE_INPLACE_BYTES * B / t_gae / 1e9, 1),
+            "frac": round(GAE_INPLACE_BYTES * B / t_gae / 1e9 / HBM_PEAK_GBS, 4),
         },
         "cpu_baseline": cpu,
     }

@@ -859,3 +859,25 @@ def test_empty_rollouts(dev, T, N):
     assert torch.isnan(stats).all()
     assert ppo_amd.normalize_advantages(adv).shape == (T, N)
     assert ppo_amd.discounted_returns(r, dones=d).shape == (T, N)
+
+
+@pytest.mark.parametrize("T,N", [(2048, 4096), (2048, 64), (300, 4096), (1, 1), (5000, 3)])
+def test_gae_normalise_in_place_matches_separate_outputs(dev, T, N):
+    """keep_raw=False (adv_norm_out aliasing adv_out, the resident pass then
+    storing no raw advantages) gives the normalised advantages and returns of
+    the separate-output call bit for bit, on the resident route at the
+    benchmark shape and on the other routes."""
+    print(f"gae in place T={T} N={N}", flush=True)
+    r, v, d, lv = (x.to(dev) for x in _inputs(T, N, 0.01, seed=31))
+    adv, ret, adv_n, st = ppo_amd.gae_normalize(r, v, d, lv, return_stats=True)
+    buf = torch.full((2, T, N), 7.0, device=dev)
+    a2, r2, n2, st2 = ppo_amd.gae_normalize(r, v, d, lv, return_stats=True,
+                                             out=(buf[0], buf[1]), keep_raw=False)
+    torch.cuda.synchronize(dev)
+    assert a2 is n2 and a2.data_ptr() == buf[0].data_ptr()
+    assert torch.equal(n2, adv_n) and torch.equal(r2, ret)
+    torch.testing.assert_close(st2, st, rtol=0, atol=0, equal_nan=True)
+    if (T, N) == (2048, 4096):
+        assert _route(T, N, True) == "resident"
+    if T * N > 1:
+        assert not torch.equal(n2, adv)

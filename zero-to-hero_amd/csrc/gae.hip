@@ -1940,10 +1940,13 @@ __global__ void __launch_bounds__(kResBlock) gae_resident_kernel(GaeArgs a) {
           // whole lines, they leave no dirty lines to be written back during
           // the next kernel.  Measured on MI355X, T x N = 2048 x 4096: PPO step
           // 294.4 -> 292.4 us, back-to-back calls 46.8 -> 40.7 us.
-          if constexpr (kStats && E >= 32)
-            store_vec_nt<VW>(at_byte(a.adv, off), r[i]);
-          else
+          // Normalised in place (adv_n aliases adv), the raw advantages are
+          // overwritten below from these registers: not stored at all.
+          if constexpr (kStats && E >= 32) {
+            if (a.adv != a.adv_n) store_vec_nt<VW>(at_byte(a.adv, off), r[i]);
+          } else if (!kStats || a.adv != a.adv_n) {
             store_vec<VW>(at_byte(a.adv, off), r[i]);
+          }
           if (a.ret) {
             float rt[VW];
 #pragma unroll

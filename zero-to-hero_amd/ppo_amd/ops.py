@@ -317,14 +317,26 @@ def gae_normalize(
     eps: float = 1e-8,
     return_stats: bool = False,
     out: Optional[tuple] = None,
+    keep_raw: bool = True,
 ):
     """gae() plus the normalised advantages of ppo.py:126-127, fused: the
     advantage mean/std are accumulated inside the GAE pass.  Returns
     (advantages, returns, normalized_advantages[, stats]) where stats is a
     [2] fp32 device tensor {mean, std}; the first three are written into
-    `out` when given."""
+    `out` when given.
+
+    keep_raw=False drops the unnormalised advantages, as ppo.py:127 does by
+    rebinding `advantages`: the normalised ones are written where the raw
+    ones would be (the resident pass then skips one store per element), the
+    returned tuple holds that tensor first and third, and `out` is
+    (normalized_advantages, returns)."""
     device, T, N = _gae_inputs(rewards, values, dones, last_value)
-    adv, ret, adv_n = _outputs(out, 3, rewards, (rewards, values, dones, last_value))
+    inputs = (rewards, values, dones, last_value)
+    if keep_raw:
+        adv, ret, adv_n = _outputs(out, 3, rewards, inputs)
+    else:
+        adv, ret = _outputs(out, 2, rewards, inputs)
+        adv_n = adv
     stats = torch.empty(2, dtype=torch.float32, device=device)
     if T * N == 0:
         stats.fill_(float("nan"))  # torch's mean and std of no elements

@@ -53,7 +53,7 @@ class RolloutBuffer:
         self.dones = torch.zeros((T, N), dtype=torch.uint8, device=dev)
         self.last_value = torch.zeros(N, **f32)
         self.step = 0
-        self._gae_out: Optional[list] = None  # advantages, returns, normalised ([T,N] each)
+        self._gae_out: Optional[list] = None  # normalised advantages, returns ([T,N] each)
 
     def add(self, observations, actions, rewards, dones, values, log_probs) -> None:
         """Store step `self.step` for all N envs (ppo.py:93-106, batched)."""
@@ -103,14 +103,16 @@ class RolloutBuffer:
     def _advantages_in_place(self, gamma: float, lam: float, eps: float = 1e-8):
         """compute_advantages(normalize=True) into storage the buffer keeps:
         the same addresses on every call (graph replays read them), contents
-        overwritten by the next call."""
+        overwritten by the next call.  The raw advantages are not kept (the
+        first and third items are the normalised ones)."""
         T = self.step
         if self._gae_out is None:
             self._gae_out = [torch.empty((self.T, self.N), dtype=torch.float32, device=self.device)
-                             for _ in range(3)]
+                             for _ in range(2)]
         out = tuple(o[:T] for o in self._gae_out)
         r, v, d = self.rewards[:T], self.values[:T], self.dones[:T]
-        return ops.gae_normalize(r, v, d, self.last_value, gamma, lam, eps, out=out)
+        return ops.gae_normalize(r, v, d, self.last_value, gamma, lam, eps, out=out,
+                                 keep_raw=False)
 
 
 class VecPPO:
