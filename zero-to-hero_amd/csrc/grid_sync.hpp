@@ -9,7 +9,8 @@
 // the slots it will fill and then arrives at a start barrier (res_arrive);
 // slots are read only after the barrier is complete, so no reader sees what
 // a slot held before the call.  Waits are bounded: a slot still empty after
-// kSlotSpin polls reads as NaN, which then shows in the outputs.
+// the launch's poll limit reads as NaN and raises the device's wait-status
+// word; the kernels then write NaN over their outputs or skip their writes.
 #pragma once
 
 #include <atomic>
