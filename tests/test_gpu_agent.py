@@ -421,8 +421,35 @@ def test_mlp_forward_categorical_matches_torch(dev, H, A, act):
     lo, vo = io[6:6 + A].view(1, A), io[6 + A:]
     ppo_amd.mlp_forward_categorical(pol, val, io[:6].view(1, 6), logits_out=lo, values_out=vo)
     torch.cuda.synchronize(dev)
-    torch.testing.assert_close(lo[0], logits[7].cpu(), rtol=1e-6, atol=1e-6)
-    torch.testing.assert_close(vo[0], values[7].cpu(), rtol=1e-6, atol=1e-6)
+    # (the one-row launch runs the one-workgroup form, whose arithmetic is
+    # the many-row form's step for step)
+    assert torch.equal(lo[0], logits[7].cpu()) and torch.equal(vo[0], values[7].cpu())
+
+
+@pytest.mark.parametrize("D,H,A,act", [(4, 128, 2, "relu"), (64, 128, 32, "tanh"),
+                                       (6, 64, 18, "relu"), (5, 32, 17, "tanh"),
+                                       (3, 16, 1, "relu")])
+def test_act_one_workgroup_form_matches_many_row_form(dev, D, H, A, act):
+    """Launches of at most 16 rows (one workgroup, weights loaded up front)
+    give the rows of a 40-row launch bit for bit: logits and values of
+    ppo_mlp_forward_cat_f32, actions, log-probabilities and values of
+    ppo_mlp_act_cat_f32 (the same uniforms)."""
+    print(f"act forms D={D} H={H} A={A} {act}", flush=True)
+    torch.manual_seed(D * H + A)
+    pol, val = MLP(D, H, A, act).to(dev), MLP(D, H, 1, act).to(dev)
+    obs = torch.randn(40, D, device=dev)
+    u = torch.rand(40, device=dev)
+    logits, values = ppo_amd.mlp_forward_categorical(pol, val, obs)
+    acts, lps, vals = ppo_amd.mlp_act_categorical(pol, val, obs, uniforms=u)
+    for lo, hi in ((0, 16), (16, 17), (23, 40 - 11)):
+        l2, v2 = ppo_amd.mlp_forward_categorical(pol, val, obs[lo:hi].contiguous())
+        a2, p2, w2 = ppo_amd.mlp_act_categorical(pol, val, obs[lo:hi].contiguous(),
+                                                 uniforms=u[lo:hi].contiguous())
+        assert torch.equal(l2, logits[lo:hi]) and torch.equal(v2, values[lo:hi])
+        assert torch.equal(a2, acts[lo:hi]) and torch.equal(p2, lps[lo:hi])
+        assert torch.equal(w2, vals[lo:hi])
+    with torch.no_grad():
+        torch.testing.assert_close(logits, pol(obs), rtol=1e-5, atol=1e-5)
 
 
 def test_select_action_after_network_replaced(dev):

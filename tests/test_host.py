@@ -101,3 +101,40 @@ def test_vecppo_graph_options_validated():
         ppo_amd.VecPPO(pol, val, graphs=True, fused_update=False)
     with pytest.raises(ValueError, match="graph_chunk"):
         ppo_amd.VecPPO(pol, val, graphs=True, graph_chunk=0)
+
+
+def test_sample_categorical_matches_torch_distribution():
+    """agent.sample_categorical draws the action a Categorical(logits) draws
+    from the same global-generator state, returns its log_prob bit for bit,
+    and leaves the generator in the same state (ppo.py:72-78)."""
+    from torch.distributions import Categorical
+
+    from ppo_amd.agent import sample_categorical
+
+    g = torch.Generator().manual_seed(3)
+    cases = [torch.randn(A, generator=g) * s for A in (1, 2, 3, 18) for s in (1e-3, 1.0, 40.0)
+             for _ in range(30)]
+    cases += [torch.tensor([0.0, float("-inf")]), torch.tensor([-1e30, 0.0, 1e30])]
+    for k, logits in enumerate(cases):
+        torch.manual_seed(k)
+        dist = Categorical(logits=logits)
+        a_ref = dist.sample()
+        lp_ref = dist.log_prob(a_ref)
+        state_ref = torch.get_rng_state()
+        torch.manual_seed(k)
+        a, lp = sample_categorical(logits)
+        assert a == int(a_ref) and lp.dim() == 0 and lp.dtype == torch.float32
+        assert torch.equal(lp, lp_ref), (k, lp, lp_ref)
+        assert torch.equal(torch.get_rng_state(), state_ref)
+
+
+def test_sample_categorical_rejects_nan_logits_like_the_distribution():
+    from torch.distributions import Categorical
+
+    from ppo_amd.agent import sample_categorical
+
+    bad = torch.tensor([0.5, float("nan")])
+    with pytest.raises(ValueError):
+        Categorical(logits=bad)
+    with pytest.raises(ValueError):
+        sample_categorical(bad)

@@ -285,14 +285,15 @@ __device__ __forceinline__ void net_backward(const MlpNet& net, const NetOffsets
 // Forward of both networks for the workgroup's 16 rows x (observations in
 // s_x): hidden activations into a1/a2 (actor) and c1/c2 (critic), logits into
 // z [16][kZld], values into v [16].  Tiles (network, column tile) over the
-// waves; LDS-only barriers between the layers and after the last.
-template <int H, int kAct>
+// waves of a kBlock-thread workgroup; LDS-only barriers between the layers
+// and after the last.
+template <int H, int kAct, int kBlock = kMlpBlock>
 __device__ __forceinline__ void mlp_forward(const MlpNet& actor, const MlpNet& critic,
                                             const float* x, int D, int A, float* a1, float* a2,
                                             float* c1, float* c2, float* z, float* v) {
   constexpr int ld = act_ld<H>();
   constexpr int NT = H / 16;
-  constexpr int kWaves = kMlpBlock / kWave;
+  constexpr int kWaves = kBlock / kWave;
   const int w = threadIdx.x / kWave;
   for (int t = w; t < 2 * NT; t += kWaves) {
     const MlpNet& net = t < NT ? actor : critic;
@@ -525,8 +526,18 @@ struct ActArgs {
   float* logits;
 };
 
-template <int H, int kAct>
-__global__ void __launch_bounds__(kMlpBlock) mlp_act_cat_kernel(ActArgs a) {
+// Threads of the one-workgroup act launch (at most kMlpRows rows, where the
+// chain of dependent loads and barriers is the kernel's time): a wave per
+// 16-column tile of both networks' hidden layers (2 H / 16 tiles), so that no
+// wave works through several tiles one after another; at least kMlpBlock.
+template <int H>
+constexpr int act_wide_block() {
+  return 2 * (H / 16) * kWave > kMlpBlock ? 2 * (H / 16) * kWave : kMlpBlock;
+}
+
+// kBlock threads: kMlpBlock, or act_wide_block<H>() for one workgroup.
+template <int H, int kAct, int kBlock = kMlpBlock>
+__global__ void __launch_bounds__(kBlock) mlp_act_cat_kernel(ActArgs a) {
   constexpr int R = kMlpRows;
   constexpr int ld = act_ld<H>();
   __shared__ float s_x[R * kXld];
@@ -536,7 +547,7 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_act_cat_kernel(ActArgs a) {
   const int tid = threadIdx.x;
   const long row0 = (long)blockIdx.x * R;
   const int D = a.D;
-  for (int e = tid; e < R * D; e += kMlpBlock) {
+  for (int e = tid; e < R * D; e += kBlock) {
     const int r = e / D, c = e - (e / D) * D;
     const long row = row0 + r;
     float x = 0.0f;
@@ -548,9 +559,10 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_act_cat_kernel(ActArgs a) {
   }
   const float u = a.u && tid < R && row0 + tid < a.N ? a.u[row0 + tid] : 0.0f;
   lds_barrier();
-  mlp_forward<H, kAct>(a.actor, a.critic, s_x, D, a.A, s_a1, s_a2, s_c1, s_c2, s_z, s_v);
+  mlp_forward<H, kAct, kBlock>(a.actor, a.critic, s_x, D, a.A, s_a1, s_a2, s_c1, s_c2, s_z,
+                               s_v);
   if (a.logits) {
-    for (int e = tid; e < R * a.A; e += kMlpBlock) {
+    for (int e = tid; e < R * a.A; e += kBlock) {
       const int r = e / a.A, j = e - r * a.A;
       if (row0 + r < a.N) a.logits[(row0 + r) * a.A + j] = s_z[r * kZld + j];
     }
@@ -970,13 +982,25 @@ const void* mlp_kernel_act(int H) {
   }
 }
 
+int act_wide_threads(int H) {
+  switch (H) {
+    case 64: return act_wide_block<64>();
+    case 128: return act_wide_block<128>();
+    default: return kMlpBlock;
+  }
+}
+
 template <int kAct>
-const void* act_kernel_act(int H) {
+const void* act_kernel_act(int H, bool wide) {
   switch (H) {
     case 16: return (const void*)mlp_act_cat_kernel<16, kAct>;
     case 32: return (const void*)mlp_act_cat_kernel<32, kAct>;
-    case 64: return (const void*)mlp_act_cat_kernel<64, kAct>;
-    case 128: return (const void*)mlp_act_cat_kernel<128, kAct>;
+    case 64:
+      return wide ? (const void*)mlp_act_cat_kernel<64, kAct, act_wide_block<64>()>
+                  : (const void*)mlp_act_cat_kernel<64, kAct>;
+    case 128:
+      return wide ? (const void*)mlp_act_cat_kernel<128, kAct, act_wide_block<128>()>
+                  : (const void*)mlp_act_cat_kernel<128, kAct>;
     default: return nullptr;
   }
 }
@@ -1244,8 +1268,10 @@ int launch_act(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic, int32_t ob
   if (a.N < 0) return PPO_ERR_INVALID_ARG;
   if (obs_dim <= 0 || obs_dim > kMlpMaxIn || A <= 0 || A > kMlpMaxA) return PPO_ERR_UNSUPPORTED;
   if (activation != PPO_ACT_RELU && activation != PPO_ACT_TANH) return PPO_ERR_INVALID_ARG;
-  const void* kern = activation == PPO_ACT_TANH ? act_kernel_act<PPO_ACT_TANH>(hidden)
-                                                : act_kernel_act<PPO_ACT_RELU>(hidden);
+  // (one workgroup: the wide form, measured on MI355X at H = 128: 9.6 -> 8.4 us)
+  const bool wide = a.N <= kMlpRows;
+  const void* kern = activation == PPO_ACT_TANH ? act_kernel_act<PPO_ACT_TANH>(hidden, wide)
+                                                : act_kernel_act<PPO_ACT_RELU>(hidden, wide);
   if (!kern) return PPO_ERR_UNSUPPORTED;
   if (!mlp_net_weights_ok(actor) || !mlp_net_weights_ok(critic)) return PPO_ERR_INVALID_ARG;
   if (a.N == 0) return PPO_OK;
@@ -1257,7 +1283,8 @@ int launch_act(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic, int32_t ob
   a.A = A;
   void* args[] = {&a};
   const long blocks = (a.N + kMlpRows - 1) / kMlpRows;
-  return hip_status(hipLaunchKernel(kern, dim3((unsigned)blocks), dim3(kMlpBlock), args, 0,
+  const int threads = wide ? act_wide_threads(hidden) : kMlpBlock;
+  return hip_status(hipLaunchKernel(kern, dim3((unsigned)blocks), dim3(threads), args, 0,
                                     reinterpret_cast<hipStream_t>(stream_ptr)));
 }
 

@@ -17,7 +17,8 @@ this one unchanged.  Differences, all on the device side:
   * otherwise `_update_batch` computes the loss and its gradient with the
     fused loss kernel and the MLPs, clip_grad_norm_ and Adam stay in torch;
   * `select_action` brings the logits and the value to the host in one copy
-    (one forward launch for both networks when fused).
+    (one forward launch for both networks when fused) and draws the action
+    with the operations of a Categorical, not the distribution object.
 The environment is duck-typed (anything with observation_space.shape and
 action_space.n), since gymnasium is not a dependency here.
 """
@@ -31,7 +32,6 @@ from typing import Optional
 import numpy as np
 import torch
 from torch import nn
-from torch.distributions import Categorical
 
 from . import ops
 
@@ -120,6 +120,29 @@ class PendingStep:
     value: torch.Tensor
 
 
+def sample_categorical(logits: torch.Tensor) -> tuple[int, torch.Tensor]:
+    """Categorical(logits=logits).sample() and .log_prob() of that sample, as
+    ppo.py:72-78 uses them, for one CPU row of logits [A]: the operations
+    torch.distributions.Categorical runs (normalise by logsumexp, softmax,
+    one torch.multinomial draw with replacement on the global generator,
+    gather of the normalised logit), without building the distribution
+    object, whose construction costs more than the draw.  Same action, same
+    log-probability bits and same generator state as the distribution for
+    the same logits.  Returns (action, 0-d log-probability tensor).  NaN
+    logits raise ValueError, as the distribution's argument validation does
+    (checked only once the draw has failed on them)."""
+    normalized = logits - logits.logsumexp(-1, keepdim=True)
+    try:
+        drawn = torch.multinomial(torch.softmax(normalized, -1).reshape(1, -1), 1, True)
+    except RuntimeError:
+        if bool(torch.isnan(logits).any()):
+            raise ValueError("Expected parameter logits to satisfy the constraint "
+                             f"IndependentConstraint(Real(), 1), but found invalid values:\n{logits}")
+        raise
+    action = int(drawn[0, 0])
+    return action, normalized[action].clone()
+
+
 def cartpole_sizes(env) -> tuple[int, int]:
     """rl/deep/agents/common.py:82-87 for duck-typed spaces: a Box-like
     observation space (has .shape) and a Discrete-like action space (has .n);
@@ -143,8 +166,8 @@ class PPOAgent:
     takes the fused minibatch step described in the module docstring;
     `graphs` (default True) lets the fused loop replay captured graphs for
     episodes of a length seen in the previous update.  Both follow the
-    reference's randomness: actions are sampled by a CPU Categorical and the
-    minibatches come from torch.randperm, both on the global CPU generator,
+    reference's randomness: actions are drawn as a CPU Categorical draws them
+    (sample_categorical) and the minibatches come from torch.randperm, both on the global CPU generator,
     so one seed gives the reference's trajectories and index stream."""
 
     name = "ppo"
@@ -208,9 +231,9 @@ class PPOAgent:
     @torch.no_grad()
     def select_action(self, observation: np.ndarray, training: bool = True) -> int:
         """ppo.py:65-79.  The networks run on the device and the logits and
-        the value come back to the host in one copy; sampling uses a CPU
-        Categorical so the global CPU generator is consumed as in the
-        reference.  log_prob and value are 0-d CPU tensors, as there."""
+        the value come back to the host in one copy; the action is drawn with
+        a Categorical's operations on the host (sample_categorical), so the
+        global CPU generator is consumed as in the reference.  log_prob and value are 0-d CPU tensors, as there."""
         A = self.action_count
         if self._fused_act and np.ndim(observation) == 1 and self._act_ready():
             logits, value = self._forward_pinned(observation)
@@ -221,15 +244,9 @@ class PPOAgent:
         if not training:
             return int(torch.argmax(logits).item())
 
-        # (validation only raises on invalid logits; skipping it changes no
-        # result and no generator draw)
-        distribution = Categorical(logits=logits, validate_args=False)
-        action = distribution.sample()
-        self.pending_step = PendingStep(
-            log_prob=distribution.log_prob(action),
-            value=value,
-        )
-        return int(action.item())
+        action, log_prob = sample_categorical(logits)
+        self.pending_step = PendingStep(log_prob=log_prob, value=value)
+        return action
 
     def _act_ready(self) -> bool:
         """The networks are still ones the fused forward runs (checked again
