@@ -216,6 +216,8 @@ class PPOAgent:
             self.optimizer = torch.optim.Adam(self.parameters, lr=config.lr)
         self.graphs = graphs
         self._stage: dict = {}  # rollout length -> persistent device arrays (graph replays)
+        self._host: Optional[torch.Tensor] = None  # pinned staging buffer of _upload_rollout
+        self._host_ready = None  # event: the last upload has read _host
         self._last_n = -1
         self._act_ctx = None  # select_action's launch arguments and pinned buffer
         self._act_ids: tuple = ()
@@ -332,41 +334,33 @@ class PPOAgent:
         """ppo.py:113-139 with the GAE, normalisation and loss on the GPU.
         The permutation comes from torch.randperm on the global CPU
         generator, as at :130, so the minibatch index stream is the
-        reference's bit for bit."""
+        reference's bit for bit.  The rollout's arrays reach the device in
+        one copy (_upload_rollout)."""
         dev = self.device
-        observations = torch.as_tensor(
-            np.array([step.transition.observation for step in self.rollout]),
-            dtype=torch.float32,
-        ).to(dev)
-        actions_host = torch.as_tensor(
-            [step.transition.action for step in self.rollout], dtype=torch.int64
-        )
-        action_count = self.policy.net[-1].out_features
-        # checked on the host copy (no device synchronisation); torch.
-        # distributions' support check raises this inside :151
-        if bool(((actions_host < 0) | (actions_host >= action_count)).any()):
-            raise ValueError(
-                "The value argument must be within the support of the categorical "
-                f"distribution (actions in [0, {action_count}))"
-            )
-        actions = actions_host.to(dev)
-        old_log_probs = torch.stack([step.log_prob for step in self.rollout]).to(dev)
-        old_values = torch.stack([step.value for step in self.rollout]).to(
-            device=dev, dtype=torch.float32
-        )
-        advantages = self._advantages(old_values)
-        returns = advantages + old_values
-
-        if len(advantages) > 1:
-            advantages = ops.normalize_advantages(advantages)
+        staged = self._upload_rollout()
+        observations, actions = staged["obs"], staged["act"]
+        old_log_probs, old_values = staged["lp"], staged["val"]
+        fused = self.fused_update and "_update_batch" not in self.__dict__ and (
+            type(self)._update_batch is PPOAgent._update_batch)
+        if fused and "_advantages" not in self.__dict__ and (
+                type(self)._advantages is PPOAgent._advantages):
+            # :123-127 in one launch: advantages, returns = advantages +
+            # old_values, and the normalised advantages written over the raw
+            # ones (the identity for a single step, as the :126 guard)
+            advantages, returns, _ = ops.gae_normalize(
+                staged["rew"], old_values, staged["done"], None, self.config.gamma,
+                self.ppo_config.gae_lambda, out=(staged["adv"], staged["ret"]), keep_raw=False)
+        else:
+            advantages = self._advantages(old_values)
+            returns = advantages + old_values
+            if len(advantages) > 1:
+                advantages = ops.normalize_advantages(advantages)
 
         # The fused loop stands in for the minibatch loop below unless
         # _update_batch was replaced (a subclass or an instance attribute),
         # in which case that method is what must run per minibatch.
-        if self.fused_update and "_update_batch" not in self.__dict__ and (
-                type(self)._update_batch is PPOAgent._update_batch):
-            self._update_fused(observations, actions, old_log_probs.reshape(-1),
-                               advantages, returns, old_values)
+        if fused:
+            self._update_fused(staged, advantages, returns)
             return
 
         for _ in range(self.ppo_config.epochs):
@@ -388,28 +382,100 @@ class PPOAgent:
         if dev.type == "cuda":
             ops.check_waits(dev)
 
-    def _update_fused(self, observations, actions, old_log_probs, advantages, returns,
-                      old_values) -> None:
+    def _upload_rollout(self) -> dict:
+        """The rollout's observations [n,D] fp32, actions [n] int64, old
+        log-probabilities, old values and rewards [n] fp32 and done flags
+        (terminated or truncated) [n] uint8, written into one pinned host
+        buffer and copied to the device in one transfer (ppo.py:114-122, and
+        the rewards and flags :173-193 reads), into device arrays kept per
+        rollout length (the two most recent lengths), with room for the
+        advantages and returns: a repeated length reuses the addresses its
+        captured graphs read.  Out-of-range actions raise ValueError here,
+        checked on the host (torch.distributions' support check raises it
+        inside :151)."""
+        steps = self.rollout
+        n = len(steps)
+        D = int(np.asarray(steps[0].transition.observation).size) if n else 0
+        # byte offsets of the arrays, each 16-byte aligned
+        sizes = (("obs", n * D * 4), ("lp", n * 4), ("val", n * 4), ("rew", n * 4),
+                 ("act", n * 8), ("done", n))
+        offsets, nbytes = {}, 0
+        for name, size in sizes:
+            offsets[name] = nbytes
+            nbytes += (size + 15) // 16 * 16
+        if self._host is None or self._host.numel() < nbytes:
+            self._host = torch.empty(max(nbytes, 2 * (0 if self._host is None else
+                                                          self._host.numel())),
+                                     dtype=torch.uint8, pin_memory=self.device.type == "cuda")
+        elif self._host_ready is not None:
+            self._host_ready.synchronize()  # the previous upload has read the buffer
+
+        def views(buf):
+            def f32(name, *shape):
+                o = offsets[name]
+                return buf[o : o + 4 * int(np.prod(shape))].view(torch.float32).view(*shape)
+
+            return {"obs": f32("obs", n, D), "lp": f32("lp", n), "val": f32("val", n),
+                    "rew": f32("rew", n),
+                    "act": buf[offsets["act"] : offsets["act"] + 8 * n].view(torch.int64),
+                    "done": buf[offsets["done"] : offsets["done"] + n]}
+
+        host = views(self._host)
+        if n:
+            np.stack([s.transition.observation for s in steps], out=host["obs"].numpy(),
+                     casting="unsafe")
+        acts = host["act"].numpy()
+        acts[:] = [s.transition.action for s in steps]
+        A = self.policy.net[-1].out_features
+        if n and (acts.min() < 0 or acts.max() >= A):
+            raise ValueError(
+                "The value argument must be within the support of the categorical "
+                f"distribution (actions in [0, {A}))"
+            )
+        for key, attr in (("lp", "log_prob"), ("val", "value")):
+            parts = [getattr(s, attr) for s in steps]
+            if parts[0].dim() == 0:  # (stack needs equal shapes: all 0-d)
+                torch.stack(parts, out=host[key])
+            else:  # e.g. [1]-shaped
+                host[key].copy_(torch.stack(parts).reshape(n))
+        host["rew"].numpy()[:] = [s.transition.reward for s in steps]
+        host["done"].numpy()[:] = [bool(s.transition.terminated or s.transition.truncated)
+                                   for s in steps]
+
+        stage = self._stage.pop(n, None)
+        if stage is None:
+            buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            stage = views(buf)
+            stage["buf"] = buf
+            stage["adv"] = torch.empty(n, dtype=torch.float32, device=self.device)
+            stage["ret"] = torch.empty(n, dtype=torch.float32, device=self.device)
+        self._stage[n] = stage  # most recent last
+        while len(self._stage) > 2:
+            self._stage.pop(next(iter(self._stage)))
+        stage["buf"].copy_(self._host[:nbytes], non_blocking=True)
+        if self.device.type == "cuda":
+            if self._host_ready is None:
+                self._host_ready = torch.cuda.Event()
+            self._host_ready.record()
+        return stage
+
+    def _update_fused(self, staged: dict, advantages: torch.Tensor,
+                      returns: torch.Tensor) -> None:
         """ppo.py:129-171 as VecPPO's fused minibatch loop over the episode's
         arrays: the same torch.randperm draws on the global CPU generator
         (all epochs drawn before the first minibatch, which consumes the
         generator identically: nothing between the reference's draws uses
         it), one upload, two launches per minibatch, one wait-status check.
-        An episode as long as the previous one is copied into that length's
-        persistent arrays and its loop replayed from graphs."""
-        n = observations.shape[0]
-        arrays = (observations, actions, old_log_probs, advantages, returns, old_values)
+        An episode as long as the previous one has the same device arrays
+        (_upload_rollout), and its loop is replayed from graphs."""
+        n = staged["obs"].shape[0]
+        if advantages.data_ptr() != staged["adv"].data_ptr():
+            staged["adv"].copy_(advantages)
+        if returns.data_ptr() != staged["ret"].data_ptr():
+            staged["ret"].copy_(returns)
+        arrays = (staged["obs"], staged["act"], staged["lp"], staged["adv"], staged["ret"],
+                  staged["val"])
         use_graphs = self.graphs and n == self._last_n
-        if self.graphs:
-            stage = self._stage.pop(n, None)
-            if stage is None:
-                stage = tuple(torch.empty_like(x) for x in arrays)
-            self._stage[n] = stage  # most recent last
-            while len(self._stage) > 2:
-                self._stage.pop(next(iter(self._stage)))
-            for dst, src in zip(stage, arrays):
-                dst.copy_(src)
-            arrays = stage
         self._last_n = n
         self._vec.update_flat(arrays, self.device, graphs=use_graphs)
 
