@@ -235,9 +235,11 @@ __device__ __forceinline__ void wgrad_tile(const float* d, int ldd, int M, const
   }
 }
 
-// Bias gradient: gb[m] = sum over the 16 rows of d[r][m], threads t < M.
+// Bias gradient: gb[m] = sum over the 16 rows of d[r][m], threads t < M of a
+// kBlock-thread workgroup.
+template <int kBlock>
 __device__ __forceinline__ void bgrad(const float* d, int ldd, int M, float* __restrict__ gb) {
-  for (int m = threadIdx.x; m < M; m += kMlpBlock) {
+  for (int m = threadIdx.x; m < M; m += kBlock) {
     float s = 0.0f;
 #pragma unroll
     for (int r = 0; r < kMlpRows; ++r) s += d[r * ldd + m];
@@ -251,7 +253,7 @@ __device__ __forceinline__ void bgrad(const float* d, int ldd, int M, float* __r
 // between the phases (the gradient partials go to global memory and are read
 // by the next kernel); phase 3 leaves without one (the caller's next phase
 // must not write g1 before a barrier).
-template <int H, int kAct>
+template <int H, int kAct, int kBlock>
 __device__ __forceinline__ void net_backward(const MlpNet& net, const NetOffsets& o, float* gp,
                                              const float* d3, int ld3, int M3, const float* x,
                                              int D, const float* h1, const float* h2, float* g1,
@@ -259,27 +261,27 @@ __device__ __forceinline__ void net_backward(const MlpNet& net, const NetOffsets
   constexpr int ld = act_ld<H>();
   constexpr int NT = H / 16;
   const int w = threadIdx.x / kWave;
-  constexpr int kWaves = kMlpBlock / kWave;
+  constexpr int kWaves = kBlock / kWave;
   const int MT3 = (M3 + 15) / 16;
   // phase 1
   for (int t = w; t < MT3 * NT + NT; t += kWaves) {
     if (t < MT3 * NT) wgrad_tile(d3, ld3, M3, h2, ld, H, gp + o.w[2], t / NT, t % NT);
     else back_tile<H, 0, kAct>(d3, ld3, M3, net.w[2], net.ldw[2], h2, g2, t - MT3 * NT);
   }
-  bgrad(d3, ld3, M3, gp + o.b[2]);
+  bgrad<kBlock>(d3, ld3, M3, gp + o.b[2]);
   lds_barrier();
   // phase 2
   for (int t = w; t < NT * NT + NT; t += kWaves) {
     if (t < NT * NT) wgrad_tile(g2, ld, H, h1, ld, H, gp + o.w[1], t / NT, t % NT);
     else back_tile<H, H, kAct>(g2, ld, H, net.w[1], net.ldw[1], h1, g1, t - NT * NT);
   }
-  bgrad(g2, ld, H, gp + o.b[1]);
+  bgrad<kBlock>(g2, ld, H, gp + o.b[1]);
   lds_barrier();
   // phase 3
   const int DT = (D + 15) / 16;
   for (int t = w; t < NT * DT; t += kWaves)
     wgrad_tile(g1, ld, H, x, kXld, D, gp + o.w[0], t / DT, t % DT);
-  bgrad(g1, ld, H, gp + o.b[0]);
+  bgrad<kBlock>(g1, ld, H, gp + o.b[0]);
 }
 
 // Forward of both networks for the workgroup's 16 rows x (observations in
@@ -382,13 +384,13 @@ __device__ __forceinline__ MlpNet stage_net(const MlpNet& g, int D, int O, float
 // Forward of one network for the workgroup's 16 rows (observations in x):
 // hidden activations into h1/h2, the O outputs into out [16][ldout].  Column
 // tiles over the waves; LDS-only barriers between the layers and after the
-// last.
-template <int H, int kAct>
+// last.  kBlock threads.
+template <int H, int kAct, int kBlock>
 __device__ __forceinline__ void net_forward(const MlpNet& net, const float* x, int D, int O,
                                             float* h1, float* h2, float* out, int ldout) {
   constexpr int ld = act_ld<H>();
   constexpr int NT = H / 16;
-  constexpr int kWaves = kMlpBlock / kWave;
+  constexpr int kWaves = kBlock / kWave;
   const int w = threadIdx.x / kWave;
   for (int t = w; t < NT; t += kWaves)
     fwd_tile<0, kAct>(x, kXld, D, net.w[0], net.ldw[0], net.b[0], H, h1, ld, t);
@@ -409,8 +411,19 @@ __device__ __forceinline__ void net_forward(const MlpNet& net, const float* x, i
 // gpart row b; the policy / entropy / kl / clip-fraction sums and the value
 // sum of spart column b), so the reduction sees exactly the values one
 // workgroup doing both networks would leave.
+//
+// Workgroups of grad_block<H>() threads: at H = 128 (weights read from
+// global memory, not staged in LDS) 16 waves, so that each wave takes a
+// quarter of the tiles it would among 4 (measured on MI355X, minibatches of
+// 128 rows: 20.1 -> 16.0 us per launch).
+template <int H>
+constexpr int grad_block() {
+  return H == 128 ? 1024 : kMlpBlock;
+}
+
 template <int H, int kAct>
-__global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
+__global__ void __launch_bounds__(grad_block<H>()) mlp_cat_grad_kernel(MlpArgs a) {
+  constexpr int kBlock = grad_block<H>();
   constexpr int R = kMlpRows;
   constexpr int ld = act_ld<H>();
   __shared__ float s_x[R * kXld];
@@ -428,6 +441,7 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   // this workgroup's network, its weights staged in LDS when they fit
   constexpr bool kStage = H <= kMlpLdsMaxH;
   __shared__ __attribute__((aligned(16))) float s_w[kStage ? net_lds_floats<H>() : 1];
+  static_assert(!kStage || kBlock == kMlpBlock, "stage_net strides by kMlpBlock");
   MlpNet net = critic ? a.critic : a.actor;
   if constexpr (kStage) net = stage_net<H>(net, D, critic ? 1 : A, s_w);
   // the loss inputs of row `tid` (tid < R) are loaded now, ahead of the
@@ -451,15 +465,15 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   }
   lds_barrier();
   // gather the observation rows (padding rows past B are zeros)
-  for (int e = tid; e < R * D; e += kMlpBlock) {
+  for (int e = tid; e < R * D; e += kBlock) {
     const int r = e / D, c = e - (e / D) * D;
     const long src = s_row[r];
     s_x[r * kXld + c] = (src >= 0 && src < a.n) ? a.obs[src * D + c] : 0.0f;
   }
   lds_barrier();
 
-  if (critic) net_forward<H, kAct>(net, s_x, D, 1, s_h1, s_h2, s_v, 1);
-  else net_forward<H, kAct>(net, s_x, D, A, s_h1, s_h2, s_z, kZld);
+  if (critic) net_forward<H, kAct, kBlock>(net, s_x, D, 1, s_h1, s_h2, s_v, 1);
+  else net_forward<H, kAct, kBlock>(net, s_x, D, A, s_h1, s_h2, s_z, kZld);
 
   // loss rows: logits -> dlogits in place (actor), value -> dvalue in place
   // (critic; the value terms do not depend on the log-prob, which is given
@@ -502,8 +516,10 @@ __global__ void __launch_bounds__(kMlpBlock) mlp_cat_grad_kernel(MlpArgs a) {
   }
 
   float* gp = a.gpart + blk * a.P;
-  if (critic) net_backward<H, kAct>(net, a.oc, gp, s_v, 1, 1, s_x, D, s_h1, s_h2, s_g1, s_g2);
-  else net_backward<H, kAct>(net, a.oa, gp, s_z, kZld, A, s_x, D, s_h1, s_h2, s_g1, s_g2);
+  if (critic)
+    net_backward<H, kAct, kBlock>(net, a.oc, gp, s_v, 1, 1, s_x, D, s_h1, s_h2, s_g1, s_g2);
+  else
+    net_backward<H, kAct, kBlock>(net, a.oa, gp, s_z, kZld, A, s_x, D, s_h1, s_h2, s_g1, s_g2);
 }
 
 // Action selection through both networks (ppo.py:65-79 for N observations):
@@ -944,6 +960,7 @@ NetOffsets net_offsets(long base, int D, int H, int O) {
 
 struct MlpLayout {
   long P, nblocks, rblocks;
+  int threads;  // of the gradient kernel's workgroups
   long tblk[kMlpTensors + 1], toff[kMlpTensors], tnum[kMlpTensors];
   size_t gpart, spart, sqpart, sync, total;
 };
@@ -951,6 +968,7 @@ struct MlpLayout {
 MlpLayout mlp_layout(long B, int D, int H, int A) {
   MlpLayout l;
   l.P = mlp_params(D, H, A) + mlp_params(D, H, 1);
+  l.threads = H == 128 ? grad_block<128>() : kMlpBlock;
   l.nblocks = (B + kMlpRows - 1) / kMlpRows;
   const NetOffsets o[2] = {net_offsets(0, D, H, A), net_offsets(mlp_params(D, H, A), D, H, 1)};
   const int outs[2] = {A, 1};
@@ -1133,7 +1151,7 @@ int mlp_setup(const ppo_mlp3_f32* actor, const ppo_mlp3_f32* critic, int32_t obs
 // The gradient kernel (two workgroups per 16-row block) and the reduction.
 int mlp_launch(const void* kern, MlpArgs& a, const MlpLayout& l, hipStream_t stream) {
   void* args[] = {&a};
-  int st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(kMlpBlock),
+  int st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(l.threads),
                                       args, 0, stream));
   if (st) return st;
   const bool wide = l.nblocks >= kRedWideRows;
@@ -1219,7 +1237,7 @@ extern "C" int ppo_mlp_cat_step_f32(const ppo_mlp3_f32* actor, const ppo_mlp3_f3
     u.nonce = next_nonce();
     if ((st = wait_ctl(u.wc))) return st;
     void* gargs[] = {&a};
-    if ((st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(kMlpBlock),
+    if ((st = hip_status(hipLaunchKernel(kern, dim3((unsigned)(2 * l.nblocks)), dim3(l.threads),
                                          gargs, 0, stream))))
       return st;
     void* fargs[] = {&a, &u};
