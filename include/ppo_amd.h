@@ -155,7 +155,7 @@ int ppo_gae_f32(const float* rewards, const float* values, const uint8_t* dones,
  * GAE pass and rounded to fp32; the final expression is evaluated in fp32.
  * adv_norm_out may alias adv_out (normalisation in place, as ppo.py:127 keeps
  * only the normalised advantages; the unnormalised ones are then not stored at
- * all on the single-launch route, which saves a quarter of the writes).
+ * all on the single-launch route, which saves a third of the writes).
  * stats_out (may be NULL) receives {mean, std} as two floats.
  */
 int ppo_gae_norm_f32(const float* rewards, const float* values,
