@@ -791,6 +791,7 @@ def main():
             "avg_launch_us": round(t_loss * 1e6, 2),
         },
         "gae_norm": {
+            "form": "normalised in place (adv_norm_out = adv_out; no raw-advantage store)",
             "avg_call_us": round(t_gae * 1e6, 2),
             "bytes_per_sample": GAE_INPLACE_BYTES,
             "achieved_GBs": round(GAE_INPLACE_BYTES * B / t_gae / 1e9, 1),
