@@ -138,3 +138,58 @@ def test_sample_categorical_rejects_nan_logits_like_the_distribution():
         Categorical(logits=bad)
     with pytest.raises(ValueError):
         sample_categorical(bad)
+
+
+def _steps(n, obs_dim=4, shape=()):
+    from ppo_amd.agent import RolloutStep, Transition
+
+    g = torch.Generator().manual_seed(n)
+    out = []
+    for t in range(n):
+        obs = torch.rand(obs_dim, generator=g).numpy().astype(np.float64)
+        tr = Transition(observation=obs, action=int(t % 2), reward=0.5 * t,
+                        next_observation=obs, terminated=t == n - 1, truncated=t == n // 2)
+        out.append(RolloutStep(tr, log_prob=torch.randn(shape, generator=g),
+                               value=torch.randn(shape, generator=g)))
+    return out
+
+
+@pytest.mark.parametrize("n,shape", [(1, ()), (37, ()), (37, (1,)), (500, ())])
+def test_upload_rollout_packs_every_array(n, shape):
+    """PPOAgent._upload_rollout (one pinned buffer, one copy; on a CPU agent
+    the same packing into host memory) holds ppo.py:114-122's arrays and the
+    rewards and done flags :173-193 reads, with the dtypes the kernels take."""
+    agent = PPOAgent(cartpole_like(), TrainingConfig(hidden_size=16), device="cpu")
+    agent.rollout = _steps(n, shape=shape)
+    st = agent._upload_rollout()
+    steps = agent.rollout
+    assert st["obs"].dtype == torch.float32 and st["obs"].shape == (n, 4)
+    assert torch.equal(st["obs"], torch.as_tensor(
+        np.array([s.transition.observation for s in steps]), dtype=torch.float32))
+    assert st["act"].dtype == torch.int64
+    assert st["act"].tolist() == [s.transition.action for s in steps]
+    assert torch.equal(st["lp"], torch.stack([s.log_prob for s in steps]).reshape(n))
+    assert torch.equal(st["val"], torch.stack([s.value for s in steps]).reshape(n))
+    assert st["rew"].tolist() == [s.transition.reward for s in steps]
+    assert st["done"].dtype == torch.uint8
+    assert st["done"].tolist() == [int(s.transition.terminated or s.transition.truncated)
+                                   for s in steps]
+    for a in ("obs", "lp", "val", "rew", "act", "done"):
+        assert st[a].data_ptr() % 16 == 0, a
+    # a second episode of the same length reuses the same arrays
+    agent.rollout = _steps(n, shape=shape)[::-1]
+    st2 = agent._upload_rollout()
+    assert st2["obs"].data_ptr() == st["obs"].data_ptr()
+    assert st2["act"].tolist() == [s.transition.action for s in agent.rollout]
+
+
+def test_upload_rollout_rejects_out_of_range_actions():
+    agent = PPOAgent(cartpole_like(), TrainingConfig(hidden_size=16), device="cpu")
+    steps = _steps(5)
+    from ppo_amd.agent import RolloutStep
+
+    steps[3] = RolloutStep(steps[3].transition.__class__(
+        **{**steps[3].transition.__dict__, "action": 2}), steps[3].log_prob, steps[3].value)
+    agent.rollout = steps
+    with pytest.raises(ValueError, match="support"):
+        agent._upload_rollout()
