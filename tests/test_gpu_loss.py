@@ -551,3 +551,24 @@ def test_cat_past_2_31_elements(dev):
         del sc, dlc, dvc
     # every scalar is linear in the chunks' (fp32-rounded) means
     torch.testing.assert_close(scalars.double().cpu(), weighted, rtol=2e-5, atol=1e-6)
+
+
+def test_empty_batches_raise_like_the_reference(dev):
+    """A minibatch of no rows: the reference's Categorical / Normal on an
+    empty batch raises (torch cannot validate a [0, A] tensor, and the means
+    of ppo.py:159-167 would be NaN); the fused losses raise ValueError before
+    any launch, also for A = 0 or D = 0."""
+    e = torch.zeros(0, device=dev)
+    with pytest.raises(ValueError, match="B > 0"):
+        ppo_amd.ppo_loss_discrete(torch.zeros(0, 18, device=dev),
+                                  torch.zeros(0, dtype=torch.int32, device=dev), e, e, e, e)
+    with pytest.raises(ValueError, match="A > 0"):
+        z = torch.zeros(4, device=dev)
+        ppo_amd.ppo_loss_discrete(torch.zeros(4, 0, device=dev),
+                                  torch.zeros(4, dtype=torch.int32, device=dev), z, z, z, z)
+    with pytest.raises(ValueError, match="B > 0"):
+        ppo_amd.ppo_loss_gaussian(torch.zeros(0, 6, device=dev), torch.zeros(6, device=dev),
+                                  torch.zeros(0, 6, device=dev), e, e, e, e)
+    with pytest.raises(Exception):
+        torch.distributions.Categorical(logits=torch.zeros(0, 18)).log_prob(
+            torch.zeros(0, dtype=torch.int64))
