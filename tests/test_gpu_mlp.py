@@ -81,6 +81,8 @@ def _check(dev, n, D, H, A, act, B, seed, vf_clip=None, act64=False, use_index=T
         (64, 6, 16, 3, "tanh", 64),        # H = 16
         (5000, 4, 64, 2, "tanh", 4096),    # a large minibatch (256 workgroups)
         (50, 3, 128, 32, "relu", 1),       # one row, the widest action set
+        (300, 7, 128, 9, "tanh", 37),      # H = 128 (16-wave workgroups), a partial block
+        (5000, 4, 128, 2, "relu", 4096),   # H = 128, 256 row blocks
     ],
 )
 def test_mlp_grads_match_oracle(dev, n, D, H, A, act, B):
