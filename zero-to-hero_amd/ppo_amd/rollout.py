@@ -130,8 +130,9 @@ class VecPPO:
     categorical and both networks are MLPs that ops.mlp_fusable accepts) each
     minibatch's gather, MLP forwards, loss and backward are the two launches
     of ops.ppo_mlp_cat_grads, which write the parameters' gradients directly,
-    and the clip + Adam step joins them (ops.ppo_mlp_cat_step: three
-    launches per minibatch).
+    and the clip + Adam step joins the second (ops.ppo_mlp_cat_step: two
+    launches per minibatch, three when the reduction's grid cannot be
+    resident at once).
 
     With `graphs=True` (requires `fused_update`) the minibatch loop is replayed
     from CUDA/HIP graphs: the whole update runs on a private stream; the
