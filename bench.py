@@ -3,8 +3,9 @@
 A "step" is one pass of the PPO update hot path over one synthetic rollout of
 T x N = 2048 x 4096 = 8,388,608 samples (the benchmark's GAE + normalise rollout):
   1. ppo_gae_norm_f32  — GAE with bootstrap + returns + advantage
-                         normalisation (rl/deep/agents/ppo.py:123-127), the
-                         normalised advantages written over the raw ones
+                         normalisation (rl/deep/agents/ppo.py:123-127): the
+                         advantages, returns and normalised advantages of
+                         BASELINE config 2
   2. ppo_loss_cat_f32  — fused categorical PPO loss forward+backward over all
                          B = T*N samples, A = 18 actions, vf_clip = 0.2
                          (ppo.py:150-169; A = 18, value clipping 0.2)
@@ -103,9 +104,10 @@ ROLLOUT_KEYS = ("rewards", "values", "dones", "last_value")
 class Step:
     """The two C-ABI calls of one update step, on torch's current stream,
     with preallocated outputs (nothing allocated inside the timed loop).
-    The advantages are normalised in place, as ppo.py:127 keeps only the
-    normalised ones: the GAE call writes the returns and the normalised
-    advantages (17 bytes per sample with its inputs).
+    The GAE call writes all three outputs BASELINE config 2 names
+    (advantages, returns, normalised advantages: 21 bytes per sample with its
+    inputs); `--suite` also times the in-place form the library's own update
+    loop uses (config2_gae_norm_in_place).
 
     With copies > 1 the step keeps that many copies of the rollout (rewards,
     values, dones, last value: 75 MB each at T x N = 2048 x 4096) and next()
@@ -126,6 +128,7 @@ class Step:
         B, A = x["logits"].shape
         self.T, self.N, self.B, self.A = T, N, B, A
         f32 = dict(dtype=torch.float32, device=dev)
+        self.adv = torch.empty(T, N, **f32)
         self.ret = torch.empty(T, N, **f32)
         self.adv_n = torch.empty(T, N, **f32)
         self.stats = torch.empty(2, **f32)
@@ -147,7 +150,7 @@ class Step:
         rc = self.lib.ppo_gae_norm_f32(
             x["rewards"].data_ptr(), x["values"].data_ptr(), x["dones"].data_ptr(),
             x["last_value"].data_ptr(), self.T, self.N, 0.99, 0.95, 1e-8,
-            self.adv_n.data_ptr(), self.ret.data_ptr(), self.adv_n.data_ptr(),
+            self.adv.data_ptr(), self.ret.data_ptr(), self.adv_n.data_ptr(),
             self.stats.data_ptr(), self.ws_gae.data_ptr(), self.ws_gae.numel(), self.stream)
         if rc:
             raise RuntimeError(f"ppo_gae_norm_f32 returned {rc}")
@@ -446,7 +449,7 @@ def suite(torch, lib, dev, stream_timing=True, cpu=True):
     out.append(("north_star_A2_loss", st.B, LOSS_CAT_A2_BYTES,
                 time_events(torch, st.loss, 30, flush),
                 time_stream(torch, [s_.loss for s_ in steps], 8) if stream_timing else None))
-    out.append(("north_star_A2_step", st.B, GAE_INPLACE_BYTES + LOSS_CAT_A2_BYTES,
+    out.append(("north_star_A2_step", st.B, GAE_BYTES + LOSS_CAT_A2_BYTES,
                 time_events(torch, lambda: (st.gae(), st.loss()), 30, flush),
                 time_stream(torch, [lambda s_=s_: (s_.gae(), s_.loss()) for s_ in steps], 8)
                 if stream_timing else None))
@@ -791,11 +794,10 @@ def main():
             "avg_launch_us": round(t_loss * 1e6, 2),
         },
         "gae_norm": {
-            "form": "normalised in place (adv_norm_out = adv_out; no raw-advantage store)",
             "avg_call_us": round(t_gae * 1e6, 2),
-            "bytes_per_sample": GAE_INPLACE_BYTES,
-            "achieved_GBs": round(GAE_INPLACE_BYTES * B / t_gae / 1e9, 1),
-            "frac": round(GAE_INPLACE_BYTES * B / t_gae / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_sample": GAE_BYTES,
+            "achieved_GBs": round(GAE_BYTES * B / t_gae / 1e9, 1),
+            "frac": round(GAE_BYTES * B / t_gae / 1e9 / HBM_PEAK_GBS, 4),
         },
         "cpu_baseline": cpu,
     }

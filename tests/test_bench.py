@@ -36,8 +36,7 @@ def _bytes_per_element(name):
 
 
 def test_gae_profiles_traffic_near_algorithmic_bytes():
-    # 17 algorithmic bytes per element each (the step's GAE call normalises in
-    # place: no raw-advantage store); the resident pass re-reads only each
-    # segment's following value row and its slots
-    assert 17.0 <= _bytes_per_element("gae_norm_config2") <= 19.0
+    # 21 and 17 algorithmic bytes per element; the resident pass re-reads
+    # only each segment's following value row and its slots
+    assert 21.0 <= _bytes_per_element("gae_norm_config2") <= 23.0
     assert 17.0 <= _bytes_per_element("gae_resident_config3") <= 20.0
